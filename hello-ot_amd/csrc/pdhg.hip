@@ -1,0 +1,563 @@
+// Restricted-OT Halpern-PDHG on gfx950.
+//
+// Algorithm: _native/cpp/solver.cpp:39-378 (= _internal/lp/torch_restricted_ot.py:105-393; the same update
+// CuPDLPx runs in cupdlpx/solver.cu:581-715): degree-sqrt constraint scaling, variable scale sqrt(2),
+// constant step 0.998, reflected Halpern iterations, PID primal-weight restarts and relative L2 KKT checks
+// every `evaluation_frequency` iterations.
+//
+// Device layout: per edge e (x_e >= 0): endpoints (int32), scaled cost cs, iterate x, anchor ax, PDHG point px
+// (stored only when the next iteration evaluates), reflection rx, checkpoint delta dx. Per node (sources then
+// targets): scale, bs, ns, y, ay, py, dy and the target duals td = y / ns. Each node's incident edges are
+// listed in ascending edge id (stable radix sort), so every per-node sum runs in the same order as the CPU
+// restatement; only the global norms/dots use a fixed-shape tree.
+//
+// One iteration = edge pass (primal projection, reflection, Halpern) + node pass (A * reflected primal,
+// dual update, reflection, Halpern). Scalars read back to the host only at evaluations and checkpoints.
+#include <hipcub/hipcub.hpp>
+
+#include <chrono>
+#include <vector>
+
+#include "common.h"
+
+namespace hm {
+namespace {
+
+constexpr int RB = 1024;     // blocks of the fixed-shape reductions
+constexpr int RT = 256;      // threads per reduction block
+
+struct Pdhg {
+    int64_t n, nt, nodes, e;
+    // edges
+    int32_t *row, *col;
+    double *cs, *x, *ax, *px, *rx, *dx;
+    // nodes
+    double *scale, *bs, *ns, *y, *ay, *py, *dy, *td;
+    int32_t *deg, *off, *eid;
+    // sort scratch
+    uint32_t *keys_in, *keys_out;
+    int32_t *vals_in;
+    void* sort_tmp;
+    size_t sort_tmp_bytes;
+    // reductions
+    double* partial;   // RB * 4
+    double* result;    // 4
+    int* flag;         // 1
+};
+
+template <class A>
+void pdhg_layout(A& a, int64_t n, int64_t nt, int64_t e, size_t sort_tmp, Pdhg& P) {
+    const int64_t nodes = n + nt;
+    P.row = a.template take<int32_t>(e);
+    P.col = a.template take<int32_t>(e);
+    P.cs = a.template take<double>(e);
+    P.x = a.template take<double>(e);
+    P.ax = a.template take<double>(e);
+    P.px = a.template take<double>(e);
+    P.rx = a.template take<double>(e);
+    P.dx = a.template take<double>(e);
+    P.scale = a.template take<double>(nodes);
+    P.bs = a.template take<double>(nodes);
+    P.ns = a.template take<double>(nodes);
+    P.y = a.template take<double>(nodes);
+    P.ay = a.template take<double>(nodes);
+    P.py = a.template take<double>(nodes);
+    P.dy = a.template take<double>(nodes);
+    P.td = a.template take<double>(nt);
+    P.deg = a.template take<int32_t>(nodes + 1);
+    P.off = a.template take<int32_t>(nodes + 1);
+    P.eid = a.template take<int32_t>(2 * e);
+    P.keys_in = a.template take<uint32_t>(2 * e);
+    P.keys_out = a.template take<uint32_t>(2 * e);
+    P.vals_in = a.template take<int32_t>(2 * e);
+    P.sort_tmp = a.template take<char>(sort_tmp > 0 ? sort_tmp : 1);
+    P.sort_tmp_bytes = sort_tmp;
+    P.partial = a.template take<double>((size_t)RB * 4);
+    P.result = a.template take<double>(4);
+    P.flag = a.template take<int>(4);
+}
+
+inline int end_bit_for(int64_t nodes) {
+    int b = 1;
+    while (b < 32 && (int64_t(1) << b) < nodes) ++b;
+    return b;
+}
+
+inline size_t sort_tmp_bytes(int64_t nodes, int64_t e) {
+    size_t bytes = 0;
+    hipcub::DeviceRadixSort::SortPairs(nullptr, bytes, (const uint32_t*)nullptr, (uint32_t*)nullptr,
+                                       (const int32_t*)nullptr, (int32_t*)nullptr, (int)(2 * e), 0,
+                                       end_bit_for(nodes));
+    return bytes;
+}
+
+// ---------------------------------------------------------------------------------------------------------
+// setup kernels
+// ---------------------------------------------------------------------------------------------------------
+__global__ void k_fill_i32(int32_t* p, int64_t count, int32_t v) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < count; i += (int64_t)gridDim.x * blockDim.x)
+        p[i] = v;
+}
+
+__global__ void k_edges(const int64_t* __restrict__ rows, const int64_t* __restrict__ cols, int64_t e, int64_t n,
+                        int64_t nt, int32_t* __restrict__ row, int32_t* __restrict__ col, int32_t* __restrict__ deg,
+                        uint32_t* __restrict__ keys, int32_t* __restrict__ vals, int* __restrict__ flag) {
+    for (int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; j < e; j += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t r = rows[j], c = cols[j];
+        if (r < 0 || r >= n || c < 0 || c >= nt) {
+            atomicOr(flag, 1);
+            row[j] = 0;
+            col[j] = 0;
+            keys[j] = 0;
+            keys[e + j] = (uint32_t)n;
+        } else {
+            row[j] = (int32_t)r;
+            col[j] = (int32_t)c;
+            atomicAdd(&deg[r], 1);
+            atomicAdd(&deg[n + c], 1);
+            keys[j] = (uint32_t)r;
+            keys[e + j] = (uint32_t)(n + c);
+        }
+        vals[j] = (int32_t)j;
+        vals[e + j] = (int32_t)j;
+    }
+}
+
+// exclusive scan of deg[0..nodes) into off[0..nodes] with a single workgroup (setup only)
+__global__ void k_scan(const int32_t* __restrict__ deg, int64_t nodes, int32_t* __restrict__ off) {
+    __shared__ int64_t sums[1024];
+    const int t = threadIdx.x;
+    const int64_t per = (nodes + 1023) / 1024;
+    const int64_t b0 = t * per, b1 = (b0 + per < nodes) ? b0 + per : nodes;
+    int64_t s = 0;
+    for (int64_t i = b0; i < b1; ++i) s += deg[i];
+    sums[t] = s;
+    __syncthreads();
+    if (t == 0) {
+        int64_t run = 0;
+        for (int i = 0; i < 1024; ++i) {
+            const int64_t v = sums[i];
+            sums[i] = run;
+            run += v;
+        }
+    }
+    __syncthreads();
+    int64_t run = sums[t];
+    for (int64_t i = b0; i < b1; ++i) {
+        off[i] = (int32_t)run;
+        run += deg[i];
+    }
+    if (t == 1023) off[nodes] = (int32_t)run;  // the last range ends at `nodes`, so run is the total
+}
+
+__global__ void k_node_setup(const int32_t* __restrict__ deg, const double* __restrict__ b,
+                             const double* __restrict__ y0, int64_t nodes, int64_t n, double bound, double objective,
+                             double variable, double* __restrict__ scale, double* __restrict__ bs,
+                             double* __restrict__ ns, double* __restrict__ y, double* __restrict__ ay,
+                             double* __restrict__ py, double* __restrict__ dy, double* __restrict__ td) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < nodes; i += (int64_t)gridDim.x * blockDim.x) {
+        const double sc = sqrt((double)(deg[i] > 1 ? deg[i] : 1));
+        scale[i] = sc;
+        bs[i] = b[i] * bound / sc;
+        const double nsv = variable * sc;
+        ns[i] = nsv;
+        const double a = y0 ? y0[i] * sc * objective : 0.0;
+        ay[i] = a;
+        y[i] = a;
+        py[i] = a;
+        dy[i] = 0.0;
+        if (i >= n) td[i - n] = a / nsv;
+    }
+}
+
+__global__ void k_edge_setup(const double* __restrict__ c, const double* __restrict__ x0, int64_t e, double bound,
+                             double objective, double variable, double* __restrict__ cs, double* __restrict__ x,
+                             double* __restrict__ ax, double* __restrict__ px, double* __restrict__ rx,
+                             double* __restrict__ dx) {
+    for (int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; j < e; j += (int64_t)gridDim.x * blockDim.x) {
+        cs[j] = c[j] * objective / variable;
+        const double a = x0 ? fmax(x0[j], 0.0) * variable * bound : 0.0;
+        ax[j] = a;
+        x[j] = a;
+        px[j] = a;
+        rx[j] = 0.0;
+        dx[j] = 0.0;
+    }
+}
+
+// ---------------------------------------------------------------------------------------------------------
+// fixed-shape reductions: grid RB x RT, grid-stride partial sums, then one block combines RB partials
+// ---------------------------------------------------------------------------------------------------------
+template <int Q>
+__device__ inline void block_reduce_store(double (&v)[Q], double* __restrict__ partial) {
+    __shared__ double s[RT / 64][4];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+    for (int q = 0; q < Q; ++q)
+        for (int o = 32; o >= 1; o >>= 1) v[q] = v[q] + __shfl_xor(v[q], o, 64);
+    if (lane == 0)
+        for (int q = 0; q < Q; ++q) s[wave][q] = v[q];
+    __syncthreads();
+    if (threadIdx.x == 0)
+        for (int q = 0; q < Q; ++q) {
+            double t = s[0][q];
+            for (int w = 1; w < RT / 64; ++w) t = t + s[w][q];
+            partial[(size_t)blockIdx.x * 4 + q] = t;
+        }
+}
+
+__global__ void k_combine(const double* __restrict__ partial, double* __restrict__ result, int q) {
+    __shared__ double s[RT][4];
+    const int t = threadIdx.x;
+    double v[4] = {0, 0, 0, 0};
+    for (int b = t; b < RB; b += RT)
+        for (int k = 0; k < q; ++k) v[k] = v[k] + partial[(size_t)b * 4 + k];
+    for (int k = 0; k < 4; ++k) s[t][k] = v[k];
+    __syncthreads();
+    for (int w = RT / 2; w >= 1; w >>= 1) {
+        if (t < w)
+            for (int k = 0; k < 4; ++k) s[t][k] = s[t][k] + s[t + w][k];
+        __syncthreads();
+    }
+    if (t == 0)
+        for (int k = 0; k < q; ++k) result[k] = s[0][k];
+}
+
+__global__ void k_sumsq(const double* __restrict__ a, int64_t count, double* __restrict__ partial) {
+    double v[1] = {0.0};
+    for (int64_t i = (int64_t)blockIdx.x * RT + threadIdx.x; i < count; i += (int64_t)RB * RT) v[0] = v[0] + a[i] * a[i];
+    block_reduce_store<1>(v, partial);
+}
+
+__global__ void k_diffsq2(const double* __restrict__ a, const double* __restrict__ b, int64_t na,
+                          const double* __restrict__ c, const double* __restrict__ d, int64_t nc,
+                          double* __restrict__ partial) {
+    double v[2] = {0.0, 0.0};
+    for (int64_t i = (int64_t)blockIdx.x * RT + threadIdx.x; i < na; i += (int64_t)RB * RT) {
+        const double t = a[i] - b[i];
+        v[0] = v[0] + t * t;
+    }
+    for (int64_t i = (int64_t)blockIdx.x * RT + threadIdx.x; i < nc; i += (int64_t)RB * RT) {
+        const double t = c[i] - d[i];
+        v[1] = v[1] + t * t;
+    }
+    block_reduce_store<2>(v, partial);
+}
+
+// evaluation: [primal_sq, dobj, dual_sq, pobj]
+__global__ void k_evaluate(const Pdhg P, const double* __restrict__ b, const double* __restrict__ c, double variable,
+                           double bound, double objective, double* __restrict__ partial) {
+    double v[4] = {0.0, 0.0, 0.0, 0.0};
+    const double vb = variable * bound;
+    for (int64_t i = (int64_t)blockIdx.x * RT + threadIdx.x; i < P.nodes; i += (int64_t)RB * RT) {
+        double sum = 0.0;
+        for (int32_t k = P.off[i]; k < P.off[i + 1]; ++k) sum += P.px[P.eid[k]] / vb;
+        const double delta = sum - b[i];
+        v[0] = v[0] + delta * delta;
+        v[1] = v[1] + b[i] * (P.py[i] / (P.scale[i] * objective));
+    }
+    for (int64_t j = (int64_t)blockIdx.x * RT + threadIdx.x; j < P.e; j += (int64_t)RB * RT) {
+        const int32_t r = P.row[j], cc = P.col[j];
+        const double score = P.py[r] / (P.scale[r] * objective) + P.py[P.n + cc] / (P.scale[P.n + cc] * objective) - c[j];
+        const double viol = fmax(score, 0.0);
+        v[2] = v[2] + viol * viol;
+        v[3] = v[3] + c[j] * (P.px[j] / vb);
+    }
+    block_reduce_store<4>(v, partial);
+}
+
+// fixed-point error pieces: [movement, dual_movement, interaction]
+__global__ void k_fixed_point(const Pdhg P, double* __restrict__ partial) {
+    double v[3] = {0.0, 0.0, 0.0};
+    for (int64_t j = (int64_t)blockIdx.x * RT + threadIdx.x; j < P.e; j += (int64_t)RB * RT) {
+        const double d = P.dx[j];
+        const int32_t r = P.row[j], cc = P.col[j];
+        v[0] = v[0] + d * d;
+        v[2] = v[2] + (P.dy[r] / P.ns[r] + P.dy[P.n + cc] / P.ns[P.n + cc]) * d;
+    }
+    for (int64_t i = (int64_t)blockIdx.x * RT + threadIdx.x; i < P.nodes; i += (int64_t)RB * RT)
+        v[1] = v[1] + P.dy[i] * P.dy[i];
+    block_reduce_store<3>(v, partial);
+}
+
+// ---------------------------------------------------------------------------------------------------------
+// iteration kernels
+// ---------------------------------------------------------------------------------------------------------
+template <bool CHECKPOINT, bool STORE>
+__global__ __launch_bounds__(256) void k_edge_pass(const Pdhg P, double primal_step, double halpern) {
+    const double keep = 1.0 - halpern;
+    for (int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; j < P.e; j += (int64_t)gridDim.x * blockDim.x) {
+        const int32_t r = P.row[j], c = P.col[j];
+        const double at = P.y[r] / P.ns[r] + P.td[c];
+        const double xj = P.x[j];
+        const double pxj = fmax(xj - primal_step * (P.cs[j] - at), 0.0);
+        const double rxj = 2.0 * pxj - xj;
+        if (STORE) P.px[j] = pxj;
+        if (CHECKPOINT) P.dx[j] = rxj - xj;
+        P.rx[j] = rxj;
+        P.x[j] = halpern * rxj + keep * P.ax[j];
+    }
+}
+
+template <bool CHECKPOINT, bool STORE>
+__global__ __launch_bounds__(256) void k_node_pass(const Pdhg P, double dual_step, double halpern) {
+    const double keep = 1.0 - halpern;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < P.nodes; i += (int64_t)gridDim.x * blockDim.x) {
+        double sum = 0.0;
+        const int32_t k1 = P.off[i + 1];
+        for (int32_t k = P.off[i]; k < k1; ++k) sum += P.rx[P.eid[k]];
+        const double yi = P.y[i];
+        const double pyi = yi - dual_step * (sum / P.ns[i] - P.bs[i]);
+        const double refl = 2.0 * pyi - yi;
+        if (STORE) P.py[i] = pyi;
+        if (CHECKPOINT) P.dy[i] = refl - yi;
+        const double yn = halpern * refl + keep * P.ay[i];
+        P.y[i] = yn;
+        if (i >= P.n) P.td[i - P.n] = yn / P.ns[i];
+    }
+}
+
+__global__ void k_restart(const Pdhg P) {
+    const int64_t total = P.e > P.nodes ? P.e : P.nodes;
+    for (int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; j < total; j += (int64_t)gridDim.x * blockDim.x) {
+        if (j < P.e) {
+            const double v = P.px[j];
+            P.ax[j] = v;
+            P.x[j] = v;
+        }
+        if (j < P.nodes) {
+            const double v = P.py[j];
+            P.ay[j] = v;
+            P.y[j] = v;
+            if (j >= P.n) P.td[j - P.n] = v / P.ns[j];
+        }
+    }
+}
+
+__global__ void k_output(const Pdhg P, double vb, double objective, double* __restrict__ xo, double* __restrict__ yo) {
+    const int64_t total = P.e > P.nodes ? P.e : P.nodes;
+    for (int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; j < total; j += (int64_t)gridDim.x * blockDim.x) {
+        if (j < P.e) xo[j] = P.px[j] / vb;
+        if (j < P.nodes) yo[j] = P.py[j] / (P.scale[j] * objective);
+    }
+}
+
+inline unsigned grid_of(int64_t items) {
+    int64_t b = (items + 255) / 256;
+    if (b > 8192) b = 8192;
+    if (b < 1) b = 1;
+    return (unsigned)b;
+}
+
+int read_result(hipStream_t st, const Pdhg& P, int q, double* host) {
+    hipLaunchKernelGGL(k_combine, dim3(1), dim3(RT), 0, st, P.partial, P.result, q);
+    HM_LAUNCH_CHECK("k_combine");
+    HM_HIP(hipMemcpyAsync(host, P.result, sizeof(double) * q, hipMemcpyDeviceToHost, st));
+    HM_HIP(hipStreamSynchronize(st));
+    return HM_OK;
+}
+
+}  // namespace
+}  // namespace hm
+
+using namespace hm;
+
+extern "C" size_t hm_pdhg_workspace_bytes(int64_t n_source, int64_t n_target, int64_t e) {
+    if (n_source < 1 || n_target < 1 || e < 1) return 0;
+    Sizer s;
+    Pdhg P;
+    pdhg_layout(s, n_source, n_target, e, sort_tmp_bytes(n_source + n_target, e), P);
+    return s.used;
+}
+
+extern "C" int hm_pdhg_solve(void* stream, const int64_t* rows, const int64_t* cols, const double* costs,
+                             const double* masses, const double* x0, const double* y0, int64_t n_source,
+                             int64_t n_target, int64_t e, const hm_pdhg_params* params, double* x_out, double* y_out,
+                             hm_pdhg_result* result, void* workspace, size_t workspace_bytes) {
+    const auto started = std::chrono::steady_clock::now();
+    HM_CHECK_ARG(params && result, "PDHG: params and result are required");
+    HM_CHECK_ARG(n_source >= 1 && n_target >= 1 && e >= 1, "invalid restricted OT dimensions");
+    HM_CHECK_ARG(2 * e < INT32_MAX && n_source + n_target < INT32_MAX, "restricted OT too large for int32 indexing");
+    HM_CHECK_ARG(rows && cols && costs && masses && x_out && y_out, "PDHG: null pointer argument");
+    const int freq = params->evaluation_frequency;
+    HM_CHECK_ARG(freq >= 1 && params->iteration_limit >= 1 && params->time_limit_seconds > 0,
+                 "invalid restricted OT dimensions or runtime limits");
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    const int64_t n = n_source, nt = n_target, nodes = n + nt;
+    const size_t tmp = sort_tmp_bytes(nodes, e);
+    Sizer sz;
+    Pdhg P;
+    pdhg_layout(sz, n, nt, e, tmp, P);
+    HM_CHECK_ARG(workspace != nullptr, "workspace is required");
+    if (workspace_bytes < sz.used) return fail(HM_ENOSPC, "PDHG workspace too small: %zu < %zu", workspace_bytes, sz.used);
+    Arena a(workspace, workspace_bytes);
+    pdhg_layout(a, n, nt, e, tmp, P);
+    P.n = n;
+    P.nt = nt;
+    P.nodes = nodes;
+    P.e = e;
+
+    // ---- LP assembly: endpoints, degrees, per-node incident edge lists (ascending edge id) ----
+    hipLaunchKernelGGL(k_fill_i32, dim3(grid_of(nodes + 1)), dim3(256), 0, st, P.deg, nodes + 1, 0);
+    hipLaunchKernelGGL(k_fill_i32, dim3(1), dim3(64), 0, st, P.flag, 4, 0);
+    hipLaunchKernelGGL(k_edges, dim3(grid_of(e)), dim3(256), 0, st, rows, cols, e, n, nt, P.row, P.col, P.deg,
+                       P.keys_in, P.vals_in, P.flag);
+    HM_LAUNCH_CHECK("k_edges");
+    int flag = 0;
+    HM_HIP(hipMemcpyAsync(&flag, P.flag, sizeof(int), hipMemcpyDeviceToHost, st));
+    HM_HIP(hipStreamSynchronize(st));
+    if (flag) return fail(HM_EINVAL, "active-support endpoint index is out of bounds");
+    hipLaunchKernelGGL(k_scan, dim3(1), dim3(1024), 0, st, P.deg, nodes, P.off);
+    HM_LAUNCH_CHECK("k_scan");
+    size_t tmp_bytes = P.sort_tmp_bytes;
+    HM_HIP(hipcub::DeviceRadixSort::SortPairs(P.sort_tmp, tmp_bytes, P.keys_in, P.keys_out, P.vals_in, P.eid,
+                                              (int)(2 * e), 0, end_bit_for(nodes), st));
+
+    // ---- scaling (solver.cpp:91-110) ----
+    double host[4];
+    hipLaunchKernelGGL(k_sumsq, dim3(RB), dim3(RT), 0, st, masses, nodes, P.partial);
+    HM_LAUNCH_CHECK("k_sumsq");
+    if (int rc = read_result(st, P, 1, host)) return rc;
+    const double mass_norm = std::sqrt(host[0]);
+    hipLaunchKernelGGL(k_sumsq, dim3(RB), dim3(RT), 0, st, costs, e, P.partial);
+    HM_LAUNCH_CHECK("k_sumsq");
+    if (int rc = read_result(st, P, 1, host)) return rc;
+    const double cost_norm = std::sqrt(host[0]);
+    const bool rescale = params->rescale != 0;
+    const double bound = rescale ? 1.0 / std::max(1.0, mass_norm) : 1.0;
+    const double objective = rescale ? 1.0 / std::max(1.0, cost_norm) : 1.0;
+    const double variable = std::sqrt(2.0);
+    hipLaunchKernelGGL(k_edge_setup, dim3(grid_of(e)), dim3(256), 0, st, costs, x0, e, bound, objective, variable, P.cs,
+                       P.x, P.ax, P.px, P.rx, P.dx);
+    HM_LAUNCH_CHECK("k_edge_setup");
+    hipLaunchKernelGGL(k_node_setup, dim3(grid_of(nodes)), dim3(256), 0, st, P.deg, masses, y0, nodes, n, bound, objective,
+                       variable, P.scale, P.bs, P.ns, P.y, P.ay, P.py, P.dy, P.td);
+    HM_LAUNCH_CHECK("k_node_setup");
+    double weight = 1.0;
+    if (!rescale) {
+        hipLaunchKernelGGL(k_sumsq, dim3(RB), dim3(RT), 0, st, P.cs, e, P.partial);
+        if (int rc = read_result(st, P, 1, host)) return rc;
+        const double ncs = std::sqrt(host[0]);
+        hipLaunchKernelGGL(k_sumsq, dim3(RB), dim3(RT), 0, st, P.bs, nodes, P.partial);
+        if (int rc = read_result(st, P, 1, host)) return rc;
+        const double nbs = std::sqrt(host[0]);
+        weight = std::max(ncs / std::max(nbs, 1e-16), 1e-16);
+    }
+
+    // ---- Halpern PDHG loop (solver.cpp:157-312) ----
+    double best_weight = weight, error_sum = 0.0;
+    const double inf = INFINITY;
+    double best_balance = inf, initial_error = inf, last_trial_error = inf, fixed_error = inf;
+    bool restart = false;
+    int32_t reason = 0;
+    int64_t count = 0, inner = 0, restarts = 0;
+    double pobj = 0, dobj = 0, ap = 0, rp = 0, ad = 0, rd = 0, gap = 0;
+    int64_t local_count = 0, local_inner = 0;
+    const unsigned ge = grid_of(e), gn = grid_of(nodes), gr = grid_of(e > nodes ? e : nodes);
+    for (;;) {
+        if (local_count % freq == 0) {
+            hipLaunchKernelGGL(k_evaluate, dim3(RB), dim3(RT), 0, st, P, masses, costs, variable, bound, objective,
+                               P.partial);
+            HM_LAUNCH_CHECK("k_evaluate");
+            if (int rc = read_result(st, P, 4, host)) return rc;
+            count = local_count;
+            inner = local_inner;
+            ap = std::sqrt(host[0]);
+            dobj = host[1];
+            ad = std::sqrt(host[2]);
+            pobj = host[3];
+            rp = ap / (1.0 + mass_norm);
+            rd = ad / (1.0 + cost_norm);
+            gap = std::fabs(pobj - dobj) / (1.0 + std::fabs(pobj) + std::fabs(dobj));
+            const bool finite = std::isfinite(pobj) && std::isfinite(dobj) && std::isfinite(ap) && std::isfinite(rp) &&
+                                std::isfinite(ad) && std::isfinite(rd) && std::isfinite(gap);
+            const double elapsed = std::chrono::duration<double>(std::chrono::steady_clock::now() - started).count();
+            if (!finite || !std::isfinite(weight)) reason = 3;
+            else if (rp < params->tol_primal && rd < params->tol_dual && gap < params->tol_objective) reason = 1;
+            else if (count >= params->iteration_limit) reason = 2;
+            else if (elapsed >= params->time_limit_seconds) reason = 4;
+            if (reason != 0) break;
+            restart = false;
+            if (count == freq) restart = true;
+            else if (count > freq)
+                restart = inner >= 0.36 * count || fixed_error <= 0.2 * initial_error ||
+                          (fixed_error <= 0.5 * initial_error && fixed_error > last_trial_error);
+            last_trial_error = fixed_error;
+            if (restart) {
+                hipLaunchKernelGGL(k_diffsq2, dim3(RB), dim3(RT), 0, st, P.px, P.ax, e, P.py, P.ay, nodes, P.partial);
+                HM_LAUNCH_CHECK("k_diffsq2");
+                if (int rc = read_result(st, P, 2, host)) return rc;
+                const double pd = std::sqrt(host[0]), dd = std::sqrt(host[1]);
+                const double ratio = rd / std::max(rp, 1e-300);
+                if (pd > 1e-16 && pd < 1e12 && dd > 1e-16 && dd < 1e12 && ratio > 1e-8 && ratio < 1e8) {
+                    const double error = std::log(dd) - std::log(pd) - std::log(weight);
+                    error_sum = 0.3 * error_sum + error;
+                    weight *= std::exp(0.99 * error + 0.01 * error_sum);
+                } else {
+                    weight = best_weight;
+                    error_sum = 0;
+                }
+                if (rp > 0 && rd > 0) {
+                    const double balance = std::fabs(std::log10(rd / rp));
+                    if (balance < best_balance) {
+                        best_balance = balance;
+                        best_weight = weight;
+                    }
+                }
+                inner = 0;
+                last_trial_error = inf;
+                ++restarts;
+                hipLaunchKernelGGL(k_restart, dim3(gr), dim3(256), 0, st, P);
+                HM_LAUNCH_CHECK("k_restart");
+                local_inner = 0;
+            }
+        }
+        const double primal_step = 0.998 / weight;
+        const double dual_step = 0.998 * weight;
+        const double halpern = double(local_inner + 1) / double(local_inner + 2);
+        const bool major = ((local_count + 1) % freq) == 0;
+        const bool is_restart = (local_count % freq == 0) && restart;
+        const bool checkpoint = major || is_restart;
+        // px / py are read only by the evaluation that follows a major iteration
+        if (checkpoint) {
+            if (major) {
+                hipLaunchKernelGGL((k_edge_pass<true, true>), dim3(ge), dim3(256), 0, st, P, primal_step, halpern);
+                hipLaunchKernelGGL((k_node_pass<true, true>), dim3(gn), dim3(256), 0, st, P, dual_step, halpern);
+            } else {
+                hipLaunchKernelGGL((k_edge_pass<true, false>), dim3(ge), dim3(256), 0, st, P, primal_step, halpern);
+                hipLaunchKernelGGL((k_node_pass<true, false>), dim3(gn), dim3(256), 0, st, P, dual_step, halpern);
+            }
+        } else {
+            hipLaunchKernelGGL((k_edge_pass<false, false>), dim3(ge), dim3(256), 0, st, P, primal_step, halpern);
+            hipLaunchKernelGGL((k_node_pass<false, false>), dim3(gn), dim3(256), 0, st, P, dual_step, halpern);
+        }
+        HM_LAUNCH_CHECK("pdhg iteration");
+        if (checkpoint) {
+            hipLaunchKernelGGL(k_fixed_point, dim3(RB), dim3(RT), 0, st, P, P.partial);
+            HM_LAUNCH_CHECK("k_fixed_point");
+            if (int rc = read_result(st, P, 3, host)) return rc;
+            const double squared = host[0] * weight + host[1] / weight + 2.0 * 0.998 * host[2];
+            fixed_error = std::sqrt(std::max(0.0, squared));
+            if (is_restart) initial_error = fixed_error;
+        }
+        ++local_count;
+        ++local_inner;
+    }
+    hipLaunchKernelGGL(k_output, dim3(gr), dim3(256), 0, st, P, variable * bound, objective, x_out, y_out);
+    HM_LAUNCH_CHECK("k_output");
+    HM_HIP(hipStreamSynchronize(st));
+    result->iterations = count;
+    result->restarts = restarts;
+    result->reason = reason;
+    result->pad = 0;
+    result->primal_objective = pobj;
+    result->dual_objective = dobj;
+    result->abs_primal = ap;
+    result->rel_primal = rp;
+    result->abs_dual = ad;
+    result->rel_dual = rd;
+    result->rel_gap = gap;
+    result->primal_weight = weight;
+    result->seconds = std::chrono::duration<double>(std::chrono::steady_clock::now() - started).count();
+    return HM_OK;
+}

@@ -1,0 +1,6 @@
+// l2^2 pricing scan driver instantiated for per-lane lists of 8 entries.
+#include "l2sq_impl.h"
+
+namespace hm {
+int l2sq_run_k8(L2SQ_RUN_ARGS) { return run_direction<8>(L2SQ_RUN_PASS); }
+}  // namespace hm

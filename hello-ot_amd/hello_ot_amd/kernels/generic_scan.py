@@ -1,0 +1,184 @@
+"""MI355X pricing scans behind the reference's ``ScanExtension`` interface.
+
+Mirrors ``hello_ot.kernels.generic_scan.ScanExtension`` (``kernels/generic_scan.py:468-597``): same method
+names, argument meaning, return shapes and validation errors. Each method calls one C-ABI entry point of
+``libhelloot_hip.so``; there is no CPU or PyTorch fallback.
+"""
+from __future__ import annotations
+
+from collections import Counter
+
+import torch
+
+from .. import _lib
+
+_ROUTES = Counter()
+_BUCKETS = (1, 2, 4, 8, 16, 32)
+
+
+def scan_routes(*, reset=False):
+    """Route counters, as ``generic_scan.scan_routes`` (generic_scan.py:22-30)."""
+    result = dict(_ROUTES)
+    if reset:
+        _ROUTES.clear()
+    return result
+
+
+def _check(x, y, k, *vectors):
+    """Validation of ``generic_scan._check`` (generic_scan.py:42-56), restricted to fp32 features."""
+    if k not in _BUCKETS:
+        raise ValueError("generic scan requires a power-of-two bucket in [1,32]")
+    if (not x.is_cuda or not y.is_cuda or x.device != y.device
+            or x.dtype not in (torch.float32, torch.float64) or y.dtype != x.dtype
+            or x.ndim != 2 or y.ndim != 2 or x.shape[1] != y.shape[1]
+            or min(*x.shape, *y.shape) < 1 or max(*x.shape, *y.shape) >= 2**31):
+        raise ValueError("generic scan requires nonempty matching CUDA FP32/FP64 feature matrices with int32 dimensions")
+    if x.dtype != torch.float32:
+        raise ValueError("the MI355X scan computes from FP32 feature storage (compute_precision='fp32')")
+    for v, count in vectors:
+        if v.device != x.device or v.dtype != torch.float64 or v.numel() != count:
+            raise ValueError("generic scan requires matching CUDA FP64 bias vectors")
+
+
+def _c(t):
+    return t.contiguous()
+
+
+def _workspace(nbytes: int, device) -> torch.Tensor:
+    return torch.empty(max(int(nbytes), 256), dtype=torch.uint8, device=device)
+
+
+def pricing_l2sq(x, y, nx, ny, qb, dbb, k, *, dot_scale=2.0, rows=True, cols=True, stats=True, linf=False):
+    """Raw l2^2 pricing: returns (row_vals, row_idx, col_vals, col_idx, stats5) with None for skipped parts.
+
+    ``stats5`` = (num, den, count, max sigma+, max|cost|); max|cost| is 0 unless ``linf``.
+    """
+    lib = _lib.load()
+    x, y, nx, ny, qb, dbb = map(_c, (x, y, nx, ny, qb, dbb))
+    m, n, d = x.shape[0], y.shape[0], x.shape[1]
+    flags = (_lib.HM_ROWS if rows else 0) | (_lib.HM_COLS if cols else 0) | (_lib.HM_STATS if stats else 0) \
+        | (_lib.HM_LINF if (stats and linf) else 0)
+    dev = x.device
+    rv = torch.empty((m, k), dtype=torch.float64, device=dev) if rows else None
+    ri = torch.empty((m, k), dtype=torch.int32, device=dev) if rows else None
+    cv = torch.empty((n, k), dtype=torch.float64, device=dev) if cols else None
+    ci = torch.empty((n, k), dtype=torch.int32, device=dev) if cols else None
+    st = torch.zeros(5, dtype=torch.float64, device=dev) if stats else None
+    ws_bytes = lib.hm_pricing_l2sq_workspace_bytes(m, n, d, k, flags)
+    ws = _workspace(ws_bytes, dev)
+    with torch.cuda.device(dev):
+        rc = lib.hm_pricing_l2sq(_lib.stream_handle(dev), _lib.ptr(x), _lib.ptr(y), _lib.ptr(nx), _lib.ptr(ny),
+                                 _lib.ptr(qb), _lib.ptr(dbb), m, n, d, k, float(dot_scale), flags, _lib.ptr(rv),
+                                 _lib.ptr(ri), _lib.ptr(cv), _lib.ptr(ci), _lib.ptr(st), _lib.ptr(ws), ws.numel())
+    _lib.check(rc, "hm_pricing_l2sq")
+    return rv, ri, cv, ci, st
+
+
+def pricing_norm(x, y, f, g, k, cost_type, *, rows=True, cols=True, stats=True, linf=True):
+    """l1 / linf / l2 pricing (cost_type 0/1/2): (row_vals, row_idx, col_vals, col_idx, stats5)."""
+    lib = _lib.load()
+    x, y, f, g = map(_c, (x, y, f, g))
+    m, n, d = x.shape[0], y.shape[0], x.shape[1]
+    flags = (_lib.HM_ROWS if (rows or stats) else 0) | (_lib.HM_COLS if cols else 0) \
+        | (_lib.HM_STATS if stats else 0) | (_lib.HM_LINF if (stats and linf) else 0)
+    dev = x.device
+    need_rows = bool(flags & _lib.HM_ROWS)
+    rv = torch.empty((m, k), dtype=torch.float64, device=dev) if need_rows else None
+    ri = torch.empty((m, k), dtype=torch.int32, device=dev) if need_rows else None
+    cv = torch.empty((n, k), dtype=torch.float64, device=dev) if cols else None
+    ci = torch.empty((n, k), dtype=torch.int32, device=dev) if cols else None
+    st = torch.zeros(5, dtype=torch.float64, device=dev) if stats else None
+    ws = _workspace(lib.hm_pricing_norm_workspace_bytes(m, n, d, k, flags), dev)
+    with torch.cuda.device(dev):
+        rc = lib.hm_pricing_norm(_lib.stream_handle(dev), _lib.ptr(x), _lib.ptr(y), _lib.ptr(f), _lib.ptr(g), m, n, d,
+                                 k, int(cost_type), flags, _lib.ptr(rv), _lib.ptr(ri), _lib.ptr(cv), _lib.ptr(ci),
+                                 _lib.ptr(st), _lib.ptr(ws), ws.numel())
+    _lib.check(rc, "hm_pricing_norm")
+    return (rv if rows else None), (ri if rows else None), cv, ci, st
+
+
+class ScanExtension:
+    """Unified scan entry points (generic_scan.py:468-597) on MI355X HIP kernels."""
+
+    supports_assignment_statistics = False
+    supports_cost_perturbation = False
+    supports_fp64_accumulation = True
+    index_hash_arithmetic = None
+
+    def __init__(self):
+        self.routes = Counter()
+        self.last_backend = "mi355x"
+
+    def _record(self, name):
+        key = name + ":mi355x"
+        self.routes[key] += 1
+        _ROUTES[key] += 1
+
+    # -- (a) l2^2 pricing -------------------------------------------------------------------------------
+    def fused_bidir_topk_stats_raw(self, query_feat, db_feat, query_cost, db_cost, query_bias, db_bias,
+                                   query_tile, db_tile, col_reduce_tile, k, compute_stats,
+                                   collect_linf_stats, collect_timing, col_kernel, dot_scale):
+        """generic_scan.py:577-597 -> [q_vals f64(q,k), q_idx i32(q,k), r_vals f64(n,k), r_idx i32(n,k),
+        stats f64(4) = (num, den, count, max|cost| if collect_linf_stats), timing f64(4) on CPU (zeros)]."""
+        x, y, nx, ny, qb, dbb = query_feat, db_feat, query_cost, db_cost, query_bias, db_bias
+        if x.dtype != y.dtype:
+            raise RuntimeError("query/db feature dtypes must match")
+        _check(x, y, k, (nx, len(x)), (ny, len(y)), (qb, len(x)), (dbb, len(y)))
+        if (query_tile <= 0 or db_tile <= 0 or not 0 < col_reduce_tile <= 256 or dot_scale not in (1., 2.)
+                or col_kernel not in (0, 1, 2) or (col_kernel == 1 and k != 4) or (col_kernel == 2 and k != 2)):
+            raise ValueError("invalid raw pricing tile, scale or column mode")
+        self._record("raw_pricing")
+        rv, ri, cv, ci, st = pricing_l2sq(x, y, nx, ny, qb, dbb, k, dot_scale=float(dot_scale), rows=True, cols=True,
+                                          stats=bool(compute_stats), linf=bool(collect_linf_stats))
+        if compute_stats:
+            stats = torch.stack((st[0], st[1], st[2], st[4] if collect_linf_stats else st[4].new_zeros(())))
+        else:
+            stats = torch.zeros(4, dtype=torch.float64, device=x.device)
+        return [rv, ri, cv, ci, stats, torch.zeros(4, dtype=torch.float64, device="cpu")]
+
+    def raw_lowrank_stats_only(self, x, y, nx, ny, f, g, query_tile, db_tile, dot_scale):
+        """Certificate only (generic_scan.py:502-510): f64(5) = (num, den, count, max, costmax)."""
+        if query_tile <= 0 or db_tile <= 0:
+            raise ValueError("tile sizes must be positive")
+        _check(x, y, 1, (nx, len(x)), (ny, len(y)), (f, len(x)), (g, len(y)))
+        if dot_scale not in (1., 2.):
+            raise ValueError("invalid raw certificate scale or precision")
+        self._record("raw_certificate")
+        qb, dbb = f - nx, g - ny
+        _, _, _, _, st = pricing_l2sq(x, y, nx, ny, qb, dbb, 1, dot_scale=float(dot_scale), rows=False, cols=False,
+                                      stats=True, linf=True)
+        return st
+
+    # -- (a) norm pricing -----------------------------------------------------------------------------
+    def fused_gcost_bidir_certificate(self, query, db, query_dual, db_dual, k, cost_type,
+                                      query_global_index=None, database_global_index=None, sigma=0., seed=0,
+                                      perturb_mode=1, row_is_source=True, index_hash_coeffs=None,
+                                      compute_precision=0, rows_per_block_hint=8):
+        """generic_scan.py:533-543 -> [q_vals, q_idx i64, r_vals, r_idx i64, num, den, max, costmax, count]."""
+        _check(query, db, k, (query_dual, len(query)), (db_dual, len(db)))
+        if cost_type not in (0, 1, 2):
+            raise ValueError("generic bidirectional cost must be l1, linf, l2 or raw")
+        if compute_precision not in (0, 1):
+            raise ValueError("norm scans require FP32 coordinate storage and precision 0 or 1")
+        if compute_precision == 1:
+            raise ValueError("the MI355X norm scan evaluates costs in FP32 (compute_precision=0)")
+        if float(sigma) != 0.0:
+            raise NotImplementedError("cost perturbation is not part of the MI355X native pricing path")
+        self._record("norm_pricing")
+        rv, ri, cv, ci, st = pricing_norm(query, db, query_dual, db_dual, k, cost_type, rows=True, cols=True,
+                                          stats=True, linf=True)
+        return [rv, ri.long(), cv, ci.long(), st[0], st[1], st[3], st[4], st[2].long()]
+
+    # -- (b) SDDMM / pair costs -------------------------------------------------------------------------
+    def fused_gcost_pairs(self, query, db, rows, cols, cost_type, source_index=None, target_index=None,
+                          sigma=0.0, seed=0, mode=1, coefficients=None):
+        """fp64 norm costs of selected pairs (norm_cost_scan_kernel.cu:249-275), without perturbation."""
+        if float(sigma) != 0.0:
+            raise NotImplementedError("cost perturbation is not part of the MI355X native pair-cost path")
+        from ..costs.pairs import norm_pair_costs
+
+        self._record("norm_pairs")
+        return norm_pair_costs(query, db, rows, cols, cost_type)
+
+
+__all__ = ["ScanExtension", "pricing_l2sq", "pricing_norm", "scan_routes"]

@@ -1,0 +1,157 @@
+/*
+ * helloot_hip.h -- C ABI of the MI355X (gfx950) HELLO hot path.
+ *
+ * Conventions
+ *   - Every array argument is a DEVICE pointer (e.g. torch.Tensor.data_ptr() of a ROCm tensor) unless the
+ *     parameter comment says "host".
+ *   - `stream` is a hipStream_t passed as void* (0 = the legacy default stream). All work is ordered on
+ *     that stream. Functions that must read a device scalar back to decide what to launch next say so.
+ *   - Outputs are caller-allocated. Scratch memory comes from `workspace` (device, 256-byte aligned,
+ *     size from the matching *_workspace_bytes() query). Nothing here calls hipMalloc.
+ *   - Return value: HM_OK (0) or an HM_E* code; hm_last_error() then describes the failure (thread-local).
+ *     No function aborts the process (the reference's CuPDLPx exits on CUDA errors, cupdlpx/utils.h:104-138).
+ *   - Scores follow the reference's dual score sigma_ij = f_i + g_j - c_ij ("reduced cost" r_ij = -sigma_ij);
+ *     candidate lists are sorted by sigma descending, ties to the lowest index, missing slots (-inf, -1).
+ */
+#ifndef HELLOOT_HIP_H
+#define HELLOOT_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define HM_OK 0
+#define HM_EINVAL 1   /* invalid argument (ValueError in the Python mirror) */
+#define HM_EHIP 2     /* HIP runtime / launch error (RuntimeError) */
+#define HM_ENOSPC 3   /* workspace too small (RuntimeError) */
+
+/* Pricing flags */
+#define HM_ROWS 1u    /* per-row (query-side) top-k */
+#define HM_COLS 2u    /* per-column (database-side) top-k */
+#define HM_STATS 4u   /* certificate sums num, den, count, max */
+#define HM_LINF 8u    /* also max|cost| (collect_linf_stats) */
+
+/* Norm cost kinds (generic_scan.py cost_type: 0=l1, 1=linf, 2=l2) */
+#define HM_COST_L1 0
+#define HM_COST_LINF 1
+#define HM_COST_L2 2
+
+const char* hm_last_error(void);
+int hm_abi_version(void); /* 1 */
+
+/* ---------------------------------------------------------------------------------------------------- */
+/* (a) Full-space pricing scan                                                                           */
+/* ---------------------------------------------------------------------------------------------------- */
+
+/*
+ * l2^2 ("raw lowrank") bidirectional pricing scan with the full-edge certificate.
+ * Replaces ScanExtension.fused_bidir_topk_stats_raw (kernels/generic_scan.py:577-597), i.e. the native
+ * modules pricing_small.raw_scan_tiled (pricing_small.cu:281-304) and pricing.scan + merge
+ * (pricing.cu:185-229) with their cuBLAS SGEMM tiles.
+ *
+ *   sigma_ij = (scale*<x_i,y_j> + qb_i) + db_j,   c_ij = (p_i + q_j) - scale*<x_i,y_j>
+ *   X: m x d fp32 row-major, Y: n x d fp32 row-major; p, q (query_cost/db_cost), qb = f - p, db = g - q fp64.
+ *   scale (dot_scale) must be 1 or 2.  1 <= k <= 32.
+ * Outputs (each may be NULL when its flag is off):
+ *   row_val[m*k] fp64, row_idx[m*k] int32  -- per X row, best k columns (HM_ROWS)
+ *   col_val[n*k] fp64, col_idx[n*k] int32  -- per Y row, best k X rows    (HM_COLS)
+ *   stats[5] fp64 = (num = sum sigma+^2, den = sum c^2, count #{sigma>0}, max sigma+, max|c| (HM_LINF))
+ * Values are exact fp64 re-evaluations (fixed-order fp64 dot) of candidates found by an fp32 MFMA sweep
+ * with a rigorous error bound; rows whose bound cannot separate the k-th candidate are rescanned exactly
+ * on the device. Certificate sums come from the fp32 sweep (relative error ~1e-6).
+ */
+size_t hm_pricing_l2sq_workspace_bytes(int64_t m, int64_t n, int32_t d, int32_t k, uint32_t flags);
+int hm_pricing_l2sq(void* stream, const float* X, const float* Y, const double* p, const double* q,
+                    const double* qb, const double* db, int64_t m, int64_t n, int32_t d, int32_t k,
+                    double scale, uint32_t flags, double* row_val, int32_t* row_idx, double* col_val,
+                    int32_t* col_idx, double* stats, void* workspace, size_t workspace_bytes);
+
+/*
+ * Norm-cost (l1 / linf / l2) bidirectional pricing scan on VALU with the full-edge certificate.
+ * Replaces ScanExtension.fused_gcost_bidir_certificate (kernels/generic_scan.py:533-543) ->
+ * bidirectional(kind 0/1/2) (generic_scan.py:328-405), i.e. pricing.cu scan_kernel (pricing.cu:71-161)
+ * and the direct_norm tiles (cost.cu:10-157) for fp32 cost precision.
+ *   c_ij = fp32 distance (l1 sum|x-y|, linf max|x-y|, l2 sqrt(sum (x-y)^2), 32-feature chunks),
+ *   sigma_ij = (g_j - c_ij) + f_i in fp64. Exact (bit-reproducible) values; no perturbation.
+ */
+size_t hm_pricing_norm_workspace_bytes(int64_t m, int64_t n, int32_t d, int32_t k, uint32_t flags);
+int hm_pricing_norm(void* stream, const float* X, const float* Y, const double* f, const double* g,
+                    int64_t m, int64_t n, int32_t d, int32_t k, int32_t kind, uint32_t flags,
+                    double* row_val, int32_t* row_idx, double* col_val, int32_t* col_idx, double* stats,
+                    void* workspace, size_t workspace_bytes);
+
+/* ---------------------------------------------------------------------------------------------------- */
+/* (b) SDDMM cost evaluation on the active support                                                       */
+/* ---------------------------------------------------------------------------------------------------- */
+
+/*
+ * l2^2 costs on a CSR support: out[e] = (p_i + q_j) - scale*dot64(x_i, y_j) for e in [rowptr[i], rowptr[i+1]).
+ * Replaces costs/pairs._cost_pairs_lowrank_batched (pairs.py:221-437, torch.sparse.sampled_addmm at
+ * :394-407) and gpu_resident/cost.Cost.pairs (gpu_resident/cost.py:59-71), with fp64 accumulation.
+ * rowptr[m+1] int32, col[nnz] int32 (any order within a row).
+ */
+int hm_sddmm_l2sq_csr(void* stream, const float* X, const float* Y, const double* p, const double* q,
+                      const int32_t* rowptr, const int32_t* col, int64_t m, int64_t nnz, int32_t d,
+                      double scale, double* out);
+
+/* Same costs for an arbitrary pair list (rows[e], cols[e]) int64, as HierarchicalOTSolver passes new pairs
+ * (core/solver.py:331-362). */
+int hm_pair_costs_l2sq(void* stream, const float* X, const float* Y, const double* p, const double* q,
+                       const int64_t* rows, const int64_t* cols, int64_t count, int32_t d, double scale,
+                       double* out);
+
+/* fp64 l1 / linf / l2 pair costs. Replaces fused_gcost_pairs without perturbation
+ * (norm_cost_scan_kernel.cu:233-275; costs/metric.py:85-159). */
+int hm_pair_costs_norm(void* stream, const float* X, const float* Y, const int64_t* rows,
+                       const int64_t* cols, int64_t count, int32_t d, int32_t kind, double* out);
+
+/* ---------------------------------------------------------------------------------------------------- */
+/* (c) Restricted-LP Halpern-PDHG                                                                          */
+/* ---------------------------------------------------------------------------------------------------- */
+
+typedef struct {
+    int32_t evaluation_frequency;  /* restart / termination checks every this many iterations (200) */
+    int32_t rescale;               /* scalar bound/objective rescaling (the NUMERICAL_DIVERGENCE retry) */
+    int64_t iteration_limit;
+    double tol_objective, tol_primal, tol_dual;
+    double time_limit_seconds;
+} hm_pdhg_params;
+
+typedef struct {
+    int64_t iterations;
+    int64_t restarts;
+    int32_t reason;                /* 0 UNSPECIFIED, 1 OPTIMAL, 2 ITERATION_LIMIT, 3 NUMERICAL_DIVERGENCE,
+                                      4 TIME_LIMIT */
+    int32_t pad;
+    double primal_objective, dual_objective;
+    double abs_primal, rel_primal, abs_dual, rel_dual, rel_gap;
+    double primal_weight;
+    double seconds;
+} hm_pdhg_result;
+
+/*
+ * Balanced restricted OT: min c^T x  s.t.  sum_{e: rows[e]=i} x_e = a_i, sum_{e: cols[e]=j} x_e = b_j, x >= 0.
+ * Halpern-reflected PDHG with degree-sqrt constraint scaling, variable scale sqrt(2), step 0.998,
+ * PID primal-weight restarts and relative L2 KKT termination, as _native/cpp/solver.cpp:39-378 and
+ * _internal/lp/torch_restricted_ot.py:105-393 (the same update CuPDLPx runs: cupdlpx/solver.cu:581-715).
+ * Replaces TorchRestrictedOTPDLP._solve_once / CppRestrictedOTPDLP._solve_once / CuPDLPxSolver.solve
+ * (_internal/lp/cupdlpx.py:658) for one scaling mode; the NUMERICAL_DIVERGENCE retry
+ * (restricted_ot_pdlp.py:76-100) is the caller's.
+ *   rows[e], cols[e] int64 endpoints; costs[e]; masses[n_source + n_target] (source then target);
+ *   x0[e], y0[n_source+n_target] warm start (NULL = zeros). Outputs x_out[e], y_out[nodes] (unscaled).
+ * Reads device scalars back to the host at every evaluation (every evaluation_frequency iterations).
+ */
+size_t hm_pdhg_workspace_bytes(int64_t n_source, int64_t n_target, int64_t e);
+int hm_pdhg_solve(void* stream, const int64_t* rows, const int64_t* cols, const double* costs,
+                  const double* masses, const double* x0, const double* y0, int64_t n_source,
+                  int64_t n_target, int64_t e, const hm_pdhg_params* params /* host */, double* x_out,
+                  double* y_out, hm_pdhg_result* result /* host */, void* workspace, size_t workspace_bytes);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* HELLOOT_HIP_H */

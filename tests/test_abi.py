@@ -1,0 +1,86 @@
+"""C-ABI library checks that need no GPU: it loads, exports every declared symbol, and rejects invalid
+arguments before touching a device."""
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from hello_ot_amd import _lib
+
+
+def test_library_exports_every_header_symbol():
+    lib = _lib.load()
+    declared = _lib.header_symbols()
+    assert len(declared) >= 11
+    for name in declared:
+        assert hasattr(lib, name), name
+    assert set(declared) == set(_lib.SIGNATURES)
+    assert lib.hm_abi_version() == 1
+
+
+def test_invalid_arguments_fail_before_any_device_work():
+    lib = _lib.load()
+    one = ctypes.c_void_p(16)  # never dereferenced: validation rejects the call first
+    rc = lib.hm_pricing_l2sq(None, one, one, one, one, one, one, 10, 10, 4, 0, 2.0, 1, one, one, one, one, one,
+                             one, 1 << 20)
+    assert rc == _lib.HM_EINVAL and "1 <= k <= 32" in _lib.last_error()
+    rc = lib.hm_pricing_l2sq(None, one, one, one, one, one, one, 10, 10, 4, 2, 3.0, 1, one, one, one, one, one,
+                             one, 1 << 20)
+    assert rc == _lib.HM_EINVAL and "dot_scale" in _lib.last_error()
+    rc = lib.hm_pricing_l2sq(None, one, one, one, one, one, one, 10, 10, 4, 2, 2.0, 1, one, one, one, one, one,
+                             one, 16)
+    assert rc == _lib.HM_ENOSPC
+    rc = lib.hm_pricing_norm(None, one, one, one, one, 10, 10, 4, 2, 7, 1, one, one, one, one, one, one, 1 << 20)
+    assert rc == _lib.HM_EINVAL and "unsupported norm cost" in _lib.last_error()
+    rc = lib.hm_sddmm_l2sq_csr(None, one, one, one, one, one, one, 10, 10, 4, 3.0, one)
+    assert rc == _lib.HM_EINVAL
+    assert lib.hm_sddmm_l2sq_csr(None, None, None, None, None, None, None, 0, 0, 4, 2.0, None) == _lib.HM_OK
+    assert lib.hm_pair_costs_norm(None, None, None, None, None, 0, 4, 0, None) == _lib.HM_OK
+    params = _lib.PdhgParams(0, 0, 10, 1e-6, 1e-6, 1e-6, 1.0)
+    res = _lib.PdhgResult()
+    rc = lib.hm_pdhg_solve(None, one, one, one, one, None, None, 2, 2, 4, params, one, one, res, one, 1 << 20)
+    assert rc == _lib.HM_EINVAL and "runtime limits" in _lib.last_error()
+
+
+def test_workspace_queries_are_host_arithmetic():
+    lib = _lib.load()
+    small = lib.hm_pricing_l2sq_workspace_bytes(1000, 1000, 64, 8, 7)
+    big = lib.hm_pricing_l2sq_workspace_bytes(131072, 131072, 64, 8, 7)
+    assert 0 < small < big
+    # C5: per-row candidate lists stay small next to the 2 x 39 GiB feature matrices
+    c5 = lib.hm_pricing_l2sq_workspace_bytes(1_280_000, 1_280_000, 8192, 2, 7)
+    assert c5 < 1 << 30
+    assert lib.hm_pricing_l2sq_workspace_bytes(0, 10, 4, 2, 7) == 0
+    assert lib.hm_pricing_norm_workspace_bytes(524288, 524288, 8, 2, 7) > 0
+
+
+def test_python_mirror_rejects_host_tensors_like_the_reference():
+    from hello_ot_amd.kernels.generic_scan import ScanExtension
+
+    x = torch.zeros(4, 2)
+    v = torch.zeros(4, dtype=torch.float64)
+    with pytest.raises(ValueError, match="CUDA FP32/FP64 feature matrices"):
+        ScanExtension().fused_bidir_topk_stats_raw(x, x, v, v, v, v, 4, 4, 256, 2, True, False, False, 2, 2.0)
+    with pytest.raises(ValueError, match="power-of-two bucket"):
+        ScanExtension().fused_bidir_topk_stats_raw(x, x, v, v, v, v, 4, 4, 256, 3, True, False, False, 0, 2.0)
+
+
+def test_pdlp_mirror_contract_on_host():
+    from hello_ot_amd.lp import NativeRestrictedOTPDLP, SolverResult
+
+    with pytest.raises(ValueError):
+        NativeRestrictedOTPDLP(device="cpu")
+    fields = set(SolverResult.__dataclass_fields__)
+    assert {"success", "x", "y", "obj_val", "dual_obj_val", "iterations", "termination_reason", "primal_feas",
+            "dual_feas", "gap", "solver_diag"} <= fields
+
+
+def test_native_gate_reports_missing_gpu():
+    from hello_ot_amd import native_runtime_compatibility
+
+    ok, detail = native_runtime_compatibility()
+    if not torch.cuda.is_available():
+        assert not ok and detail

@@ -1,0 +1,177 @@
+"""Parity of the MI355X pricing scans with the CPU oracle (GPU only)."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from hello_ot_amd.kernels.generic_scan import ScanExtension, pricing_l2sq, pricing_norm
+
+pytestmark = pytest.mark.gpu
+
+
+def _l2sq_case(m, n, d, seed, *, dual_mean=None, dup=False, integer=False):
+    rng = np.random.default_rng(seed)
+    if integer:
+        X = rng.integers(-3, 4, (m, d)).astype(np.float32)
+        Y = rng.integers(-3, 4, (n, d)).astype(np.float32)
+    else:
+        X = rng.standard_normal((m, d)).astype(np.float32)
+        Y = rng.standard_normal((n, d)).astype(np.float32)
+    if dup and n > 8:
+        Y[n // 2] = Y[1]
+        Y[n - 1] = Y[1]
+    p = (X.astype(np.float64) ** 2).sum(1)
+    q = (Y.astype(np.float64) ** 2).sum(1)
+    mean = float(d) if dual_mean is None else dual_mean
+    f = rng.normal(mean, 2.0, m)
+    g = rng.normal(mean, 2.0, n)
+    if dup and n > 8:
+        g[n // 2] = g[1]
+        g[n - 1] = g[1]
+    if integer:
+        f = np.round(f)
+        g = np.round(g)
+    return X, Y, p, q, f - p, g - q
+
+
+def _to(dev, *arrays):
+    return [torch.as_tensor(a).to(dev) for a in arrays]
+
+
+def _assert_stats(gpu, ref, rtol=2e-5):
+    gpu = gpu.cpu().numpy()
+    np.testing.assert_allclose(gpu[0], ref[0], rtol=rtol)
+    np.testing.assert_allclose(gpu[1], ref[1], rtol=rtol)
+    assert abs(gpu[2] - ref[2]) <= max(2.0, 2e-5 * ref[2])
+    np.testing.assert_allclose(gpu[3], ref[3], rtol=1e-15)
+
+
+@pytest.mark.parametrize("m,n,d,k,scale", [
+    (257, 300, 64, 8, 2.0),     # ragged rows/cols, C2 dimension
+    (130, 129, 3, 1, 2.0),      # tiny d, one candidate
+    (64, 1000, 33, 2, 1.0),     # dot_scale 1, d not a multiple of 4
+    (100, 200, 7, 17, 2.0),     # irregular k (reference tests k in {1,3,8,17,32})
+    (50, 40, 100, 32, 2.0),     # k close to n
+    (300, 500, 300, 3, 2.0),    # two-level fp32 accumulation (d > 256)
+    (1, 1, 1, 1, 2.0),          # smallest problem
+    (5, 3, 16, 8, 2.0),         # k > n: sentinel slots
+])
+def test_l2sq_bidirectional_matches_oracle(cuda, m, n, d, k, scale):
+    X, Y, p, q, qb, db = _l2sq_case(m, n, d, seed=m + 7 * n + d)
+    orv, ori, ocv, oci, ost = oracle.l2sq_scan(X, Y, p, q, qb, db, k, scale)
+    tX, tY, tp, tq, tqb, tdb = _to(cuda, X, Y, p, q, qb, db)
+    rv, ri, cv, ci, st = pricing_l2sq(tX, tY, tp, tq, tqb, tdb, k, dot_scale=scale, rows=True, cols=True,
+                                      stats=True, linf=True)
+    np.testing.assert_array_equal(ri.cpu().numpy(), ori)
+    np.testing.assert_array_equal(ci.cpu().numpy(), oci)
+    np.testing.assert_array_equal(rv.cpu().numpy(), orv)   # exact fp64 re-evaluation: same bits
+    np.testing.assert_array_equal(cv.cpu().numpy(), ocv)
+    _assert_stats(st, ost)
+    np.testing.assert_allclose(st[4].item(), ost[4], rtol=2e-5)
+
+
+def test_l2sq_ties_and_duplicates_lowest_index_wins(cuda):
+    X, Y, p, q, qb, db = _l2sq_case(200, 301, 8, seed=5, dup=True, integer=True)
+    for k in (1, 4, 16):
+        orv, ori, ocv, oci, _ = oracle.l2sq_scan(X, Y, p, q, qb, db, k, 2.0)
+        rv, ri, cv, ci, _ = pricing_l2sq(*_to(cuda, X, Y, p, q, qb, db), k, stats=False)
+        np.testing.assert_array_equal(ri.cpu().numpy(), ori)
+        np.testing.assert_array_equal(ci.cpu().numpy(), oci)
+        np.testing.assert_array_equal(rv.cpu().numpy(), orv)
+
+
+def test_l2sq_all_equal_scores_take_lowest_indices(cuda):
+    # every pair ties exactly: integer-valued identical points -> every row's top-k is columns 0..k-1
+    m, n, d, k = 70, 500, 4, 8
+    X = np.ones((m, d), np.float32)
+    Y = np.ones((n, d), np.float32)
+    p = (X.astype(np.float64) ** 2).sum(1)
+    q = (Y.astype(np.float64) ** 2).sum(1)
+    qb, db = -p, -q
+    rv, ri, cv, ci, st = pricing_l2sq(*_to(cuda, X, Y, p, q, qb, db), k)
+    assert (ri.cpu().numpy() == np.arange(k)[None, :]).all()
+    assert (ci.cpu().numpy() == np.arange(k)[None, :]).all()
+    assert (rv.cpu().numpy() == 0.0).all()
+
+
+def test_l2sq_c2_shape_properties_and_sampled_rows(cuda):
+    """C2 (131072 x 131072, d=64, k=8): full-size run, every row sorted with valid indices, and 96 random
+    rows plus 96 random columns re-derived by the oracle."""
+    m = n = 131072
+    d, k = 64, 8
+    g = torch.Generator(device="cpu").manual_seed(42)
+    X = torch.randn(m, d, generator=g, dtype=torch.float32)
+    Y = torch.randn(n, d, generator=g, dtype=torch.float32)
+    f = 64.0 + 2.0 * torch.randn(m, generator=g, dtype=torch.float64)
+    gg = 64.0 + 2.0 * torch.randn(n, generator=g, dtype=torch.float64)
+    p = (X.double() ** 2).sum(1)
+    q = (Y.double() ** 2).sum(1)
+    rv, ri, cv, ci, st = pricing_l2sq(*[t.to(cuda) for t in (X, Y, p, q, f - p, gg - q)], k)
+    rv, ri, cv, ci = rv.cpu().numpy(), ri.cpu().numpy(), cv.cpu().numpy(), ci.cpu().numpy()
+    assert (np.diff(rv, axis=1) <= 0).all() and (np.diff(cv, axis=1) <= 0).all()
+    assert ri.min() >= 0 and ri.max() < n and ci.min() >= 0 and ci.max() < m
+    rng = np.random.default_rng(0)
+    Xn, Yn, pn, qn = X.numpy(), Y.numpy(), p.numpy(), q.numpy()
+    qbn, dbn = (f - p).numpy(), (gg - q).numpy()
+    rows = rng.choice(m, 96, replace=False)
+    orv, ori = oracle.topk(oracle.l2sq_matrices(Xn[rows], Yn, pn[rows], qn, qbn[rows], dbn, 2.0)[0], k)
+    np.testing.assert_array_equal(ri[rows], ori)
+    np.testing.assert_array_equal(rv[rows], orv)
+    cols = rng.choice(n, 96, replace=False)
+    sig_c = oracle.l2sq_matrices(Xn, Yn[cols], pn, qn[cols], qbn, dbn[cols], 2.0)[0]
+    ocv, oci = oracle.topk(sig_c, k, transpose=True)
+    np.testing.assert_array_equal(ci[cols], oci)
+    np.testing.assert_array_equal(cv[cols], ocv)
+
+
+@pytest.mark.parametrize("kind", [0, 1, 2])
+@pytest.mark.parametrize("m,n,d,k", [(300, 257, 8, 2), (129, 700, 3, 8), (64, 64, 40, 1), (20, 30, 100, 5)])
+def test_norm_bidirectional_matches_oracle(cuda, kind, m, n, d, k):
+    rng = np.random.default_rng(m + n + d + kind)
+    X = rng.random((m, d)).astype(np.float32)
+    Y = rng.random((n, d)).astype(np.float32)
+    f = rng.normal(0.3, 0.2, m)
+    g = rng.normal(0.3, 0.2, n)
+    orv, ori, ocv, oci, ost = oracle.norm_scan(X, Y, f, g, k, kind)
+    rv, ri, cv, ci, st = pricing_norm(*_to(cuda, X, Y, f, g), k, kind)
+    np.testing.assert_array_equal(ri.cpu().numpy(), ori)
+    np.testing.assert_array_equal(ci.cpu().numpy(), oci)
+    np.testing.assert_array_equal(rv.cpu().numpy(), orv)
+    np.testing.assert_array_equal(cv.cpu().numpy(), ocv)
+    _assert_stats(st, ost)
+    np.testing.assert_allclose(st[4].item(), ost[4], rtol=1e-7)
+
+
+def test_norm_ties_on_a_grid(cuda):
+    # integer grid points: many exactly equal l1 distances
+    rng = np.random.default_rng(2)
+    X = rng.integers(0, 4, (100, 2)).astype(np.float32)
+    Y = rng.integers(0, 4, (150, 2)).astype(np.float32)
+    f = np.zeros(100)
+    g = np.zeros(150)
+    for kind in (0, 1):
+        orv, ori, ocv, oci, _ = oracle.norm_scan(X, Y, f, g, 4, kind)
+        rv, ri, cv, ci, _ = pricing_norm(*_to(cuda, X, Y, f, g), 4, kind, stats=False)
+        np.testing.assert_array_equal(ri.cpu().numpy(), ori)
+        np.testing.assert_array_equal(ci.cpu().numpy(), oci)
+
+
+def test_scan_extension_reference_layouts(cuda):
+    ext = ScanExtension()
+    X, Y, p, q, qb, db = _l2sq_case(90, 110, 16, seed=3)
+    out = ext.fused_bidir_topk_stats_raw(*_to(cuda, X, Y, p, q, qb, db), 4096, 4096, 256, 2, True, True, False, 2, 2.0)
+    assert out[0].shape == (90, 2) and out[0].dtype == torch.float64
+    assert out[1].dtype == torch.int32 and out[3].dtype == torch.int32
+    assert out[4].shape == (4,) and out[5].device.type == "cpu"
+    _, _, _, _, ost = oracle.l2sq_scan(X, Y, p, q, qb, db, 2, 2.0)
+    np.testing.assert_allclose(out[4].cpu().numpy(), [ost[0], ost[1], ost[2], ost[4]], rtol=2e-5)
+    with pytest.raises(ValueError, match="power-of-two bucket"):
+        ext.fused_bidir_topk_stats_raw(*_to(cuda, X, Y, p, q, qb, db), 1, 1, 256, 3, True, True, False, 0, 2.0)
+    with pytest.raises(ValueError, match="invalid raw pricing tile"):
+        ext.fused_bidir_topk_stats_raw(*_to(cuda, X, Y, p, q, qb, db), 1, 1, 256, 2, True, True, False, 2, 3.0)
+    f = np.random.default_rng(1).random(90)
+    g = np.random.default_rng(2).random(110)
+    norm = ext.fused_gcost_bidir_certificate(*_to(cuda, X, Y, f, g), 4, 0)
+    assert len(norm) == 9 and norm[1].dtype == torch.int64 and norm[8].dtype == torch.int64

@@ -1,0 +1,164 @@
+"""Parity of the MI355X SDDMM and Halpern-PDHG kernels with the CPU oracle (GPU only)."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from hello_ot_amd.costs.pairs import lowrank_csr_costs, lowrank_pair_costs, norm_pair_costs
+from hello_ot_amd.lp import NativeRestrictedOTPDLP
+
+pytestmark = pytest.mark.gpu
+
+
+def _csr(rng, m, n, per_row):
+    cols = [np.sort(rng.choice(n, per_row, replace=False)) for _ in range(m)]
+    rowptr = np.concatenate([[0], np.cumsum([len(c) for c in cols])]).astype(np.int32)
+    return rowptr, np.concatenate(cols).astype(np.int32)
+
+
+@pytest.mark.parametrize("m,n,d,per_row", [(300, 400, 256, 16), (100, 90, 7, 5), (64, 64, 600, 3), (33, 50, 64, 50)])
+def test_sddmm_csr_bit_exact(cuda, m, n, d, per_row):
+    rng = np.random.default_rng(m + d)
+    X = rng.standard_normal((m, d)).astype(np.float32)
+    Y = rng.standard_normal((n, d)).astype(np.float32)
+    p = (X.astype(np.float64) ** 2).sum(1)
+    q = (Y.astype(np.float64) ** 2).sum(1)
+    rowptr, col = _csr(rng, m, n, per_row)
+    ref = oracle.sddmm_l2sq(X, Y, p, q, rowptr, col, 2.0)
+    t = [torch.as_tensor(a).to(cuda) for a in (X, Y, p, q, rowptr, col)]
+    out = lowrank_csr_costs(t[0], t[1], t[2], t[3], t[4], t[5], dot_scale=2.0)
+    np.testing.assert_array_equal(out.cpu().numpy(), ref)
+
+
+def test_sddmm_csr_empty_rows_and_validation(cuda):
+    rng = np.random.default_rng(1)
+    X = rng.standard_normal((6, 8)).astype(np.float32)
+    Y = rng.standard_normal((5, 8)).astype(np.float32)
+    p = (X.astype(np.float64) ** 2).sum(1)
+    q = (Y.astype(np.float64) ** 2).sum(1)
+    rowptr = np.array([0, 0, 2, 2, 3, 3, 3], np.int32)
+    col = np.array([4, 1, 0], np.int32)
+    ref = oracle.sddmm_l2sq(X, Y, p, q, rowptr, col, 2.0)
+    t = [torch.as_tensor(a).to(cuda) for a in (X, Y, p, q, rowptr, col)]
+    np.testing.assert_array_equal(lowrank_csr_costs(*t).cpu().numpy(), ref)
+    bad = torch.as_tensor(np.array([4, 1, 5], np.int32)).to(cuda)
+    with pytest.raises(ValueError, match="out of bounds"):
+        lowrank_csr_costs(t[0], t[1], t[2], t[3], t[4], bad)
+
+
+@pytest.mark.parametrize("d", [1, 8, 20, 64, 130])
+def test_pair_costs_l2sq_and_norms_bit_exact(cuda, d):
+    rng = np.random.default_rng(d)
+    X = rng.random((40, d)).astype(np.float32)
+    Y = rng.random((50, d)).astype(np.float32)
+    p = (X.astype(np.float64) ** 2).sum(1)
+    q = (Y.astype(np.float64) ** 2).sum(1)
+    rows = rng.integers(0, 40, 777)
+    cols = rng.integers(0, 50, 777)
+    order = np.lexsort((cols, rows))
+    rows_s, cols_s = rows[order], cols[order]
+    rowptr = np.searchsorted(rows_s, np.arange(41)).astype(np.int32)
+    ref = oracle.sddmm_l2sq(X, Y, p, q, rowptr, cols_s.astype(np.int32), 2.0)
+    tX, tY, tp, tq = (torch.as_tensor(a).to(cuda) for a in (X, Y, p, q))
+    out = lowrank_pair_costs(tX, tY, tp, tq, torch.as_tensor(rows_s).to(cuda), torch.as_tensor(cols_s).to(cuda))
+    np.testing.assert_array_equal(out.cpu().numpy(), ref)
+    for kind in (0, 1, 2):
+        refn = oracle.pair_costs_norm(X, Y, rows, cols, kind)
+        outn = norm_pair_costs(tX, tY, torch.as_tensor(rows).to(cuda), torch.as_tensor(cols).to(cuda), kind)
+        np.testing.assert_array_equal(outn.cpu().numpy(), refn)
+
+
+def _small_problem():
+    return dict(rows=np.array([0, 0, 1, 1]), cols=np.array([0, 1, 0, 1]), costs=np.array([0.0, 2.0, 1.0, 0.0]),
+                source_mass=np.array([0.4, 0.6]), target_mass=np.array([0.5, 0.5]))
+
+
+@pytest.mark.parametrize("warm", [False, True])
+def test_pdhg_kat_small_problem(cuda, warm):
+    # tests/torch_restricted_ot_pdlp_test.py:58-80
+    kw = {}
+    if warm:
+        kw = dict(warm_start_primal=np.array([0.35, 0.05, 0.15, 0.45]), warm_start_dual=np.zeros(4))
+    r = NativeRestrictedOTPDLP(device=cuda, evaluation_frequency=20, iteration_limit=200_000).solve_restricted(
+        **_small_problem(), tolerance=1e-7, **kw)
+    assert r.success, r.solver_diag
+    assert r.x.dtype == torch.float64 and r.y.dtype == torch.float64
+    assert r.obj_val == pytest.approx(0.1, abs=2e-6)
+    assert r.primal_feas < 1e-7 and r.dual_feas < 1e-7 and r.gap < 1e-7
+
+
+def test_pdhg_rejects_unbalanced_mass(cuda):
+    problem = _small_problem()
+    problem["target_mass"] = np.array([0.4, 0.5])
+    with pytest.raises(ValueError, match="equal source and target total mass"):
+        NativeRestrictedOTPDLP(device=cuda).solve_restricted(**problem)
+
+
+def _sparse_lp(seed, ns, nt, extra):
+    rng = np.random.default_rng(seed)
+    rows = np.concatenate([np.arange(ns), rng.integers(0, ns, extra), rng.integers(0, ns, nt)])
+    cols = np.concatenate([rng.integers(0, nt, ns), rng.integers(0, nt, extra), np.arange(nt)])
+    perm = rng.permutation(rows.size)  # arbitrary edge order
+    rows, cols = rows[perm], cols[perm]
+    costs = rng.random(rows.size)
+    a = rng.random(ns)
+    a /= a.sum()
+    b = rng.random(nt)
+    b /= b.sum()
+    return rows.astype(np.int64), cols.astype(np.int64), costs, a, b
+
+
+@pytest.mark.parametrize("freq,limit,tol", [(5, 40, 0.0), (50, 3000, 1e-9), (200, 100000, 1e-7)])
+def test_pdhg_matches_oracle_iterates(cuda, freq, limit, tol):
+    rows, cols, costs, a, b = _sparse_lp(4, 60, 45, 400)
+    ref = oracle.pdhg_solve(rows, cols, costs, a, b, evaluation_frequency=freq, iteration_limit=limit, tolerance=tol)
+    r = NativeRestrictedOTPDLP(device=cuda, evaluation_frequency=freq, iteration_limit=limit).solve_restricted(
+        rows=rows, cols=cols, costs=costs, source_mass=a, target_mass=b, tolerance=tol)
+    assert r.iterations == ref["iterations"]
+    assert r.termination_reason == ref["termination_reason"]
+    assert r.solver_diag["restart_count"] == ref["restart_count"]
+    np.testing.assert_allclose(r.x.cpu().numpy(), ref["x"], rtol=1e-9, atol=1e-12)
+    np.testing.assert_allclose(r.y.cpu().numpy(), ref["y"], rtol=1e-9, atol=1e-12)
+    assert r.obj_val == pytest.approx(ref["obj_val"], rel=1e-10)
+
+
+def test_pdhg_warm_start_matches_oracle(cuda):
+    rows, cols, costs, a, b = _sparse_lp(9, 30, 25, 120)
+    rng = np.random.default_rng(0)
+    x0 = rng.random(rows.size) * 0.01
+    y0 = rng.normal(0, 0.1, a.size + b.size)
+    ref = oracle.pdhg_solve(rows, cols, costs, a, b, warm_start_primal=x0, warm_start_dual=y0,
+                            evaluation_frequency=50, iteration_limit=3000, tolerance=1e-9)
+    r = NativeRestrictedOTPDLP(device=cuda, evaluation_frequency=50, iteration_limit=3000).solve_restricted(
+        rows=rows, cols=cols, costs=costs, source_mass=a, target_mass=b, warm_start_primal=x0,
+        warm_start_dual=y0, tolerance=1e-9)
+    assert r.iterations == ref["iterations"]
+    np.testing.assert_allclose(r.x.cpu().numpy(), ref["x"], rtol=1e-9, atol=1e-12)
+    np.testing.assert_allclose(r.y.cpu().numpy(), ref["y"], rtol=1e-9, atol=1e-12)
+
+
+def test_pdhg_c3_shape_1000_iterations_against_oracle(cuda):
+    """C3 structure (16 sorted uniform columns per row, uniform marginals, SDDMM costs), 1000 iterations,
+    at m = n = 8192 where the CPU oracle finishes in seconds."""
+    m = n = 8192
+    d = 256
+    rng = np.random.default_rng(3)
+    X = rng.standard_normal((m, d)).astype(np.float32)
+    Y = rng.standard_normal((n, d)).astype(np.float32)
+    rowptr, col = _csr(rng, m, n, 16)
+    p = (X.astype(np.float64) ** 2).sum(1)
+    q = (Y.astype(np.float64) ** 2).sum(1)
+    costs = oracle.sddmm_l2sq(X, Y, p, q, rowptr, col, 2.0)
+    rows = np.repeat(np.arange(m), 16)
+    a = np.full(m, 1.0 / m)
+    b = np.full(n, 1.0 / n)
+    ref = oracle.pdhg_solve(rows, col, costs, a, b, evaluation_frequency=200, iteration_limit=1000, tolerance=0.0)
+    r = NativeRestrictedOTPDLP(device=cuda, evaluation_frequency=200, iteration_limit=1000).solve_restricted(
+        rows=rows, cols=col, costs=costs, source_mass=a, target_mass=b, tolerance=0.0)
+    assert r.iterations == ref["iterations"] == 1000
+    assert r.solver_diag["restart_count"] == ref["restart_count"]
+    np.testing.assert_allclose(r.x.cpu().numpy(), ref["x"], rtol=1e-8, atol=1e-14)
+    np.testing.assert_allclose(r.y.cpu().numpy(), ref["y"], rtol=1e-8, atol=1e-10)
+    assert r.obj_val == pytest.approx(ref["obj_val"], rel=1e-9)
