@@ -1,0 +1,378 @@
+"""Benchmark of the MI355X HELLO hot path (one GPU).
+
+Headline (BASELINE.json metric "pricing pairs/s ..., m=n=1.28M d=8192 l2^2"): one step = the l2^2
+bidirectional pricing scan with the full-edge certificate (the work of ``check_optimality``) of one query chunk
+against the resident side of the C5 instance: resident Y = 1,280,000 x 8192 fp32 drawn from a 64-component
+Gaussian mixture (means ~ N(0, 4I), identity covariance, equal weights), query chunk X = ``--chunk`` rows of an
+independent mixture; k = 2 (pricing_topk default). Inputs are resident in HBM before timing starts.
+``value`` = pairs scanned per second (chunk x 1.28M per step).
+
+Extra fields measure the other configurations: C2 (isolated 131072^2 d=64 k=8 scan), C3 (SDDMM + 1000 PDHG
+iterations, m=n=262144 d=256, 16 nnz/row) and C4 (l1 / linf scans, m=n=524288 d=8).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for _p in (ROOT, ROOT / "hello-ot_amd"):
+    if str(_p) not in sys.path:
+        sys.path.insert(0, str(_p))
+
+import numpy as np  # noqa: E402
+import torch  # noqa: E402
+
+PEAK_FP32_MFMA = 157.3e12   # MI355X dense fp32 matrix FLOP/s
+PEAK_HBM = 8.0e12           # MI355X HBM3E bytes/s
+PEAK_VALU_OPS = 256 * 64 * 2.4e9  # non-packed fp32 VALU lane-ops/s (256 CU x 64 lanes/clk x 2.4 GHz)
+
+C5_N = 1_280_000
+C5_D = 8192
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def sync():
+    torch.cuda.synchronize()
+
+
+def gmm(rows, d, seed, dev, means_seed, chunk=32768):
+    """Rows of a 64-component Gaussian mixture (means ~ N(0, 4I), identity covariance), generated on device."""
+    g = torch.Generator(device=dev)
+    g.manual_seed(means_seed)
+    means = 2.0 * torch.randn(64, d, generator=g, device=dev)
+    g.manual_seed(seed)
+    out = torch.empty(rows, d, dtype=torch.float32, device=dev)
+    for s in range(0, rows, chunk):
+        e = min(rows, s + chunk)
+        lab = torch.randint(0, 64, (e - s,), generator=g, device=dev)
+        out[s:e] = torch.randn(e - s, d, generator=g, device=dev) + means[lab]
+    return out
+
+
+def sqnorms(x, chunk=65536):
+    out = torch.empty(x.shape[0], dtype=torch.float64, device=x.device)
+    for s in range(0, x.shape[0], chunk):
+        out[s:s + chunk] = (x[s:s + chunk].double() ** 2).sum(1)
+    return out
+
+
+def time_steps(fn, steps, warmup):
+    for _ in range(warmup):
+        fn()
+    sync()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        fn()
+    sync()
+    return (time.perf_counter() - t0) / steps
+
+
+# ----------------------------------------------------------------------------------------------------------
+# headline: C5 pricing chunk
+# ----------------------------------------------------------------------------------------------------------
+
+def c5_inputs(dev, chunk):
+    log(f"[bench] generating C5 resident side {C5_N} x {C5_D} fp32 ({C5_N * C5_D * 4 / 2**30:.1f} GiB) ...")
+    Y = gmm(C5_N, C5_D, seed=2, dev=dev, means_seed=12)
+    X = gmm(chunk, C5_D, seed=1, dev=dev, means_seed=11)
+    p, q = sqnorms(X), sqnorms(Y)
+    # duals: g = 0 and f_i = min_j c_ij over 4096 sampled resident rows (a c-transform estimate), so a few
+    # hundred pairs per row have sigma > 0, as in a refinement iteration
+    idx = torch.randperm(C5_N, device=dev)[:4096]
+    Ys = Y[idx]
+    f = torch.empty(chunk, dtype=torch.float64, device=dev)
+    for s in range(0, chunk, 4096):
+        dots = (X[s:s + 4096] @ Ys.T).double()
+        f[s:s + 4096] = (p[s:s + 4096, None] + q[idx][None, :] - 2.0 * dots).min(1).values
+    g = torch.zeros(C5_N, dtype=torch.float64, device=dev)
+    sync()
+    return X, Y, p, q, f, g
+
+
+def bench_c5(dev, chunk, steps, warmup):
+    from hello_ot_amd import _lib
+    from hello_ot_amd.kernels.generic_scan import pricing_l2sq
+
+    X, Y, p, q, f, g = c5_inputs(dev, chunk)
+    qb, db = f - p, g - q
+    k = 2
+
+    def step():
+        return pricing_l2sq(X, Y, p, q, qb, db, k, dot_scale=2.0, rows=True, cols=True, stats=True, linf=True)
+
+    log(f"[bench] C5 chunk {chunk} x {C5_N}, d={C5_D}, k={k}: warmup {warmup}, steps {steps}")
+    for _ in range(warmup):
+        step()
+    sync()
+    _lib.profile_reset()
+    _lib.profile_enable(True)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        out = step()
+    sync()
+    sec = (time.perf_counter() - t0) / steps
+    sweep_ms, sweeps = _lib.profile_query("l2sq_sweep")
+    fin_ms, fins = _lib.profile_query("l2sq_finalize")
+    res_ms, _ = _lib.profile_query("l2sq_rescan")
+    _lib.profile_enable(False)
+    pairs = chunk * C5_N
+    sweep_avg = sweep_ms / max(sweeps, 1) / 1e3
+    achieved = 2.0 * C5_D * pairs / sweep_avg
+    st = out[4].cpu().numpy()
+    info = {
+        "sweep_ms_avg": sweep_ms / max(sweeps, 1), "sweep_launches": sweeps,
+        "finalize_ms_avg": fin_ms / max(fins, 1), "rescan_ms_total": res_ms,
+        "positive_pairs": float(st[2]), "max_violation": float(st[3]),
+    }
+    del X, Y, p, q, f, g, qb, db, out
+    torch.cuda.empty_cache()
+    return sec, pairs, achieved, info
+
+
+def cpu_baseline_c5(dev, sample_rows=1024, sample_cols=65536, threads=16):
+    """Reference CPU backend path (cpp_scan.fused_dot_tile: torch.mm fp32 dots + _scan.dot_tile epilogue,
+    kernels/cpp_scan.py:9-21, _native/cpp/scan.cpp:136-227) on a sample of the C5 pricing work."""
+    import oracle
+
+    threads = min(threads, os.cpu_count() or 1)
+    torch.set_num_threads(threads)
+    X = gmm(sample_rows, C5_D, seed=1, dev=dev, means_seed=11).cpu()
+    Y = gmm(sample_cols, C5_D, seed=2, dev=dev, means_seed=12).cpu()
+    p = (X.double() ** 2).sum(1).numpy()
+    q = (Y.double() ** 2).sum(1).numpy()
+    f = p.copy() * 0.0
+    g = q.copy() * 0.0
+    sc = oracle.ref_scan()
+    k = 2
+    rv = np.full((sample_rows, k), -np.inf)
+    ri = np.full((sample_rows, k), -1, np.int64)
+    cv = np.full((sample_cols, k), -np.inf)
+    ci = np.full((sample_cols, k), -1, np.int64)
+    if sc is not None:
+        kind = "reference"
+        tile = 8192
+        t0 = time.perf_counter()
+        for s in range(0, sample_cols, tile):
+            dots = torch.mm(X, Y[s:s + tile].T).numpy()
+            cvv = np.ascontiguousarray(cv[s:s + tile])
+            cii = np.ascontiguousarray(ci[s:s + tile])
+            sc.dot_tile(dots, p, q[s:s + tile], f, g[s:s + tile], rv, ri, cvv, cii, 2.0, 0, s, 0, threads)
+            cv[s:s + tile], ci[s:s + tile] = cvv, cii
+        sec = time.perf_counter() - t0
+    else:
+        kind = "port"
+        sample_cols = 4096
+        Y = Y[:sample_cols]
+        q = q[:sample_cols]
+        t0 = time.perf_counter()
+        oracle.l2sq_scan(X.numpy(), Y.numpy(), p, q, f - p, g[:sample_cols] - q, k, 2.0)
+        sec = time.perf_counter() - t0
+    pairs = sample_rows * sample_cols
+    return {"value": pairs / sec, "unit": "pairs/s", "cores": threads, "kind": kind,
+            "sample": f"{sample_rows} query x {sample_cols} resident rows of the C5 mixture, d={C5_D}, k=2, "
+                      f"bidirectional + certificate ({sec:.1f} s)"}
+
+
+# ----------------------------------------------------------------------------------------------------------
+# extras: C2, C3, C4
+# ----------------------------------------------------------------------------------------------------------
+
+def bench_c2(dev, steps=3):
+    from hello_ot_amd import _lib
+    from hello_ot_amd.kernels.generic_scan import pricing_l2sq
+
+    m = n = 131072
+    d, k = 64, 8
+    rng = np.random.default_rng(42)
+    X = torch.as_tensor(rng.standard_normal((m, d)).astype(np.float32)).to(dev)
+    Y = torch.as_tensor(rng.standard_normal((n, d)).astype(np.float32)).to(dev)
+    f = torch.as_tensor(rng.normal(64.0, 2.0, m)).to(dev)
+    g = torch.as_tensor(rng.normal(64.0, 2.0, n)).to(dev)
+    p, q = sqnorms(X), sqnorms(Y)
+    qb, db = f - p, g - q
+    out = {}
+    for name, kw in (("rows", dict(rows=True, cols=False, stats=False)),
+                     ("bidir_stats", dict(rows=True, cols=True, stats=True, linf=True))):
+        fn = lambda: pricing_l2sq(X, Y, p, q, qb, db, k, **kw)  # noqa: E731
+        fn()
+        sync()
+        _lib.profile_reset()
+        _lib.profile_enable(True)
+        sec = time_steps(fn, steps, 0)
+        sw_ms, sw_n = _lib.profile_query("l2sq_sweep")
+        _lib.profile_enable(False)
+        sweep_s = sw_ms / max(sw_n, 1) / 1e3
+        out[name] = {"seconds": sec, "pairs_per_s": m * n / sec,
+                     "sweep_ms": sweep_s * 1e3, "sweep_tflops": 2 * d * m * n / sweep_s / 1e12,
+                     "sweep_mfma_frac": 2 * d * m * n / sweep_s / PEAK_FP32_MFMA}
+    return out
+
+
+def _c3_csr(rng, m, n, per_row):
+    """CSR with `per_row` distinct uniformly random columns per row, sorted within each row."""
+    cols = np.empty((m, per_row), np.int64)
+    todo = np.arange(m)
+    while todo.size:
+        draw = np.sort(rng.integers(0, n, (todo.size, per_row + 8)), axis=1)
+        dup = np.zeros_like(draw, bool)
+        dup[:, 1:] = draw[:, 1:] == draw[:, :-1]
+        ok = (~dup).sum(1) >= per_row
+        prio = rng.random(draw.shape)
+        prio[dup] = np.inf
+        pick = np.argsort(prio, axis=1)[:, :per_row]  # a uniform subset of the distinct draws
+        chosen = np.sort(np.take_along_axis(draw, pick, axis=1), axis=1)
+        cols[todo[ok]] = chosen[ok]
+        todo = todo[~ok]
+    rowptr = np.arange(0, m * per_row + 1, per_row, dtype=np.int32)
+    return rowptr, cols.reshape(-1).astype(np.int32)
+
+
+def bench_c3(dev):
+    from hello_ot_amd import _lib
+    from hello_ot_amd.costs.pairs import lowrank_csr_costs
+    from hello_ot_amd.lp import NativeRestrictedOTPDLP
+
+    m = n = 262144
+    d, per = 256, 16
+    rng = np.random.default_rng(3)
+    X = torch.as_tensor(rng.standard_normal((m, d)).astype(np.float32)).to(dev)
+    Y = torch.as_tensor(rng.standard_normal((n, d)).astype(np.float32)).to(dev)
+    rowptr, col = _c3_csr(rng, m, n, per)
+    nnz = col.size
+    p, q = sqnorms(X), sqnorms(Y)
+    trp, tcol = torch.as_tensor(rowptr).to(dev), torch.as_tensor(col).to(dev)
+    costs = lowrank_csr_costs(X, Y, p, q, trp, tcol)
+    sync()
+    _lib.profile_reset()
+    _lib.profile_enable(True)
+    reps = 5
+    for _ in range(reps):
+        costs = lowrank_csr_costs(X, Y, p, q, trp, tcol)
+    sync()
+    sd_ms, sd_n = _lib.profile_query("sddmm_l2sq_csr")
+    sd_s = sd_ms / max(sd_n, 1) / 1e3
+    gather_bytes = m * d * 4 + nnz * d * 4 + nnz * (4 + 8) + (m + 1) * 4 + (m + n) * 8
+    rows = torch.as_tensor(np.repeat(np.arange(m), per)).to(dev)
+    a = torch.full((m,), 1.0 / m, dtype=torch.float64, device=dev)
+    b = torch.full((n,), 1.0 / n, dtype=torch.float64, device=dev)
+    solver = NativeRestrictedOTPDLP(device=dev, evaluation_frequency=200, iteration_limit=1000)
+    _lib.profile_reset()
+    t0 = time.perf_counter()
+    r = solver.solve_restricted(rows=rows, cols=tcol, costs=costs, source_mass=a, target_mass=b, tolerance=0.0)
+    sync()
+    pd_s = time.perf_counter() - t0
+    it_ms, it_n = _lib.profile_query("pdhg_iteration")
+    _lib.profile_enable(False)
+    E, V = nnz, m + n
+    iter_bytes = 120 * E + 76 * V
+    it_s = it_ms / max(it_n, 1) / 1e3
+    return {
+        "sddmm_ms": sd_s * 1e3, "sddmm_gather_model_GBps": gather_bytes / sd_s / 1e9,
+        "sddmm_hbm_frac_gather_model": gather_bytes / sd_s / PEAK_HBM,
+        "pdhg_1000_iterations_s": pd_s, "pdhg_device_loop_s": r.solver_diag["device_loop_sec"],
+        "pdhg_iteration_us": it_s * 1e6, "pdhg_model_GBps": iter_bytes / it_s / 1e9,
+        "pdhg_hbm_frac_model": iter_bytes / it_s / PEAK_HBM, "pdhg_iterations": r.iterations,
+        "pdhg_restarts": r.solver_diag["restart_count"], "pdhg_objective": r.obj_val,
+    }
+
+
+def bench_c4(dev):
+    from hello_ot_amd import _lib
+    from hello_ot_amd.kernels.generic_scan import pricing_norm
+
+    m = n = 524288
+    d = 8
+    rng = np.random.default_rng(4)
+    X = torch.as_tensor(rng.random((m, d)).astype(np.float32)).to(dev)
+    Y = torch.as_tensor(rng.random((n, d)).astype(np.float32)).to(dev)
+    f = torch.as_tensor(rng.normal(1.2, 0.1, m)).to(dev)
+    g = torch.as_tensor(rng.normal(1.2, 0.1, n)).to(dev)
+    out = {}
+    for kind, name in ((0, "l1"), (1, "linf")):
+        pricing_norm(X, Y, f, g, 2, kind)
+        sync()
+        _lib.profile_reset()
+        _lib.profile_enable(True)
+        t0 = time.perf_counter()
+        pricing_norm(X, Y, f, g, 2, kind)
+        sync()
+        sec = time.perf_counter() - t0
+        sw_ms, sw_n = _lib.profile_query("norm_sweep")
+        _lib.profile_enable(False)
+        sweep_s = sw_ms / max(sw_n, 1) / 1e3
+        out[name] = {"bidir_stats_seconds": sec, "pairs_per_s_per_direction": m * n / sweep_s,
+                     "sweep_valu_frac_3d_ops": 3 * d * m * n / sweep_s / PEAK_VALU_OPS}
+    return out
+
+
+# ----------------------------------------------------------------------------------------------------------
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=3)
+    ap.add_argument("--warmup", type=int, default=1)
+    ap.add_argument("--chunk", type=int, default=8192, help="query rows per step against the 1.28M resident rows")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-extras", action="store_true")
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        if int(os.environ.get("RANK", "0")) == 0:
+            print("bench.py measures one MI355X: this build runs the hot path on a single GPU "
+                  "(multi-GPU sharding is a design note, not an implemented path).", file=sys.stderr)
+        sys.exit(2)
+    from hello_ot_amd import _lib
+
+    _lib.load()
+    dev = torch.device("cuda", 0)
+    sec, pairs, achieved, info = bench_c5(dev, args.chunk, args.steps, args.warmup)
+    extras = {}
+    if not args.no_extras:
+        log("[bench] C2 ...")
+        extras["c2_scan_131072x131072_d64_k8"] = bench_c2(dev)
+        log("[bench] C3 ...")
+        extras["c3_sddmm_pdhg_262144_d256"] = bench_c3(dev)
+        log("[bench] C4 ...")
+        extras["c4_norm_scan_524288_d8"] = bench_c4(dev)
+    cpu = None
+    if not args.no_cpu_baseline:
+        log("[bench] CPU baseline ...")
+        cpu = cpu_baseline_c5(dev)
+    line = {
+        "metric": "pricing pairs/s (l2^2 bidirectional scan + certificate, m=n=1.28M d=8192)",
+        "value": pairs / sec,
+        "unit": "pairs/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": sec * 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32 MFMA sweep, f64 exact re-check",
+        "data": "synthetic 64-component Gaussian mixtures (C5 recipe), generated on device",
+        "config": {"workload": f"C5 pricing step: {args.chunk} query rows x 1,280,000 resident rows, d=8192, k=2, "
+                               "rows+cols top-k + certificate", "chunk": args.chunk, "n_resident": C5_N,
+                   "d": C5_D, "k": 2},
+        "roofline": {"bound": "mfma", "achieved": achieved / 1e12, "peak": PEAK_FP32_MFMA / 1e12,
+                     "unit": "TFLOP/s", "frac": achieved / PEAK_FP32_MFMA, "traffic": None,
+                     "kernel": "l2sq_sweep", "flops_per_pair": 2 * C5_D},
+        "cpu_baseline": cpu,
+        "detail": info,
+        "extras": extras,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

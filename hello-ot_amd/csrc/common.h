@@ -18,6 +18,11 @@ namespace hm {
 void set_error(const char* fmt, ...);
 int fail(int code, const char* fmt, ...);
 
+// Per-kernel HIP-event timing (hm_profile_enable); no-ops unless enabled.
+bool profiling();
+void prof_begin(hipStream_t st, const char* name);
+void prof_end(hipStream_t st);
+
 #define HM_CHECK_ARG(cond, ...)                                  \
     do {                                                         \
         if (!(cond)) return ::hm::fail(HM_EINVAL, __VA_ARGS__);  \

@@ -544,8 +544,10 @@ int run_direction(hipStream_t st, const float* X, const float* Y, int64_t m, int
 #define HM_SWEEP(TL)                                                                                       \
     hipLaunchKernelGGL((l2sq_sweep<K1, TL>), grid, dim3(256), 0, st, X, Y, m, n, d, qb32, db32, p32, ge32,       \
                        (float)scale, plan.seg_len, part, blockstats, (int)vec4, (int)stats)
+    prof_begin(st, "l2sq_sweep");
     if (two_level) HM_SWEEP(true);
     else HM_SWEEP(false);
+    prof_end(st);
 #undef HM_SWEEP
     HM_LAUNCH_CHECK("l2sq_sweep");
     if (stats) {
@@ -566,16 +568,20 @@ int run_direction(hipStream_t st, const float* X, const float* Y, int64_t m, int
     hipLaunchKernelGGL(zero_words, dim3(1), dim3(64), 0, st, reinterpret_cast<unsigned long long*>(redo_count), 1);
     HM_LAUNCH_CHECK("zero_words");
     const unsigned fin_blocks = (unsigned)((m + 3) / 4);
+    prof_begin(st, "l2sq_finalize");
     hipLaunchKernelGGL((l2sq_finalize<K1>), dim3(fin_blocks), dim3(256), 0, st, X, Y, m, d, plan.S, part, qb, db, xnorm,
                        ymaxima, scale, k, bnd, out_val, out_idx, redo, redo_count, (int)transposed);
+    prof_end(st);
     HM_LAUNCH_CHECK("l2sq_finalize");
     const unsigned rescan_blocks = (unsigned)(m < 1024 ? m : 1024);
 #define HM_RESCAN(KK)                                                                                        \
     hipLaunchKernelGGL((l2sq_rescan<KK>), dim3(rescan_blocks), dim3(64), 0, st, X, Y, n, d, qb, db, scale, k, redo, \
                        redo_count, out_val, out_idx, (int)transposed)
+    prof_begin(st, "l2sq_rescan");
     if (k <= 2) HM_RESCAN(2);
     else if (k <= 8) HM_RESCAN(8);
     else HM_RESCAN(32);
+    prof_end(st);
 #undef HM_RESCAN
     HM_LAUNCH_CHECK("l2sq_rescan");
     return HM_OK;

@@ -519,6 +519,7 @@ extern "C" int hm_pdhg_solve(void* stream, const int64_t* rows, const int64_t* c
         const bool is_restart = (local_count % freq == 0) && restart;
         const bool checkpoint = major || is_restart;
         // px / py are read only by the evaluation that follows a major iteration
+        prof_begin(st, "pdhg_iteration");
         if (checkpoint) {
             if (major) {
                 hipLaunchKernelGGL((k_edge_pass<true, true>), dim3(ge), dim3(256), 0, st, P, primal_step, halpern);
@@ -531,6 +532,7 @@ extern "C" int hm_pdhg_solve(void* stream, const int64_t* rows, const int64_t* c
             hipLaunchKernelGGL((k_edge_pass<false, false>), dim3(ge), dim3(256), 0, st, P, primal_step, halpern);
             hipLaunchKernelGGL((k_node_pass<false, false>), dim3(gn), dim3(256), 0, st, P, dual_step, halpern);
         }
+        prof_end(st);
         HM_LAUNCH_CHECK("pdhg iteration");
         if (checkpoint) {
             hipLaunchKernelGGL(k_fixed_point, dim3(RB), dim3(RT), 0, st, P, P.partial);

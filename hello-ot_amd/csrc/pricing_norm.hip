@@ -40,7 +40,7 @@ __device__ inline float distance_reg(const float (&x)[DR], const float* __restri
             acc = (KIND == HM_COST_LINF) ? fmaxf(acc, part) : acc + part;
         }
     }
-    return (KIND == HM_COST_L2) ? __fsqrt_rn(acc) : acc;
+    return (KIND == HM_COST_L2) ? (float)sqrt((double)acc) : acc;  // fp64 sqrt rounded once: correctly rounded
 }
 
 // distance with x streamed from global memory (any d)
@@ -53,7 +53,7 @@ __device__ inline float distance_mem(const float* __restrict__ x, const float* _
         for (int k = base; k < end; ++k) part = feature_op<KIND>(part, x[k] - y[k]);
         acc = (KIND == HM_COST_LINF) ? fmaxf(acc, part) : acc + part;
     }
-    return (KIND == HM_COST_L2) ? __fsqrt_rn(acc) : acc;
+    return (KIND == HM_COST_L2) ? (float)sqrt((double)acc) : acc;  // fp64 sqrt rounded once: correctly rounded
 }
 
 __global__ void norm_prep(const float* __restrict__ Y, int64_t n, int d, const double* __restrict__ g,
@@ -288,8 +288,10 @@ int norm_direction_t(hipStream_t st, const float* X, const float* Y, int64_t m, 
     while (ntile > 1 && (size_t)ntile * (d + 1) > LDS_FLOATS) ntile >>= 1;
     if ((size_t)ntile * (d + 1) > LDS_FLOATS) return fail(HM_EINVAL, "norm pricing supports d <= %d", LDS_FLOATS - 1);
     const size_t shmem = ((size_t)ntile * d + ntile) * sizeof(float);
+    prof_begin(st, "norm_sweep");
     hipLaunchKernelGGL((norm_sweep<KIND, K, DR>), grid, dim3(256), shmem, st, X, Y, m, n, d, rb, cb, ymaxima, k,
                        plan.seg_len, pv, pi, bs, (int)stats, (int)transposed, ntile);
+    prof_end(st);
     HM_LAUNCH_CHECK("norm_sweep");
     hipLaunchKernelGGL((norm_merge<K>), dim3((unsigned)((m + 255) / 256)), dim3(256), 0, st, pv, pi, m, plan.S, k,
                        out_v, out_i);

@@ -152,11 +152,13 @@ extern "C" int hm_sddmm_l2sq_csr(void* stream, const float* X, const float* Y, c
     const unsigned grid = grid_for(m, 4);
 #define HM_SDDMM(XR) \
     hipLaunchKernelGGL((sddmm_l2sq_csr_kernel<XR>), dim3(grid), dim3(256), 0, st, X, Y, p, q, rowptr, col, m, d, scale, out)
+    prof_begin(st, "sddmm_l2sq_csr");
     if (d <= 64) HM_SDDMM(1);
     else if (d <= 128) HM_SDDMM(2);
     else if (d <= 256) HM_SDDMM(4);
     else if (d <= 512) HM_SDDMM(8);
     else HM_SDDMM(0);
+    prof_end(st);
 #undef HM_SDDMM
     HM_LAUNCH_CHECK("sddmm_l2sq_csr");
     return HM_OK;

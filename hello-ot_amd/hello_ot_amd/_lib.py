@@ -51,6 +51,9 @@ REASONS = {0: "UNSPECIFIED", 1: "OPTIMAL", 2: "ITERATION_LIMIT", 3: "NUMERICAL_D
 SIGNATURES = {
     "hm_last_error": (ctypes.c_char_p, []),
     "hm_abi_version": (ctypes.c_int, []),
+    "hm_profile_enable": (None, [ctypes.c_int]),
+    "hm_profile_reset": (None, []),
+    "hm_profile_query": (ctypes.c_int, [ctypes.c_char_p, ctypes.POINTER(_D), ctypes.POINTER(_I64)]),
     "hm_pricing_l2sq_workspace_bytes": (_SZ, [_I64, _I64, _I32, _I32, _U32]),
     "hm_pricing_l2sq": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I32, _I32, _D, _U32,
                                        _P, _P, _P, _P, _P, _P, _SZ]),
@@ -115,6 +118,22 @@ def ptr(t) -> ctypes.c_void_p:
     if t is None:
         return ctypes.c_void_p(0)
     return ctypes.c_void_p(int(t.data_ptr()))
+
+
+def profile_enable(on: bool = True) -> None:
+    load().hm_profile_enable(int(bool(on)))
+
+
+def profile_reset() -> None:
+    load().hm_profile_reset()
+
+
+def profile_query(name: str) -> tuple[float, int]:
+    """(total milliseconds, launches) of one kernel since the last reset (waits for pending events)."""
+    ms = _D(0.0)
+    n = _I64(0)
+    load().hm_profile_query(name.encode(), ctypes.byref(ms), ctypes.byref(n))
+    return float(ms.value), int(n.value)
 
 
 def stream_handle(device) -> ctypes.c_void_p:

@@ -42,6 +42,17 @@ extern "C" {
 const char* hm_last_error(void);
 int hm_abi_version(void); /* 1 */
 
+/*
+ * Kernel timing. No reference counterpart: the reference returns a zeroed timing slot
+ * (generic_scan.py:577-597, "collect_timing"). When enabled, every hot-path launch is bracketed by HIP
+ * events on its own stream; hm_profile_query waits for the pending events and returns the accumulated
+ * milliseconds and launch count for one kernel name: "l2sq_sweep", "l2sq_finalize", "l2sq_rescan",
+ * "norm_sweep", "sddmm_l2sq_csr", "pdhg_iteration" (edge pass + node pass of one PDHG iteration).
+ */
+void hm_profile_enable(int on);
+void hm_profile_reset(void);
+int hm_profile_query(const char* name, double* total_ms, int64_t* launches);
+
 /* ---------------------------------------------------------------------------------------------------- */
 /* (a) Full-space pricing scan                                                                           */
 /* ---------------------------------------------------------------------------------------------------- */
