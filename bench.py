@@ -32,8 +32,22 @@ PEAK_FP32_MFMA = 157.3e12   # MI355X dense fp32 matrix FLOP/s
 PEAK_HBM = 8.0e12           # MI355X HBM3E bytes/s
 PEAK_VALU_OPS = 256 * 64 * 2.4e9  # non-packed fp32 VALU lane-ops/s (256 CU x 64 lanes/clk x 2.4 GHz)
 
+TRAFFIC_PROFILE = ROOT / "profiles" / "l2sq_sweep_c5_chunk8192.md"
+
 C5_N = 1_280_000
 C5_D = 8192
+
+
+def sweep_traffic():
+    """HBM bytes per l2sq_sweep launch at the C5 workload, from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE
+    summary (scaled by a plain copy kernel's counters); None when no such summary is present."""
+    try:
+        for line in TRAFFIC_PROFILE.read_text().splitlines():
+            if line.startswith("traffic_bytes_per_launch"):
+                return float(line.split("=")[1])
+    except OSError:
+        pass
+    return None
 
 
 def log(msg):
@@ -138,7 +152,7 @@ def bench_c5(dev, chunk, steps, warmup):
     return sec, pairs, achieved, info
 
 
-def cpu_baseline_c5(dev, sample_rows=1024, sample_cols=65536, threads=16):
+def cpu_baseline_c5(dev, sample_rows=4096, sample_cols=196608, threads=16):
     """Reference CPU backend path (cpp_scan.fused_dot_tile: torch.mm fp32 dots + _scan.dot_tile epilogue,
     kernels/cpp_scan.py:9-21, _native/cpp/scan.cpp:136-227) on a sample of the C5 pricing work."""
     import oracle
@@ -324,6 +338,9 @@ def main():
     ap.add_argument("--chunk", type=int, default=8192, help="query rows per step against the 1.28M resident rows")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extras", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="first run a plain 1 GiB device-to-device copy kernel three times (the reference point "
+                         "for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE to bytes)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -335,6 +352,14 @@ def main():
 
     _lib.load()
     dev = torch.device("cuda", 0)
+    if args.copy_calibration:
+        src = torch.ones(2**28, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        sync()
+        log("[bench] copy calibration: 3 x 1 GiB read + 1 GiB written")
+        del src, dst
     sec, pairs, achieved, info = bench_c5(dev, args.chunk, args.steps, args.warmup)
     extras = {}
     if not args.no_extras:
@@ -359,13 +384,14 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32 MFMA sweep, f64 exact re-check",
+        "dtype": "f32",
         "data": "synthetic 64-component Gaussian mixtures (C5 recipe), generated on device",
         "config": {"workload": f"C5 pricing step: {args.chunk} query rows x 1,280,000 resident rows, d=8192, k=2, "
                                "rows+cols top-k + certificate", "chunk": args.chunk, "n_resident": C5_N,
                    "d": C5_D, "k": 2},
         "roofline": {"bound": "mfma", "achieved": achieved / 1e12, "peak": PEAK_FP32_MFMA / 1e12,
-                     "unit": "TFLOP/s", "frac": achieved / PEAK_FP32_MFMA, "traffic": None,
+                     "unit": "TFLOP/s", "frac": achieved / PEAK_FP32_MFMA, "traffic": sweep_traffic(),
+                     "traffic_source": TRAFFIC_PROFILE.name,
                      "kernel": "l2sq_sweep", "flops_per_pair": 2 * C5_D},
         "cpu_baseline": cpu,
         "detail": info,
