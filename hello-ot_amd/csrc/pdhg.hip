@@ -5,14 +5,25 @@
 // constant step 0.998, reflected Halpern iterations, PID primal-weight restarts and relative L2 KKT checks
 // every `evaluation_frequency` iterations.
 //
-// Device layout: per edge e (x_e >= 0): endpoints (int32), scaled cost cs, iterate x, anchor ax, PDHG point px
-// (stored only when the next iteration evaluates), reflection rx, checkpoint delta dx. Per node (sources then
-// targets): scale, bs, ns, y, ay, py, dy and the target duals td = y / ns. Each node's incident edges are
-// listed in ascending edge id (stable radix sort), so every per-node sum runs in the same order as the CPU
-// restatement; only the global norms/dots use a fixed-shape tree.
+// Device layout: the per-edge primal state is mirrored in two orders so that both halves of an iteration
+// stream their edges contiguously and never gather per-edge values.
+//   source order (position p): edges sorted by source, ascending caller edge id within a source (stable
+//     sort), so source i owns [off[i], off[i+1]); perm[p] = caller edge id. Arrays: col, row, scaled cost cs,
+//     iterate x, anchor ax, PDHG point px (stored only when the next iteration evaluates), checkpoint delta dx.
+//   target order (slot k): edges sorted by target, ascending caller edge id within a target, so target t owns
+//     [off[n+t]-e, off[n+t+1]-e). Arrays: row_t, cs_t, x_t, ax_t, px_t.
+// Both copies receive identical operands in identical order and therefore stay bit-identical.
+// Per node (sources then targets): scale, bs, ns, y, ay, py, dy; td = y / ns for targets and sd = y / ns for
+// sources (the value the current iteration's primal step used).
 //
-// One iteration = edge pass (primal projection, reflection, Halpern) + node pass (A * reflected primal,
-// dual update, reflection, Halpern). Scalars read back to the host only at evaluations and checkpoints.
+// One iteration = source pass + target pass (the restatement's two loops):
+//   source pass: a G-lane group per source node computes its edges' PDHG step and reflection, updates their
+//                iterates (Halpern), and the node's dual from the in-order sum of the reflections;
+//   target pass: a G-lane group per target node recomputes the same steps for its edges from the mirrored
+//                state and the source duals sd, and updates the target dual from its in-order sum.
+// Each group sums its lanes' values in edge order through lane shuffles (bit-identical to a sequential sum).
+// The only gathers are of node values (sd, td: a few MB, L2-resident). Scalars read back to the host only at
+// evaluations and checkpoints.
 #include <hipcub/hipcub.hpp>
 
 #include <chrono>
@@ -28,11 +39,14 @@ constexpr int RT = 256;      // threads per reduction block
 
 struct Pdhg {
     int64_t n, nt, nodes, e;
-    // edges
-    int32_t *row, *col;
-    double *cs, *x, *ax, *px, *rx, *dx;
+    // edges, source order
+    int32_t *row, *col, *perm;
+    double *cs, *x, *ax, *px, *dx;
+    // edges, target order
+    int32_t* row_t;
+    double *cs_t, *x_t, *ax_t, *px_t;
     // nodes
-    double *scale, *bs, *ns, *y, *ay, *py, *dy, *td;
+    double *scale, *bs, *ns, *y, *ay, *py, *dy, *td, *sd;
     int32_t *deg, *off, *eid;
     // sort scratch
     uint32_t *keys_in, *keys_out;
@@ -50,12 +64,17 @@ void pdhg_layout(A& a, int64_t n, int64_t nt, int64_t e, size_t sort_tmp, Pdhg& 
     const int64_t nodes = n + nt;
     P.row = a.template take<int32_t>(e);
     P.col = a.template take<int32_t>(e);
+    P.perm = a.template take<int32_t>(e);
     P.cs = a.template take<double>(e);
     P.x = a.template take<double>(e);
     P.ax = a.template take<double>(e);
     P.px = a.template take<double>(e);
-    P.rx = a.template take<double>(e);
     P.dx = a.template take<double>(e);
+    P.row_t = a.template take<int32_t>(e);
+    P.cs_t = a.template take<double>(e);
+    P.x_t = a.template take<double>(e);
+    P.ax_t = a.template take<double>(e);
+    P.px_t = a.template take<double>(e);
     P.scale = a.template take<double>(nodes);
     P.bs = a.template take<double>(nodes);
     P.ns = a.template take<double>(nodes);
@@ -64,6 +83,7 @@ void pdhg_layout(A& a, int64_t n, int64_t nt, int64_t e, size_t sort_tmp, Pdhg& 
     P.py = a.template take<double>(nodes);
     P.dy = a.template take<double>(nodes);
     P.td = a.template take<double>(nt);
+    P.sd = a.template take<double>(n);
     P.deg = a.template take<int32_t>(nodes + 1);
     P.off = a.template take<int32_t>(nodes + 1);
     P.eid = a.template take<int32_t>(2 * e);
@@ -99,20 +119,17 @@ __global__ void k_fill_i32(int32_t* p, int64_t count, int32_t v) {
         p[i] = v;
 }
 
+// validation, degrees and the (node key, caller edge id) pairs of the incidence sort
 __global__ void k_edges(const int64_t* __restrict__ rows, const int64_t* __restrict__ cols, int64_t e, int64_t n,
-                        int64_t nt, int32_t* __restrict__ row, int32_t* __restrict__ col, int32_t* __restrict__ deg,
-                        uint32_t* __restrict__ keys, int32_t* __restrict__ vals, int* __restrict__ flag) {
+                        int64_t nt, int32_t* __restrict__ deg, uint32_t* __restrict__ keys, int32_t* __restrict__ vals,
+                        int* __restrict__ flag) {
     for (int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; j < e; j += (int64_t)gridDim.x * blockDim.x) {
         const int64_t r = rows[j], c = cols[j];
         if (r < 0 || r >= n || c < 0 || c >= nt) {
             atomicOr(flag, 1);
-            row[j] = 0;
-            col[j] = 0;
             keys[j] = 0;
             keys[e + j] = (uint32_t)n;
         } else {
-            row[j] = (int32_t)r;
-            col[j] = (int32_t)c;
             atomicAdd(&deg[r], 1);
             atomicAdd(&deg[n + c], 1);
             keys[j] = (uint32_t)r;
@@ -120,6 +137,39 @@ __global__ void k_edges(const int64_t* __restrict__ rows, const int64_t* __restr
         }
         vals[j] = (int32_t)j;
         vals[e + j] = (int32_t)j;
+    }
+}
+
+// After the stable sort eid[0..e) lists caller edge ids by source and eid[e..2e) by target.
+__global__ void k_source_setup(const int32_t* __restrict__ eid, int64_t e, const int64_t* __restrict__ rows,
+                               const int64_t* __restrict__ cols, const double* __restrict__ c,
+                               const double* __restrict__ x0, double bound, double objective, double variable,
+                               Pdhg P) {
+    for (int64_t p = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; p < e; p += (int64_t)gridDim.x * blockDim.x) {
+        const int32_t j = eid[p];
+        P.perm[p] = j;
+        P.row[p] = (int32_t)rows[j];
+        P.col[p] = (int32_t)cols[j];
+        P.cs[p] = c[j] * objective / variable;
+        const double a = x0 ? fmax(x0[j], 0.0) * variable * bound : 0.0;
+        P.ax[p] = a;
+        P.x[p] = a;
+        P.px[p] = a;
+        P.dx[p] = 0.0;
+    }
+}
+
+__global__ void k_target_setup(const int32_t* __restrict__ eid, int64_t e, const int64_t* __restrict__ rows,
+                               const double* __restrict__ c, const double* __restrict__ x0, double bound,
+                               double objective, double variable, Pdhg P) {
+    for (int64_t k = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; k < e; k += (int64_t)gridDim.x * blockDim.x) {
+        const int32_t j = eid[e + k];
+        P.row_t[k] = (int32_t)rows[j];
+        P.cs_t[k] = c[j] * objective / variable;
+        const double a = x0 ? fmax(x0[j], 0.0) * variable * bound : 0.0;
+        P.ax_t[k] = a;
+        P.x_t[k] = a;
+        P.px_t[k] = a;
     }
 }
 
@@ -167,21 +217,6 @@ __global__ void k_node_setup(const int32_t* __restrict__ deg, const double* __re
         py[i] = a;
         dy[i] = 0.0;
         if (i >= n) td[i - n] = a / nsv;
-    }
-}
-
-__global__ void k_edge_setup(const double* __restrict__ c, const double* __restrict__ x0, int64_t e, double bound,
-                             double objective, double variable, double* __restrict__ cs, double* __restrict__ x,
-                             double* __restrict__ ax, double* __restrict__ px, double* __restrict__ rx,
-                             double* __restrict__ dx) {
-    for (int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; j < e; j += (int64_t)gridDim.x * blockDim.x) {
-        cs[j] = c[j] * objective / variable;
-        const double a = x0 ? fmax(x0[j], 0.0) * variable * bound : 0.0;
-        ax[j] = a;
-        x[j] = a;
-        px[j] = a;
-        rx[j] = 0.0;
-        dx[j] = 0.0;
     }
 }
 
@@ -251,17 +286,22 @@ __global__ void k_evaluate(const Pdhg P, const double* __restrict__ b, const dou
     const double vb = variable * bound;
     for (int64_t i = (int64_t)blockIdx.x * RT + threadIdx.x; i < P.nodes; i += (int64_t)RB * RT) {
         double sum = 0.0;
-        for (int32_t k = P.off[i]; k < P.off[i + 1]; ++k) sum += P.px[P.eid[k]] / vb;
+        if (i < P.n) {
+            for (int32_t k = P.off[i]; k < P.off[i + 1]; ++k) sum += P.px[k] / vb;
+        } else {
+            for (int32_t k = P.off[i]; k < P.off[i + 1]; ++k) sum += P.px_t[k - P.e] / vb;
+        }
         const double delta = sum - b[i];
         v[0] = v[0] + delta * delta;
         v[1] = v[1] + b[i] * (P.py[i] / (P.scale[i] * objective));
     }
     for (int64_t j = (int64_t)blockIdx.x * RT + threadIdx.x; j < P.e; j += (int64_t)RB * RT) {
         const int32_t r = P.row[j], cc = P.col[j];
-        const double score = P.py[r] / (P.scale[r] * objective) + P.py[P.n + cc] / (P.scale[P.n + cc] * objective) - c[j];
+        const double cj = c[P.perm[j]];
+        const double score = P.py[r] / (P.scale[r] * objective) + P.py[P.n + cc] / (P.scale[P.n + cc] * objective) - cj;
         const double viol = fmax(score, 0.0);
         v[2] = v[2] + viol * viol;
-        v[3] = v[3] + c[j] * (P.px[j] / vb);
+        v[3] = v[3] + cj * (P.px[j] / vb);
     }
     block_reduce_store<4>(v, partial);
 }
@@ -283,37 +323,104 @@ __global__ void k_fixed_point(const Pdhg P, double* __restrict__ partial) {
 // ---------------------------------------------------------------------------------------------------------
 // iteration kernels
 // ---------------------------------------------------------------------------------------------------------
-template <bool CHECKPOINT, bool STORE>
-__global__ __launch_bounds__(256) void k_edge_pass(const Pdhg P, double primal_step, double halpern) {
+// Sum of the group's per-lane values in lane order 0..count-1 (every lane of the group gets the same bits as
+// a sequential loop over the group's edges).
+template <int G>
+__device__ inline double group_ordered_sum(double running, double value, int count) {
+    for (int t = 0; t < count; ++t) running += __shfl(value, t, G);
+    return running;
+}
+
+// Source pass: a G-lane group per source node (the restatement's first loop, solver.cpp:210-251 order).
+// A chunk covers G*U edges: lane g owns edges g, g+G, ..., g+(U-1)G of the chunk, all loaded before any sum.
+template <int G, int U, bool CHECKPOINT, bool STORE>
+__global__ __launch_bounds__(256) void k_source_pass(const Pdhg P, double primal_step, double dual_step,
+                                                     double halpern) {
     const double keep = 1.0 - halpern;
-    for (int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; j < P.e; j += (int64_t)gridDim.x * blockDim.x) {
-        const int32_t r = P.row[j], c = P.col[j];
-        const double at = P.y[r] / P.ns[r] + P.td[c];
-        const double xj = P.x[j];
-        const double pxj = fmax(xj - primal_step * (P.cs[j] - at), 0.0);
-        const double rxj = 2.0 * pxj - xj;
-        if (STORE) P.px[j] = pxj;
-        if (CHECKPOINT) P.dx[j] = rxj - xj;
-        P.rx[j] = rxj;
-        P.x[j] = halpern * rxj + keep * P.ax[j];
+    const int g = threadIdx.x % G;
+    const int64_t stride = (int64_t)gridDim.x * (blockDim.x / G);
+    for (int64_t i = (int64_t)blockIdx.x * (blockDim.x / G) + threadIdx.x / G; i < P.n; i += stride) {
+        const int32_t k0 = P.off[i], k1 = P.off[i + 1];
+        const double yi = P.y[i], nsi = P.ns[i];
+        const double source_dual = yi / nsi;
+        double sum = 0.0;
+        for (int32_t base = k0; base < k1; base += G * U) {
+            double r[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int32_t p = base + u * G + g;
+                r[u] = 0.0;
+                if (p < k1) {
+                    const double at = source_dual + P.td[P.col[p]];
+                    const double xj = P.x[p];
+                    const double pxj = fmax(xj - primal_step * (P.cs[p] - at), 0.0);
+                    r[u] = 2.0 * pxj - xj;
+                    if (STORE) P.px[p] = pxj;
+                    if (CHECKPOINT) P.dx[p] = r[u] - xj;
+                    P.x[p] = halpern * r[u] + keep * P.ax[p];
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int32_t left = k1 - (base + u * G);
+                if (left > 0) sum = group_ordered_sum<G>(sum, r[u], left < G ? left : G);
+            }
+        }
+        if (g == 0) {
+            P.sd[i] = source_dual;
+            const double pyi = yi - dual_step * (sum / nsi - P.bs[i]);
+            const double refl = 2.0 * pyi - yi;
+            if (STORE) P.py[i] = pyi;
+            if (CHECKPOINT) P.dy[i] = refl - yi;
+            P.y[i] = halpern * refl + keep * P.ay[i];
+        }
     }
 }
 
-template <bool CHECKPOINT, bool STORE>
-__global__ __launch_bounds__(256) void k_node_pass(const Pdhg P, double dual_step, double halpern) {
+// Target pass: a G-lane group per target node recomputes its edges' steps from the target-order mirror (the
+// operands are those the source pass used: sd of this iteration, td before this update) and updates the dual.
+template <int G, int U, bool CHECKPOINT, bool STORE>
+__global__ __launch_bounds__(256) void k_target_pass(const Pdhg P, double primal_step, double dual_step,
+                                                     double halpern) {
     const double keep = 1.0 - halpern;
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < P.nodes; i += (int64_t)gridDim.x * blockDim.x) {
+    const int g = threadIdx.x % G;
+    const int64_t stride = (int64_t)gridDim.x * (blockDim.x / G);
+    for (int64_t t = (int64_t)blockIdx.x * (blockDim.x / G) + threadIdx.x / G; t < P.nt; t += stride) {
+        const int64_t i = P.n + t;
+        const int32_t k0 = P.off[i] - (int32_t)P.e, k1 = P.off[i + 1] - (int32_t)P.e;
+        const double target_dual = P.td[t];
         double sum = 0.0;
-        const int32_t k1 = P.off[i + 1];
-        for (int32_t k = P.off[i]; k < k1; ++k) sum += P.rx[P.eid[k]];
-        const double yi = P.y[i];
-        const double pyi = yi - dual_step * (sum / P.ns[i] - P.bs[i]);
-        const double refl = 2.0 * pyi - yi;
-        if (STORE) P.py[i] = pyi;
-        if (CHECKPOINT) P.dy[i] = refl - yi;
-        const double yn = halpern * refl + keep * P.ay[i];
-        P.y[i] = yn;
-        if (i >= P.n) P.td[i - P.n] = yn / P.ns[i];
+        for (int32_t base = k0; base < k1; base += G * U) {
+            double r[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int32_t k = base + u * G + g;
+                r[u] = 0.0;
+                if (k < k1) {
+                    const double at = P.sd[P.row_t[k]] + target_dual;
+                    const double xj = P.x_t[k];
+                    const double pxj = fmax(xj - primal_step * (P.cs_t[k] - at), 0.0);
+                    r[u] = 2.0 * pxj - xj;
+                    if (STORE) P.px_t[k] = pxj;
+                    P.x_t[k] = halpern * r[u] + keep * P.ax_t[k];
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int32_t left = k1 - (base + u * G);
+                if (left > 0) sum = group_ordered_sum<G>(sum, r[u], left < G ? left : G);
+            }
+        }
+        if (g == 0) {
+            const double yi = P.y[i], nsi = P.ns[i];
+            const double pyi = yi - dual_step * (sum / nsi - P.bs[i]);
+            const double refl = 2.0 * pyi - yi;
+            if (STORE) P.py[i] = pyi;
+            if (CHECKPOINT) P.dy[i] = refl - yi;
+            const double yn = halpern * refl + keep * P.ay[i];
+            P.y[i] = yn;
+            P.td[t] = yn / nsi;
+        }
     }
 }
 
@@ -324,6 +431,9 @@ __global__ void k_restart(const Pdhg P) {
             const double v = P.px[j];
             P.ax[j] = v;
             P.x[j] = v;
+            const double vt = P.px_t[j];
+            P.ax_t[j] = vt;
+            P.x_t[j] = vt;
         }
         if (j < P.nodes) {
             const double v = P.py[j];
@@ -337,7 +447,7 @@ __global__ void k_restart(const Pdhg P) {
 __global__ void k_output(const Pdhg P, double vb, double objective, double* __restrict__ xo, double* __restrict__ yo) {
     const int64_t total = P.e > P.nodes ? P.e : P.nodes;
     for (int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; j < total; j += (int64_t)gridDim.x * blockDim.x) {
-        if (j < P.e) xo[j] = P.px[j] / vb;
+        if (j < P.e) xo[P.perm[j]] = P.px[j] / vb;
         if (j < P.nodes) yo[j] = P.py[j] / (P.scale[j] * objective);
     }
 }
@@ -347,6 +457,52 @@ inline unsigned grid_of(int64_t items) {
     if (b > 8192) b = 8192;
     if (b < 1) b = 1;
     return (unsigned)b;
+}
+
+inline unsigned group_grid(int64_t nodes, int g) {
+    int64_t b = (nodes + (256 / g) - 1) / (256 / g);
+    if (b > 65536) b = 65536;
+    if (b < 1) b = 1;
+    return (unsigned)b;
+}
+
+// Both passes run GL-lane groups with U edges per lane per chunk (U = 1, 2 or 4 from the side's mean degree).
+constexpr int GL = 8;
+
+inline int edges_per_lane(int64_t e, int64_t nodes) {
+    const int64_t mean = (e + nodes - 1) / nodes;
+    return mean <= GL ? 1 : (mean <= 12 ? 2 : 4);
+}
+
+template <int US, int UT, bool C, bool S>
+void launch_pair(hipStream_t st, const Pdhg& P, double ps, double ds, double h) {
+    hipLaunchKernelGGL((k_source_pass<GL, US, C, S>), dim3(group_grid(P.n, GL)), dim3(256), 0, st, P, ps, ds, h);
+    hipLaunchKernelGGL((k_target_pass<GL, UT, C, S>), dim3(group_grid(P.nt, GL)), dim3(256), 0, st, P, ps, ds, h);
+}
+
+template <int US, bool C, bool S>
+void launch_ut(hipStream_t st, const Pdhg& P, int ut, double ps, double ds, double h) {
+    if (ut == 1) launch_pair<US, 1, C, S>(st, P, ps, ds, h);
+    else if (ut == 2) launch_pair<US, 2, C, S>(st, P, ps, ds, h);
+    else launch_pair<US, 4, C, S>(st, P, ps, ds, h);
+}
+
+template <bool C, bool S>
+void launch_us(hipStream_t st, const Pdhg& P, int us, int ut, double ps, double ds, double h) {
+    if (us == 1) launch_ut<1, C, S>(st, P, ut, ps, ds, h);
+    else if (us == 2) launch_ut<2, C, S>(st, P, ut, ps, ds, h);
+    else launch_ut<4, C, S>(st, P, ut, ps, ds, h);
+}
+
+// One PDHG iteration (source pass + target pass). px / py are stored only on major iterations: they are read
+// only by the evaluation that follows one.
+int launch_iteration(hipStream_t st, const Pdhg& P, int us, int ut, bool checkpoint, bool major, double ps,
+                     double ds, double h) {
+    if (major) launch_us<true, true>(st, P, us, ut, ps, ds, h);
+    else if (checkpoint) launch_us<true, false>(st, P, us, ut, ps, ds, h);
+    else launch_us<false, false>(st, P, us, ut, ps, ds, h);
+    HM_LAUNCH_CHECK("pdhg iteration");
+    return HM_OK;
 }
 
 int read_result(hipStream_t st, const Pdhg& P, int q, double* host) {
@@ -400,8 +556,8 @@ extern "C" int hm_pdhg_solve(void* stream, const int64_t* rows, const int64_t* c
     // ---- LP assembly: endpoints, degrees, per-node incident edge lists (ascending edge id) ----
     hipLaunchKernelGGL(k_fill_i32, dim3(grid_of(nodes + 1)), dim3(256), 0, st, P.deg, nodes + 1, 0);
     hipLaunchKernelGGL(k_fill_i32, dim3(1), dim3(64), 0, st, P.flag, 4, 0);
-    hipLaunchKernelGGL(k_edges, dim3(grid_of(e)), dim3(256), 0, st, rows, cols, e, n, nt, P.row, P.col, P.deg,
-                       P.keys_in, P.vals_in, P.flag);
+    hipLaunchKernelGGL(k_edges, dim3(grid_of(e)), dim3(256), 0, st, rows, cols, e, n, nt, P.deg, P.keys_in, P.vals_in,
+                       P.flag);
     HM_LAUNCH_CHECK("k_edges");
     int flag = 0;
     HM_HIP(hipMemcpyAsync(&flag, P.flag, sizeof(int), hipMemcpyDeviceToHost, st));
@@ -427,9 +583,13 @@ extern "C" int hm_pdhg_solve(void* stream, const int64_t* rows, const int64_t* c
     const double bound = rescale ? 1.0 / std::max(1.0, mass_norm) : 1.0;
     const double objective = rescale ? 1.0 / std::max(1.0, cost_norm) : 1.0;
     const double variable = std::sqrt(2.0);
-    hipLaunchKernelGGL(k_edge_setup, dim3(grid_of(e)), dim3(256), 0, st, costs, x0, e, bound, objective, variable, P.cs,
-                       P.x, P.ax, P.px, P.rx, P.dx);
-    HM_LAUNCH_CHECK("k_edge_setup");
+    // source-order edge state and its target-order mirror
+    hipLaunchKernelGGL(k_source_setup, dim3(grid_of(e)), dim3(256), 0, st, P.eid, e, rows, cols, costs, x0, bound,
+                       objective, variable, P);
+    HM_LAUNCH_CHECK("k_source_setup");
+    hipLaunchKernelGGL(k_target_setup, dim3(grid_of(e)), dim3(256), 0, st, P.eid, e, rows, costs, x0, bound, objective,
+                       variable, P);
+    HM_LAUNCH_CHECK("k_target_setup");
     hipLaunchKernelGGL(k_node_setup, dim3(grid_of(nodes)), dim3(256), 0, st, P.deg, masses, y0, nodes, n, bound, objective,
                        variable, P.scale, P.bs, P.ns, P.y, P.ay, P.py, P.dy, P.td);
     HM_LAUNCH_CHECK("k_node_setup");
@@ -453,7 +613,8 @@ extern "C" int hm_pdhg_solve(void* stream, const int64_t* rows, const int64_t* c
     int64_t count = 0, inner = 0, restarts = 0;
     double pobj = 0, dobj = 0, ap = 0, rp = 0, ad = 0, rd = 0, gap = 0;
     int64_t local_count = 0, local_inner = 0;
-    const unsigned ge = grid_of(e), gn = grid_of(nodes), gr = grid_of(e > nodes ? e : nodes);
+    const unsigned gr = grid_of(e > nodes ? e : nodes);
+    const int us = edges_per_lane(e, n), ut = edges_per_lane(e, nt);
     for (;;) {
         if (local_count % freq == 0) {
             hipLaunchKernelGGL(k_evaluate, dim3(RB), dim3(RT), 0, st, P, masses, costs, variable, bound, objective,
@@ -520,18 +681,7 @@ extern "C" int hm_pdhg_solve(void* stream, const int64_t* rows, const int64_t* c
         const bool checkpoint = major || is_restart;
         // px / py are read only by the evaluation that follows a major iteration
         prof_begin(st, "pdhg_iteration");
-        if (checkpoint) {
-            if (major) {
-                hipLaunchKernelGGL((k_edge_pass<true, true>), dim3(ge), dim3(256), 0, st, P, primal_step, halpern);
-                hipLaunchKernelGGL((k_node_pass<true, true>), dim3(gn), dim3(256), 0, st, P, dual_step, halpern);
-            } else {
-                hipLaunchKernelGGL((k_edge_pass<true, false>), dim3(ge), dim3(256), 0, st, P, primal_step, halpern);
-                hipLaunchKernelGGL((k_node_pass<true, false>), dim3(gn), dim3(256), 0, st, P, dual_step, halpern);
-            }
-        } else {
-            hipLaunchKernelGGL((k_edge_pass<false, false>), dim3(ge), dim3(256), 0, st, P, primal_step, halpern);
-            hipLaunchKernelGGL((k_node_pass<false, false>), dim3(gn), dim3(256), 0, st, P, dual_step, halpern);
-        }
+        if (int rc = launch_iteration(st, P, us, ut, checkpoint, major, primal_step, dual_step, halpern)) return rc;
         prof_end(st);
         HM_LAUNCH_CHECK("pdhg iteration");
         if (checkpoint) {

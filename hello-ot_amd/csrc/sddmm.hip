@@ -29,28 +29,37 @@ __global__ __launch_bounds__(256) void sddmm_l2sq_csr_kernel(const float* __rest
             float xv[XR > 0 ? XR : 1];
 #pragma unroll
             for (int t = 0; t < XR; ++t) xv[t] = (lane + 64 * t < d) ? xr[lane + 64 * t] : 0.0f;
+            // U gathered Y rows in flight per step; each pair keeps the fixed lane order
+            constexpr int U = 4;
             int32_t e = e0;
-            for (; e + 2 <= e1; e += 2) {
-                const int64_t j0 = col[e], j1 = col[e + 1];
-                const float* y0 = Y + j0 * d;
-                const float* y1 = Y + j1 * d;
-                double a0 = 0.0, a1 = 0.0;
+            for (; e + U <= e1; e += U) {
+                const float* yp[U];
+                double a[U];
+#pragma unroll
+                for (int u = 0; u < U; ++u) {
+                    yp[u] = Y + (int64_t)col[e + u] * d;
+                    a[u] = 0.0;
+                }
 #pragma unroll
                 for (int t = 0; t < XR; ++t) {
                     const int k = lane + 64 * t;
                     if (k < d) {
-                        a0 = a0 + (double)xv[t] * (double)y0[k];
-                        a1 = a1 + (double)xv[t] * (double)y1[k];
+#pragma unroll
+                        for (int u = 0; u < U; ++u) a[u] = a[u] + (double)xv[t] * (double)yp[u][k];
                     }
                 }
-                a0 = wave_tree_sum(a0);
-                a1 = wave_tree_sum(a1);
-                if (lane == 0) {
-                    out[e] = (pi + q[j0]) - scale * a0;
-                    out[e + 1] = (pi + q[j1]) - scale * a1;
+#pragma unroll
+                for (int u = 0; u < U; ++u) a[u] = wave_tree_sum(a[u]);
+                if (lane < U) {
+                    double mine = a[0];
+#pragma unroll
+                    for (int u = 1; u < U; ++u)
+                        if (lane == u) mine = a[u];
+                    const int64_t j = col[e + lane];
+                    out[e + lane] = (pi + q[j]) - scale * mine;
                 }
             }
-            if (e < e1) {
+            for (; e < e1; ++e) {
                 const int64_t j0 = col[e];
                 const float* y0 = Y + j0 * d;
                 double a0 = 0.0;
