@@ -224,9 +224,9 @@ def bench_c2(dev, steps=3):
         sec = time_steps(fn, steps, 0)
         sw_ms, sw_n = _lib.profile_query("l2sq_sweep")
         _lib.profile_enable(False)
-        sweep_s = sw_ms / max(sw_n, 1) / 1e3
-        out[name] = {"seconds": sec, "pairs_per_s": m * n / sec,
-                     "sweep_ms": sweep_s * 1e3, "sweep_tflops": 2 * d * m * n / sweep_s / 1e12,
+        sweep_s = sw_ms / max(steps, 1) / 1e3   # all sweep launches of one call (one per internal query chunk)
+        out[name] = {"seconds": sec, "pairs_per_s": m * n / sec, "sweep_launches_per_call": sw_n // max(steps, 1),
+                     "sweep_ms_per_call": sweep_s * 1e3, "sweep_tflops": 2 * d * m * n / sweep_s / 1e12,
                      "sweep_mfma_frac": 2 * d * m * n / sweep_s / PEAK_FP32_MFMA}
     return out
 

@@ -1,21 +1,25 @@
-// l2^2 ("raw lowrank") pricing scan for gfx950 -- kernels and per-K1 driver (included by pricing_l2sq*.hip): fp32 MFMA sweep + exact fp64 re-check.
+// l2^2 ("raw lowrank") pricing scan for gfx950 -- kernels and per-K1 driver (included by pricing_l2sq*.hip):
+// one fp32 MFMA sweep feeds both the row and the column candidate lists, then an exact fp64 re-check.
 //
 // Semantics (reference: generic_scan.py:577-597 -> pricing_small.cu:230-304 / pricing.cu:185-229 with
 // matrix_selection.cuh:20-74):
 //   sigma_ij = (scale*<x_i,y_j> + qb_i) + db_j,   c_ij = (p_i + q_j) - scale*<x_i,y_j>.
-// Per X row (and, in a second sweep with the roles swapped, per Y row) the k best sigma with lowest-index
-// ties; certificate sums over all pairs.
+// Per X row and per Y row the k best sigma with lowest-index ties; certificate sums over all pairs.
 //
-// Pipeline per direction:
-//   1. prep:     fp64 row norms ||x_i||, ||y_j||, their maxima, max|bias|; fp32 copies of the biases.
-//   2. sweep:    MFMA 32x32x2 fp32 tiles of Y * X^T (a lane owns one X row of a 32-row block and 16 Y
-//                columns per 32x32 block). Each lane keeps its best K1 = k + slack values of the fp32
-//                score w = scale*dot32 + db32_j (w + qb_i ranks like sigma) in registers; certificate sums
-//                are accumulated in fp32 per tile and flushed to fp64.
-//   3. finalize: one wave per row merges the lane lists, checks that the K1-th approximate value is below
-//                the k-th minus twice the rigorous error bound (otherwise the row is queued for step 4),
-//                and re-evaluates the K1 survivors with the fixed-order fp64 dot (dot64) -> exact top-k.
-//   4. rescan:   queued rows are scanned exactly (one wave per row, one lane per column).
+// Pipeline, per internal chunk of at most CHUNK_MAX X rows (the column lists of a chunk stay bounded):
+//   1. prep (once): fp64 row norms ||x_i||, ||y_j||, their maxima, max|bias|; fp32 copies of the biases.
+//   2. sweep:    MFMA 32x32x2 fp32 tiles of Y * X^T (a workgroup owns 128 X rows and walks one segment of Y
+//                in 128-row tiles; lane (h, r) of a wave owns X row r of the wave's 32 and 16 Y rows of each
+//                32-row block). From the same accumulators:
+//                  rows:    each lane keeps its best K1 of w = scale*dot32 + db32_j (ranks like sigma in j);
+//                  columns: the tile's scores scale*dot32 + qb32_i go through LDS and each Y row keeps its
+//                           best K1 over the workgroup's 128 X rows (one list per X panel);
+//                  certificate sums in fp32 per tile, flushed to fp64.
+//   3. finalize: one wave per row (or column) merges the partial lists, checks that the K1-th approximate
+//                value is below the k-th minus twice the rigorous error bound (otherwise the row is queued
+//                for step 4), and re-evaluates the K1 survivors with the fixed-order fp64 dot (dot64).
+//   4. rescan:   queued rows / columns are scanned exactly (one wave each, one lane per candidate).
+//   5. columns:  each chunk's exact column lists are merged into the output (tie rule kept).
 #pragma once
 
 #include "common.h"
@@ -42,8 +46,13 @@ constexpr int NB = 4;              // 32-wide Y blocks per wave
 constexpr int BY = 32 * NB;        // Y rows per tile
 constexpr int KC = 32;             // features per LDS chunk
 constexpr int STR = KC + 4;        // LDS row stride (floats)
+constexpr int CST = BX + 1;        // LDS row stride of the column-score tile (floats)
 constexpr int FLUSH_CHUNKS = 8;    // fp32 block length 256 features before folding into the outer sum
-
+constexpr int64_t CHUNK_MAX = 65536;          // X rows per internal chunk
+constexpr int FUSE_MIN_D = 256;               // columns ride on the row sweep from this d on (below it the
+                                              // per-tile column epilogue outweighs the MFMA work: two sweeps)
+constexpr int64_t SWEEP_WGS = 1024;           // target workgroups per sweep launch (sets the Y segments)
+constexpr size_t COLPART_CAP = size_t(12) << 30;  // bytes of per-chunk column partial lists
 
 // fp32 unit roundoff doubled (covers truncating accumulation) and the classic gamma_n bound.
 inline double gamma_fp32(double n) {
@@ -51,45 +60,90 @@ inline double gamma_fp32(double n) {
     return n * u2 / (1.0 - n * u2);
 }
 
-// -------------------------------------------------------------------------------------------------
-// prep: norms, maxima and fp32 bias copies
-// -------------------------------------------------------------------------------------------------
-__global__ void l2sq_prep_rows(const float* __restrict__ X, int64_t m, int d, const double* __restrict__ p,
-                               const double* __restrict__ qb, const double* __restrict__ db_for_ge,
-                               double* __restrict__ norm, float* __restrict__ qb32, float* __restrict__ p32,
-                               unsigned long long* __restrict__ maxima /*[norm, |qb|]*/) {
-    // one wave per row
-    const int lane = threadIdx.x & 63;
-    const int64_t row = (int64_t)blockIdx.x * (blockDim.x / 64) + threadIdx.x / 64;
-    if (row >= m) return;
-    const float* x = X + row * (int64_t)d;
-    double s = 0.0;
-    for (int k = lane; k < d; k += 64) s += (double)x[k] * (double)x[k];
-    for (int o = 32; o >= 1; o >>= 1) s += __shfl_xor(s, o, 64);
-    if (lane == 0) {
-        const double nrm = std::sqrt(s) * (1.0 + 1e-12);
-        norm[row] = nrm;
-        qb32[row] = (float)qb[row];
-        // "ge" = q + db for the cost of the certificate, "p" = p for the row side
-        p32[row] = db_for_ge ? (float)(p[row] + db_for_ge[row]) : (float)p[row];
-        atomicMax(&maxima[0], double_key(nrm));
-        atomicMax(&maxima[1], double_key(std::fabs(qb[row])));
+// better() on fp32 list entries (lowest index wins ties; missing entries lose)
+__device__ inline bool better_e(float av, int ai, float bv, int bi) {
+    return av > bv || (av == bv && ai >= 0 && (bi < 0 || ai < bi));
+}
+
+template <int K>
+__device__ inline void insert_e(float (&w)[K], int (&id)[K], float v, int i) {
+    float cv = v;
+    int ci = i;
+#pragma unroll
+    for (int s = 0; s < K; ++s) {
+        if (better_e(cv, ci, w[s], id[s])) {
+            const float tv = w[s];
+            const int ti = id[s];
+            w[s] = cv;
+            id[s] = ci;
+            cv = tv;
+            ci = ti;
+        }
     }
 }
 
 // -------------------------------------------------------------------------------------------------
-// sweep
+// prep: norms, maxima and fp32 bias copies
 // -------------------------------------------------------------------------------------------------
-template <int K1, bool TWO_LEVEL>
+// one wave per row (grid-stride); the maxima are reduced per workgroup before one atomic each
+__global__ __launch_bounds__(256) void l2sq_prep_rows(const float* __restrict__ X, int64_t m, int d,
+                                                      const double* __restrict__ p, const double* __restrict__ qb,
+                                                      const double* __restrict__ db_for_ge, double* __restrict__ norm,
+                                                      float* __restrict__ qb32, float* __restrict__ p32,
+                                                      unsigned long long* __restrict__ maxima /*[norm, |qb|]*/) {
+    __shared__ double sM[4][2];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    double mx_norm = 0.0, mx_bias = 0.0;
+    for (int64_t row = (int64_t)blockIdx.x * 4 + wave; row < m; row += (int64_t)gridDim.x * 4) {
+        const float* x = X + row * (int64_t)d;
+        double s = 0.0;
+        for (int k = lane; k < d; k += 64) s += (double)x[k] * (double)x[k];
+        for (int o = 32; o >= 1; o >>= 1) s += __shfl_xor(s, o, 64);
+        const double nrm = std::sqrt(s) * (1.0 + 1e-12);
+        mx_norm = fmax(mx_norm, nrm);
+        mx_bias = fmax(mx_bias, std::fabs(qb[row]));
+        if (lane == 0) {
+            norm[row] = nrm;
+            qb32[row] = (float)qb[row];
+            // "ge" = q + db for the cost of the certificate, "p" = p for the row side
+            p32[row] = db_for_ge ? (float)(p[row] + db_for_ge[row]) : (float)p[row];
+        }
+    }
+    if (lane == 0) {
+        sM[wave][0] = mx_norm;
+        sM[wave][1] = mx_bias;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < 4; ++w) {
+            mx_norm = fmax(mx_norm, sM[w][0]);
+            mx_bias = fmax(mx_bias, sM[w][1]);
+        }
+        atomicMax(&maxima[0], double_key(mx_norm));
+        atomicMax(&maxima[1], double_key(mx_bias));
+    }
+}
+
+inline unsigned prep_grid(int64_t rows) {
+    const int64_t b = (rows + 3) / 4;
+    return (unsigned)(b < 2048 ? b : 2048);
+}
+
+// -------------------------------------------------------------------------------------------------
+// sweep over X rows [xb, xe) of one chunk
+// -------------------------------------------------------------------------------------------------
+template <int K1, bool TWO_LEVEL, bool COLS>
 __global__ __launch_bounds__(256) void l2sq_sweep(
-    const float* __restrict__ X, const float* __restrict__ Y, int64_t m, int64_t n, int d,
+    const float* __restrict__ X, const float* __restrict__ Y, int64_t xb, int64_t xe, int64_t n, int d,
     const float* __restrict__ qb32, const float* __restrict__ db32, const float* __restrict__ p32,
     const float* __restrict__ ge32, float scale, int64_t seg_len, Entry* __restrict__ part,
-    double* __restrict__ blockstats, int VEC4, int STATS) {
+    Entry* __restrict__ colpart, unsigned int* __restrict__ colthr, double* __restrict__ blockstats, int VEC4,
+    int STATS) {
     __shared__ float sX[BX * STR];
     __shared__ float sY[BY * STR];
     __shared__ float sDB[BY];
     __shared__ float sGE[BY];
+    __shared__ float sC[COLS ? BY * CST : 1];
     __shared__ double sRed[4][5];
 
     const int tid = threadIdx.x;
@@ -97,12 +151,13 @@ __global__ __launch_bounds__(256) void l2sq_sweep(
     const int wave = tid >> 6;
     const int h = lane >> 5;    // which half of the 2-wide MFMA k slot
     const int r = lane & 31;    // X row within the wave's 32-row block
-    const int64_t x0 = (int64_t)blockIdx.x * BX;
+    const int64_t rows = xe - xb;
+    const int64_t x0 = xb + (int64_t)blockIdx.x * BX;
     const int64_t seg = blockIdx.y;
     const int64_t y_begin = seg * seg_len;
     const int64_t y_end = (y_begin + seg_len < n) ? (y_begin + seg_len) : n;
     const int64_t my_row = x0 + wave * 32 + r;
-    const bool row_ok = my_row < m;
+    const bool row_ok = my_row < xe;
 
     float lv[K1];
     int li[K1];
@@ -127,13 +182,13 @@ __global__ __launch_bounds__(256) void l2sq_sweep(
             const int k = k0 + 4 * c4;
             const int64_t xr = x0 + row, yr = ytile + row;
             if (VEC4) {
-                gx[i] = (xr < m && k < d) ? *reinterpret_cast<const float4*>(X + xr * d + k) : make_float4(0, 0, 0, 0);
+                gx[i] = (xr < xe && k < d) ? *reinterpret_cast<const float4*>(X + xr * d + k) : make_float4(0, 0, 0, 0);
                 gy[i] = (yr < y_end && k < d) ? *reinterpret_cast<const float4*>(Y + yr * d + k) : make_float4(0, 0, 0, 0);
             } else {
                 float a[4], b[4];
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    a[e] = (xr < m && k + e < d) ? X[xr * d + k + e] : 0.0f;
+                    a[e] = (xr < xe && k + e < d) ? X[xr * d + k + e] : 0.0f;
                     b[e] = (yr < y_end && k + e < d) ? Y[yr * d + k + e] : 0.0f;
                 }
                 gx[i] = make_float4(a[0], a[1], a[2], a[3]);
@@ -246,6 +301,7 @@ __global__ __launch_bounds__(256) void l2sq_sweep(
                             ++tcnt;
                         }
                     }
+                    if (COLS) sC[(jl0 + cc) * CST + wave * 32 + r] = row_ok ? fmaf(scale, tot, qbi) : -INFINITY;
                 }
             }
         }
@@ -254,12 +310,44 @@ __global__ __launch_bounds__(256) void l2sq_sweep(
             den64 += (double)tden;
             cnt64 += (double)tcnt;
         }
-        __syncthreads();  // all epilogue reads of sDB/sGE finish before the next tile rewrites them
+        if (COLS) {
+            // each Y row of the tile: its best K1 over this workgroup's 128 X rows (two threads per row, folded).
+            // colthr[j] is the K1-th value of some full list of this chunk, a lower bound of the chunk's K1-th
+            // value: scores at or below it cannot enter the merged top-K1 and are skipped.
+            __syncthreads();
+            const int jl = tid >> 1, half = tid & 1;
+            const int64_t j = ytile + jl;
+            const float thr = j < y_end ? key_float(colthr[j]) : INFINITY;
+            float cw[K1];
+            int cidx[K1];
+#pragma unroll
+            for (int s = 0; s < K1; ++s) { cw[s] = -INFINITY; cidx[s] = -1; }
+            const float* src = &sC[jl * CST + half * 64];
+            const int base = (int)(x0 + half * 64);
+            for (int xx = 0; xx < 64; ++xx) {
+                const float v = src[xx];
+                if (v > thr && v > cw[K1 - 1]) insert_e<K1>(cw, cidx, v, base + xx);
+            }
+#pragma unroll
+            for (int s = 0; s < K1; ++s) {
+                const float pv = __shfl_xor(cw[s], 1, 64);
+                const int pi2 = __shfl_xor(cidx[s], 1, 64);
+                if (half == 0 && pi2 >= 0 && better_e(pv, pi2, cw[K1 - 1], cidx[K1 - 1]))
+                    insert_e<K1>(cw, cidx, pv, pi2);
+            }
+            if (half == 0 && j < y_end) {
+                Entry* dst = colpart + ((int64_t)blockIdx.x * n + j) * K1;
+#pragma unroll
+                for (int s = 0; s < K1; ++s) dst[s] = Entry{cw[s], cidx[s]};
+                if (cidx[K1 - 1] >= 0) atomicMax(&colthr[j], float_key(cw[K1 - 1]));
+            }
+        }
+        __syncthreads();  // all epilogue reads of sDB/sGE/sC finish before the next tile rewrites them
     }
 
-    // lane lists -> part[(seg*m + row)*2 + h][K1]
+    // lane lists -> part[(seg*rows + local row)*2 + h][K1]
     if (row_ok) {
-        Entry* out = part + ((seg * m + my_row) * 2 + h) * K1;
+        Entry* out = part + ((seg * rows + (my_row - xb)) * 2 + h) * K1;
 #pragma unroll
         for (int s = 0; s < K1; ++s) out[s] = Entry{lv[s], li[s]};
     }
@@ -289,9 +377,9 @@ __global__ __launch_bounds__(256) void l2sq_sweep(
     }
 }
 
-// deterministic reduction of per-block certificate partials (single block)
+// deterministic reduction of per-block certificate partials (single block); later chunks accumulate
 __global__ void l2sq_reduce_stats(const double* __restrict__ blockstats, int64_t blocks, double* __restrict__ stats,
-                                  int linf) {
+                                  int linf, int accumulate) {
     __shared__ double s[256][5];
     const int t = threadIdx.x;
     double v[5] = {0, 0, 0, 0, 0};
@@ -306,76 +394,102 @@ __global__ void l2sq_reduce_stats(const double* __restrict__ blockstats, int64_t
         __syncthreads();
     }
     if (t == 0) {
-        stats[0] = s[0][0];
-        stats[1] = s[0][1];
-        stats[2] = s[0][2];
-        stats[3] = s[0][3];  // replaced by the exact row maximum when rows are computed
-        stats[4] = linf ? s[0][4] : 0.0;
+        double o[5] = {s[0][0], s[0][1], s[0][2], s[0][3], linf ? s[0][4] : 0.0};
+        if (accumulate) {
+            o[0] += stats[0];
+            o[1] += stats[1];
+            o[2] += stats[2];
+            o[3] = fmax(o[3], stats[3]);
+            o[4] = fmax(o[4], stats[4]);
+        }
+        // stats[3] is replaced by the exact row maximum when rows are computed
+        for (int e = 0; e < 5; ++e) stats[e] = o[e];
     }
 }
 
 // -------------------------------------------------------------------------------------------------
-// finalize: one wave per row
+// finalize: one wave per row (rows of a chunk, or Y rows for the column lists)
 // -------------------------------------------------------------------------------------------------
 struct BoundArgs {
     double acc_rel;   // relative bound on |dot32 - dot| in units of ||x||*||y||, plus fp64 slack
-    double db_rel;    // relative bound contribution of fp32 bias rounding, in units of max|db|
+    double db_rel;    // relative bound contribution of fp32 bias rounding, in units of max|bias|
     double abs_slack; // absolute slack (flushed denormals)
 };
 
-constexpr int FIN_MAX = 512;   // entries one finalize wave can rank (2 * S * K1 <= FIN_MAX)
-
-template <int K1>
+// Lists of row r: L in [0, nlists), at base + (((L / G) * R + r) * G + L % G) * K1 (sorted, missing = -1).
+// The row side A (rows A[r], row bias abias[r], norm anorm[r]) pairs with candidates from side B (B[c],
+// bias bbias[c]); sigma = COLS ? (s*dot + bbias[c]) + abias[r] : (s*dot + abias[r]) + bbias[c], which keeps
+// the (dot + qb) + db association of the caller's (x, y) pair in both directions.
+template <int K1, int G, bool COLS>
 __global__ __launch_bounds__(256) void l2sq_finalize(
-    const float* __restrict__ X, const float* __restrict__ Y, int64_t m, int d, int S,
-    const Entry* __restrict__ part, const double* __restrict__ qb, const double* __restrict__ db,
-    const double* __restrict__ xnorm, const unsigned long long* __restrict__ ymaxima, double scale, int k,
+    const float* __restrict__ A, const float* __restrict__ B, int64_t R, int d, int nlists,
+    const Entry* __restrict__ lists, const double* __restrict__ abias, const double* __restrict__ bbias,
+    const double* __restrict__ anorm, const unsigned long long* __restrict__ bmaxima, double scale, int k,
     BoundArgs bnd, double* __restrict__ out_val, int* __restrict__ out_idx, int* __restrict__ redo,
-    int* __restrict__ redo_count, int TRANSPOSED) {
-    __shared__ Entry sE[4][FIN_MAX];
-    __shared__ Entry sS[4][64];
+    int* __restrict__ redo_count) {
     const int lane = threadIdx.x & 63;
-    const int wv = threadIdx.x >> 6;
-    const int64_t row = (int64_t)blockIdx.x * 4 + wv;
-    const bool valid = row < m;
-    const int N = 2 * S * K1;
-    // gather this row's lane lists; empty slots become (-inf, -1)
-    int nreal = 0;
-    for (int e = lane; e < N; e += 64) {
-        Entry en{-INFINITY, -1};
-        if (valid) {
-            const int list = e / K1, slot = e % K1;
-            en = part[(((int64_t)(list >> 1) * m + row) * 2 + (list & 1)) * K1 + slot];
-            if (en.j < 0) en.w = -INFINITY;
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const bool valid = row < R;   // uniform per wave
+    float lw[K1];
+    int li[K1];
+#pragma unroll
+    for (int s = 0; s < K1; ++s) { lw[s] = -INFINITY; li[s] = -1; }
+    int nreal = 0, full = 0;
+    if (valid) {
+        for (int L = lane; L < nlists; L += 64) {
+            const Entry* src = lists + ((((int64_t)(L / G)) * R + row) * G + (L % G)) * K1;
+            int cnt = 0;
+            for (int s = 0; s < K1; ++s) {
+                const Entry e = src[s];
+                if (e.j < 0) break;
+                ++cnt;
+                if (better_e(e.w, e.j, lw[K1 - 1], li[K1 - 1])) insert_e<K1>(lw, li, e.w, e.j);
+            }
+            nreal += cnt;
+            full |= (cnt == K1) ? 1 : 0;
         }
-        sE[wv][e] = en;
-        nreal += en.j >= 0 ? 1 : 0;
     }
-    for (int o = 32; o >= 1; o >>= 1) nreal += __shfl_xor(nreal, o, 64);
-    __syncthreads();
-    // rank of each real entry by (w desc, j asc); j is unique within a row
-    for (int e = lane; e < N; e += 64) {
-        const Entry me = sE[wv][e];
-        if (me.j < 0) continue;
-        int rank = 0;
-        for (int f = 0; f < N; ++f) {
-            const Entry o = sE[wv][f];
-            if (o.j >= 0 && (o.w > me.w || (o.w == me.w && o.j < me.j))) ++rank;
+    for (int o = 32; o >= 1; o >>= 1) {
+        nreal += __shfl_xor(nreal, o, 64);
+        full |= __shfl_xor(full, o, 64);
+    }
+    // wave top-K1: K1 rounds of an arg-best over the lanes' list heads
+    float tw[K1];
+    int ti[K1];
+#pragma unroll
+    for (int t = 0; t < K1; ++t) {
+        float bw = lw[0];
+        int bi = li[0];
+        int bl = lane;
+        for (int o = 32; o >= 1; o >>= 1) {
+            const float ow = __shfl_xor(bw, o, 64);
+            const int oi = __shfl_xor(bi, o, 64);
+            const int ol = __shfl_xor(bl, o, 64);
+            if (better_e(ow, oi, bw, bi)) { bw = ow; bi = oi; bl = ol; }
         }
-        if (rank < K1) sS[wv][rank] = me;
+        tw[t] = bw;
+        ti[t] = bi;
+        if (lane == bl) {
+#pragma unroll
+            for (int s = 0; s + 1 < K1; ++s) { lw[s] = lw[s + 1]; li[s] = li[s + 1]; }
+            lw[K1 - 1] = -INFINITY;
+            li[K1 - 1] = -1;
+        }
     }
-    __syncthreads();
     if (!valid) return;
     const int kept = nreal < K1 ? nreal : K1;
-    const float wk = nreal >= k ? sS[wv][k - 1].w : -INFINITY;
-    const float wK1 = nreal >= K1 ? sS[wv][K1 - 1].w : -INFINITY;
-    const double ymax = key_double(ymaxima[0]);
-    const double dmax = key_double(ymaxima[1]);
-    const double nxy = scale * xnorm[row] * ymax;
-    const double b = (nxy * bnd.acc_rel + dmax * bnd.db_rel + fabs(qb[row]) * 1e-15 + bnd.abs_slack) * (1.0 + 1e-6);
-    // pairs outside the kept list have w <= wK1; they cannot reach the exact top-k when wK1 < wk - 2b
-    const bool unsafe = (nreal > K1) && ((double)wK1 >= (double)wk - 2.0 * b);
-    if (unsafe) {
+    float wk = -INFINITY, wK1 = tw[K1 - 1];
+#pragma unroll
+    for (int t = 0; t < K1; ++t)
+        if (t == k - 1) wk = tw[t];
+    if (nreal < k) wk = -INFINITY;
+    const double bmax = key_double(bmaxima[0]);
+    const double dmax = key_double(bmaxima[1]);
+    const double nxy = scale * anorm[row] * bmax;
+    const double b = (nxy * bnd.acc_rel + dmax * bnd.db_rel + fabs(abias[row]) * 1e-15 + bnd.abs_slack) * (1.0 + 1e-6);
+    // candidates outside the kept list have w <= wK1; they cannot reach the exact top-k when wK1 < wk - 2b
+    const bool maybe_dropped = full || nreal > K1;
+    if (maybe_dropped && (double)wK1 >= (double)wk - 2.0 * b) {
         if (lane == 0) {
             const int slot = atomicAdd(redo_count, 1);
             redo[slot] = (int)row;
@@ -385,13 +499,16 @@ __global__ __launch_bounds__(256) void l2sq_finalize(
     // exact re-evaluation of the kept entries; lane e owns kept entry e
     double sv = -INFINITY;
     int sj = -1;
-    const float* xr = X + row * (int64_t)d;
-    for (int e = 0; e < kept; ++e) {
-        const int jj = sS[wv][e].j;
-        const double dot = wave_dot64(xr, Y + (int64_t)jj * d, d, lane);
-        const double sdot = scale * dot;
-        const double sig = TRANSPOSED ? (sdot + db[jj]) + qb[row] : (sdot + qb[row]) + db[jj];
-        if (lane == e) { sv = sig; sj = jj; }
+    const float* ar = A + row * (int64_t)d;
+#pragma unroll
+    for (int e = 0; e < K1; ++e) {
+        if (e < kept) {
+            const int c = ti[e];
+            const double dot = wave_dot64(ar, B + (int64_t)c * d, d, lane);
+            const double sdot = scale * dot;
+            const double sig = COLS ? (sdot + bbias[c]) + abias[row] : (sdot + abias[row]) + bbias[c];
+            if (lane == e) { sv = sig; sj = c; }
+        }
     }
     int er = 0;
     for (int src = 0; src < kept; ++src) {
@@ -410,40 +527,41 @@ __global__ __launch_bounds__(256) void l2sq_finalize(
 }
 
 // -------------------------------------------------------------------------------------------------
-// exact rescan of queued rows: one wave per row; each lane scores one column per step with the register
-// form of dot64, and the wave inserts the few winners into one replicated list (ballot loop)
+// exact rescan of queued rows: one wave per row; each lane scores one candidate per step with the register
+// form of dot64, and the wave inserts the few winners into one replicated list (ballot loop). Candidates
+// are B rows [0, nb); reported indices are cbase + local index.
 // -------------------------------------------------------------------------------------------------
 template <int K>
-__global__ __launch_bounds__(64) void l2sq_rescan(const float* __restrict__ X, const float* __restrict__ Y,
-                                                  int64_t n, int d, const double* __restrict__ qb,
-                                                  const double* __restrict__ db, double scale, int k,
+__global__ __launch_bounds__(64) void l2sq_rescan(const float* __restrict__ A, const float* __restrict__ B,
+                                                  int64_t nb, int d, const double* __restrict__ abias,
+                                                  const double* __restrict__ bbias, double scale, int k,
                                                   const int* __restrict__ redo, const int* __restrict__ redo_count,
                                                   double* __restrict__ out_val, int* __restrict__ out_idx,
-                                                  int TRANSPOSED) {
+                                                  int COLS, int cbase) {
     const int lane = threadIdx.x;
     const int count = *redo_count;
     for (int slot = blockIdx.x; slot < count; slot += gridDim.x) {
         const int64_t row = redo[slot];
-        const float* xr = X + row * (int64_t)d;
+        const float* ar = A + row * (int64_t)d;
         double v[K];
         int id[K];
 #pragma unroll
         for (int s = 0; s < K; ++s) { v[s] = -INFINITY; id[s] = -1; }
-        for (int64_t j0 = 0; j0 < n; j0 += 64) {
+        for (int64_t j0 = 0; j0 < nb; j0 += 64) {
             const int64_t j = j0 + lane;
             double sig = -INFINITY;
-            if (j < n) {
-                const double sdot = scale * lane_dot64(xr, Y + j * d, d);
-                sig = TRANSPOSED ? (sdot + db[j]) + qb[row] : (sdot + qb[row]) + db[j];
+            if (j < nb) {
+                const double sdot = scale * lane_dot64(ar, B + j * d, d);
+                sig = COLS ? (sdot + bbias[j]) + abias[row] : (sdot + abias[row]) + bbias[j];
             }
-            const bool cand = j < n && sig == sig && better(sig, (int)j, v[k - 1], id[k - 1]);
+            const bool cand = j < nb && sig == sig && better(sig, (int)(cbase + j), v[k - 1], id[k - 1]);
             unsigned long long mask = __ballot(cand);
             while (mask) {
                 const int src = __ffsll((long long)mask) - 1;
                 mask &= mask - 1;
-                const double sv = __shfl(sig, src, 64);
-                const int sjv = (int)(j0 + src);
-                put_sorted<K>(v, id, k, sv, sjv);
+                const double svv = __shfl(sig, src, 64);
+                const int sjv = (int)(cbase + j0 + src);
+                put_sorted<K>(v, id, k, svv, sjv);
             }
         }
         if (lane < k) {
@@ -456,6 +574,29 @@ __global__ __launch_bounds__(64) void l2sq_rescan(const float* __restrict__ X, c
             out_idx[row * k + lane] = oi;
         }
     }
+}
+
+// merge a chunk's exact column lists into the running ones (both sorted by the tie rule)
+__global__ void l2sq_merge_columns(double* __restrict__ val, int* __restrict__ idx, const double* __restrict__ cval,
+                                   const int* __restrict__ cidx, int64_t n, int k, int first) {
+    const int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (j >= n) return;
+    double* v = val + j * k;
+    int* id = idx + j * k;
+    const double* cv = cval + j * k;
+    const int* ci = cidx + j * k;
+    if (first) {
+        for (int s = 0; s < k; ++s) { v[s] = cv[s]; id[s] = ci[s]; }
+        return;
+    }
+    double ov[32];
+    int oi[32];
+    int a = 0, b = 0;
+    for (int s = 0; s < k; ++s) {
+        if (better(cv[b], ci[b], v[a], id[a])) { ov[s] = cv[b]; oi[s] = ci[b]; ++b; }
+        else { ov[s] = v[a]; oi[s] = id[a]; ++a; }
+    }
+    for (int s = 0; s < k; ++s) { v[s] = ov[s]; id[s] = oi[s]; }
 }
 
 __global__ void exact_row_max(const double* __restrict__ row_val, int64_t m, int k, double* __restrict__ stats) {
@@ -475,29 +616,48 @@ __global__ void zero_words(unsigned long long* p, int count) {
     if ((int)threadIdx.x < count) p[threadIdx.x] = 0ull;
 }
 
+__global__ void fill_u32(unsigned int* p, int64_t count, unsigned int v) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < count; i += (int64_t)gridDim.x * blockDim.x)
+        p[i] = v;
+}
+
 // -------------------------------------------------------------------------------------------------
 // host orchestration
 // -------------------------------------------------------------------------------------------------
 inline int bucket_k1(int k) { return k <= 2 ? 8 : (k <= 8 ? 16 : 40); }
 
-inline int choose_segments(int64_t m, int64_t n, int k) {
+inline bool fused_columns(int d, uint32_t flags) { return (flags & HM_COLS) && d >= FUSE_MIN_D; }
+
+// Rows per internal chunk of the swept side (m rows against n): whole 128-row panels, and with fused columns
+// the chunk's column partial lists within COLPART_CAP.
+inline int64_t chunk_rows(int64_t m, int64_t n, int k, bool fused) {
+    int64_t ch = CHUNK_MAX;
+    if (fused) {
+        const int64_t per_panel = n * (int64_t)bucket_k1(k) * (int64_t)sizeof(Entry);
+        int64_t panels = (int64_t)(COLPART_CAP / (size_t)per_panel);
+        if (panels < 1) panels = 1;
+        if (panels * BX < ch) ch = panels * BX;
+    }
+    const int64_t whole = (m + BX - 1) / BX * BX;
+    return ch < whole ? ch : whole;
+}
+
+inline int choose_segments(int64_t m, int64_t n) {
     const int64_t panels = (m + BX - 1) / BX;
     const int64_t tiles = (n + BY - 1) / BY;
-    int64_t s = (2048 + panels - 1) / panels;
+    int64_t s = (SWEEP_WGS + panels - 1) / panels;
     const int64_t max_s = tiles / 4 > 0 ? tiles / 4 : 1;
     if (s > max_s) s = max_s;
-    const int64_t cap = 256 / bucket_k1(k);  // finalize ranks at most 2 * S * K1 <= 512 entries
-    if (s > cap) s = cap;
+    if (s > 64) s = 64;
     if (s < 1) s = 1;
     return (int)s;
 }
 
-
-inline DirPlan plan_dir(int64_t rows, int64_t cols, int k) {
+inline DirPlan plan_dir(int64_t rows, int64_t cols) {
     DirPlan p;
     p.rows = rows;
     p.cols = cols;
-    p.S = choose_segments(rows, cols, k);
+    p.S = choose_segments(rows, cols);
     const int64_t tiles = (cols + BY - 1) / BY;
     const int64_t tiles_per = (tiles + p.S - 1) / p.S;
     p.seg_len = tiles_per * BY;
@@ -506,10 +666,20 @@ inline DirPlan plan_dir(int64_t rows, int64_t cols, int k) {
 }
 
 template <class A>
-void layout(A& a, int64_t m, int64_t n, int k, uint32_t flags, DirPlan pr, DirPlan pc, double** xnorm,
-            double** ynorm, float** qb32, float** p32, float** db32, float** ge32,
-            unsigned long long** maxima, Entry** part, double** blockstats, int** redo, int** redo_count) {
+void layout(A& a, int64_t m, int64_t n, int d, int k, uint32_t flags, double** xnorm, double** ynorm, float** qb32,
+            float** p32, float** db32, float** ge32, unsigned long long** maxima, Entry** part, Entry** colpart,
+            unsigned int** colthr, double** cval, int** cidx, double** blockstats, int** redo, int** redo_count) {
     const int K1 = bucket_k1(k);
+    const bool fused = fused_columns(d, flags);
+    const int64_t ch = chunk_rows(m, n, k, fused);
+    const DirPlan plan = plan_dir(ch, n);
+    const int64_t panels = ch / BX;
+    // second sweep with the roles swapped (columns without fusion): Y chunks against X
+    const bool swapped = (flags & HM_COLS) && !fused;
+    const int64_t ch2 = swapped ? chunk_rows(n, m, k, false) : 0;
+    const DirPlan plan2 = plan_dir(swapped ? ch2 : 1, m);
+    size_t part_entries = (size_t)plan.S * ch * 2 * K1;
+    if (swapped && (size_t)plan2.S * ch2 * 2 * K1 > part_entries) part_entries = (size_t)plan2.S * ch2 * 2 * K1;
     *xnorm = a.template take<double>(m);
     *ynorm = a.template take<double>(n);
     *qb32 = a.template take<float>(m);
@@ -517,45 +687,32 @@ void layout(A& a, int64_t m, int64_t n, int k, uint32_t flags, DirPlan pr, DirPl
     *db32 = a.template take<float>(n);
     *ge32 = a.template take<float>(n);
     *maxima = a.template take<unsigned long long>(4);
-    size_t part_entries = 0;
-    if (flags & (HM_ROWS | HM_STATS)) part_entries = (size_t)pr.S * m * 2 * K1;
-    if (flags & HM_COLS) {
-        const size_t c = (size_t)pc.S * n * 2 * K1;
-        if (c > part_entries) part_entries = c;
-    }
-    *part = a.template take<Entry>(part_entries > 0 ? part_entries : 1);
-    const int64_t blocks_r = (int64_t)((m + BX - 1) / BX) * pr.S;
-    const int64_t blocks_c = (int64_t)((n + BX - 1) / BX) * pc.S;
-    *blockstats = a.template take<double>((size_t)5 * (blocks_r > blocks_c ? blocks_r : blocks_c));
-    *redo = a.template take<int>((size_t)(m > n ? m : n));
+    *part = a.template take<Entry>(part_entries);
+    *colpart = a.template take<Entry>(fused ? (size_t)panels * n * K1 : 1);
+    *colthr = a.template take<unsigned int>(fused ? (size_t)n : 1);
+    *cval = a.template take<double>(fused ? (size_t)n * k : 1);
+    *cidx = a.template take<int>(fused ? (size_t)n * k : 1);
+    *blockstats = a.template take<double>((size_t)5 * panels * plan.S);
+    *redo = a.template take<int>((size_t)(m + n));
     *redo_count = a.template take<int>(2);
 }
 
 template <int K1>
-int run_direction(hipStream_t st, const float* X, const float* Y, int64_t m, int64_t n, int d, int k,
-                  double scale, bool stats, bool transposed, const double* qb, const double* db,
-                  const double* xnorm, const unsigned long long* ymaxima, const float* qb32, const float* db32,
-                  const float* p32, const float* ge32, DirPlan plan, Entry* part, double* blockstats,
-                  int* redo, int* redo_count, double* out_val, int* out_idx, double* stats_out, int linf,
-                  bool want_rows) {
+int run_bidir(hipStream_t st, const float* X, const float* Y, int64_t m, int64_t n, int d, int k, double scale,
+              uint32_t flags, const double* qb, const double* db, const double* xnorm, const double* ynorm,
+              const unsigned long long* maxima, const float* qb32, const float* db32, const float* p32,
+              const float* ge32, Entry* part, Entry* colpart, unsigned int* colthr, double* cval, int* cidx,
+              double* blockstats, int* redo, int* redo_count, double* row_val, int* row_idx, double* col_val,
+              int* col_idx, double* stats) {
+    const bool want_rows = (flags & HM_ROWS) != 0;
+    const bool fused = fused_columns(d, flags);
+    const bool swapped = (flags & HM_COLS) && !fused;
+    const bool want_stats = (flags & HM_STATS) != 0;
+    const int linf = (flags & HM_LINF) ? 1 : 0;
     const bool two_level = d > KC * FLUSH_CHUNKS;
     const bool vec4 = (d % 4) == 0;
-    dim3 grid((unsigned)((m + BX - 1) / BX), (unsigned)plan.S);
-#define HM_SWEEP(TL)                                                                                       \
-    hipLaunchKernelGGL((l2sq_sweep<K1, TL>), grid, dim3(256), 0, st, X, Y, m, n, d, qb32, db32, p32, ge32,       \
-                       (float)scale, plan.seg_len, part, blockstats, (int)vec4, (int)stats)
-    prof_begin(st, "l2sq_sweep");
-    if (two_level) HM_SWEEP(true);
-    else HM_SWEEP(false);
-    prof_end(st);
-#undef HM_SWEEP
-    HM_LAUNCH_CHECK("l2sq_sweep");
-    if (stats) {
-        hipLaunchKernelGGL(l2sq_reduce_stats, dim3(1), dim3(256), 0, st, blockstats, (int64_t)grid.x * grid.y,
-                           stats_out, linf);
-        HM_LAUNCH_CHECK("l2sq_reduce_stats");
-    }
-    if (!want_rows) return HM_OK;
+    const int64_t ch = chunk_rows(m, n, k, fused);
+    const DirPlan plan = plan_dir(ch, n);
     // rigorous bound constants
     const double kb = two_level ? (double)(KC * FLUSH_CHUNKS) : (double)d;
     const double nblk = two_level ? std::ceil((double)d / (KC * FLUSH_CHUNKS)) : 1.0;
@@ -565,25 +722,126 @@ int run_direction(hipStream_t st, const float* X, const float* Y, int64_t m, int
     bnd.acc_rel = ea + u * (1.0 + ea) + 4e-15 * (d / 64.0 + 8.0);
     bnd.db_rel = 2.0 * u + 1e-15;
     bnd.abs_slack = 1e-30 * (double)d;
-    hipLaunchKernelGGL(zero_words, dim3(1), dim3(64), 0, st, reinterpret_cast<unsigned long long*>(redo_count), 1);
-    HM_LAUNCH_CHECK("zero_words");
-    const unsigned fin_blocks = (unsigned)((m + 3) / 4);
-    prof_begin(st, "l2sq_finalize");
-    hipLaunchKernelGGL((l2sq_finalize<K1>), dim3(fin_blocks), dim3(256), 0, st, X, Y, m, d, plan.S, part, qb, db, xnorm,
-                       ymaxima, scale, k, bnd, out_val, out_idx, redo, redo_count, (int)transposed);
-    prof_end(st);
-    HM_LAUNCH_CHECK("l2sq_finalize");
-    const unsigned rescan_blocks = (unsigned)(m < 1024 ? m : 1024);
-#define HM_RESCAN(KK)                                                                                        \
-    hipLaunchKernelGGL((l2sq_rescan<KK>), dim3(rescan_blocks), dim3(64), 0, st, X, Y, n, d, qb, db, scale, k, redo, \
-                       redo_count, out_val, out_idx, (int)transposed)
-    prof_begin(st, "l2sq_rescan");
-    if (k <= 2) HM_RESCAN(2);
-    else if (k <= 8) HM_RESCAN(8);
-    else HM_RESCAN(32);
-    prof_end(st);
+    int chunk_index = 0;
+    for (int64_t xb = 0; xb < m; xb += ch, ++chunk_index) {
+        const int64_t xe = xb + ch < m ? xb + ch : m;
+        const int64_t rows = xe - xb;
+        const int64_t panels = (rows + BX - 1) / BX;
+        dim3 grid((unsigned)panels, (unsigned)plan.S);
+        if (fused) {
+            // column thresholds start at -inf for every chunk (its lists only rank its own X rows)
+            const unsigned neg_inf_key = 0x007fffffu;  // float_key(-INFINITY)
+            hipLaunchKernelGGL(fill_u32, dim3((unsigned)((n + 255) / 256 < 4096 ? (n + 255) / 256 : 4096)), dim3(256), 0,
+                               st, colthr, n, neg_inf_key);
+            HM_LAUNCH_CHECK("fill_u32");
+        }
+#define HM_SWEEP(TL, CL)                                                                                            \
+    hipLaunchKernelGGL((l2sq_sweep<K1, TL, CL>), grid, dim3(256), 0, st, X, Y, xb, xe, n, d, qb32, db32, p32, ge32, \
+                       (float)scale, plan.seg_len, part, colpart, colthr, blockstats, (int)vec4, (int)want_stats)
+        prof_begin(st, "l2sq_sweep");
+        if (two_level) {
+            if (fused) HM_SWEEP(true, true);
+            else HM_SWEEP(true, false);
+        } else {
+            if (fused) HM_SWEEP(false, true);
+            else HM_SWEEP(false, false);
+        }
+        prof_end(st);
+#undef HM_SWEEP
+        HM_LAUNCH_CHECK("l2sq_sweep");
+        if (want_stats) {
+            hipLaunchKernelGGL(l2sq_reduce_stats, dim3(1), dim3(256), 0, st, blockstats, (int64_t)grid.x * grid.y,
+                               stats, linf, chunk_index > 0 ? 1 : 0);
+            HM_LAUNCH_CHECK("l2sq_reduce_stats");
+        }
+        const unsigned rescan_blocks_rows = (unsigned)(rows < 1024 ? rows : 1024);
+        if (want_rows) {
+            // row finalize: lists (seg, half) of each chunk row; candidates are Y rows
+            hipLaunchKernelGGL(zero_words, dim3(1), dim3(64), 0, st, reinterpret_cast<unsigned long long*>(redo_count), 1);
+            prof_begin(st, "l2sq_finalize");
+            hipLaunchKernelGGL((l2sq_finalize<K1, 2, false>), dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, st,
+                               X + xb * d, Y, rows, d, 2 * plan.S, part, qb + xb, db, xnorm + xb, maxima + 2, scale, k,
+                               bnd, row_val + xb * k, row_idx + xb * k, redo, redo_count);
+            prof_end(st);
+            HM_LAUNCH_CHECK("l2sq_finalize");
+            prof_begin(st, "l2sq_rescan");
+#define HM_RESCAN(KK)                                                                                                  \
+    hipLaunchKernelGGL((l2sq_rescan<KK>), dim3(rescan_blocks_rows), dim3(64), 0, st, X + xb * d, Y, n, d, qb + xb, db, \
+                       scale, k, redo, redo_count, row_val + xb * k, row_idx + xb * k, 0, 0)
+            if (k <= 2) HM_RESCAN(2);
+            else if (k <= 8) HM_RESCAN(8);
+            else HM_RESCAN(32);
 #undef HM_RESCAN
-    HM_LAUNCH_CHECK("l2sq_rescan");
+            prof_end(st);
+            HM_LAUNCH_CHECK("l2sq_rescan");
+        }
+        if (fused) {
+            // column finalize: one list per X panel of this chunk; candidates are the chunk's X rows (global ids)
+            hipLaunchKernelGGL(zero_words, dim3(1), dim3(64), 0, st, reinterpret_cast<unsigned long long*>(redo_count), 1);
+            prof_begin(st, "l2sq_col_finalize");
+            hipLaunchKernelGGL((l2sq_finalize<K1, 1, true>), dim3((unsigned)((n + 3) / 4)), dim3(256), 0, st, Y, X, n, d,
+                               (int)panels, colpart, db, qb, ynorm, maxima, scale, k, bnd, cval, cidx, redo,
+                               redo_count);
+            prof_end(st);
+            HM_LAUNCH_CHECK("l2sq_col_finalize");
+            const unsigned rescan_blocks_cols = (unsigned)(n < 1024 ? n : 1024);
+            prof_begin(st, "l2sq_rescan");
+#define HM_RESCAN(KK)                                                                                                \
+    hipLaunchKernelGGL((l2sq_rescan<KK>), dim3(rescan_blocks_cols), dim3(64), 0, st, Y, X + xb * d, rows, d, db,     \
+                       qb + xb, scale, k, redo, redo_count, cval, cidx, 1, (int)xb)
+            if (k <= 2) HM_RESCAN(2);
+            else if (k <= 8) HM_RESCAN(8);
+            else HM_RESCAN(32);
+#undef HM_RESCAN
+            prof_end(st);
+            HM_LAUNCH_CHECK("l2sq_rescan");
+            hipLaunchKernelGGL(l2sq_merge_columns, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, col_val, col_idx,
+                               cval, cidx, n, k, chunk_index == 0 ? 1 : 0);
+            HM_LAUNCH_CHECK("l2sq_merge_columns");
+        }
+    }
+    if (swapped) {
+        // columns by a second sweep with the roles swapped: Y chunks are the rows, X is segmented; the
+        // finalize keeps the (dot + qb) + db association of the caller's pairs
+        const int64_t ch2 = chunk_rows(n, m, k, false);
+        const DirPlan plan2 = plan_dir(ch2, m);
+        for (int64_t yb = 0; yb < n; yb += ch2) {
+            const int64_t ye = yb + ch2 < n ? yb + ch2 : n;
+            const int64_t rows = ye - yb;
+            dim3 grid((unsigned)((rows + BX - 1) / BX), (unsigned)plan2.S);
+#define HM_SWEEP2(TL)                                                                                               \
+    hipLaunchKernelGGL((l2sq_sweep<K1, TL, false>), grid, dim3(256), 0, st, Y, X, yb, ye, m, d, db32, qb32, ge32,   \
+                       p32, (float)scale, plan2.seg_len, part, colpart, colthr, blockstats, (int)vec4, 0)
+            prof_begin(st, "l2sq_sweep");
+            if (two_level) HM_SWEEP2(true);
+            else HM_SWEEP2(false);
+            prof_end(st);
+#undef HM_SWEEP2
+            HM_LAUNCH_CHECK("l2sq_sweep");
+            hipLaunchKernelGGL(zero_words, dim3(1), dim3(64), 0, st, reinterpret_cast<unsigned long long*>(redo_count), 1);
+            prof_begin(st, "l2sq_col_finalize");
+            hipLaunchKernelGGL((l2sq_finalize<K1, 2, true>), dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, st,
+                               Y + yb * d, X, rows, d, 2 * plan2.S, part, db + yb, qb, ynorm + yb, maxima, scale, k,
+                               bnd, col_val + yb * k, col_idx + yb * k, redo, redo_count);
+            prof_end(st);
+            HM_LAUNCH_CHECK("l2sq_col_finalize");
+            const unsigned rescan_blocks = (unsigned)(rows < 1024 ? rows : 1024);
+            prof_begin(st, "l2sq_rescan");
+#define HM_RESCAN(KK)                                                                                               \
+    hipLaunchKernelGGL((l2sq_rescan<KK>), dim3(rescan_blocks), dim3(64), 0, st, Y + yb * d, X, m, d, db + yb, qb,   \
+                       scale, k, redo, redo_count, col_val + yb * k, col_idx + yb * k, 1, 0)
+            if (k <= 2) HM_RESCAN(2);
+            else if (k <= 8) HM_RESCAN(8);
+            else HM_RESCAN(32);
+#undef HM_RESCAN
+            prof_end(st);
+            HM_LAUNCH_CHECK("l2sq_rescan");
+        }
+    }
+    if (want_stats && want_rows) {
+        hipLaunchKernelGGL(exact_row_max, dim3(1), dim3(256), 0, st, row_val, m, k, stats);
+        HM_LAUNCH_CHECK("exact_row_max");
+    }
     return HM_OK;
 }
 
@@ -591,12 +849,12 @@ int run_direction(hipStream_t st, const float* X, const float* Y, int64_t m, int
 }  // namespace hm
 
 // driver signature shared by the per-K1 translation units
-#define L2SQ_RUN_ARGS                                                                                             \
-    hipStream_t st, const float *X, const float *Y, int64_t m, int64_t n, int d, int k, double scale, bool stats,      \
-        bool transposed, const double *qb, const double *db, const double *xnorm, const unsigned long long *ymaxima,  \
-        const float *qb32, const float *db32, const float *p32, const float *ge32, ::hm::DirPlan plan,             \
-        ::hm::Entry *part, double *blockstats, int *redo, int *redo_count, double *out_val, int *out_idx,           \
-        double *stats_out, int linf, bool want_rows
-#define L2SQ_RUN_PASS                                                                                              \
-    st, X, Y, m, n, d, k, scale, stats, transposed, qb, db, xnorm, ymaxima, qb32, db32, p32, ge32, plan, part,         \
-        blockstats, redo, redo_count, out_val, out_idx, stats_out, linf, want_rows
+#define L2SQ_RUN_ARGS                                                                                              \
+    hipStream_t st, const float *X, const float *Y, int64_t m, int64_t n, int d, int k, double scale, uint32_t flags, \
+        const double *qb, const double *db, const double *xnorm, const double *ynorm,                              \
+        const unsigned long long *maxima, const float *qb32, const float *db32, const float *p32, const float *ge32, \
+        ::hm::Entry *part, ::hm::Entry *colpart, unsigned int *colthr, double *cval, int *cidx, double *blockstats, \
+        int *redo, int *redo_count, double *row_val, int *row_idx, double *col_val, int *col_idx, double *stats
+#define L2SQ_RUN_PASS                                                                                               \
+    st, X, Y, m, n, d, k, scale, flags, qb, db, xnorm, ynorm, maxima, qb32, db32, p32, ge32, part, colpart, colthr, \
+        cval, cidx, blockstats, redo, redo_count, row_val, row_idx, col_val, col_idx, stats

@@ -6,11 +6,7 @@ int l2sq_run_k8(L2SQ_RUN_ARGS);
 int l2sq_run_k16(L2SQ_RUN_ARGS);
 int l2sq_run_k40(L2SQ_RUN_ARGS);
 namespace {
-int run_direction_k(hipStream_t st, const float* X, const float* Y, int64_t m, int64_t n, int d, int k, double scale,
-                    bool stats, bool transposed, const double* qb, const double* db, const double* xnorm,
-                    const unsigned long long* ymaxima, const float* qb32, const float* db32, const float* p32,
-                    const float* ge32, DirPlan plan, Entry* part, double* blockstats, int* redo, int* redo_count,
-                    double* out_val, int* out_idx, double* stats_out, int linf, bool want_rows) {
+int run_k(L2SQ_RUN_ARGS) {
     switch (bucket_k1(k)) {
         case 8:
             return l2sq_run_k8(L2SQ_RUN_PASS);
@@ -27,15 +23,15 @@ int run_direction_k(hipStream_t st, const float* X, const float* Y, int64_t m, i
 using namespace hm;
 
 extern "C" size_t hm_pricing_l2sq_workspace_bytes(int64_t m, int64_t n, int32_t d, int32_t k, uint32_t flags) {
-    (void)d;
     if (m < 1 || n < 1 || k < 1 || k > 32) return 0;
     Sizer s;
-    double *a, *b, *bs;
+    double *a, *b, *bs, *cv;
     float *c, *e, *f, *g;
     unsigned long long* mx;
-    Entry* part;
-    int *redo, *rc;
-    layout(s, m, n, k, flags, plan_dir(m, n, k), plan_dir(n, m, k), &a, &b, &c, &e, &f, &g, &mx, &part, &bs, &redo, &rc);
+    Entry *part, *colpart;
+    unsigned int* thr;
+    int *redo, *rc, *ci;
+    layout(s, m, n, d, k, flags, &a, &b, &c, &e, &f, &g, &mx, &part, &colpart, &thr, &cv, &ci, &bs, &redo, &rc);
     return s.used;
 }
 
@@ -53,47 +49,28 @@ extern "C" int hm_pricing_l2sq(void* stream, const float* X, const float* Y, con
     HM_CHECK_ARG(!(flags & HM_COLS) || (col_val && col_idx), "HM_COLS requires column outputs");
     HM_CHECK_ARG(!(flags & HM_STATS) || stats, "HM_STATS requires a stats output");
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-    const DirPlan pr = plan_dir(m, n, k), pc = plan_dir(n, m, k);
     const size_t need = hm_pricing_l2sq_workspace_bytes(m, n, d, k, flags);
     HM_CHECK_ARG(workspace != nullptr, "workspace is required");
     if (workspace_bytes < need)
         return fail(HM_ENOSPC, "l2sq pricing workspace too small: %zu < %zu bytes", workspace_bytes, need);
     Arena a(workspace, workspace_bytes);
-    double *xnorm, *ynorm, *blockstats;
+    double *xnorm, *ynorm, *blockstats, *cval;
     float *qb32, *p32, *db32, *ge32;
     unsigned long long* maxima;
-    Entry* part;
-    int *redo, *redo_count;
-    layout(a, m, n, k, flags, pr, pc, &xnorm, &ynorm, &qb32, &p32, &db32, &ge32, &maxima, &part, &blockstats, &redo,
-           &redo_count);
+    Entry *part, *colpart;
+    unsigned int* colthr;
+    int *redo, *redo_count, *cidx;
+    layout(a, m, n, d, k, flags, &xnorm, &ynorm, &qb32, &p32, &db32, &ge32, &maxima, &part, &colpart, &colthr, &cval,
+           &cidx, &blockstats, &redo, &redo_count);
     hipLaunchKernelGGL(zero_words, dim3(1), dim3(64), 0, st, maxima, 4);
     HM_LAUNCH_CHECK("zero_words");
     // X side: ||x||, qb32, p32 (maxima[0..1] = max||x||, max|qb|); Y side: ||y||, db32, ge32 = q + db
-    hipLaunchKernelGGL(l2sq_prep_rows, dim3((unsigned)((m + 3) / 4)), dim3(256), 0, st, X, m, d, p, qb,
+    hipLaunchKernelGGL(l2sq_prep_rows, dim3(prep_grid(m)), dim3(256), 0, st, X, m, d, p, qb,
                        (const double*)nullptr, xnorm, qb32, p32, maxima);
     HM_LAUNCH_CHECK("l2sq_prep_rows");
-    hipLaunchKernelGGL(l2sq_prep_rows, dim3((unsigned)((n + 3) / 4)), dim3(256), 0, st, Y, n, d, q, db, db, ynorm,
+    hipLaunchKernelGGL(l2sq_prep_rows, dim3(prep_grid(n)), dim3(256), 0, st, Y, n, d, q, db, db, ynorm,
                        db32, ge32, maxima + 2);
     HM_LAUNCH_CHECK("l2sq_prep_rows");
-    const bool want_stats = (flags & HM_STATS) != 0;
-    const int linf = (flags & HM_LINF) ? 1 : 0;
-    // rows (and certificate)
-    if (flags & (HM_ROWS | HM_STATS)) {
-        // ymaxima for the row direction = (max||y||, max|db|) = maxima[2..3]
-        int rc = run_direction_k(st, X, Y, m, n, d, k, scale, want_stats, false, qb, db, xnorm, maxima + 2, qb32, db32,
-                                 p32, ge32, pr, part, blockstats, redo, redo_count, row_val, row_idx, stats, linf,
-                                 (flags & HM_ROWS) != 0);
-        if (rc != HM_OK) return rc;
-        if (want_stats && (flags & HM_ROWS)) {
-            hipLaunchKernelGGL(exact_row_max, dim3(1), dim3(256), 0, st, row_val, m, k, stats);
-            HM_LAUNCH_CHECK("exact_row_max");
-        }
-    }
-    if (flags & HM_COLS) {
-        // swapped roles: rows are Y, columns are X; biases swap, the exact score keeps the original association
-        int rc = run_direction_k(st, Y, X, n, m, d, k, scale, false, true, db, qb, ynorm, maxima, db32, qb32, ge32,
-                                 p32, pc, part, blockstats, redo, redo_count, col_val, col_idx, nullptr, 0, true);
-        if (rc != HM_OK) return rc;
-    }
-    return HM_OK;
+    return run_k(st, X, Y, m, n, d, k, scale, flags, qb, db, xnorm, ynorm, maxima, qb32, db32, p32, ge32, part,
+                 colpart, colthr, cval, cidx, blockstats, redo, redo_count, row_val, row_idx, col_val, col_idx, stats);
 }

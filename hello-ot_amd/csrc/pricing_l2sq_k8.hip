@@ -2,5 +2,5 @@
 #include "l2sq_impl.h"
 
 namespace hm {
-int l2sq_run_k8(L2SQ_RUN_ARGS) { return run_direction<8>(L2SQ_RUN_PASS); }
+int l2sq_run_k8(L2SQ_RUN_ARGS) { return run_bidir<8>(L2SQ_RUN_PASS); }
 }  // namespace hm

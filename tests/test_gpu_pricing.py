@@ -82,6 +82,33 @@ def test_l2sq_ties_and_duplicates_lowest_index_wins(cuda):
         np.testing.assert_array_equal(rv.cpu().numpy(), orv)
 
 
+@pytest.mark.parametrize("m,n,d,k,integer", [
+    (65536 + 300, 97, 256, 2, True),    # columns fused into the row sweep, merged across two query chunks
+    (65536 + 300, 97, 256, 8, False),
+    (65536 + 300, 97, 12, 8, True),     # columns by a second, role-swapped sweep; query side in two chunks
+    (97, 65536 + 300, 12, 3, True),     # role-swapped sweep over two resident-side chunks
+])
+def test_l2sq_chunked_sides_and_ties(cuda, m, n, d, k, integer):
+    """Shapes with more than 65536 rows on one side: the kernel processes that side in internal chunks (and,
+    with fused columns, merges the exact column lists across query chunks). With integer data every score is
+    exact and ties abound; duplicated rows placed in different chunks must resolve to the lower index."""
+    X, Y, p, q, qb, db = _l2sq_case(m, n, d, seed=31 + k + d, integer=integer)
+    big, side = (X, "x") if m > n else (Y, "y")
+    for src, dst in ((3, 65536 + 7), (40, 65536 + 250), (5000, 65536 + 1)):
+        big[dst] = big[src]
+        if side == "x":
+            p[dst], qb[dst] = p[src], qb[src]
+        else:
+            q[dst], db[dst] = q[src], db[src]
+    orv, ori, ocv, oci, ost = oracle.l2sq_scan(X, Y, p, q, qb, db, k, 2.0)
+    rv, ri, cv, ci, st = pricing_l2sq(*_to(cuda, X, Y, p, q, qb, db), k, linf=True)
+    np.testing.assert_array_equal(ci.cpu().numpy(), oci)
+    np.testing.assert_array_equal(cv.cpu().numpy(), ocv)
+    np.testing.assert_array_equal(ri.cpu().numpy(), ori)
+    np.testing.assert_array_equal(rv.cpu().numpy(), orv)
+    _assert_stats(st, ost)
+
+
 def test_l2sq_all_equal_scores_take_lowest_indices(cuda):
     # every pair ties exactly: integer-valued identical points -> every row's top-k is columns 0..k-1
     m, n, d, k = 70, 500, 4, 8
