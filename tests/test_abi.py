@@ -50,9 +50,12 @@ def test_workspace_queries_are_host_arithmetic():
     small = lib.hm_pricing_l2sq_workspace_bytes(1000, 1000, 64, 8, 7)
     big = lib.hm_pricing_l2sq_workspace_bytes(131072, 131072, 64, 8, 7)
     assert 0 < small < big
-    # C5: per-row candidate lists stay small next to the 2 x 39 GiB feature matrices
+    # C5: the per-chunk column partial lists are capped at 12 GiB (query chunks shrink to fit), the rest is
+    # small next to the 2 x 39 GiB feature matrices
     c5 = lib.hm_pricing_l2sq_workspace_bytes(1_280_000, 1_280_000, 8192, 2, 7)
-    assert c5 < 1 << 30
+    assert 12 << 30 < c5 < 14 << 30
+    c5_rows = lib.hm_pricing_l2sq_workspace_bytes(1_280_000, 1_280_000, 8192, 2, 5)  # rows + stats only
+    assert c5_rows < 1 << 30
     assert lib.hm_pricing_l2sq_workspace_bytes(0, 10, 4, 2, 7) == 0
     assert lib.hm_pricing_norm_workspace_bytes(524288, 524288, 8, 2, 7) > 0
 
