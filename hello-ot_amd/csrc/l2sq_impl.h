@@ -723,7 +723,8 @@ int run_bidir(hipStream_t st, const float* X, const float* Y, int64_t m, int64_t
     bnd.db_rel = 2.0 * u + 1e-15;
     bnd.abs_slack = 1e-30 * (double)d;
     int chunk_index = 0;
-    for (int64_t xb = 0; xb < m; xb += ch, ++chunk_index) {
+    const bool row_pass = want_rows || fused || want_stats;  // a columns-only call without fusion skips it
+    for (int64_t xb = 0; row_pass && xb < m; xb += ch, ++chunk_index) {
         const int64_t xe = xb + ch < m ? xb + ch : m;
         const int64_t rows = xe - xb;
         const int64_t panels = (rows + BX - 1) / BX;

@@ -136,6 +136,32 @@ __global__ __launch_bounds__(256) void pair_costs_norm_kernel(const float* __res
     }
 }
 
+// fp32 norm costs exactly as the pricing scan forms them: 32-feature chunks accumulated sequentially in fp32,
+// chunk results combined in order, l2 = sqrt in fp64 of the fp32 sum, rounded once to fp32.
+template <int KIND>
+__global__ __launch_bounds__(256) void pair_costs_norm32_kernel(const float* __restrict__ X, const float* __restrict__ Y,
+                                                                const int64_t* __restrict__ rows,
+                                                                const int64_t* __restrict__ cols, int64_t count, int d,
+                                                                double* __restrict__ out) {
+    for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < count; e += (int64_t)gridDim.x * blockDim.x) {
+        const float* x = X + rows[e] * d;
+        const float* y = Y + cols[e] * d;
+        float acc = 0.0f;
+        for (int base = 0; base < d; base += 32) {
+            float part = 0.0f;
+            const int end = base + 32 < d ? base + 32 : d;
+            for (int k = base; k < end; ++k) {
+                const float z = x[k] - y[k];
+                if (KIND == HM_COST_L1) part = part + fabsf(z);
+                else if (KIND == HM_COST_LINF) part = fmaxf(part, fabsf(z));
+                else part = fmaf(z, z, part);
+            }
+            acc = (KIND == HM_COST_LINF) ? fmaxf(acc, part) : acc + part;
+        }
+        out[e] = (KIND == HM_COST_L2) ? (double)(float)sqrt((double)acc) : (double)acc;
+    }
+}
+
 inline int group_for(int d) { return d <= 8 ? 8 : (d <= 16 ? 16 : (d <= 32 ? 32 : 64)); }
 
 inline unsigned grid_for(int64_t items, int per_block) {
@@ -218,5 +244,26 @@ extern "C" int hm_pair_costs_norm(void* stream, const float* X, const float* Y, 
 #undef HM_NORM_K
 #undef HM_NORM
     HM_LAUNCH_CHECK("pair_costs_norm");
+    return HM_OK;
+}
+
+extern "C" int hm_pair_costs_norm_fp32(void* stream, const float* X, const float* Y, const int64_t* rows,
+                                       const int64_t* cols, int64_t count, int32_t d, int32_t kind, double* out) {
+    HM_CHECK_ARG(count >= 0 && d >= 1, "pair costs require count >= 0 and d >= 1");
+    HM_CHECK_ARG(kind == HM_COST_L1 || kind == HM_COST_LINF || kind == HM_COST_L2, "unsupported norm cost %d", kind);
+    if (count == 0) return HM_OK;
+    HM_CHECK_ARG(X && Y && rows && cols && out, "pair costs: null pointer argument");
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    const unsigned grid = grid_for(count, 256);
+    if (kind == HM_COST_L1)
+        hipLaunchKernelGGL((pair_costs_norm32_kernel<HM_COST_L1>), dim3(grid), dim3(256), 0, st, X, Y, rows, cols, count, d,
+                           out);
+    else if (kind == HM_COST_LINF)
+        hipLaunchKernelGGL((pair_costs_norm32_kernel<HM_COST_LINF>), dim3(grid), dim3(256), 0, st, X, Y, rows, cols, count,
+                           d, out);
+    else
+        hipLaunchKernelGGL((pair_costs_norm32_kernel<HM_COST_L2>), dim3(grid), dim3(256), 0, st, X, Y, rows, cols, count, d,
+                           out);
+    HM_LAUNCH_CHECK("pair_costs_norm_fp32");
     return HM_OK;
 }

@@ -1,0 +1,131 @@
+"""``solve`` -- the HELLO front end of the MI355X build (``src/hello_ot/__init__.py:40-90``, ``api.py:353-372``).
+
+Array calls default to squared-Euclidean cost and uniform masses; ``max_iterations`` bounds the refinement
+iterations per level and ``random_seed`` fixes the global shuffle. Inputs may be numpy arrays or tensors; the
+solve runs on ``cuda:0`` (or the device of CUDA input tensors) and returns a device-resident ``Result``.
+"""
+from __future__ import annotations
+
+import sys
+import time
+from typing import Any, Optional
+
+import numpy as np
+import torch
+
+from ._native_compat import require_native_runtime_compatibility
+from .config import SolverOptions
+from .resident.cost import Cost
+from .resident.solver import level_sizes, refine, shuffle_once_permutation, solve_leaf
+from .resident.support import normalize_masses
+from .types import Problem, Result, SolveStageResult, SparseOTSolution
+
+
+def solve(source_points: Problem | Any, target_points: Any | None = None, *, source_mass: Any | None = None,
+          target_mass: Any | None = None, cost: str | None = None, max_iterations: int = 100,
+          random_seed: int = 42, options: SolverOptions | None = None) -> Result:
+    if isinstance(source_points, Problem):
+        if target_points is not None or source_mass is not None or target_mass is not None or cost is not None:
+            raise TypeError("When the first argument is Problem, target_points, masses, and cost must not be repeated.")
+        problem = source_points
+    else:
+        if target_points is None:
+            raise TypeError("target_points is required when solving from arrays")
+        problem = Problem(source_points, target_points, "l2^2" if cost is None else cost, source_mass, target_mass)
+    if int(max_iterations) < 1:
+        raise ValueError("max_iterations must be >= 1")
+    if not isinstance(random_seed, int):
+        raise TypeError("random_seed must be an int")
+    options = SolverOptions() if options is None else options
+    if not isinstance(options, SolverOptions):
+        raise TypeError("options must be SolverOptions or None")
+    return solve_problem(problem, options, max_iterations=int(max_iterations), random_seed=int(random_seed))
+
+
+def _device_of(problem: Problem) -> torch.device:
+    for value in (problem.source_points, problem.target_points):
+        if torch.is_tensor(value) and value.is_cuda:
+            return value.device
+    return torch.device("cuda", 0)
+
+
+def _to_device(value, device, dtype):
+    if torch.is_tensor(value):
+        return value.to(device=device, dtype=dtype)
+    return torch.as_tensor(np.asarray(value), dtype=dtype, device=device)
+
+
+@torch.no_grad()
+def solve_problem(problem: Problem, options: SolverOptions, *, max_iterations: int = 100,
+                  random_seed: int = 42) -> Result:
+    options.check_supported()
+    if options.stopping_norm != "l2":
+        raise NotImplementedError("the MI355X build stops on the relative l2 dual infeasibility (stopping_norm='l2')")
+    require_native_runtime_compatibility()
+    device = _device_of(problem)
+    n, m = problem.shape
+    with torch.cuda.device(device):
+        torch.cuda.synchronize(device)
+        torch.cuda.reset_peak_memory_stats(device)
+        started = time.perf_counter()
+        perm_s, perm_t = shuffle_once_permutation(n, m, random_seed, options.split_count)
+        si = torch.as_tensor(perm_s, device=device)
+        ti = torch.as_tensor(perm_t, device=device)
+        a = (torch.full((n,), 1.0 / n, dtype=torch.float64, device=device) if problem.source_mass is None
+             else _to_device(problem.source_mass, device, torch.float64))[si]
+        b = (torch.full((m,), 1.0 / m, dtype=torch.float64, device=device) if problem.target_mass is None
+             else _to_device(problem.target_mass, device, torch.float64))[ti]
+        x = _to_device(problem.source_points, device, torch.float32)[si].contiguous()
+        y = _to_device(problem.target_points, device, torch.float32)[ti].contiguous()
+        full = Cost.create(x, y, problem.cost_type)
+        sizes = level_sizes(n, m, options.coarsest_size_threshold, options.split_count)
+        levels, previous, triggers = [], None, []
+        support = dual = None
+        for level_index in reversed(range(len(sizes))):
+            nn, mm = sizes[level_index]
+            cost = full.sliced(nn, mm)
+            aa, bb = normalize_masses(a[:nn].clone(), b[:mm].clone())
+            if previous is None:
+                support, dual, level = solve_leaf(cost, aa, bb, level_index, options.tolerance)
+            else:
+                known = "target" if nn >= mm else "source"
+                support, dual, level, triggered = refine(cost, aa, bb, previous, known, options, level_index,
+                                                         max_iterations, options.cost_perturbation == "auto")
+                if triggered:
+                    triggers.append(level_index)
+            levels.append(level)
+            previous = dual
+        rows, cols = support.rows_cols()
+        objective = float(full.pairs(rows, cols) @ support.values)
+        keys = si[rows] * m + ti[cols]
+        order = torch.argsort(keys, stable=True)
+        f = torch.empty(n, dtype=torch.float64, device=device)
+        g = torch.empty(m, dtype=torch.float64, device=device)
+        f[si], g[ti] = dual[:n], dual[n:]
+        solution = SparseOTSolution((n, m), si[rows][order], ti[cols][order], support.values[order], f, g)
+        torch.cuda.synchronize(device)
+        wall = time.perf_counter() - started
+        peak = torch.cuda.max_memory_allocated(device) / 2**20
+    stage = SolveStageResult(tuple(levels), wall)
+    metadata = {
+        "gpu_resident": True, "backend": "native", "device": str(device), "cost_type": problem.cost_type,
+        "cost_precision": options.cost_precision, "stopping_norm": options.stopping_norm,
+        "coarsest_solver": "mi355x_pdhg_dense", "lp_solver": "mi355x_halpern_pdhg",
+        "hierarchy_sizes": [list(s) for s in sizes],
+        "total_refinement_iterations": sum(len(l.solve.iterations) for l in levels if l.kind == "refined"),
+        "total_lp_solve_time": sum(i.solve_lp.wall_time for l in levels if l.kind == "refined"
+                                   for i in l.solve.iterations),
+        "total_scan_time": sum(i.full_scan_time for l in levels if l.kind == "refined" for i in l.solve.iterations),
+        "cost_perturbation": {"policy": options.cost_perturbation, "activated": False,
+                              "reentry_trigger_levels": triggers},
+    }
+    result = Result(objective, solution, stage, wall, peak, None, metadata, ())
+    if options.verbose != "off":
+        finest = levels[-1]
+        state = finest.solve.summary.stop_reason if finest.kind == "refined" else "coarsest"
+        print(f"[hello-mi355x] n={n} m={m} cost={problem.cost_type} objective={objective:.12g} "
+              f"time={wall:.3f}s levels={len(levels)} finest={state}", file=sys.stderr)
+    return result
+
+
+__all__ = ["solve", "solve_problem"]

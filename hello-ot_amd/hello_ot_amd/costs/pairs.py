@@ -74,8 +74,13 @@ def lowrank_csr_costs(source_feat, target_feat, source_offset, target_offset, ro
     return out
 
 
-def norm_pair_costs(query, db, rows, cols, cost_type):
+def norm_pair_costs(query, db, rows, cols, cost_type, *, precision="fp64"):
+    """fp64 norm costs (``precision="fp64"``), or the fp32 cost the norm pricing scan ranks with, widened to fp64
+    (``precision="fp32"``: 32-feature chunks accumulated in fp32, as ``costs/pairs.py:88-218`` evaluates
+    pairs for ``cost_precision="fp32"``)."""
     x, y = _features(query, db)
+    if precision not in ("fp32", "fp64"):
+        raise ValueError("precision must be fp32 or fp64")
     if cost_type not in (0, 1, 2):
         raise ValueError("unsupported norm cost")
     rows = torch.as_tensor(rows, device=x.device).to(torch.int64).contiguous().view(-1)
@@ -88,9 +93,10 @@ def norm_pair_costs(query, db, rows, cols, cost_type):
     if int(rows.min()) < 0 or int(rows.max()) >= x.shape[0] or int(cols.min()) < 0 or int(cols.max()) >= y.shape[0]:
         raise ValueError("pair index is out of bounds")
     lib = _lib.load()
+    fn = lib.hm_pair_costs_norm if precision == "fp64" else lib.hm_pair_costs_norm_fp32
     with torch.cuda.device(x.device):
-        rc = lib.hm_pair_costs_norm(_lib.stream_handle(x.device), _lib.ptr(x), _lib.ptr(y), _lib.ptr(rows),
-                                    _lib.ptr(cols), rows.numel(), x.shape[1], int(cost_type), _lib.ptr(out))
+        rc = fn(_lib.stream_handle(x.device), _lib.ptr(x), _lib.ptr(y), _lib.ptr(rows), _lib.ptr(cols), rows.numel(),
+                x.shape[1], int(cost_type), _lib.ptr(out))
     _lib.check(rc, "hm_pair_costs_norm")
     return out
 

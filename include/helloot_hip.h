@@ -115,9 +115,15 @@ int hm_pair_costs_l2sq(void* stream, const float* X, const float* Y, const doubl
                        double* out);
 
 /* fp64 l1 / linf / l2 pair costs. Replaces fused_gcost_pairs without perturbation
- * (norm_cost_scan_kernel.cu:233-275; costs/metric.py:85-159). */
+ * (norm_cost_scan_kernel.cu:233-275, costs/metric.py:85-159). */
 int hm_pair_costs_norm(void* stream, const float* X, const float* Y, const int64_t* rows,
                        const int64_t* cols, int64_t count, int32_t d, int32_t kind, double* out);
+
+/* fp32 l1 / linf / l2 pair costs, bit-identical to the cost the norm pricing scan ranks with (32-feature chunks
+ * accumulated in fp32, chunks combined in order, l2 = sqrt rounded once to fp32), widened to fp64. Replaces the
+ * reference's fp32 batched pair costs for cost_precision="fp32" (costs/pairs.py:88-218, costs/metric.py:85-159). */
+int hm_pair_costs_norm_fp32(void* stream, const float* X, const float* Y, const int64_t* rows,
+                            const int64_t* cols, int64_t count, int32_t d, int32_t kind, double* out);
 
 /* ---------------------------------------------------------------------------------------------------- */
 /* (c) Restricted-LP Halpern-PDHG                                                                          */

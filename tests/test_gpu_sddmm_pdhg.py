@@ -70,6 +70,23 @@ def test_pair_costs_l2sq_and_norms_bit_exact(cuda, d):
         np.testing.assert_array_equal(outn.cpu().numpy(), refn)
 
 
+@pytest.mark.parametrize("d", [3, 8, 33, 100])
+def test_norm_pair_costs_fp32_match_the_pricing_cost(cuda, d):
+    """fp32 pair costs equal, bit for bit, the fp32 chunked cost the norm pricing scan ranks with (the oracle's
+    cost matrix), so restricted LPs and pricing see the same c_ij."""
+    rng = np.random.default_rng(100 + d)
+    X = rng.random((30, d)).astype(np.float32)
+    Y = rng.random((45, d)).astype(np.float32)
+    rows = rng.integers(0, 30, 500)
+    cols = rng.integers(0, 45, 500)
+    tX, tY = torch.as_tensor(X).to(cuda), torch.as_tensor(Y).to(cuda)
+    for kind in (0, 1, 2):
+        _, cost = oracle.norm_matrices(X, Y, np.zeros(30), np.zeros(45), kind)
+        out = norm_pair_costs(tX, tY, torch.as_tensor(rows).to(cuda), torch.as_tensor(cols).to(cuda), kind,
+                              precision="fp32")
+        np.testing.assert_array_equal(out.cpu().numpy(), cost[rows, cols])
+
+
 def _small_problem():
     return dict(rows=np.array([0, 0, 1, 1]), cols=np.array([0, 1, 0, 1]), costs=np.array([0.0, 2.0, 1.0, 0.0]),
                 source_mass=np.array([0.4, 0.6]), target_mass=np.array([0.5, 0.5]))

@@ -1,0 +1,88 @@
+"""End-to-end HELLO solves on the MI355X path against exact LP optima (GPU only).
+
+The reference pins its solver end to end against POT's exact ``emd2`` (tests/cpp_backend_test.py:38-69,
+tests/hello_gpu_resident_test.py:73-104: objective rel 5e-5 / 1e-5, marginals 3e-6 / 4e-6); POT is absent here, so
+the exact optimum comes from scipy's HiGHS LP on the dense problem, and C1 is checked against its analytic
+Brenier plan (examples/quickstart.py:83-94)."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from hello_ot_amd import SolverOptions, solve
+
+pytestmark = pytest.mark.gpu
+
+
+def _cost_matrix(X, Y, kind):
+    if kind == "l2^2":
+        X64, Y64 = X.astype(np.float64), Y.astype(np.float64)
+        return (X64 ** 2).sum(1)[:, None] + (Y64 ** 2).sum(1)[None, :] - 2.0 * X64 @ Y64.T
+    code = {"l1": 0, "linf": 1, "l2": 2}[kind]
+    _, cost = oracle.norm_matrices(X, Y, np.zeros(len(X)), np.zeros(len(Y)), code)
+    return cost
+
+
+def _exact(C, a, b):
+    from scipy.optimize import linprog
+
+    n, m = C.shape
+    A = np.zeros((n + m, n * m))
+    for i in range(n):
+        A[i, i * m:(i + 1) * m] = 1.0
+    for j in range(m):
+        A[n + j, j::m] = 1.0
+    res = linprog(C.reshape(-1), A_eq=A, b_eq=np.concatenate((a, b)), bounds=(0, None), method="highs")
+    assert res.status == 0
+    return res.fun
+
+
+@pytest.mark.parametrize("kind,n,m,d,uniform", [
+    ("l2^2", 240, 240, 5, True),
+    ("l2^2", 130, 170, 300, False),   # d >= 256: fused-column pricing path
+    ("l1", 200, 150, 4, False),
+    ("linf", 160, 190, 3, False),
+    ("l2", 150, 150, 6, True),
+])
+def test_solve_matches_exact_lp(cuda, kind, n, m, d, uniform):
+    rng = np.random.default_rng(n + m + d)
+    X = rng.random((n, d)).astype(np.float32)
+    Y = (rng.random((m, d)) + 0.2).astype(np.float32)
+    if uniform:
+        a, b = np.full(n, 1.0 / n), np.full(m, 1.0 / m)
+    else:
+        a, b = rng.uniform(0.5, 1.5, n), rng.uniform(0.5, 1.5, m)
+        a, b = a / a.sum(), b / b.sum()
+    opts = SolverOptions(coarsest_size_threshold=40, verbose="off", cost_perturbation="off")
+    r = solve(X, Y, source_mass=a, target_mass=b, cost=kind, options=opts)
+    assert len(r.solve_stage.levels) >= 3
+    assert all(l.solve.summary.converged for l in r.solve_stage.levels if l.kind == "refined")
+    exact = _exact(_cost_matrix(X, Y, kind), a, b)
+    assert abs(r.objective - exact) <= 2e-5 * abs(exact)
+    sol = r.solution.to_cpu()
+    rows = np.bincount(sol.rows, weights=sol.values, minlength=n)
+    cols = np.bincount(sol.cols, weights=sol.values, minlength=m)
+    np.testing.assert_allclose(rows, a, atol=5e-6)
+    np.testing.assert_allclose(cols, b, atol=5e-6)
+
+
+def test_brenier_c1_recovers_the_analytic_plan(cuda):
+    """C1: x ~ N(0, I) (2048 x 32, seed 42), y = x + 2 tanh(x) rows permuted; the optimal plan is the permutation
+    (examples/quickstart.py:83-94) and the objective is mean ||x - T(x)||^2."""
+    n, dim, seed = 2048, 32, 42
+    rng = np.random.default_rng(seed)
+    source = rng.normal(size=(n, dim)).astype(np.float32)
+    mapped = source + np.float32(2.0) * np.tanh(source)
+    perm = rng.permutation(n)
+    target = mapped[perm]
+    disp = source.astype(np.float64) - mapped.astype(np.float64)
+    truth = float(np.mean(np.sum(disp * disp, axis=1)))
+    r = solve(source, target, options=SolverOptions(verbose="off"))
+    assert abs(r.objective - truth) <= 1e-6 * truth
+    sol = r.solution.to_cpu()
+    inverse = np.argsort(perm)          # target index of source i's image
+    big = sol.values > 0.5 / n
+    assert big.sum() == n
+    np.testing.assert_array_equal(sol.cols[big], inverse[sol.rows[big]])
