@@ -8,7 +8,8 @@ independent mixture; k = 2 (pricing_topk default). Inputs are resident in HBM be
 ``value`` = pairs scanned per second (chunk x 1.28M per step).
 
 Extra fields measure the other configurations: C2 (isolated 131072^2 d=64 k=8 scan), C3 (SDDMM + 1000 PDHG
-iterations, m=n=262144 d=256, 16 nnz/row) and C4 (l1 / linf scans, m=n=524288 d=8).
+iterations, m=n=262144 d=256, 16 nnz/row), C4 (l1 / linf scans, m=n=524288 d=8) and the full HELLO solve seconds
+of C1 (Brenier, 2048, d=32) and C4 (l1 and linf, 524288, d=8).
 """
 from __future__ import annotations
 
@@ -328,6 +329,56 @@ def bench_c4(dev):
     return out
 
 
+def _level_summary(result):
+    out = []
+    for level in result.solve_stage.levels:
+        if level.kind == "refined":
+            its = level.solve.iterations
+            out.append({"n": level.n_source, "m": level.n_target, "iterations": len(its),
+                        "seconds": round(level.wall_time, 3),
+                        "lp_seconds": round(sum(i.solve_lp.wall_time for i in its), 3),
+                        "scan_seconds": round(sum(i.full_scan_time for i in its), 3),
+                        "init_seconds": round(level.initialization.wall_time, 3)})
+        else:
+            out.append({"n": level.n_source, "m": level.n_target, "coarsest": True, "seconds": round(level.wall_time, 3)})
+    return out
+
+
+def bench_solves(dev):
+    """Solve seconds of the full HELLO loop: C1 (Brenier, m=n=2048, d=32, examples/quickstart.py:83-94) and C4
+    (l1 and linf, m=n=524288, d=8, U[0,1]^8 features, U(0.5,1.5) masses normalised, seed 4), tolerance 1e-6."""
+    from hello_ot_amd import SolverOptions, solve
+
+    out = {}
+    rng = np.random.default_rng(42)
+    n, dim = 2048, 32
+    src = rng.normal(size=(n, dim)).astype(np.float32)
+    mapped = src + np.float32(2.0) * np.tanh(src)
+    tgt = mapped[rng.permutation(n)]
+    truth = float(np.mean(np.sum((src.astype(np.float64) - mapped.astype(np.float64)) ** 2, axis=1)))
+    solve(src, tgt, options=SolverOptions(verbose="off"))  # warm-up (library load, first kernels)
+    r = solve(src, tgt, options=SolverOptions(verbose="off"))
+    out["c1_brenier_2048_d32"] = {"seconds": r.total_wall_time, "objective": r.objective,
+                                  "closed_form": truth, "rel_error": abs(r.objective - truth) / truth,
+                                  "levels": _level_summary(r)}
+    rng = np.random.default_rng(4)
+    m = 524288
+    X = torch.as_tensor(rng.random((m, 8)).astype(np.float32)).to(dev)
+    Y = torch.as_tensor(rng.random((m, 8)).astype(np.float32)).to(dev)
+    a, b = rng.uniform(0.5, 1.5, m), rng.uniform(0.5, 1.5, m)
+    a, b = a / a.sum(), b / b.sum()
+    for kind in ("l1", "linf"):
+        log(f"[bench] C4 solve {kind} ...")
+        r = solve(X, Y, source_mass=a, target_mass=b, cost=kind, options=SolverOptions(verbose="off"))
+        finest = r.solve_stage.levels[-1].solve.summary
+        out[f"c4_{kind}_524288_d8"] = {"seconds": r.total_wall_time, "objective": r.objective,
+                                       "converged": bool(finest.converged),
+                                       "peak_gpu_memory_mib": r.peak_gpu_memory_mib,
+                                       "refinement_iterations": r.metadata["total_refinement_iterations"],
+                                       "levels": _level_summary(r)}
+    return out
+
+
 # ----------------------------------------------------------------------------------------------------------
 
 def main():
@@ -369,6 +420,8 @@ def main():
         extras["c3_sddmm_pdhg_262144_d256"] = bench_c3(dev)
         log("[bench] C4 ...")
         extras["c4_norm_scan_524288_d8"] = bench_c4(dev)
+        log("[bench] solves (C1, C4) ...")
+        extras["solve_seconds"] = bench_solves(dev)
     cpu = None
     if not args.no_cpu_baseline:
         log("[bench] CPU baseline ...")

@@ -80,13 +80,15 @@ def solve_problem(problem: Problem, options: SolverOptions, *, max_iterations: i
         full = Cost.create(x, y, problem.cost_type)
         sizes = level_sizes(n, m, options.coarsest_size_threshold, options.split_count)
         levels, previous, triggers = [], None, []
+        coarsest_refinement = None
         support = dual = None
         for level_index in reversed(range(len(sizes))):
             nn, mm = sizes[level_index]
             cost = full.sliced(nn, mm)
             aa, bb = normalize_masses(a[:nn].clone(), b[:mm].clone())
             if previous is None:
-                support, dual, level = solve_leaf(cost, aa, bb, level_index, options.tolerance)
+                support, dual, level, coarsest_refinement = solve_leaf(cost, aa, bb, level_index, options,
+                                                                       max_iterations)
             else:
                 known = "target" if nn >= mm else "source"
                 support, dual, level, triggered = refine(cost, aa, bb, previous, known, options, level_index,
@@ -110,7 +112,8 @@ def solve_problem(problem: Problem, options: SolverOptions, *, max_iterations: i
     metadata = {
         "gpu_resident": True, "backend": "native", "device": str(device), "cost_type": problem.cost_type,
         "cost_precision": options.cost_precision, "stopping_norm": options.stopping_norm,
-        "coarsest_solver": "mi355x_pdhg_dense", "lp_solver": "mi355x_halpern_pdhg",
+        "coarsest_solver": "mi355x_refinement_from_zero_duals", "lp_solver": "mi355x_halpern_pdhg",
+        "coarsest_refinement": coarsest_refinement,
         "hierarchy_sizes": [list(s) for s in sizes],
         "total_refinement_iterations": sum(len(l.solve.iterations) for l in levels if l.kind == "refined"),
         "total_lp_solve_time": sum(i.solve_lp.wall_time for l in levels if l.kind == "refined"

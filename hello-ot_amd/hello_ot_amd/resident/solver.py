@@ -4,9 +4,7 @@ Follows the reference's GPU-resident algorithm (``gpu_resident/solver.py:27-398`
 
 * one global shuffle of each side (``hierarchy/plan.py:73-87``); level l keeps the first n_l / m_l points;
   going coarser, the larger side is divided by ``split_count`` until both are <= ``coarsest_size_threshold``;
-* coarsest level: the dense restricted LP over all pairs (the reference calls POT ``emd`` on the CPU; here the
-  HIP Halpern-PDHG solves it on the GPU to a tolerance 100x tighter than the refinement LPs; only its duals
-  seed the next level unless the coarsest level is the whole problem);
+* coarsest level: refined from zero duals like any other level (the reference calls POT ``emd`` on the CPU);
 * each finer level: the side shared with the coarser level keeps its duals, the other side is completed by a
   c-transform (directional top-1 scan), both directions contribute their ``assignment_topk`` best pairs and
   the northwest-corner basis completes an initial support; then ``solve_lp -> pricing scan with certificate ->
@@ -79,24 +77,22 @@ def _sync():
     torch.cuda.synchronize()
 
 
-def solve_leaf(cost: Cost, a, b, level_index: int, tolerance: float):
-    """Coarsest level: the dense LP over all n x m pairs."""
+def solve_leaf(cost: Cost, a, b, level_index: int, options, max_iterations: int):
+    """Coarsest level. The reference solves it exactly with POT ``emd`` on the CPU (gpu_resident/solver.py:168-191);
+    here it is refined like every other level, from zero duals: both directions' ``assignment_topk`` nearest
+    pairs plus the northwest basis, then LP / pricing / support updates until the certificate passes. The
+    result is optimal to the same tolerance as the finer levels and stays on the device."""
     started = time.perf_counter()
     n, m = cost.shape
-    device = a.device
-    rows = torch.arange(n, device=device).repeat_interleave(m)
-    cols = torch.arange(m, device=device).repeat(n)
-    support = Support(rows * m + cols, torch.zeros(n * m, dtype=torch.float64, device=device),
-                      torch.zeros(n * m, dtype=torch.bool, device=device), n, m)
-    dual = torch.zeros(n + m, dtype=torch.float64, device=device)
-    dual, lp = support.solve_lp(cost, a, b, dual, min(1e-8, 0.01 * tolerance))
-    keep = support.values > 1e-12
-    support = Support(support.keys[keep], support.values[keep], torch.zeros(int(keep.sum()), dtype=torch.bool,
-                                                                             device=device), n, m)
+    zeros = torch.zeros(n + m, dtype=torch.float64, device=a.device)
+    support, dual, level, _ = refine(cost, a, b, zeros, None, options, level_index, max_iterations, False)
+    summary = level.solve.summary
+    if not summary.converged:
+        raise HelloSolveError(f"coarsest level did not converge in {max_iterations} iterations")
     _sync()
     elapsed = time.perf_counter() - started
-    return support, dual, LevelResult(level_index, "coarsest", n, m, None,
-                                      CoarsestSolveStats(elapsed, float(lp.obj_val), len(support.keys)), elapsed)
+    stats = CoarsestSolveStats(elapsed, float(summary.final_objective), len(support.keys))
+    return support, dual, LevelResult(level_index, "coarsest", n, m, level.initialization, stats, elapsed), level
 
 
 def initialize(cost: Cost, a, b, previous, known_side, options):
