@@ -22,6 +22,7 @@ int fail(int code, const char* fmt, ...);
 bool profiling();
 void prof_begin(hipStream_t st, const char* name);
 void prof_end(hipStream_t st);
+void prof_count(const char* name, int64_t count);  // adds to a name's count (queued rescans, ...)
 
 #define HM_CHECK_ARG(cond, ...)                                  \
     do {                                                         \

@@ -40,6 +40,7 @@ struct DirPlan {
 namespace {
 
 typedef float v16f __attribute__((ext_vector_type(16)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
 constexpr int BX = 128;            // X rows per workgroup (4 waves x 32)
 constexpr int NB = 4;              // 32-wide Y blocks per wave
@@ -48,10 +49,13 @@ constexpr int KC = 32;             // features per LDS chunk
 constexpr int STR = KC + 4;        // LDS row stride (floats)
 constexpr int CST = BX + 1;        // LDS row stride of the column-score tile (floats)
 constexpr int FLUSH_CHUNKS = 8;    // fp32 block length 256 features before folding into the outer sum
+constexpr int FLUSH_SPLIT = 4;     // split-bf16 block length 128 features (3 product terms per feature)
 constexpr int64_t CHUNK_MAX = 65536;          // X rows per internal chunk
 constexpr int FUSE_MIN_D = 256;               // columns ride on the row sweep from this d on (below it the
                                               // per-tile column epilogue outweighs the MFMA work: two sweeps)
 constexpr int64_t SWEEP_WGS = 1024;           // target workgroups per sweep launch (sets the Y segments)
+constexpr int64_t RESCAN_SLICE = 512;         // candidates per exact-rescan item (one wave)
+constexpr int64_t RESCAN_ITEMS = 65536;       // (row, slice) items whose partial lists fit the rescan scratch
 constexpr size_t COLPART_CAP = size_t(12) << 30;  // bytes of per-chunk column partial lists
 
 // fp32 unit roundoff doubled (covers truncating accumulation) and the classic gamma_n bound.
@@ -130,11 +134,53 @@ inline unsigned prep_grid(int64_t rows) {
 }
 
 // -------------------------------------------------------------------------------------------------
+// split-bf16 copy: x = hi + lo + e with hi = bf16(x), lo = bf16(x - hi) (round to nearest even), |e| <= 2^-16|x|.
+// Row r of the copy holds ld = roundup(d, 32) features as ld / 8 groups of 32 bytes: 8 hi, then 8 lo values;
+// padding features are zero.
+// -------------------------------------------------------------------------------------------------
+__device__ inline unsigned short bf16_rne(float x) {
+    const unsigned int u = __float_as_uint(x);
+    return (unsigned short)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+}
+
+__global__ void l2sq_split_bf16(const float* __restrict__ X, int64_t rows, int d, int ld,
+                                unsigned short* __restrict__ out) {
+    const int64_t groups = rows * (ld / 8);
+    for (int64_t gidx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; gidx < groups;
+         gidx += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t row = gidx / (ld / 8);
+        const int k0 = (int)(gidx % (ld / 8)) * 8;
+        unsigned short hi[8], lo[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const float x = (k0 + e < d) ? X[row * d + k0 + e] : 0.0f;
+            hi[e] = bf16_rne(x);
+            lo[e] = bf16_rne(x - __uint_as_float((unsigned int)hi[e] << 16));
+        }
+        uint4 a, b;
+        a.x = hi[0] | ((unsigned int)hi[1] << 16);
+        a.y = hi[2] | ((unsigned int)hi[3] << 16);
+        a.z = hi[4] | ((unsigned int)hi[5] << 16);
+        a.w = hi[6] | ((unsigned int)hi[7] << 16);
+        b.x = lo[0] | ((unsigned int)lo[1] << 16);
+        b.y = lo[2] | ((unsigned int)lo[3] << 16);
+        b.z = lo[4] | ((unsigned int)lo[5] << 16);
+        b.w = lo[6] | ((unsigned int)lo[7] << 16);
+        uint4* dst = reinterpret_cast<uint4*>(out + row * (int64_t)ld * 2 + (int64_t)k0 * 2);
+        dst[0] = a;
+        dst[1] = b;
+    }
+}
+
+// -------------------------------------------------------------------------------------------------
 // sweep over X rows [xb, xe) of one chunk
 // -------------------------------------------------------------------------------------------------
-template <int K1, bool TWO_LEVEL, bool COLS>
+// PREC 0: X / Y are the fp32 features (row stride ld = d), products on v_mfma_f32_32x32x2f32.
+// PREC 1: X / Y are their split-bf16 copies (l2sq_split_bf16: row stride ld = d padded to 32, groups of 8 hi
+//         then 8 lo bf16 per 32 bytes); dot = hi*hi + hi*lo + lo*hi on v_mfma_f32_32x32x16_bf16.
+template <int K1, bool TWO_LEVEL, bool COLS, int PREC>
 __global__ __launch_bounds__(256) void l2sq_sweep(
-    const float* __restrict__ X, const float* __restrict__ Y, int64_t xb, int64_t xe, int64_t n, int d,
+    const float* __restrict__ X, const float* __restrict__ Y, int64_t xb, int64_t xe, int64_t n, int d, int ld,
     const float* __restrict__ qb32, const float* __restrict__ db32, const float* __restrict__ p32,
     const float* __restrict__ ge32, float scale, int64_t seg_len, Entry* __restrict__ part,
     Entry* __restrict__ colpart, unsigned int* __restrict__ colthr, double* __restrict__ blockstats, int VEC4,
@@ -182,14 +228,14 @@ __global__ __launch_bounds__(256) void l2sq_sweep(
             const int k = k0 + 4 * c4;
             const int64_t xr = x0 + row, yr = ytile + row;
             if (VEC4) {
-                gx[i] = (xr < xe && k < d) ? *reinterpret_cast<const float4*>(X + xr * d + k) : make_float4(0, 0, 0, 0);
-                gy[i] = (yr < y_end && k < d) ? *reinterpret_cast<const float4*>(Y + yr * d + k) : make_float4(0, 0, 0, 0);
+                gx[i] = (xr < xe && k < d) ? *reinterpret_cast<const float4*>(X + xr * ld + k) : make_float4(0, 0, 0, 0);
+                gy[i] = (yr < y_end && k < d) ? *reinterpret_cast<const float4*>(Y + yr * ld + k) : make_float4(0, 0, 0, 0);
             } else {
                 float a[4], b[4];
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    a[e] = (xr < xe && k + e < d) ? X[xr * d + k + e] : 0.0f;
-                    b[e] = (yr < y_end && k + e < d) ? Y[yr * d + k + e] : 0.0f;
+                    a[e] = (xr < xe && k + e < d) ? X[xr * ld + k + e] : 0.0f;
+                    b[e] = (yr < y_end && k + e < d) ? Y[yr * ld + k + e] : 0.0f;
                 }
                 gx[i] = make_float4(a[0], a[1], a[2], a[3]);
                 gy[i] = make_float4(b[0], b[1], b[2], b[3]);
@@ -225,10 +271,31 @@ __global__ __launch_bounds__(256) void l2sq_sweep(
         __syncthreads();
         for (int c = 0; c < nchunks; ++c) {
             if (c + 1 < nchunks) load_chunk(c + 1, ytile);
+            if (PREC == 1) {
+                // two K-steps of 16 features; lane (h, r) supplies group 2s + h (8 features: hi, then lo)
+#pragma unroll
+                for (int s2 = 0; s2 < 2; ++s2) {
+                    const int gw = (2 * s2 + h) * 8;
+                    const bf16x8 bh = *reinterpret_cast<const bf16x8*>(&sX[(wave * 32 + r) * STR + gw]);
+                    const bf16x8 bl = *reinterpret_cast<const bf16x8*>(&sX[(wave * 32 + r) * STR + gw + 4]);
+                    bf16x8 ah[NB], al[NB];
+#pragma unroll
+                    for (int b = 0; b < NB; ++b) {
+                        ah[b] = *reinterpret_cast<const bf16x8*>(&sY[(b * 32 + r) * STR + gw]);
+                        al[b] = *reinterpret_cast<const bf16x8*>(&sY[(b * 32 + r) * STR + gw + 4]);
+                    }
+#pragma unroll
+                    for (int b = 0; b < NB; ++b) acc[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah[b], bh, acc[b], 0, 0, 0);
+#pragma unroll
+                    for (int b = 0; b < NB; ++b) acc[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah[b], bl, acc[b], 0, 0, 0);
+#pragma unroll
+                    for (int b = 0; b < NB; ++b) acc[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al[b], bh, acc[b], 0, 0, 0);
+                }
+            }
             // B operand: this lane's X row, features h*16 .. h*16+15 of the chunk
             const float* bx = &sX[(wave * 32 + r) * STR + h * 16];
 #pragma unroll
-            for (int g = 0; g < 4; ++g) {
+            for (int g = 0; g < (PREC == 0 ? 4 : 0); ++g) {
                 const float4 bv = *reinterpret_cast<const float4*>(bx + 4 * g);
                 float4 av[NB];
 #pragma unroll
@@ -242,7 +309,7 @@ __global__ __launch_bounds__(256) void l2sq_sweep(
                     acc[b] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[b].w, bv.w, acc[b], 0, 0, 0);
                 }
             }
-            if (TWO_LEVEL && ((c + 1) % FLUSH_CHUNKS == 0)) {
+            if (TWO_LEVEL && ((c + 1) % (PREC == 1 ? FLUSH_SPLIT : FLUSH_CHUNKS) == 0)) {
 #pragma unroll
                 for (int b = 0; b < NB; ++b) {
 #pragma unroll
@@ -496,13 +563,21 @@ __global__ __launch_bounds__(256) void l2sq_finalize(
         }
         return;
     }
-    // exact re-evaluation of the kept entries; lane e owns kept entry e
+    // Exact re-evaluation of the kept entries that can reach the exact top-k: an entry with w < wk - 2b has an
+    // exact score below wk - b, under each of the k entries with w >= wk, so only the sorted prefix with
+    // w >= wk - 2b is evaluated (always at least the first min(k, kept)). Lane e owns entry e.
+    const double cut = (double)wk - 2.0 * b;
+    int need = 0;
+#pragma unroll
+    for (int e = 0; e < K1; ++e)
+        if (e < kept && (double)tw[e] >= cut) need = e + 1;
+    if (need < (kept < k ? kept : k)) need = kept < k ? kept : k;
     double sv = -INFINITY;
     int sj = -1;
     const float* ar = A + row * (int64_t)d;
 #pragma unroll
     for (int e = 0; e < K1; ++e) {
-        if (e < kept) {
+        if (e < need) {
             const int c = ti[e];
             const double dot = wave_dot64(ar, B + (int64_t)c * d, d, lane);
             const double sdot = scale * dot;
@@ -511,69 +586,101 @@ __global__ __launch_bounds__(256) void l2sq_finalize(
         }
     }
     int er = 0;
-    for (int src = 0; src < kept; ++src) {
+    for (int src = 0; src < need; ++src) {
         const double v2 = __shfl(sv, src, 64);
         const int j2 = __shfl(sj, src, 64);
-        if (lane < kept && src != lane && better(v2, j2, sv, sj)) ++er;
+        if (lane < need && src != lane && better(v2, j2, sv, sj)) ++er;
     }
-    if (lane < kept && er < k) {
+    if (lane < need && er < k) {
         out_val[row * k + er] = sv;
         out_idx[row * k + er] = sj;
     }
-    if (lane >= kept && lane < k) {
+    if (lane >= need && lane < k) {
         out_val[row * k + lane] = -INFINITY;
         out_idx[row * k + lane] = -1;
     }
 }
 
-// -------------------------------------------------------------------------------------------------
-// exact rescan of queued rows: one wave per row; each lane scores one candidate per step with the register
-// form of dot64, and the wave inserts the few winners into one replicated list (ballot loop). Candidates
-// are B rows [0, nb); reported indices are cbase + local index.
-// -------------------------------------------------------------------------------------------------
+// Sliced exact rescan: item (queued row, candidate slice) is one wave. Candidates are evaluated four at a time
+// (four independent accumulators share each load of the row's features); every candidate's dot keeps the dot64
+// order (lane l sums features l, l+64, ... in order, then the halving-stride tree), so all lanes hold the same
+// exact list. Lists go to pv / pi per item.
 template <int K>
-__global__ __launch_bounds__(64) void l2sq_rescan(const float* __restrict__ A, const float* __restrict__ B,
-                                                  int64_t nb, int d, const double* __restrict__ abias,
-                                                  const double* __restrict__ bbias, double scale, int k,
-                                                  const int* __restrict__ redo, const int* __restrict__ redo_count,
-                                                  double* __restrict__ out_val, int* __restrict__ out_idx,
-                                                  int COLS, int cbase) {
-    const int lane = threadIdx.x;
-    const int count = *redo_count;
-    for (int slot = blockIdx.x; slot < count; slot += gridDim.x) {
-        const int64_t row = redo[slot];
+__global__ __launch_bounds__(256) void l2sq_rescan_slices(const float* __restrict__ A, const float* __restrict__ B,
+                                                          int64_t nb, int d, const double* __restrict__ abias,
+                                                          const double* __restrict__ bbias, double scale, int k,
+                                                          const int* __restrict__ redo, int r0, int nrows, int slices,
+                                                          int64_t per, int COLS, int cbase, double* __restrict__ pv,
+                                                          int* __restrict__ pi) {
+    const int lane = threadIdx.x & 63;
+    const int64_t items = (int64_t)nrows * slices;
+    for (int64_t item = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); item < items; item += (int64_t)gridDim.x * 4) {
+        const int64_t row = redo[r0 + item / slices];
+        const int64_t j0 = (item % slices) * per;
+        const int64_t j1 = j0 + per < nb ? j0 + per : nb;
         const float* ar = A + row * (int64_t)d;
         double v[K];
         int id[K];
 #pragma unroll
         for (int s = 0; s < K; ++s) { v[s] = -INFINITY; id[s] = -1; }
-        for (int64_t j0 = 0; j0 < nb; j0 += 64) {
-            const int64_t j = j0 + lane;
-            double sig = -INFINITY;
-            if (j < nb) {
-                const double sdot = scale * lane_dot64(ar, B + j * d, d);
-                sig = COLS ? (sdot + bbias[j]) + abias[row] : (sdot + abias[row]) + bbias[j];
+        for (int64_t j = j0; j < j1; j += 4) {
+            const float* b0 = B + j * d;
+            const bool ok1 = j + 1 < j1, ok2 = j + 2 < j1, ok3 = j + 3 < j1;
+            const float* b1 = ok1 ? b0 + d : b0;
+            const float* b2 = ok2 ? b0 + 2 * (int64_t)d : b0;
+            const float* b3 = ok3 ? b0 + 3 * (int64_t)d : b0;
+            double a0 = 0.0, a1 = 0.0, a2 = 0.0, a3 = 0.0;
+#pragma unroll 4
+            for (int f = lane; f < d; f += 64) {
+                const double x = (double)ar[f];
+                a0 = a0 + x * (double)b0[f];
+                a1 = a1 + x * (double)b1[f];
+                a2 = a2 + x * (double)b2[f];
+                a3 = a3 + x * (double)b3[f];
             }
-            const bool cand = j < nb && sig == sig && better(sig, (int)(cbase + j), v[k - 1], id[k - 1]);
-            unsigned long long mask = __ballot(cand);
-            while (mask) {
-                const int src = __ffsll((long long)mask) - 1;
-                mask &= mask - 1;
-                const double svv = __shfl(sig, src, 64);
-                const int sjv = (int)(cbase + j0 + src);
-                put_sorted<K>(v, id, k, svv, sjv);
+            const double dots[4] = {wave_tree_sum(a0), wave_tree_sum(a1), wave_tree_sum(a2), wave_tree_sum(a3)};
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                if (j + t < j1) {
+                    const double sdot = scale * dots[t];
+                    const double sig = COLS ? (sdot + bbias[j + t]) + abias[row] : (sdot + abias[row]) + bbias[j + t];
+                    if (sig == sig) put_sorted<K>(v, id, k, sig, (int)(cbase + j + t));
+                }
             }
         }
-        if (lane < k) {
-            double ov = -INFINITY;
-            int oi = -1;
+        if (lane == 0) {
+            for (int s = 0; s < k; ++s) {
+                double ov = -INFINITY;
+                int oi = -1;
 #pragma unroll
-            for (int s = 0; s < K; ++s)
-                if (s == lane) { ov = v[s]; oi = id[s]; }
-            out_val[row * k + lane] = ov;
-            out_idx[row * k + lane] = oi;
+                for (int t = 0; t < K; ++t)
+                    if (t == s) { ov = v[t]; oi = id[t]; }
+                pv[item * k + s] = ov;
+                pi[item * k + s] = oi;
+            }
         }
     }
+}
+
+template <int K>
+__global__ void l2sq_rescan_merge(const double* __restrict__ pv, const int* __restrict__ pi, int nrows, int slices,
+                                  int k, const int* __restrict__ redo, int r0, double* __restrict__ out_val,
+                                  int* __restrict__ out_idx) {
+    const int t = blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= nrows) return;
+    double v[K];
+    int id[K];
+#pragma unroll
+    for (int s = 0; s < K; ++s) { v[s] = -INFINITY; id[s] = -1; }
+    for (int sl = 0; sl < slices; ++sl) {
+        const int64_t base = ((int64_t)t * slices + sl) * k;
+        for (int s = 0; s < k; ++s)
+            if (pi[base + s] >= 0) put_sorted<K>(v, id, k, pv[base + s], pi[base + s]);
+    }
+    const int64_t row = redo[r0 + t];
+#pragma unroll
+    for (int s = 0; s < K; ++s)
+        if (s < k) { out_val[row * k + s] = v[s]; out_idx[row * k + s] = id[s]; }
 }
 
 // merge a chunk's exact column lists into the running ones (both sorted by the tie rule)
@@ -668,7 +775,8 @@ inline DirPlan plan_dir(int64_t rows, int64_t cols) {
 template <class A>
 void layout(A& a, int64_t m, int64_t n, int d, int k, uint32_t flags, double** xnorm, double** ynorm, float** qb32,
             float** p32, float** db32, float** ge32, unsigned long long** maxima, Entry** part, Entry** colpart,
-            unsigned int** colthr, double** cval, int** cidx, double** blockstats, int** redo, int** redo_count) {
+            unsigned int** colthr, double** cval, int** cidx, double** blockstats, int** redo, int** redo_count,
+            float** xsplit, float** ysplit, double** rpv, int** rpi) {
     const int K1 = bucket_k1(k);
     const bool fused = fused_columns(d, flags);
     const int64_t ch = chunk_rows(m, n, k, fused);
@@ -695,6 +803,50 @@ void layout(A& a, int64_t m, int64_t n, int d, int k, uint32_t flags, double** x
     *blockstats = a.template take<double>((size_t)5 * panels * plan.S);
     *redo = a.template take<int>((size_t)(m + n));
     *redo_count = a.template take<int>(2);
+    const bool split = (flags & HM_BF16X3) != 0;
+    const size_t ldw = (size_t)(d + KC - 1) / KC * KC;
+    *xsplit = a.template take<float>(split ? (size_t)m * ldw : 1);
+    *ysplit = a.template take<float>(split ? (size_t)n * ldw : 1);
+    *rpv = a.template take<double>((size_t)RESCAN_ITEMS * k);
+    *rpi = a.template take<int>((size_t)RESCAN_ITEMS * k);
+}
+
+// Exact rescan of the rows queued by a finalize: reads the queue length back (one host synchronisation), then
+// splits every queued row's candidates into slices scanned by separate waves and merges the slice lists.
+inline int rescan_exact(hipStream_t st, const float* A, const float* B, int64_t nb, int d, const double* abias,
+                        const double* bbias, double scale, int k, const int* redo, const int* redo_count,
+                        double* out_val, int* out_idx, int cols, int cbase, double* pv, int* pi) {
+    int count = 0;
+    HM_HIP(hipMemcpyAsync(&count, redo_count, sizeof(int), hipMemcpyDeviceToHost, st));
+    HM_HIP(hipStreamSynchronize(st));
+    prof_count(cols ? "l2sq_rescan_columns" : "l2sq_rescan_rows", count);
+    if (count <= 0) return HM_OK;
+    int64_t slices = (nb + RESCAN_SLICE - 1) / RESCAN_SLICE;
+    if (slices > 1024) slices = 1024;
+    if (slices < 1) slices = 1;
+    const int64_t per = (nb + slices - 1) / slices;
+    const int64_t batch = RESCAN_ITEMS / slices > 0 ? RESCAN_ITEMS / slices : 1;
+    prof_begin(st, "l2sq_rescan");
+    for (int64_t r0 = 0; r0 < count; r0 += batch) {
+        const int nrows = (int)(count - r0 < batch ? count - r0 : batch);
+        const int64_t items = (int64_t)nrows * slices;
+        const unsigned grid = (unsigned)((items + 3) / 4 < 4096 ? (items + 3) / 4 : 4096);
+        const unsigned mgrid = (unsigned)((nrows + 255) / 256);
+#define HM_RESCAN(KK)                                                                                               \
+    do {                                                                                                            \
+        hipLaunchKernelGGL((l2sq_rescan_slices<KK>), dim3(grid), dim3(256), 0, st, A, B, nb, d, abias, bbias, scale, \
+                           k, redo, (int)r0, nrows, (int)slices, per, cols, cbase, pv, pi);                        \
+        hipLaunchKernelGGL((l2sq_rescan_merge<KK>), dim3(mgrid), dim3(256), 0, st, pv, pi, nrows, (int)slices, k,    \
+                           redo, (int)r0, out_val, out_idx);                                                       \
+    } while (0)
+        if (k <= 2) HM_RESCAN(2);
+        else if (k <= 8) HM_RESCAN(8);
+        else HM_RESCAN(32);
+#undef HM_RESCAN
+        HM_LAUNCH_CHECK("l2sq_rescan");
+    }
+    prof_end(st);
+    return HM_OK;
 }
 
 template <int K1>
@@ -703,23 +855,39 @@ int run_bidir(hipStream_t st, const float* X, const float* Y, int64_t m, int64_t
               const unsigned long long* maxima, const float* qb32, const float* db32, const float* p32,
               const float* ge32, Entry* part, Entry* colpart, unsigned int* colthr, double* cval, int* cidx,
               double* blockstats, int* redo, int* redo_count, double* row_val, int* row_idx, double* col_val,
-              int* col_idx, double* stats) {
+              int* col_idx, double* stats, float* xsplit, float* ysplit, double* rpv, int* rpi) {
     const bool want_rows = (flags & HM_ROWS) != 0;
     const bool fused = fused_columns(d, flags);
     const bool swapped = (flags & HM_COLS) && !fused;
     const bool want_stats = (flags & HM_STATS) != 0;
     const int linf = (flags & HM_LINF) ? 1 : 0;
-    const bool two_level = d > KC * FLUSH_CHUNKS;
-    const bool vec4 = (d % 4) == 0;
+    const bool split = (flags & HM_BF16X3) != 0;
+    const int flush = KC * (split ? FLUSH_SPLIT : FLUSH_CHUNKS);
+    const bool two_level = d > flush;
+    const bool vec4 = split || (d % 4) == 0;
+    const int ld = split ? (d + KC - 1) / KC * KC : d;  // sweep row stride and length in 4-byte words
+    const float* SX = split ? xsplit : X;
+    const float* SY = split ? ysplit : Y;
     const int64_t ch = chunk_rows(m, n, k, fused);
     const DirPlan plan = plan_dir(ch, n);
-    // rigorous bound constants
-    const double kb = two_level ? (double)(KC * FLUSH_CHUNKS) : (double)d;
-    const double nblk = two_level ? std::ceil((double)d / (KC * FLUSH_CHUNKS)) : 1.0;
-    const double ea = gamma_fp32(kb) + gamma_fp32(nblk) + gamma_fp32(kb) * gamma_fp32(nblk);
+    if (split) {
+        hipLaunchKernelGGL(l2sq_split_bf16, dim3(4096), dim3(256), 0, st, X, m, d, ld, reinterpret_cast<unsigned short*>(xsplit));
+        HM_LAUNCH_CHECK("l2sq_split_bf16");
+        hipLaunchKernelGGL(l2sq_split_bf16, dim3(4096), dim3(256), 0, st, Y, n, d, ld, reinterpret_cast<unsigned short*>(ysplit));
+        HM_LAUNCH_CHECK("l2sq_split_bf16");
+    }
+    // Rigorous bound on |w - exact| in units of scale*||x||*||y||: accumulation of B-feature blocks in fp32
+    // (gamma over the additions of a block, then over the blocks), plus for the split products the dropped
+    // terms lo*lo + hi*e + e*hi + ... <= (3 * 2^-16 * (1 + 2^-7) + 3 * 2^-24) |x_k y_k|.
+    const double fb = two_level ? (double)flush : (double)d;
+    const double nblk = two_level ? std::ceil((double)d / flush) : 1.0;
+    const double terms = split ? 3.0 * fb * (1.0 + 1.0 / 8.0) : fb;
+    const double ea = gamma_fp32(terms) + gamma_fp32(nblk) + gamma_fp32(terms) * gamma_fp32(nblk);
+    const double split_rel = split ? 3.0 * std::ldexp(1.0, -16) * (1.0 + std::ldexp(1.0, -7)) + 3.0 * std::ldexp(1.0, -24)
+                                   : 0.0;
     const double u = std::ldexp(1.0, -24);
     BoundArgs bnd;
-    bnd.acc_rel = ea + u * (1.0 + ea) + 4e-15 * (d / 64.0 + 8.0);
+    bnd.acc_rel = split_rel + ea * (split ? 1.01 : 1.0) + u * (1.0 + ea + split_rel) + 4e-15 * (d / 64.0 + 8.0);
     bnd.db_rel = 2.0 * u + 1e-15;
     bnd.abs_slack = 1e-30 * (double)d;
     int chunk_index = 0;
@@ -736,9 +904,17 @@ int run_bidir(hipStream_t st, const float* X, const float* Y, int64_t m, int64_t
                                st, colthr, n, neg_inf_key);
             HM_LAUNCH_CHECK("fill_u32");
         }
-#define HM_SWEEP(TL, CL)                                                                                            \
-    hipLaunchKernelGGL((l2sq_sweep<K1, TL, CL>), grid, dim3(256), 0, st, X, Y, xb, xe, n, d, qb32, db32, p32, ge32, \
-                       (float)scale, plan.seg_len, part, colpart, colthr, blockstats, (int)vec4, (int)want_stats)
+#define HM_SWEEP(TL, CL)                                                                                             \
+    do {                                                                                                             \
+        if (split)                                                                                                   \
+            hipLaunchKernelGGL((l2sq_sweep<K1, TL, CL, 1>), grid, dim3(256), 0, st, SX, SY, xb, xe, n, ld, ld, qb32, \
+                               db32, p32, ge32, (float)scale, plan.seg_len, part, colpart, colthr, blockstats, 1,     \
+                               (int)want_stats);                                                                     \
+        else                                                                                                         \
+            hipLaunchKernelGGL((l2sq_sweep<K1, TL, CL, 0>), grid, dim3(256), 0, st, X, Y, xb, xe, n, d, d, qb32,     \
+                               db32, p32, ge32, (float)scale, plan.seg_len, part, colpart, colthr, blockstats,        \
+                               (int)vec4, (int)want_stats);                                                          \
+    } while (0)
         prof_begin(st, "l2sq_sweep");
         if (two_level) {
             if (fused) HM_SWEEP(true, true);
@@ -755,7 +931,6 @@ int run_bidir(hipStream_t st, const float* X, const float* Y, int64_t m, int64_t
                                stats, linf, chunk_index > 0 ? 1 : 0);
             HM_LAUNCH_CHECK("l2sq_reduce_stats");
         }
-        const unsigned rescan_blocks_rows = (unsigned)(rows < 1024 ? rows : 1024);
         if (want_rows) {
             // row finalize: lists (seg, half) of each chunk row; candidates are Y rows
             hipLaunchKernelGGL(zero_words, dim3(1), dim3(64), 0, st, reinterpret_cast<unsigned long long*>(redo_count), 1);
@@ -765,16 +940,9 @@ int run_bidir(hipStream_t st, const float* X, const float* Y, int64_t m, int64_t
                                bnd, row_val + xb * k, row_idx + xb * k, redo, redo_count);
             prof_end(st);
             HM_LAUNCH_CHECK("l2sq_finalize");
-            prof_begin(st, "l2sq_rescan");
-#define HM_RESCAN(KK)                                                                                                  \
-    hipLaunchKernelGGL((l2sq_rescan<KK>), dim3(rescan_blocks_rows), dim3(64), 0, st, X + xb * d, Y, n, d, qb + xb, db, \
-                       scale, k, redo, redo_count, row_val + xb * k, row_idx + xb * k, 0, 0)
-            if (k <= 2) HM_RESCAN(2);
-            else if (k <= 8) HM_RESCAN(8);
-            else HM_RESCAN(32);
-#undef HM_RESCAN
-            prof_end(st);
-            HM_LAUNCH_CHECK("l2sq_rescan");
+            if (int rc = rescan_exact(st, X + xb * d, Y, n, d, qb + xb, db, scale, k, redo, redo_count, row_val + xb * k,
+                                      row_idx + xb * k, 0, 0, rpv, rpi))
+                return rc;
         }
         if (fused) {
             // column finalize: one list per X panel of this chunk; candidates are the chunk's X rows (global ids)
@@ -785,17 +953,9 @@ int run_bidir(hipStream_t st, const float* X, const float* Y, int64_t m, int64_t
                                redo_count);
             prof_end(st);
             HM_LAUNCH_CHECK("l2sq_col_finalize");
-            const unsigned rescan_blocks_cols = (unsigned)(n < 1024 ? n : 1024);
-            prof_begin(st, "l2sq_rescan");
-#define HM_RESCAN(KK)                                                                                                \
-    hipLaunchKernelGGL((l2sq_rescan<KK>), dim3(rescan_blocks_cols), dim3(64), 0, st, Y, X + xb * d, rows, d, db,     \
-                       qb + xb, scale, k, redo, redo_count, cval, cidx, 1, (int)xb)
-            if (k <= 2) HM_RESCAN(2);
-            else if (k <= 8) HM_RESCAN(8);
-            else HM_RESCAN(32);
-#undef HM_RESCAN
-            prof_end(st);
-            HM_LAUNCH_CHECK("l2sq_rescan");
+            if (int rc = rescan_exact(st, Y, X + xb * d, rows, d, db, qb + xb, scale, k, redo, redo_count, cval, cidx, 1,
+                                      (int)xb, rpv, rpi))
+                return rc;
             hipLaunchKernelGGL(l2sq_merge_columns, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, col_val, col_idx,
                                cval, cidx, n, k, chunk_index == 0 ? 1 : 0);
             HM_LAUNCH_CHECK("l2sq_merge_columns");
@@ -810,9 +970,17 @@ int run_bidir(hipStream_t st, const float* X, const float* Y, int64_t m, int64_t
             const int64_t ye = yb + ch2 < n ? yb + ch2 : n;
             const int64_t rows = ye - yb;
             dim3 grid((unsigned)((rows + BX - 1) / BX), (unsigned)plan2.S);
-#define HM_SWEEP2(TL)                                                                                               \
-    hipLaunchKernelGGL((l2sq_sweep<K1, TL, false>), grid, dim3(256), 0, st, Y, X, yb, ye, m, d, db32, qb32, ge32,   \
-                       p32, (float)scale, plan2.seg_len, part, colpart, colthr, blockstats, (int)vec4, 0)
+#define HM_SWEEP2(TL)                                                                                                \
+    do {                                                                                                             \
+        if (split)                                                                                                   \
+            hipLaunchKernelGGL((l2sq_sweep<K1, TL, false, 1>), grid, dim3(256), 0, st, SY, SX, yb, ye, m, ld, ld,    \
+                               db32, qb32, ge32, p32, (float)scale, plan2.seg_len, part, colpart, colthr, blockstats, \
+                               1, 0);                                                                                \
+        else                                                                                                         \
+            hipLaunchKernelGGL((l2sq_sweep<K1, TL, false, 0>), grid, dim3(256), 0, st, Y, X, yb, ye, m, d, d, db32,  \
+                               qb32, ge32, p32, (float)scale, plan2.seg_len, part, colpart, colthr, blockstats,      \
+                               (int)vec4, 0);                                                                        \
+    } while (0)
             prof_begin(st, "l2sq_sweep");
             if (two_level) HM_SWEEP2(true);
             else HM_SWEEP2(false);
@@ -826,17 +994,9 @@ int run_bidir(hipStream_t st, const float* X, const float* Y, int64_t m, int64_t
                                bnd, col_val + yb * k, col_idx + yb * k, redo, redo_count);
             prof_end(st);
             HM_LAUNCH_CHECK("l2sq_col_finalize");
-            const unsigned rescan_blocks = (unsigned)(rows < 1024 ? rows : 1024);
-            prof_begin(st, "l2sq_rescan");
-#define HM_RESCAN(KK)                                                                                               \
-    hipLaunchKernelGGL((l2sq_rescan<KK>), dim3(rescan_blocks), dim3(64), 0, st, Y + yb * d, X, m, d, db + yb, qb,   \
-                       scale, k, redo, redo_count, col_val + yb * k, col_idx + yb * k, 1, 0)
-            if (k <= 2) HM_RESCAN(2);
-            else if (k <= 8) HM_RESCAN(8);
-            else HM_RESCAN(32);
-#undef HM_RESCAN
-            prof_end(st);
-            HM_LAUNCH_CHECK("l2sq_rescan");
+            if (int rc = rescan_exact(st, Y + yb * d, X, m, d, db + yb, qb, scale, k, redo, redo_count, col_val + yb * k,
+                                      col_idx + yb * k, 1, 0, rpv, rpi))
+                return rc;
         }
     }
     if (want_stats && want_rows) {
@@ -855,7 +1015,8 @@ int run_bidir(hipStream_t st, const float* X, const float* Y, int64_t m, int64_t
         const double *qb, const double *db, const double *xnorm, const double *ynorm,                              \
         const unsigned long long *maxima, const float *qb32, const float *db32, const float *p32, const float *ge32, \
         ::hm::Entry *part, ::hm::Entry *colpart, unsigned int *colthr, double *cval, int *cidx, double *blockstats, \
-        int *redo, int *redo_count, double *row_val, int *row_idx, double *col_val, int *col_idx, double *stats
+        int *redo, int *redo_count, double *row_val, int *row_idx, double *col_val, int *col_idx, double *stats,   \
+        float *xsplit, float *ysplit, double *rpv, int *rpi
 #define L2SQ_RUN_PASS                                                                                               \
     st, X, Y, m, n, d, k, scale, flags, qb, db, xnorm, ynorm, maxima, qb32, db32, p32, ge32, part, colpart, colthr, \
-        cval, cidx, blockstats, redo, redo_count, row_val, row_idx, col_val, col_idx, stats
+        cval, cidx, blockstats, redo, redo_count, row_val, row_idx, col_val, col_idx, stats, xsplit, ysplit, rpv, rpi

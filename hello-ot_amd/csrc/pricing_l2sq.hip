@@ -31,7 +31,11 @@ extern "C" size_t hm_pricing_l2sq_workspace_bytes(int64_t m, int64_t n, int32_t 
     Entry *part, *colpart;
     unsigned int* thr;
     int *redo, *rc, *ci;
-    layout(s, m, n, d, k, flags, &a, &b, &c, &e, &f, &g, &mx, &part, &colpart, &thr, &cv, &ci, &bs, &redo, &rc);
+    float *xs, *ys;
+    double* rpv;
+    int* rpi;
+    layout(s, m, n, d, k, flags, &a, &b, &c, &e, &f, &g, &mx, &part, &colpart, &thr, &cv, &ci, &bs, &redo, &rc, &xs,
+           &ys, &rpv, &rpi);
     return s.used;
 }
 
@@ -60,8 +64,11 @@ extern "C" int hm_pricing_l2sq(void* stream, const float* X, const float* Y, con
     Entry *part, *colpart;
     unsigned int* colthr;
     int *redo, *redo_count, *cidx;
+    float *xsplit, *ysplit;
+    double* rpv;
+    int* rpi;
     layout(a, m, n, d, k, flags, &xnorm, &ynorm, &qb32, &p32, &db32, &ge32, &maxima, &part, &colpart, &colthr, &cval,
-           &cidx, &blockstats, &redo, &redo_count);
+           &cidx, &blockstats, &redo, &redo_count, &xsplit, &ysplit, &rpv, &rpi);
     hipLaunchKernelGGL(zero_words, dim3(1), dim3(64), 0, st, maxima, 4);
     HM_LAUNCH_CHECK("zero_words");
     // X side: ||x||, qb32, p32 (maxima[0..1] = max||x||, max|qb|); Y side: ||y||, db32, ge32 = q + db
@@ -72,5 +79,6 @@ extern "C" int hm_pricing_l2sq(void* stream, const float* X, const float* Y, con
                        db32, ge32, maxima + 2);
     HM_LAUNCH_CHECK("l2sq_prep_rows");
     return run_k(st, X, Y, m, n, d, k, scale, flags, qb, db, xnorm, ynorm, maxima, qb32, db32, p32, ge32, part,
-                 colpart, colthr, cval, cidx, blockstats, redo, redo_count, row_val, row_idx, col_val, col_idx, stats);
+                 colpart, colthr, cval, cidx, blockstats, redo, redo_count, row_val, row_idx, col_val, col_idx, stats,
+                 xsplit, ysplit, rpv, rpi);
 }

@@ -70,6 +70,12 @@ void prof_end(hipStream_t st) {
     g_open_event = nullptr;
 }
 
+void prof_count(const char* name, int64_t count) {
+    if (!g_on) return;
+    std::lock_guard<std::mutex> lock(g_mu);
+    g_totals[name].second += count;
+}
+
 }  // namespace hm
 
 extern "C" void hm_profile_enable(int on) {

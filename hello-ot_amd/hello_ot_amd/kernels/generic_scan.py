@@ -48,16 +48,24 @@ def _workspace(nbytes: int, device) -> torch.Tensor:
     return torch.empty(max(int(nbytes), 256), dtype=torch.uint8, device=device)
 
 
-def pricing_l2sq(x, y, nx, ny, qb, dbb, k, *, dot_scale=2.0, rows=True, cols=True, stats=True, linf=False):
+SWEEP_PRECISIONS = ("fp32", "bf16x3")
+
+
+def pricing_l2sq(x, y, nx, ny, qb, dbb, k, *, dot_scale=2.0, rows=True, cols=True, stats=True, linf=False,
+                 precision="fp32"):
     """Raw l2^2 pricing: returns (row_vals, row_idx, col_vals, col_idx, stats5) with None for skipped parts.
 
-    ``stats5`` = (num, den, count, max sigma+, max|cost|); max|cost| is 0 unless ``linf``.
+    ``stats5`` = (num, den, count, max sigma+, max|cost|); max|cost| is 0 unless ``linf``. ``precision`` picks the
+    candidate sweep: ``"fp32"`` MFMA or ``"bf16x3"`` split-bf16 MFMA (three products); both feed the same exact
+    fp64 re-evaluation, so the outputs are identical and only the speed (and the rescan rate) differs.
     """
+    if precision not in SWEEP_PRECISIONS:
+        raise ValueError(f"precision must be one of {SWEEP_PRECISIONS}")
     lib = _lib.load()
     x, y, nx, ny, qb, dbb = map(_c, (x, y, nx, ny, qb, dbb))
     m, n, d = x.shape[0], y.shape[0], x.shape[1]
     flags = (_lib.HM_ROWS if rows else 0) | (_lib.HM_COLS if cols else 0) | (_lib.HM_STATS if stats else 0) \
-        | (_lib.HM_LINF if (stats and linf) else 0)
+        | (_lib.HM_LINF if (stats and linf) else 0) | (_lib.HM_BF16X3 if precision == "bf16x3" else 0)
     dev = x.device
     rv = torch.empty((m, k), dtype=torch.float64, device=dev) if rows else None
     ri = torch.empty((m, k), dtype=torch.int32, device=dev) if rows else None
