@@ -47,6 +47,7 @@ constexpr int NB = 4;              // 32-wide Y blocks per wave
 constexpr int BY = 32 * NB;        // Y rows per tile
 constexpr int KC = 32;             // features per LDS chunk
 constexpr int STR = KC + 4;        // LDS row stride (floats)
+constexpr int STAGE = (BX + BY) * STR;  // floats per LDS stage of the sweep (X tile, then Y tile)
 constexpr int CST = BX + 1;        // LDS row stride of the column-score tile (floats)
 constexpr int FLUSH_CHUNKS = 8;    // fp32 block length 256 features before folding into the outer sum
 constexpr int FLUSH_SPLIT = 4;     // split-bf16 block length 128 features (3 product terms per feature)
@@ -135,17 +136,17 @@ inline unsigned prep_grid(int64_t rows) {
 
 // -------------------------------------------------------------------------------------------------
 // split-bf16 copy: x = hi + lo + e with hi = bf16(x), lo = bf16(x - hi) (round to nearest even), |e| <= 2^-16|x|.
-// Row r of the copy holds ld = roundup(d, 32) features as ld / 8 groups of 32 bytes: 8 hi, then 8 lo values;
-// padding features are zero.
+// Row r of the copy holds ld features (split_ld) as ld / 8 groups of 32 bytes: 8 hi, then 8 lo values; padding
+// features and the padding rows up to a whole 128-row panel are zero.
 // -------------------------------------------------------------------------------------------------
 __device__ inline unsigned short bf16_rne(float x) {
     const unsigned int u = __float_as_uint(x);
     return (unsigned short)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
 }
 
-__global__ void l2sq_split_bf16(const float* __restrict__ X, int64_t rows, int d, int ld,
+__global__ void l2sq_split_bf16(const float* __restrict__ X, int64_t rows, int64_t padded_rows, int d, int ld,
                                 unsigned short* __restrict__ out) {
-    const int64_t groups = rows * (ld / 8);
+    const int64_t groups = padded_rows * (ld / 8);
     for (int64_t gidx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; gidx < groups;
          gidx += (int64_t)gridDim.x * blockDim.x) {
         const int64_t row = gidx / (ld / 8);
@@ -153,7 +154,7 @@ __global__ void l2sq_split_bf16(const float* __restrict__ X, int64_t rows, int d
         unsigned short hi[8], lo[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-            const float x = (k0 + e < d) ? X[row * d + k0 + e] : 0.0f;
+            const float x = (row < rows && k0 + e < d) ? X[row * d + k0 + e] : 0.0f;
             hi[e] = bf16_rne(x);
             lo[e] = bf16_rne(x - __uint_as_float((unsigned int)hi[e] << 16));
         }
@@ -176,8 +177,9 @@ __global__ void l2sq_split_bf16(const float* __restrict__ X, int64_t rows, int d
 // sweep over X rows [xb, xe) of one chunk
 // -------------------------------------------------------------------------------------------------
 // PREC 0: X / Y are the fp32 features (row stride ld = d), products on v_mfma_f32_32x32x2f32.
-// PREC 1: X / Y are their split-bf16 copies (l2sq_split_bf16: row stride ld = d padded to 32, groups of 8 hi
-//         then 8 lo bf16 per 32 bytes); dot = hi*hi + hi*lo + lo*hi on v_mfma_f32_32x32x16_bf16.
+// PREC 1: X / Y are their split-bf16 copies (l2sq_split_bf16: d = features padded to 32, row stride ld, groups
+//         of 8 hi then 8 lo bf16 per 32 bytes, rows padded to whole 128-row panels); dot = hi*hi + hi*lo + lo*hi
+//         on v_mfma_f32_32x32x16_bf16.
 template <int K1, bool TWO_LEVEL, bool COLS, int PREC>
 __global__ __launch_bounds__(256) void l2sq_sweep(
     const float* __restrict__ X, const float* __restrict__ Y, int64_t xb, int64_t xe, int64_t n, int d, int ld,
@@ -185,8 +187,7 @@ __global__ __launch_bounds__(256) void l2sq_sweep(
     const float* __restrict__ ge32, float scale, int64_t seg_len, Entry* __restrict__ part,
     Entry* __restrict__ colpart, unsigned int* __restrict__ colthr, double* __restrict__ blockstats, int VEC4,
     int STATS) {
-    __shared__ float sX[BX * STR];
-    __shared__ float sY[BY * STR];
+    __shared__ float sT[2 * STAGE];  // two LDS stages of (X tile, Y tile), 32 features each
     __shared__ float sDB[BY];
     __shared__ float sGE[BY];
     __shared__ float sC[COLS ? BY * CST : 1];
@@ -216,112 +217,152 @@ __global__ __launch_bounds__(256) void l2sq_sweep(
     float mx = 0.0f, cmax = 0.0f;
 
     const int nchunks = (d + KC - 1) / KC;
+    constexpr int BLK = PREC == 1 ? FLUSH_SPLIT : FLUSH_CHUNKS;  // chunks per fp32 accumulation block
 
-    // global -> register staging for one chunk: 4 float4 of X and 4 of Y per thread
-    float4 gx[4], gy[4];
+    // global -> register staging for one chunk: 4 float4 of X and 4 of Y per thread (named registers: an array
+    // indexed before unrolling would be moved to LDS or scratch). The split copies are padded to whole 128-row
+    // panels and 32-feature chunks, so their loads need no bounds checks.
+    float4 gx0, gx1, gx2, gx3, gy0, gy1, gy2, gy3;
+    const float* Xp = X + x0 * ld;  // this workgroup's X panel (uniform base; 32-bit lane offsets below)
+    auto load_one = [&](int i, int k0, int64_t ytile, const float* Yp, float4& ox, float4& oy) {
+        const int lin = tid + 256 * i;
+        const int row = lin >> 3, c4 = lin & 7;
+        const int k = k0 + 4 * c4;
+        const int64_t xr = x0 + row, yr = ytile + row;
+        if (PREC == 1) {
+            const unsigned off = (unsigned)row * (unsigned)ld + (unsigned)k;
+            ox = *reinterpret_cast<const float4*>(Xp + off);
+            oy = *reinterpret_cast<const float4*>(Yp + off);
+        } else if (VEC4) {
+            ox = (xr < xe && k < d) ? *reinterpret_cast<const float4*>(X + xr * ld + k) : make_float4(0, 0, 0, 0);
+            oy = (yr < y_end && k < d) ? *reinterpret_cast<const float4*>(Y + yr * ld + k) : make_float4(0, 0, 0, 0);
+        } else {
+            ox.x = (xr < xe && k < d) ? X[xr * ld + k] : 0.0f;
+            ox.y = (xr < xe && k + 1 < d) ? X[xr * ld + k + 1] : 0.0f;
+            ox.z = (xr < xe && k + 2 < d) ? X[xr * ld + k + 2] : 0.0f;
+            ox.w = (xr < xe && k + 3 < d) ? X[xr * ld + k + 3] : 0.0f;
+            oy.x = (yr < y_end && k < d) ? Y[yr * ld + k] : 0.0f;
+            oy.y = (yr < y_end && k + 1 < d) ? Y[yr * ld + k + 1] : 0.0f;
+            oy.z = (yr < y_end && k + 2 < d) ? Y[yr * ld + k + 2] : 0.0f;
+            oy.w = (yr < y_end && k + 3 < d) ? Y[yr * ld + k + 3] : 0.0f;
+        }
+    };
     auto load_chunk = [&](int c, int64_t ytile) {
-        const int k0 = c * KC;
+        const float* Yp = Y + ytile * ld;
+        load_one(0, c * KC, ytile, Yp, gx0, gy0);
+        load_one(1, c * KC, ytile, Yp, gx1, gy1);
+        load_one(2, c * KC, ytile, Yp, gx2, gy2);
+        load_one(3, c * KC, ytile, Yp, gx3, gy3);
+    };
+    auto store_one = [&](float* stage, int i, const float4& vx, const float4& vy) {
+        const int lin = tid + 256 * i;
+        const int row = lin >> 3, c4 = lin & 7;
+        *reinterpret_cast<float4*>(&stage[row * STR + 4 * c4]) = vx;
+        *reinterpret_cast<float4*>(&stage[BX * STR + row * STR + 4 * c4]) = vy;
+    };
+    auto store_chunk = [&](float* stage) {
+        store_one(stage, 0, gx0, gy0);
+        store_one(stage, 1, gx1, gy1);
+        store_one(stage, 2, gx2, gy2);
+        store_one(stage, 3, gx3, gy3);
+    };
+
+    v16f acc[NB];
+    float outer[NB][16];
+    // products of one 32-feature chunk held in an LDS stage
+    auto compute = [&](const float* sx, const float* sy) {
+        if (PREC == 1) {
+            // two K-steps of 16 features; lane (h, r) supplies group 2s + h (8 features: hi, then lo)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int lin = tid + 256 * i;
-            const int row = lin >> 3, c4 = lin & 7;
-            const int k = k0 + 4 * c4;
-            const int64_t xr = x0 + row, yr = ytile + row;
-            if (VEC4) {
-                gx[i] = (xr < xe && k < d) ? *reinterpret_cast<const float4*>(X + xr * ld + k) : make_float4(0, 0, 0, 0);
-                gy[i] = (yr < y_end && k < d) ? *reinterpret_cast<const float4*>(Y + yr * ld + k) : make_float4(0, 0, 0, 0);
-            } else {
-                float a[4], b[4];
+            for (int s2 = 0; s2 < 2; ++s2) {
+                const int gw = (2 * s2 + h) * 8;
+                const bf16x8 bh = *reinterpret_cast<const bf16x8*>(&sx[(wave * 32 + r) * STR + gw]);
+                const bf16x8 bl = *reinterpret_cast<const bf16x8*>(&sx[(wave * 32 + r) * STR + gw + 4]);
+                bf16x8 ah[NB], al[NB];
+#pragma unroll
+                for (int b = 0; b < NB; ++b) {
+                    ah[b] = *reinterpret_cast<const bf16x8*>(&sy[(b * 32 + r) * STR + gw]);
+                    al[b] = *reinterpret_cast<const bf16x8*>(&sy[(b * 32 + r) * STR + gw + 4]);
+                }
+#pragma unroll
+                for (int b = 0; b < NB; ++b) acc[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah[b], bh, acc[b], 0, 0, 0);
+#pragma unroll
+                for (int b = 0; b < NB; ++b) acc[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah[b], bl, acc[b], 0, 0, 0);
+#pragma unroll
+                for (int b = 0; b < NB; ++b) acc[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al[b], bh, acc[b], 0, 0, 0);
+            }
+        } else {
+            // B operand: this lane's X row, features h*16 .. h*16+15 of the chunk
+            const float* bx = &sx[(wave * 32 + r) * STR + h * 16];
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const float4 bv = *reinterpret_cast<const float4*>(bx + 4 * g);
+                float4 av[NB];
+#pragma unroll
+                for (int b = 0; b < NB; ++b)
+                    av[b] = *reinterpret_cast<const float4*>(&sy[(b * 32 + r) * STR + h * 16 + 4 * g]);
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    a[e] = (xr < xe && k + e < d) ? X[xr * ld + k + e] : 0.0f;
-                    b[e] = (yr < y_end && k + e < d) ? Y[yr * ld + k + e] : 0.0f;
+#pragma unroll
+                    for (int b = 0; b < NB; ++b) {
+                        const float ae = e == 0 ? av[b].x : e == 1 ? av[b].y : e == 2 ? av[b].z : av[b].w;
+                        const float be = e == 0 ? bv.x : e == 1 ? bv.y : e == 2 ? bv.z : bv.w;
+                        acc[b] = __builtin_amdgcn_mfma_f32_32x32x2f32(ae, be, acc[b], 0, 0, 0);
+                    }
                 }
-                gx[i] = make_float4(a[0], a[1], a[2], a[3]);
-                gy[i] = make_float4(b[0], b[1], b[2], b[3]);
             }
         }
     };
-    auto store_chunk = [&]() {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int lin = tid + 256 * i;
-            const int row = lin >> 3, c4 = lin & 7;
-            *reinterpret_cast<float4*>(&sX[row * STR + 4 * c4]) = gx[i];
-            *reinterpret_cast<float4*>(&sY[row * STR + 4 * c4]) = gy[i];
-        }
-    };
 
+    // Software pipeline with two LDS stages and one barrier per chunk: while the chunk in stage g&1 is multiplied,
+    // the next chunk (of this tile, or chunk 0 of the next tile) is loaded into registers, then stored to the other
+    // stage. The barrier ending a chunk both publishes the next stage and retires all reads of the current one.
+    unsigned g = 0;
+    load_chunk(0, y_begin);
+    store_chunk(sT);
+    __syncthreads();
     for (int64_t ytile = y_begin; ytile < y_end; ytile += BY) {
-        v16f acc[NB];
-        float outer[NB][16];
 #pragma unroll
         for (int b = 0; b < NB; ++b) {
 #pragma unroll
             for (int q = 0; q < 16; ++q) { acc[b][q] = 0.0f; outer[b][q] = 0.0f; }
         }
-        // biases of this tile's Y rows
+        // biases of this tile's Y rows (read in the epilogue, after at least one chunk barrier)
         if (tid < BY) {
             const int64_t j = ytile + tid;
             sDB[tid] = j < y_end ? db32[j] : 0.0f;
             sGE[tid] = (STATS && j < y_end) ? ge32[j] : 0.0f;
         }
-        load_chunk(0, ytile);
-        store_chunk();
-        __syncthreads();
-        for (int c = 0; c < nchunks; ++c) {
-            if (c + 1 < nchunks) load_chunk(c + 1, ytile);
-            if (PREC == 1) {
-                // two K-steps of 16 features; lane (h, r) supplies group 2s + h (8 features: hi, then lo)
+        const int64_t next_tile = ytile + BY < y_end ? ytile + BY : ytile;
+        auto step = [&](int c) {
+            const bool last = c + 1 >= nchunks;
+            load_chunk(last ? 0 : c + 1, last ? next_tile : ytile);
+            // keep the order loads -> products -> stores: stores hoisted above the products would wait for the
+            // loads at once and expose their latency
+            asm volatile("" ::: "memory");
+            __builtin_amdgcn_sched_barrier(0);
+            const float* cur = sT + (g & 1u) * STAGE;
+            compute(cur, cur + BX * STR);
+            asm volatile("" ::: "memory");
+            __builtin_amdgcn_sched_barrier(0);
+            store_chunk(sT + ((g + 1u) & 1u) * STAGE);
+            __syncthreads();
+            ++g;
+        };
+        int c = 0;
+        if (TWO_LEVEL) {
+            // fp32 blocks of BLK chunks folded into the outer sums (the error bound assumes this blocking)
+            for (; c + BLK <= nchunks; c += BLK) {
 #pragma unroll
-                for (int s2 = 0; s2 < 2; ++s2) {
-                    const int gw = (2 * s2 + h) * 8;
-                    const bf16x8 bh = *reinterpret_cast<const bf16x8*>(&sX[(wave * 32 + r) * STR + gw]);
-                    const bf16x8 bl = *reinterpret_cast<const bf16x8*>(&sX[(wave * 32 + r) * STR + gw + 4]);
-                    bf16x8 ah[NB], al[NB];
-#pragma unroll
-                    for (int b = 0; b < NB; ++b) {
-                        ah[b] = *reinterpret_cast<const bf16x8*>(&sY[(b * 32 + r) * STR + gw]);
-                        al[b] = *reinterpret_cast<const bf16x8*>(&sY[(b * 32 + r) * STR + gw + 4]);
-                    }
-#pragma unroll
-                    for (int b = 0; b < NB; ++b) acc[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah[b], bh, acc[b], 0, 0, 0);
-#pragma unroll
-                    for (int b = 0; b < NB; ++b) acc[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah[b], bl, acc[b], 0, 0, 0);
-#pragma unroll
-                    for (int b = 0; b < NB; ++b) acc[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al[b], bh, acc[b], 0, 0, 0);
-                }
-            }
-            // B operand: this lane's X row, features h*16 .. h*16+15 of the chunk
-            const float* bx = &sX[(wave * 32 + r) * STR + h * 16];
-#pragma unroll
-            for (int g = 0; g < (PREC == 0 ? 4 : 0); ++g) {
-                const float4 bv = *reinterpret_cast<const float4*>(bx + 4 * g);
-                float4 av[NB];
-#pragma unroll
-                for (int b = 0; b < NB; ++b)
-                    av[b] = *reinterpret_cast<const float4*>(&sY[(b * 32 + r) * STR + h * 16 + 4 * g]);
-#pragma unroll
-                for (int b = 0; b < NB; ++b) {
-                    acc[b] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[b].x, bv.x, acc[b], 0, 0, 0);
-                    acc[b] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[b].y, bv.y, acc[b], 0, 0, 0);
-                    acc[b] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[b].z, bv.z, acc[b], 0, 0, 0);
-                    acc[b] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[b].w, bv.w, acc[b], 0, 0, 0);
-                }
-            }
-            if (TWO_LEVEL && ((c + 1) % (PREC == 1 ? FLUSH_SPLIT : FLUSH_CHUNKS) == 0)) {
+                for (int u = 0; u < BLK; ++u) step(c + u);
 #pragma unroll
                 for (int b = 0; b < NB; ++b) {
 #pragma unroll
                     for (int q = 0; q < 16; ++q) { outer[b][q] += acc[b][q]; acc[b][q] = 0.0f; }
                 }
             }
-            __syncthreads();
-            if (c + 1 < nchunks) {
-                store_chunk();
-                __syncthreads();
-            }
         }
+        for (; c < nchunks; ++c) step(c);
         // epilogue: lane (h, r) holds D[m][n] for n = r (X row) and m = b*32 + 8*(q/4) + 4*h + q%4 (Y row)
         float tnum = 0.0f, tden = 0.0f;
         unsigned int tcnt = 0;
@@ -735,6 +776,12 @@ inline int bucket_k1(int k) { return k <= 2 ? 8 : (k <= 8 ? 16 : 40); }
 
 inline bool fused_columns(int d, uint32_t flags) { return (flags & HM_COLS) && d >= FUSE_MIN_D; }
 
+// split copies: features padded to whole 32-feature chunks; a row stride that is a multiple of 2 KiB gets one
+// more chunk so the rows of a panel do not all start on the same memory channel
+inline int split_features(int d) { return (d + KC - 1) / KC * KC; }
+inline int split_ld(int d) { return split_features(d) + (split_features(d) % 512 == 0 ? KC : 0); }
+inline int64_t panel_rows(int64_t rows) { return (rows + BX - 1) / BX * BX; }
+
 // Rows per internal chunk of the swept side (m rows against n): whole 128-row panels, and with fused columns
 // the chunk's column partial lists within COLPART_CAP.
 inline int64_t chunk_rows(int64_t m, int64_t n, int k, bool fused) {
@@ -804,9 +851,9 @@ void layout(A& a, int64_t m, int64_t n, int d, int k, uint32_t flags, double** x
     *redo = a.template take<int>((size_t)(m + n));
     *redo_count = a.template take<int>(2);
     const bool split = (flags & HM_BF16X3) != 0;
-    const size_t ldw = (size_t)(d + KC - 1) / KC * KC;
-    *xsplit = a.template take<float>(split ? (size_t)m * ldw : 1);
-    *ysplit = a.template take<float>(split ? (size_t)n * ldw : 1);
+    const size_t ldw = (size_t)split_ld(d);
+    *xsplit = a.template take<float>(split ? (size_t)panel_rows(m) * ldw : 1);
+    *ysplit = a.template take<float>(split ? (size_t)panel_rows(n) * ldw : 1);
     *rpv = a.template take<double>((size_t)RESCAN_ITEMS * k);
     *rpi = a.template take<int>((size_t)RESCAN_ITEMS * k);
 }
@@ -865,15 +912,18 @@ int run_bidir(hipStream_t st, const float* X, const float* Y, int64_t m, int64_t
     const int flush = KC * (split ? FLUSH_SPLIT : FLUSH_CHUNKS);
     const bool two_level = d > flush;
     const bool vec4 = split || (d % 4) == 0;
-    const int ld = split ? (d + KC - 1) / KC * KC : d;  // sweep row stride and length in 4-byte words
+    const int sd = split ? split_features(d) : d;  // swept features (4-byte words per row of the split copy)
+    const int ld = split ? split_ld(d) : d;         // sweep row stride in 4-byte words
     const float* SX = split ? xsplit : X;
     const float* SY = split ? ysplit : Y;
     const int64_t ch = chunk_rows(m, n, k, fused);
     const DirPlan plan = plan_dir(ch, n);
     if (split) {
-        hipLaunchKernelGGL(l2sq_split_bf16, dim3(4096), dim3(256), 0, st, X, m, d, ld, reinterpret_cast<unsigned short*>(xsplit));
+        hipLaunchKernelGGL(l2sq_split_bf16, dim3(4096), dim3(256), 0, st, X, m, panel_rows(m), d, ld,
+                           reinterpret_cast<unsigned short*>(xsplit));
         HM_LAUNCH_CHECK("l2sq_split_bf16");
-        hipLaunchKernelGGL(l2sq_split_bf16, dim3(4096), dim3(256), 0, st, Y, n, d, ld, reinterpret_cast<unsigned short*>(ysplit));
+        hipLaunchKernelGGL(l2sq_split_bf16, dim3(4096), dim3(256), 0, st, Y, n, panel_rows(n), d, ld,
+                           reinterpret_cast<unsigned short*>(ysplit));
         HM_LAUNCH_CHECK("l2sq_split_bf16");
     }
     // Rigorous bound on |w - exact| in units of scale*||x||*||y||: accumulation of B-feature blocks in fp32
@@ -907,7 +957,7 @@ int run_bidir(hipStream_t st, const float* X, const float* Y, int64_t m, int64_t
 #define HM_SWEEP(TL, CL)                                                                                             \
     do {                                                                                                             \
         if (split)                                                                                                   \
-            hipLaunchKernelGGL((l2sq_sweep<K1, TL, CL, 1>), grid, dim3(256), 0, st, SX, SY, xb, xe, n, ld, ld, qb32, \
+            hipLaunchKernelGGL((l2sq_sweep<K1, TL, CL, 1>), grid, dim3(256), 0, st, SX, SY, xb, xe, n, sd, ld, qb32, \
                                db32, p32, ge32, (float)scale, plan.seg_len, part, colpart, colthr, blockstats, 1,     \
                                (int)want_stats);                                                                     \
         else                                                                                                         \
@@ -973,7 +1023,7 @@ int run_bidir(hipStream_t st, const float* X, const float* Y, int64_t m, int64_t
 #define HM_SWEEP2(TL)                                                                                                \
     do {                                                                                                             \
         if (split)                                                                                                   \
-            hipLaunchKernelGGL((l2sq_sweep<K1, TL, false, 1>), grid, dim3(256), 0, st, SY, SX, yb, ye, m, ld, ld,    \
+            hipLaunchKernelGGL((l2sq_sweep<K1, TL, false, 1>), grid, dim3(256), 0, st, SY, SX, yb, ye, m, sd, ld,    \
                                db32, qb32, ge32, p32, (float)scale, plan2.seg_len, part, colpart, colthr, blockstats, \
                                1, 0);                                                                                \
         else                                                                                                         \
