@@ -1,5 +1,5 @@
-// l2^2 ("raw lowrank") pricing scan for gfx950 -- kernels and per-K1 driver (included by pricing_l2sq*.hip):
-// one fp32 MFMA sweep feeds both the row and the column candidate lists, then an exact fp64 re-check.
+// l2^2 ("raw lowrank") pricing scan for gfx950 -- kernels and the driver (instantiated by pricing_l2sq_l*_m*.hip):
+// one MFMA sweep feeds both the row and the column candidate lists, then an exact fp64 re-check.
 //
 // Semantics (reference: generic_scan.py:577-597 -> pricing_small.cu:230-304 / pricing.cu:185-229 with
 // matrix_selection.cuh:20-74):
@@ -7,18 +7,20 @@
 // Per X row and per Y row the k best sigma with lowest-index ties; certificate sums over all pairs.
 //
 // Pipeline, per internal chunk of at most CHUNK_MAX X rows (the column lists of a chunk stay bounded):
-//   1. prep (once): fp64 row norms ||x_i||, ||y_j||, their maxima, max|bias|; fp32 copies of the biases.
-//   2. sweep:    MFMA 32x32x2 fp32 tiles of Y * X^T (a workgroup owns 128 X rows and walks one segment of Y
-//                in 128-row tiles; lane (h, r) of a wave owns X row r of the wave's 32 and 16 Y rows of each
-//                32-row block). From the same accumulators:
+//   1. prep (once): fp64 row norms ||x_i||, ||y_j||, their maxima, max|bias|; fp32 copies of the biases; with
+//                HM_BF16X3 the split-bf16 copies of X and Y.
+//   2. sweep:    MFMA tiles of Y * X^T, fp32 32x32x2 or split-bf16 32x32x16 (a workgroup owns 128 X rows and
+//                walks one segment of Y in 128-row tiles; lane (h, r) of a wave owns X row r of the wave's 32 and
+//                16 Y rows of each 32-row block). From the same accumulators:
 //                  rows:    each lane keeps its best K1 of w = scale*dot32 + db32_j (ranks like sigma in j);
 //                  columns: the tile's scores scale*dot32 + qb32_i go through LDS and each Y row keeps its
 //                           best K1 over the workgroup's 128 X rows (one list per X panel);
 //                  certificate sums in fp32 per tile, flushed to fp64.
-//   3. finalize: one wave per row (or column) merges the partial lists, checks that the K1-th approximate
-//                value is below the k-th minus twice the rigorous error bound (otherwise the row is queued
-//                for step 4), and re-evaluates the K1 survivors with the fixed-order fp64 dot (dot64).
-//   4. rescan:   queued rows / columns are scanned exactly (one wave each, one lane per candidate).
+//   3. finalize: one wave per row (or column) merges the partial lists into the best KM, checks that every
+//                dropped value is below the k-th minus twice the rigorous error bound (otherwise the row is
+//                queued for step 4), and re-evaluates the survivors that can still reach the top k with the
+//                fixed-order fp64 dot (dot64).
+//   4. rescan:   queued rows / columns are scanned exactly (sliced over waves, then merged).
 //   5. columns:  each chunk's exact column lists are merged into the output (tie rule kept).
 #pragma once
 
@@ -222,7 +224,8 @@ __global__ __launch_bounds__(256) void l2sq_sweep(
     // global -> register staging for one chunk: 4 float4 of X and 4 of Y per thread (named registers: an array
     // indexed before unrolling would be moved to LDS or scratch). The split copies are padded to whole 128-row
     // panels and 32-feature chunks, so their loads need no bounds checks.
-    float4 gx0, gx1, gx2, gx3, gy0, gy1, gy2, gy3;
+    float4 gx0, gx1, gx2, gx3, gy0, gy1, gy2, gy3;  // set A: the chunk after the one being multiplied
+    float4 hx0, hx1, hx2, hx3, hy0, hy1, hy2, hy3;  // set B: the chunk after that
     const float* Xp = X + x0 * ld;  // this workgroup's X panel (uniform base; 32-bit lane offsets below)
     auto load_one = [&](int i, int k0, int64_t ytile, const float* Yp, float4& ox, float4& oy) {
         const int lin = tid + 256 * i;
@@ -247,12 +250,37 @@ __global__ __launch_bounds__(256) void l2sq_sweep(
             oy.w = (yr < y_end && k + 3 < d) ? Y[yr * ld + k + 3] : 0.0f;
         }
     };
-    auto load_chunk = [&](int c, int64_t ytile) {
+    auto load_a = [&](int c, int64_t ytile) {
         const float* Yp = Y + ytile * ld;
         load_one(0, c * KC, ytile, Yp, gx0, gy0);
         load_one(1, c * KC, ytile, Yp, gx1, gy1);
         load_one(2, c * KC, ytile, Yp, gx2, gy2);
         load_one(3, c * KC, ytile, Yp, gx3, gy3);
+    };
+    auto load_b = [&](int c, int64_t ytile) {
+        const float* Yp = Y + ytile * ld;
+        load_one(0, c * KC, ytile, Yp, hx0, hy0);
+        load_one(1, c * KC, ytile, Yp, hx1, hy1);
+        load_one(2, c * KC, ytile, Yp, hx2, hy2);
+        load_one(3, c * KC, ytile, Yp, hx3, hy3);
+    };
+    auto rotate = [&]() {
+        gx0 = hx0; gx1 = hx1; gx2 = hx2; gx3 = hx3;
+        gy0 = hy0; gy1 = hy1; gy2 = hy2; gy3 = hy3;
+    };
+    // chunk f of the tile sequence starting at `tile` (f may run past the tile's chunks into the next tiles); past
+    // the segment's end any in-bounds chunk will do, its data is never multiplied
+    auto locate = [&](int64_t tile, int f, int64_t& t, int& cc) {
+        t = tile;
+        cc = f;
+        while (cc >= nchunks) {
+            cc -= nchunks;
+            t += BY;
+        }
+        if (t >= y_end) {
+            t = tile;
+            cc = 0;
+        }
     };
     auto store_one = [&](float* stage, int i, const float4& vx, const float4& vy) {
         const int lin = tid + 256 * i;
@@ -314,13 +342,20 @@ __global__ __launch_bounds__(256) void l2sq_sweep(
         }
     };
 
-    // Software pipeline with two LDS stages and one barrier per chunk: while the chunk in stage g&1 is multiplied,
-    // the next chunk (of this tile, or chunk 0 of the next tile) is loaded into registers, then stored to the other
-    // stage. The barrier ending a chunk both publishes the next stage and retires all reads of the current one.
+    // Software pipeline with two LDS stages, two register sets and one barrier per chunk: while the chunk in stage
+    // g&1 is multiplied, the chunk two ahead in the tile sequence is loaded into set B, and set A (the next chunk,
+    // loaded one step earlier) is stored to the other stage. The barrier ending a chunk both publishes the next
+    // stage and retires all reads of the current one.
     unsigned g = 0;
-    load_chunk(0, y_begin);
-    store_chunk(sT);
-    __syncthreads();
+    {
+        int64_t t1;
+        int c1;
+        load_a(0, y_begin);
+        store_chunk(sT);
+        locate(y_begin, 1, t1, c1);
+        load_a(c1, t1);
+        __syncthreads();
+    }
     for (int64_t ytile = y_begin; ytile < y_end; ytile += BY) {
 #pragma unroll
         for (int b = 0; b < NB; ++b) {
@@ -333,10 +368,11 @@ __global__ __launch_bounds__(256) void l2sq_sweep(
             sDB[tid] = j < y_end ? db32[j] : 0.0f;
             sGE[tid] = (STATS && j < y_end) ? ge32[j] : 0.0f;
         }
-        const int64_t next_tile = ytile + BY < y_end ? ytile + BY : ytile;
         auto step = [&](int c) {
-            const bool last = c + 1 >= nchunks;
-            load_chunk(last ? 0 : c + 1, last ? next_tile : ytile);
+            int64_t t2;
+            int c2;
+            locate(ytile, c + 2, t2, c2);
+            load_b(c2, t2);
             // keep the order loads -> products -> stores: stores hoisted above the products would wait for the
             // loads at once and expose their latency
             asm volatile("" ::: "memory");
@@ -347,6 +383,7 @@ __global__ __launch_bounds__(256) void l2sq_sweep(
             __builtin_amdgcn_sched_barrier(0);
             store_chunk(sT + ((g + 1u) & 1u) * STAGE);
             __syncthreads();
+            rotate();
             ++g;
         };
         int c = 0;
@@ -524,48 +561,55 @@ struct BoundArgs {
     double abs_slack; // absolute slack (flushed denormals)
 };
 
-// Lists of row r: L in [0, nlists), at base + (((L / G) * R + r) * G + L % G) * K1 (sorted, missing = -1).
+// Lists of row r: L in [0, nlists), each of KL entries at base + (((L / G) * R + r) * G + L % G) * KL (sorted,
+// missing = -1). One wave per row merges them into the best KM (KM >= KL).
 // The row side A (rows A[r], row bias abias[r], norm anorm[r]) pairs with candidates from side B (B[c],
 // bias bbias[c]); sigma = COLS ? (s*dot + bbias[c]) + abias[r] : (s*dot + abias[r]) + bbias[c], which keeps
 // the (dot + qb) + db association of the caller's (x, y) pair in both directions.
-template <int K1, int G, bool COLS>
+template <int KL, int KM, int G, bool COLS>
 __global__ __launch_bounds__(256) void l2sq_finalize(
     const float* __restrict__ A, const float* __restrict__ B, int64_t R, int d, int nlists,
     const Entry* __restrict__ lists, const double* __restrict__ abias, const double* __restrict__ bbias,
     const double* __restrict__ anorm, const unsigned long long* __restrict__ bmaxima, double scale, int k,
     BoundArgs bnd, double* __restrict__ out_val, int* __restrict__ out_idx, int* __restrict__ redo,
     int* __restrict__ redo_count) {
+    static_assert(KL <= KM, "merged lists hold at least one partial list");
     const int lane = threadIdx.x & 63;
     const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     const bool valid = row < R;   // uniform per wave
-    float lw[K1];
-    int li[K1];
+    float lw[KM];
+    int li[KM];
 #pragma unroll
-    for (int s = 0; s < K1; ++s) { lw[s] = -INFINITY; li[s] = -1; }
+    for (int s = 0; s < KM; ++s) { lw[s] = -INFINITY; li[s] = -1; }
     int nreal = 0, full = 0;
+    float tail = -INFINITY;  // largest last entry of a full list: everything its sweep dropped is <= it
     if (valid) {
         for (int L = lane; L < nlists; L += 64) {
-            const Entry* src = lists + ((((int64_t)(L / G)) * R + row) * G + (L % G)) * K1;
+            const Entry* src = lists + ((((int64_t)(L / G)) * R + row) * G + (L % G)) * KL;
             int cnt = 0;
-            for (int s = 0; s < K1; ++s) {
+            for (int s = 0; s < KL; ++s) {
                 const Entry e = src[s];
                 if (e.j < 0) break;
                 ++cnt;
-                if (better_e(e.w, e.j, lw[K1 - 1], li[K1 - 1])) insert_e<K1>(lw, li, e.w, e.j);
+                if (better_e(e.w, e.j, lw[KM - 1], li[KM - 1])) insert_e<KM>(lw, li, e.w, e.j);
             }
             nreal += cnt;
-            full |= (cnt == K1) ? 1 : 0;
+            if (cnt == KL) {
+                full = 1;
+                tail = fmaxf(tail, src[KL - 1].w);
+            }
         }
     }
     for (int o = 32; o >= 1; o >>= 1) {
         nreal += __shfl_xor(nreal, o, 64);
         full |= __shfl_xor(full, o, 64);
+        tail = fmaxf(tail, __shfl_xor(tail, o, 64));
     }
-    // wave top-K1: K1 rounds of an arg-best over the lanes' list heads
-    float tw[K1];
-    int ti[K1];
+    // wave top-KM: KM rounds of an arg-best over the lanes' list heads
+    float tw[KM];
+    int ti[KM];
 #pragma unroll
-    for (int t = 0; t < K1; ++t) {
+    for (int t = 0; t < KM; ++t) {
         float bw = lw[0];
         int bi = li[0];
         int bl = lane;
@@ -579,25 +623,28 @@ __global__ __launch_bounds__(256) void l2sq_finalize(
         ti[t] = bi;
         if (lane == bl) {
 #pragma unroll
-            for (int s = 0; s + 1 < K1; ++s) { lw[s] = lw[s + 1]; li[s] = li[s + 1]; }
-            lw[K1 - 1] = -INFINITY;
-            li[K1 - 1] = -1;
+            for (int s = 0; s + 1 < KM; ++s) { lw[s] = lw[s + 1]; li[s] = li[s + 1]; }
+            lw[KM - 1] = -INFINITY;
+            li[KM - 1] = -1;
         }
     }
     if (!valid) return;
-    const int kept = nreal < K1 ? nreal : K1;
-    float wk = -INFINITY, wK1 = tw[K1 - 1];
+    const int kept = nreal < KM ? nreal : KM;
+    float wk = -INFINITY;
 #pragma unroll
-    for (int t = 0; t < K1; ++t)
+    for (int t = 0; t < KM; ++t)
         if (t == k - 1) wk = tw[t];
     if (nreal < k) wk = -INFINITY;
     const double bmax = key_double(bmaxima[0]);
     const double dmax = key_double(bmaxima[1]);
     const double nxy = scale * anorm[row] * bmax;
     const double b = (nxy * bnd.acc_rel + dmax * bnd.db_rel + fabs(abias[row]) * 1e-15 + bnd.abs_slack) * (1.0 + 1e-6);
-    // candidates outside the kept list have w <= wK1; they cannot reach the exact top-k when wK1 < wk - 2b
-    const bool maybe_dropped = full || nreal > K1;
-    if (maybe_dropped && (double)wK1 >= (double)wk - 2.0 * b) {
+    // Candidates outside the kept list were dropped by a full partial list (w <= tail) or by the merge
+    // (w <= tw[KM-1]); they cannot reach the exact top-k when that bound is below wk - 2b.
+    const bool merge_dropped = nreal > KM;
+    float dropped = full ? tail : -INFINITY;
+    if (merge_dropped) dropped = fmaxf(dropped, tw[KM - 1]);
+    if ((full || merge_dropped) && (double)dropped >= (double)wk - 2.0 * b) {
         if (lane == 0) {
             const int slot = atomicAdd(redo_count, 1);
             redo[slot] = (int)row;
@@ -610,14 +657,14 @@ __global__ __launch_bounds__(256) void l2sq_finalize(
     const double cut = (double)wk - 2.0 * b;
     int need = 0;
 #pragma unroll
-    for (int e = 0; e < K1; ++e)
+    for (int e = 0; e < KM; ++e)
         if (e < kept && (double)tw[e] >= cut) need = e + 1;
     if (need < (kept < k ? kept : k)) need = kept < k ? kept : k;
     double sv = -INFINITY;
     int sj = -1;
     const float* ar = A + row * (int64_t)d;
 #pragma unroll
-    for (int e = 0; e < K1; ++e) {
+    for (int e = 0; e < KM; ++e) {
         if (e < need) {
             const int c = ti[e];
             const double dot = wave_dot64(ar, B + (int64_t)c * d, d, lane);
@@ -772,9 +819,23 @@ __global__ void fill_u32(unsigned int* p, int64_t count, unsigned int v) {
 // -------------------------------------------------------------------------------------------------
 // host orchestration
 // -------------------------------------------------------------------------------------------------
-inline int bucket_k1(int k) { return k <= 2 ? 8 : (k <= 8 ? 16 : 40); }
+// Candidates per row the finalize merges and keeps (KM), and entries per partial list of the sweep (KL).
+inline int merge_k(int k) { return k <= 2 ? 8 : (k <= 8 ? 16 : 40); }
 
-inline bool fused_columns(int d, uint32_t flags) { return (flags & HM_COLS) && d >= FUSE_MIN_D; }
+// A partial list sees about 1/nlists of a row's candidates. Its last entry bounds what it dropped; that bound
+// stays far below the k-th best unless the list holds KL of the best k + 2, so KL = 8 while (k + 2) / nlists <= 2
+// and KL = 16 while <= 6 (a row whose bound does not separate is rescanned exactly).
+inline int list_k_for(int64_t nlists, int k) {
+    if ((int64_t)(k + 2) <= 2 * nlists) return 8;
+    if ((int64_t)(k + 2) <= 6 * nlists) return 16;
+    return 40;
+}
+
+// columns ride on the row sweep when that sweep runs anyway (rows or certificate requested); a columns-only call
+// sweeps with the roles swapped, which needs no column epilogue
+inline bool fused_columns(int d, uint32_t flags) {
+    return (flags & HM_COLS) && (flags & (HM_ROWS | HM_STATS)) && d >= FUSE_MIN_D;
+}
 
 // split copies: features padded to whole 32-feature chunks; a row stride that is a multiple of 2 KiB gets one
 // more chunk so the rows of a panel do not all start on the same memory channel
@@ -782,24 +843,29 @@ inline int split_features(int d) { return (d + KC - 1) / KC * KC; }
 inline int split_ld(int d) { return split_features(d) + (split_features(d) % 512 == 0 ? KC : 0); }
 inline int64_t panel_rows(int64_t rows) { return (rows + BX - 1) / BX * BX; }
 
-// Rows per internal chunk of the swept side (m rows against n): whole 128-row panels, and with fused columns
-// the chunk's column partial lists within COLPART_CAP.
-inline int64_t chunk_rows(int64_t m, int64_t n, int k, bool fused) {
+// Rows per internal chunk of the swept side (m rows against n): balanced chunks of whole 128-row panels, and with
+// fused columns the chunk's column partial lists (kl entries per panel and column) within COLPART_CAP.
+inline int64_t chunk_rows(int64_t m, int64_t n, int kl, bool fused) {
     int64_t ch = CHUNK_MAX;
     if (fused) {
-        const int64_t per_panel = n * (int64_t)bucket_k1(k) * (int64_t)sizeof(Entry);
+        const int64_t per_panel = n * (int64_t)kl * (int64_t)sizeof(Entry);
         int64_t panels = (int64_t)(COLPART_CAP / (size_t)per_panel);
         if (panels < 1) panels = 1;
         if (panels * BX < ch) ch = panels * BX;
     }
-    const int64_t whole = (m + BX - 1) / BX * BX;
-    return ch < whole ? ch : whole;
+    const int64_t whole = panel_rows(m);
+    if (ch >= whole) return whole;
+    const int64_t nch = (m + ch - 1) / ch;
+    return panel_rows((m + nch - 1) / nch);
 }
 
-inline int choose_segments(int64_t m, int64_t n) {
+// Y segments per sweep launch: enough workgroups to fill the chip (SWEEP_WGS), and for k > 2 at least 8 so each
+// row has 16 partial lists; at most a quarter of the tiles and 64.
+inline int choose_segments(int64_t m, int64_t n, int k) {
     const int64_t panels = (m + BX - 1) / BX;
     const int64_t tiles = (n + BY - 1) / BY;
     int64_t s = (SWEEP_WGS + panels - 1) / panels;
+    if (k > 2 && s < 8) s = 8;
     const int64_t max_s = tiles / 4 > 0 ? tiles / 4 : 1;
     if (s > max_s) s = max_s;
     if (s > 64) s = 64;
@@ -807,11 +873,11 @@ inline int choose_segments(int64_t m, int64_t n) {
     return (int)s;
 }
 
-inline DirPlan plan_dir(int64_t rows, int64_t cols) {
+inline DirPlan plan_dir(int64_t rows, int64_t cols, int k) {
     DirPlan p;
     p.rows = rows;
     p.cols = cols;
-    p.S = choose_segments(rows, cols);
+    p.S = choose_segments(rows, cols, k);
     const int64_t tiles = (cols + BY - 1) / BY;
     const int64_t tiles_per = (tiles + p.S - 1) / p.S;
     p.seg_len = tiles_per * BY;
@@ -819,22 +885,52 @@ inline DirPlan plan_dir(int64_t rows, int64_t cols) {
     return p;
 }
 
+// Everything the workspace layout and the driver derive from the call's shape.
+struct CallPlan {
+    int kl, km;
+    bool fused, swapped, row_pass;
+    int64_t ch, ch2;  // chunk rows of the row pass and of the swapped pass
+    DirPlan plan, plan2;
+};
+
+inline CallPlan plan_call(int64_t m, int64_t n, int d, int k, uint32_t flags) {
+    CallPlan c;
+    c.km = merge_k(k);
+    c.fused = fused_columns(d, flags);
+    c.swapped = (flags & HM_COLS) && !c.fused;
+    c.row_pass = (flags & HM_ROWS) || c.fused || (flags & HM_STATS);
+    static const int sizes[3] = {8, 16, 40};
+    for (int t = 0; t < 3; ++t) {
+        c.kl = sizes[t];
+        c.ch = chunk_rows(m, n, c.kl, c.fused);
+        c.plan = plan_dir(c.ch, n, k);
+        c.ch2 = c.swapped ? chunk_rows(n, m, c.kl, false) : 0;
+        c.plan2 = plan_dir(c.swapped ? c.ch2 : 1, m, k);
+        if (c.kl >= c.km) break;
+        // fewest partial lists any finalized row or column of this call merges
+        int64_t nl = INT64_MAX;
+        if (flags & HM_ROWS) nl = std::min<int64_t>(nl, 2 * (int64_t)c.plan.S);
+        if (c.fused) {
+            const int64_t last = m - (m - 1) / c.ch * c.ch;
+            nl = std::min<int64_t>(nl, std::min<int64_t>(c.ch / BX, (last + BX - 1) / BX));
+        }
+        if (c.swapped) nl = std::min<int64_t>(nl, 2 * (int64_t)c.plan2.S);
+        if (nl == INT64_MAX || list_k_for(nl, k) <= c.kl) break;
+    }
+    return c;
+}
+
 template <class A>
 void layout(A& a, int64_t m, int64_t n, int d, int k, uint32_t flags, double** xnorm, double** ynorm, float** qb32,
             float** p32, float** db32, float** ge32, unsigned long long** maxima, Entry** part, Entry** colpart,
             unsigned int** colthr, double** cval, int** cidx, double** blockstats, int** redo, int** redo_count,
             float** xsplit, float** ysplit, double** rpv, int** rpi) {
-    const int K1 = bucket_k1(k);
-    const bool fused = fused_columns(d, flags);
-    const int64_t ch = chunk_rows(m, n, k, fused);
-    const DirPlan plan = plan_dir(ch, n);
-    const int64_t panels = ch / BX;
-    // second sweep with the roles swapped (columns without fusion): Y chunks against X
-    const bool swapped = (flags & HM_COLS) && !fused;
-    const int64_t ch2 = swapped ? chunk_rows(n, m, k, false) : 0;
-    const DirPlan plan2 = plan_dir(swapped ? ch2 : 1, m);
-    size_t part_entries = (size_t)plan.S * ch * 2 * K1;
-    if (swapped && (size_t)plan2.S * ch2 * 2 * K1 > part_entries) part_entries = (size_t)plan2.S * ch2 * 2 * K1;
+    const CallPlan c = plan_call(m, n, d, k, flags);
+    const int64_t panels = c.ch / BX;
+    size_t part_entries = (size_t)c.plan.S * c.ch * 2 * c.kl;
+    if (c.swapped && (size_t)c.plan2.S * c.ch2 * 2 * c.kl > part_entries)
+        part_entries = (size_t)c.plan2.S * c.ch2 * 2 * c.kl;
+    const bool fused = c.fused;
     *xnorm = a.template take<double>(m);
     *ynorm = a.template take<double>(n);
     *qb32 = a.template take<float>(m);
@@ -843,11 +939,11 @@ void layout(A& a, int64_t m, int64_t n, int d, int k, uint32_t flags, double** x
     *ge32 = a.template take<float>(n);
     *maxima = a.template take<unsigned long long>(4);
     *part = a.template take<Entry>(part_entries);
-    *colpart = a.template take<Entry>(fused ? (size_t)panels * n * K1 : 1);
+    *colpart = a.template take<Entry>(fused ? (size_t)panels * n * c.kl : 1);
     *colthr = a.template take<unsigned int>(fused ? (size_t)n : 1);
     *cval = a.template take<double>(fused ? (size_t)n * k : 1);
     *cidx = a.template take<int>(fused ? (size_t)n * k : 1);
-    *blockstats = a.template take<double>((size_t)5 * panels * plan.S);
+    *blockstats = a.template take<double>((size_t)5 * panels * c.plan.S);
     *redo = a.template take<int>((size_t)(m + n));
     *redo_count = a.template take<int>(2);
     const bool split = (flags & HM_BF16X3) != 0;
@@ -896,16 +992,19 @@ inline int rescan_exact(hipStream_t st, const float* A, const float* B, int64_t 
     return HM_OK;
 }
 
-template <int K1>
+template <int K1, int KM>
 int run_bidir(hipStream_t st, const float* X, const float* Y, int64_t m, int64_t n, int d, int k, double scale,
               uint32_t flags, const double* qb, const double* db, const double* xnorm, const double* ynorm,
               const unsigned long long* maxima, const float* qb32, const float* db32, const float* p32,
               const float* ge32, Entry* part, Entry* colpart, unsigned int* colthr, double* cval, int* cidx,
               double* blockstats, int* redo, int* redo_count, double* row_val, int* row_idx, double* col_val,
               int* col_idx, double* stats, float* xsplit, float* ysplit, double* rpv, int* rpi) {
+    // K1: entries per partial list of the sweep; KM: candidates the finalize merges and keeps
+    const CallPlan cp = plan_call(m, n, d, k, flags);
+    if (cp.kl != K1 || cp.km != KM) return fail(HM_EINVAL, "l2sq pricing: list sizes %d/%d do not match the plan %d/%d", K1, KM, cp.kl, cp.km);
     const bool want_rows = (flags & HM_ROWS) != 0;
-    const bool fused = fused_columns(d, flags);
-    const bool swapped = (flags & HM_COLS) && !fused;
+    const bool fused = cp.fused;
+    const bool swapped = cp.swapped;
     const bool want_stats = (flags & HM_STATS) != 0;
     const int linf = (flags & HM_LINF) ? 1 : 0;
     const bool split = (flags & HM_BF16X3) != 0;
@@ -916,8 +1015,8 @@ int run_bidir(hipStream_t st, const float* X, const float* Y, int64_t m, int64_t
     const int ld = split ? split_ld(d) : d;         // sweep row stride in 4-byte words
     const float* SX = split ? xsplit : X;
     const float* SY = split ? ysplit : Y;
-    const int64_t ch = chunk_rows(m, n, k, fused);
-    const DirPlan plan = plan_dir(ch, n);
+    const int64_t ch = cp.ch;
+    const DirPlan plan = cp.plan;
     if (split) {
         hipLaunchKernelGGL(l2sq_split_bf16, dim3(4096), dim3(256), 0, st, X, m, panel_rows(m), d, ld,
                            reinterpret_cast<unsigned short*>(xsplit));
@@ -941,7 +1040,7 @@ int run_bidir(hipStream_t st, const float* X, const float* Y, int64_t m, int64_t
     bnd.db_rel = 2.0 * u + 1e-15;
     bnd.abs_slack = 1e-30 * (double)d;
     int chunk_index = 0;
-    const bool row_pass = want_rows || fused || want_stats;  // a columns-only call without fusion skips it
+    const bool row_pass = cp.row_pass;  // a columns-only call without fusion skips it
     for (int64_t xb = 0; row_pass && xb < m; xb += ch, ++chunk_index) {
         const int64_t xe = xb + ch < m ? xb + ch : m;
         const int64_t rows = xe - xb;
@@ -985,7 +1084,7 @@ int run_bidir(hipStream_t st, const float* X, const float* Y, int64_t m, int64_t
             // row finalize: lists (seg, half) of each chunk row; candidates are Y rows
             hipLaunchKernelGGL(zero_words, dim3(1), dim3(64), 0, st, reinterpret_cast<unsigned long long*>(redo_count), 1);
             prof_begin(st, "l2sq_finalize");
-            hipLaunchKernelGGL((l2sq_finalize<K1, 2, false>), dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, st,
+            hipLaunchKernelGGL((l2sq_finalize<K1, KM, 2, false>), dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, st,
                                X + xb * d, Y, rows, d, 2 * plan.S, part, qb + xb, db, xnorm + xb, maxima + 2, scale, k,
                                bnd, row_val + xb * k, row_idx + xb * k, redo, redo_count);
             prof_end(st);
@@ -998,7 +1097,7 @@ int run_bidir(hipStream_t st, const float* X, const float* Y, int64_t m, int64_t
             // column finalize: one list per X panel of this chunk; candidates are the chunk's X rows (global ids)
             hipLaunchKernelGGL(zero_words, dim3(1), dim3(64), 0, st, reinterpret_cast<unsigned long long*>(redo_count), 1);
             prof_begin(st, "l2sq_col_finalize");
-            hipLaunchKernelGGL((l2sq_finalize<K1, 1, true>), dim3((unsigned)((n + 3) / 4)), dim3(256), 0, st, Y, X, n, d,
+            hipLaunchKernelGGL((l2sq_finalize<K1, KM, 1, true>), dim3((unsigned)((n + 3) / 4)), dim3(256), 0, st, Y, X, n, d,
                                (int)panels, colpart, db, qb, ynorm, maxima, scale, k, bnd, cval, cidx, redo,
                                redo_count);
             prof_end(st);
@@ -1014,8 +1113,8 @@ int run_bidir(hipStream_t st, const float* X, const float* Y, int64_t m, int64_t
     if (swapped) {
         // columns by a second sweep with the roles swapped: Y chunks are the rows, X is segmented; the
         // finalize keeps the (dot + qb) + db association of the caller's pairs
-        const int64_t ch2 = chunk_rows(n, m, k, false);
-        const DirPlan plan2 = plan_dir(ch2, m);
+        const int64_t ch2 = cp.ch2;
+        const DirPlan plan2 = cp.plan2;
         for (int64_t yb = 0; yb < n; yb += ch2) {
             const int64_t ye = yb + ch2 < n ? yb + ch2 : n;
             const int64_t rows = ye - yb;
@@ -1039,7 +1138,7 @@ int run_bidir(hipStream_t st, const float* X, const float* Y, int64_t m, int64_t
             HM_LAUNCH_CHECK("l2sq_sweep");
             hipLaunchKernelGGL(zero_words, dim3(1), dim3(64), 0, st, reinterpret_cast<unsigned long long*>(redo_count), 1);
             prof_begin(st, "l2sq_col_finalize");
-            hipLaunchKernelGGL((l2sq_finalize<K1, 2, true>), dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, st,
+            hipLaunchKernelGGL((l2sq_finalize<K1, KM, 2, true>), dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, st,
                                Y + yb * d, X, rows, d, 2 * plan2.S, part, db + yb, qb, ynorm + yb, maxima, scale, k,
                                bnd, col_val + yb * k, col_idx + yb * k, redo, redo_count);
             prof_end(st);

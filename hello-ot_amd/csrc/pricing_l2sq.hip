@@ -1,20 +1,20 @@
-// l2^2 pricing scan: C ABI entry points (kernels and the per-K1 drivers live in l2sq_impl.h and the
-// pricing_l2sq_k*.hip translation units, compiled in parallel).
+// l2^2 pricing scan: C ABI entry points (kernels and the drivers live in l2sq_impl.h; the pricing_l2sq_l*_m*.hip
+// translation units instantiate the driver per (partial list size, merged list size) and compile in parallel).
 #include "l2sq_impl.h"
 namespace hm {
-int l2sq_run_k8(L2SQ_RUN_ARGS);
-int l2sq_run_k16(L2SQ_RUN_ARGS);
-int l2sq_run_k40(L2SQ_RUN_ARGS);
+int l2sq_run_l8_m8(L2SQ_RUN_ARGS);
+int l2sq_run_l8_m16(L2SQ_RUN_ARGS);
+int l2sq_run_l16_m16(L2SQ_RUN_ARGS);
+int l2sq_run_l8_m40(L2SQ_RUN_ARGS);
+int l2sq_run_l16_m40(L2SQ_RUN_ARGS);
+int l2sq_run_l40_m40(L2SQ_RUN_ARGS);
 namespace {
 int run_k(L2SQ_RUN_ARGS) {
-    switch (bucket_k1(k)) {
-        case 8:
-            return l2sq_run_k8(L2SQ_RUN_PASS);
-        case 16:
-            return l2sq_run_k16(L2SQ_RUN_PASS);
-        default:
-            return l2sq_run_k40(L2SQ_RUN_PASS);
-    }
+    const CallPlan c = plan_call(m, n, d, k, flags);
+    if (c.km == 8) return l2sq_run_l8_m8(L2SQ_RUN_PASS);
+    if (c.km == 16) return c.kl == 8 ? l2sq_run_l8_m16(L2SQ_RUN_PASS) : l2sq_run_l16_m16(L2SQ_RUN_PASS);
+    if (c.kl == 8) return l2sq_run_l8_m40(L2SQ_RUN_PASS);
+    return c.kl == 16 ? l2sq_run_l16_m40(L2SQ_RUN_PASS) : l2sq_run_l40_m40(L2SQ_RUN_PASS);
 }
 
 }  // namespace
