@@ -60,6 +60,8 @@ constexpr int64_t SWEEP_WGS = 1024;           // target workgroups per sweep lau
 constexpr int64_t RESCAN_SLICE = 512;         // candidates per exact-rescan item (one wave)
 constexpr int64_t RESCAN_ITEMS = 65536;       // (row, slice) items whose partial lists fit the rescan scratch
 constexpr size_t COLPART_CAP = size_t(12) << 30;  // bytes of per-chunk column partial lists
+constexpr int WIDE_ROWS = 8192;               // queued rows per wide pass
+constexpr int WIDE_CAP = 512;                 // candidates a queued row may collect in the wide pass
 
 // fp32 unit roundoff doubled (covers truncating accumulation) and the classic gamma_n bound.
 inline double gamma_fp32(double n) {
@@ -182,13 +184,17 @@ __global__ void l2sq_split_bf16(const float* __restrict__ X, int64_t rows, int64
 // PREC 1: X / Y are their split-bf16 copies (l2sq_split_bf16: d = features padded to 32, row stride ld, groups
 //         of 8 hi then 8 lo bf16 per 32 bytes, rows padded to whole 128-row panels); dot = hi*hi + hi*lo + lo*hi
 //         on v_mfma_f32_32x32x16_bf16.
-template <int K1, bool TWO_LEVEL, bool COLS, int PREC>
+// APPEND (the wide pass of queued rows): no lists, columns or certificate; every candidate j of row r with
+// w >= wthr[r] is appended to wbuf[r * WIDE_CAP + ...] (wcnt[r] counts all of them, also past the capacity).
+template <int K1, bool TWO_LEVEL, bool COLS, int PREC, bool APPEND = false>
 __global__ __launch_bounds__(256) void l2sq_sweep(
     const float* __restrict__ X, const float* __restrict__ Y, int64_t xb, int64_t xe, int64_t n, int d, int ld,
     const float* __restrict__ qb32, const float* __restrict__ db32, const float* __restrict__ p32,
     const float* __restrict__ ge32, float scale, int64_t seg_len, Entry* __restrict__ part,
     Entry* __restrict__ colpart, unsigned int* __restrict__ colthr, double* __restrict__ blockstats, int VEC4,
-    int STATS) {
+    int STATS, const float* __restrict__ wthr = nullptr, int* __restrict__ wcnt = nullptr,
+    int* __restrict__ wbuf = nullptr) {
+    static_assert(!(APPEND && COLS), "the wide pass keeps no column lists");
     __shared__ float sT[2 * STAGE];  // two LDS stages of (X tile, Y tile), 32 features each
     __shared__ float sDB[BY];
     __shared__ float sGE[BY];
@@ -213,7 +219,8 @@ __global__ __launch_bounds__(256) void l2sq_sweep(
 #pragma unroll
     for (int s = 0; s < K1; ++s) { lv[s] = -INFINITY; li[s] = -1; }
 
-    const float qbi = row_ok ? qb32[my_row] : 0.0f;
+    const float qbi = (row_ok && !APPEND) ? qb32[my_row] : 0.0f;
+    const float wt = (APPEND && row_ok) ? wthr[my_row] : INFINITY;
     const float pi = (STATS && row_ok) ? p32[my_row] : 0.0f;
     double num64 = 0.0, den64 = 0.0, cnt64 = 0.0;
     float mx = 0.0f, cmax = 0.0f;
@@ -420,7 +427,12 @@ __global__ __launch_bounds__(256) void l2sq_sweep(
                     const float w = fmaf(scale, tot, dbs[cc]);
                     const int64_t j = ytile + jl0 + cc;
                     const bool ok = row_ok && j < y_end;
-                    if (ok && w > lv[K1 - 1]) {
+                    if (APPEND) {
+                        if (ok && w >= wt) {
+                            const int pos = atomicAdd(&wcnt[my_row], 1);
+                            if (pos < WIDE_CAP) wbuf[my_row * (int64_t)WIDE_CAP + pos] = (int)j;
+                        }
+                    } else if (ok && w > lv[K1 - 1]) {
                         float cv = w;
                         int ci = (int)j;
 #pragma unroll
@@ -491,7 +503,7 @@ __global__ __launch_bounds__(256) void l2sq_sweep(
     }
 
     // lane lists -> part[(seg*rows + local row)*2 + h][K1]
-    if (row_ok) {
+    if (row_ok && !APPEND) {
         Entry* out = part + ((seg * rows + (my_row - xb)) * 2 + h) * K1;
 #pragma unroll
         for (int s = 0; s < K1; ++s) out[s] = Entry{lv[s], li[s]};
@@ -572,7 +584,7 @@ __global__ __launch_bounds__(256) void l2sq_finalize(
     const Entry* __restrict__ lists, const double* __restrict__ abias, const double* __restrict__ bbias,
     const double* __restrict__ anorm, const unsigned long long* __restrict__ bmaxima, double scale, int k,
     BoundArgs bnd, double* __restrict__ out_val, int* __restrict__ out_idx, int* __restrict__ redo,
-    int* __restrict__ redo_count) {
+    float* __restrict__ redo_thr, int* __restrict__ redo_count) {
     static_assert(KL <= KM, "merged lists hold at least one partial list");
     const int lane = threadIdx.x & 63;
     const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -645,9 +657,15 @@ __global__ __launch_bounds__(256) void l2sq_finalize(
     float dropped = full ? tail : -INFINITY;
     if (merge_dropped) dropped = fmaxf(dropped, tw[KM - 1]);
     if ((full || merge_dropped) && (double)dropped >= (double)wk - 2.0 * b) {
+        // queued for the wide pass: a candidate of the exact top-k has sigma >= sigma_k* >= wk - b, hence
+        // w >= wk - 2b (the threshold is rounded down to fp32)
         if (lane == 0) {
             const int slot = atomicAdd(redo_count, 1);
             redo[slot] = (int)row;
+            const double t = (double)wk - 2.0 * b;
+            float t32 = (float)t;
+            if ((double)t32 > t) t32 = nextafterf(t32, -INFINITY);
+            redo_thr[slot] = t32;
         }
         return;
     }
@@ -771,6 +789,110 @@ __global__ void l2sq_rescan_merge(const double* __restrict__ pv, const int* __re
         if (s < k) { out_val[row * k + s] = v[s]; out_idx[row * k + s] = id[s]; }
 }
 
+// Wide pass, step 1: queued rows q0 .. q0+Q-1 of the row side's sweep copy gathered into a compact panel-padded
+// buffer (zero rows past Q), with their thresholds and cleared candidate counters.
+__global__ void l2sq_wide_gather(const float* __restrict__ src, int ld, const int* __restrict__ redo, int q0, int Q,
+                                 int Qpad, const float* __restrict__ redo_thr, float* __restrict__ dst,
+                                 float* __restrict__ thr, int* __restrict__ cnt) {
+    const int64_t total = (int64_t)Qpad * ld;
+    for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t q = e / ld;
+        const int64_t f = e % ld;
+        dst[e] = q < Q ? src[(int64_t)redo[q0 + q] * ld + f] : 0.0f;
+    }
+    for (int q = blockIdx.x * blockDim.x + threadIdx.x; q < Qpad; q += gridDim.x * blockDim.x) {
+        thr[q] = q < Q ? redo_thr[q0 + q] : INFINITY;
+        cnt[q] = 0;
+    }
+}
+
+// Wide pass, step 3: one wave per queued row evaluates the collected candidates with the fixed-order fp64 dot
+// (four at a time, as the rescan) and keeps the exact top-k under the tie rule; a row whose candidates overflowed
+// the buffer goes to the exact full rescan instead.
+template <int K>
+__global__ __launch_bounds__(256) void l2sq_wide_exact(const float* __restrict__ A, const float* __restrict__ B, int d,
+                                                       const double* __restrict__ abias, const double* __restrict__ bbias,
+                                                       double scale, int k, const int* __restrict__ redo, int q0, int Q,
+                                                       const int* __restrict__ cnt, const int* __restrict__ buf,
+                                                       int COLS, int cbase, double* __restrict__ out_val,
+                                                       int* __restrict__ out_idx, int* __restrict__ redo2,
+                                                       int* __restrict__ redo2_count) {
+    const int lane = threadIdx.x & 63;
+    const int q = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (q >= Q) return;  // uniform per wave
+    const int64_t row = redo[q0 + q];
+    const int c = cnt[q];
+    if (c > WIDE_CAP) {
+        if (lane == 0) redo2[atomicAdd(redo2_count, 1)] = (int)row;
+        return;
+    }
+    double v[K];
+    int id[K];
+#pragma unroll
+    for (int s = 0; s < K; ++s) { v[s] = -INFINITY; id[s] = -1; }
+    const float* ar = A + row * (int64_t)d;
+    const int* cand = buf + (int64_t)q * WIDE_CAP;
+    for (int t = 0; t < c; t += 4) {
+        const int j0 = cand[t];
+        const int j1 = t + 1 < c ? cand[t + 1] : j0;
+        const int j2 = t + 2 < c ? cand[t + 2] : j0;
+        const int j3 = t + 3 < c ? cand[t + 3] : j0;
+        const float* b0 = B + (int64_t)j0 * d;
+        const float* b1 = B + (int64_t)j1 * d;
+        const float* b2 = B + (int64_t)j2 * d;
+        const float* b3 = B + (int64_t)j3 * d;
+        double a0 = 0.0, a1 = 0.0, a2 = 0.0, a3 = 0.0;
+#pragma unroll 4
+        for (int f = lane; f < d; f += 64) {
+            const double x = (double)ar[f];
+            a0 = a0 + x * (double)b0[f];
+            a1 = a1 + x * (double)b1[f];
+            a2 = a2 + x * (double)b2[f];
+            a3 = a3 + x * (double)b3[f];
+        }
+        const double dots[4] = {wave_tree_sum(a0), wave_tree_sum(a1), wave_tree_sum(a2), wave_tree_sum(a3)};
+        const int js[4] = {j0, j1, j2, j3};
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            if (t + u < c) {
+                const int j = js[u];
+                const double sdot = scale * dots[u];
+                const double sig = COLS ? (sdot + bbias[j]) + abias[row] : (sdot + abias[row]) + bbias[j];
+                if (sig == sig) put_sorted<K>(v, id, k, sig, cbase + j);
+            }
+        }
+    }
+#pragma unroll
+    for (int s = 0; s < K; ++s)
+        if (s < k && lane == s) {
+            out_val[row * k + s] = v[s];
+            out_idx[row * k + s] = id[s];
+        }
+}
+
+}  // namespace
+
+// Scratch of the wide pass (workspace slices; layout() sizes them).
+struct WideBufs {
+    float* redo_thr;   // [m + n] thresholds of queued rows, by queue slot
+    float* rows;       // [panel_rows(WIDE_ROWS) * ld] gathered sweep rows
+    float* thr;        // [panel_rows(WIDE_ROWS)]
+    int* cnt;          // [panel_rows(WIDE_ROWS)]
+    int* buf;          // [WIDE_ROWS * WIDE_CAP] candidate ids
+    int* redo2;        // [m + n] rows that overflowed WIDE_CAP
+    int* redo2_count;  // [2]
+};
+
+// Resolves the rows a finalize queued (defined in pricing_l2sq.hip): the wide pass over them, then the exact full
+// rescan of rows that overflowed it. A / B are the fp32 row and candidate sides (row stride d), Asw / Bsw their
+// sweep copies (split-bf16 with row stride ld when `split`, else A / B), cand32 the candidates' fp32 biases.
+int wide_resolve(hipStream_t st, bool split, bool two_level, const float* A, const float* Asw, const float* B,
+                 const float* Bsw, int64_t nb, int d, int sd, int ld, const float* cand32, const double* abias,
+                 const double* bbias, double scale, int k, const int* redo, const int* redo_count,
+                 double* out_val, int* out_idx, int cols, int cbase, const WideBufs& w, double* rpv, int* rpi);
+
+namespace {
+
 // merge a chunk's exact column lists into the running ones (both sorted by the tie rule)
 __global__ void l2sq_merge_columns(double* __restrict__ val, int* __restrict__ idx, const double* __restrict__ cval,
                                    const int* __restrict__ cidx, int64_t n, int k, int first) {
@@ -861,23 +983,23 @@ inline int64_t chunk_rows(int64_t m, int64_t n, int kl, bool fused) {
 
 // Y segments per sweep launch: enough workgroups to fill the chip (SWEEP_WGS), and for k > 2 at least 8 so each
 // row has 16 partial lists; at most a quarter of the tiles and 64.
-inline int choose_segments(int64_t m, int64_t n, int k) {
+inline int choose_segments(int64_t m, int64_t n, int k, int cap = 64) {
     const int64_t panels = (m + BX - 1) / BX;
     const int64_t tiles = (n + BY - 1) / BY;
     int64_t s = (SWEEP_WGS + panels - 1) / panels;
     if (k > 2 && s < 8) s = 8;
     const int64_t max_s = tiles / 4 > 0 ? tiles / 4 : 1;
     if (s > max_s) s = max_s;
-    if (s > 64) s = 64;
+    if (s > cap) s = cap;
     if (s < 1) s = 1;
     return (int)s;
 }
 
-inline DirPlan plan_dir(int64_t rows, int64_t cols, int k) {
+inline DirPlan plan_dir(int64_t rows, int64_t cols, int k, int cap = 64) {
     DirPlan p;
     p.rows = rows;
     p.cols = cols;
-    p.S = choose_segments(rows, cols, k);
+    p.S = choose_segments(rows, cols, k, cap);
     const int64_t tiles = (cols + BY - 1) / BY;
     const int64_t tiles_per = (tiles + p.S - 1) / p.S;
     p.seg_len = tiles_per * BY;
@@ -924,7 +1046,7 @@ template <class A>
 void layout(A& a, int64_t m, int64_t n, int d, int k, uint32_t flags, double** xnorm, double** ynorm, float** qb32,
             float** p32, float** db32, float** ge32, unsigned long long** maxima, Entry** part, Entry** colpart,
             unsigned int** colthr, double** cval, int** cidx, double** blockstats, int** redo, int** redo_count,
-            float** xsplit, float** ysplit, double** rpv, int** rpi) {
+            float** xsplit, float** ysplit, double** rpv, int** rpi, WideBufs* wide) {
     const CallPlan c = plan_call(m, n, d, k, flags);
     const int64_t panels = c.ch / BX;
     size_t part_entries = (size_t)c.plan.S * c.ch * 2 * c.kl;
@@ -952,6 +1074,14 @@ void layout(A& a, int64_t m, int64_t n, int d, int k, uint32_t flags, double** x
     *ysplit = a.template take<float>(split ? (size_t)panel_rows(n) * ldw : 1);
     *rpv = a.template take<double>((size_t)RESCAN_ITEMS * k);
     *rpi = a.template take<int>((size_t)RESCAN_ITEMS * k);
+    const int64_t wq = panel_rows(WIDE_ROWS);
+    wide->redo_thr = a.template take<float>((size_t)(m + n));
+    wide->rows = a.template take<float>((size_t)wq * (split ? ldw : (size_t)d));
+    wide->thr = a.template take<float>((size_t)wq);
+    wide->cnt = a.template take<int>((size_t)wq);
+    wide->buf = a.template take<int>((size_t)WIDE_ROWS * WIDE_CAP);
+    wide->redo2 = a.template take<int>((size_t)(m + n));
+    wide->redo2_count = a.template take<int>(2);
 }
 
 // Exact rescan of the rows queued by a finalize: reads the queue length back (one host synchronisation), then
@@ -998,7 +1128,8 @@ int run_bidir(hipStream_t st, const float* X, const float* Y, int64_t m, int64_t
               const unsigned long long* maxima, const float* qb32, const float* db32, const float* p32,
               const float* ge32, Entry* part, Entry* colpart, unsigned int* colthr, double* cval, int* cidx,
               double* blockstats, int* redo, int* redo_count, double* row_val, int* row_idx, double* col_val,
-              int* col_idx, double* stats, float* xsplit, float* ysplit, double* rpv, int* rpi) {
+              int* col_idx, double* stats, float* xsplit, float* ysplit, double* rpv, int* rpi,
+              const WideBufs& wide) {
     // K1: entries per partial list of the sweep; KM: candidates the finalize merges and keeps
     const CallPlan cp = plan_call(m, n, d, k, flags);
     if (cp.kl != K1 || cp.km != KM) return fail(HM_EINVAL, "l2sq pricing: list sizes %d/%d do not match the plan %d/%d", K1, KM, cp.kl, cp.km);
@@ -1086,11 +1217,12 @@ int run_bidir(hipStream_t st, const float* X, const float* Y, int64_t m, int64_t
             prof_begin(st, "l2sq_finalize");
             hipLaunchKernelGGL((l2sq_finalize<K1, KM, 2, false>), dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, st,
                                X + xb * d, Y, rows, d, 2 * plan.S, part, qb + xb, db, xnorm + xb, maxima + 2, scale, k,
-                               bnd, row_val + xb * k, row_idx + xb * k, redo, redo_count);
+                               bnd, row_val + xb * k, row_idx + xb * k, redo, wide.redo_thr, redo_count);
             prof_end(st);
             HM_LAUNCH_CHECK("l2sq_finalize");
-            if (int rc = rescan_exact(st, X + xb * d, Y, n, d, qb + xb, db, scale, k, redo, redo_count, row_val + xb * k,
-                                      row_idx + xb * k, 0, 0, rpv, rpi))
+            if (int rc = wide_resolve(st, split, two_level, X + xb * d, SX + xb * ld, Y, SY, n, d, sd, ld, db32,
+                                      qb + xb, db, scale, k, redo, redo_count, row_val + xb * k, row_idx + xb * k, 0,
+                                      0, wide, rpv, rpi))
                 return rc;
         }
         if (fused) {
@@ -1099,11 +1231,12 @@ int run_bidir(hipStream_t st, const float* X, const float* Y, int64_t m, int64_t
             prof_begin(st, "l2sq_col_finalize");
             hipLaunchKernelGGL((l2sq_finalize<K1, KM, 1, true>), dim3((unsigned)((n + 3) / 4)), dim3(256), 0, st, Y, X, n, d,
                                (int)panels, colpart, db, qb, ynorm, maxima, scale, k, bnd, cval, cidx, redo,
-                               redo_count);
+                               wide.redo_thr, redo_count);
             prof_end(st);
             HM_LAUNCH_CHECK("l2sq_col_finalize");
-            if (int rc = rescan_exact(st, Y, X + xb * d, rows, d, db, qb + xb, scale, k, redo, redo_count, cval, cidx, 1,
-                                      (int)xb, rpv, rpi))
+            if (int rc = wide_resolve(st, split, two_level, Y, SY, X + xb * d, SX + xb * ld, rows, d, sd, ld,
+                                      qb32 + xb, db, qb + xb, scale, k, redo, redo_count, cval, cidx, 1, (int)xb,
+                                      wide, rpv, rpi))
                 return rc;
             hipLaunchKernelGGL(l2sq_merge_columns, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, col_val, col_idx,
                                cval, cidx, n, k, chunk_index == 0 ? 1 : 0);
@@ -1140,11 +1273,12 @@ int run_bidir(hipStream_t st, const float* X, const float* Y, int64_t m, int64_t
             prof_begin(st, "l2sq_col_finalize");
             hipLaunchKernelGGL((l2sq_finalize<K1, KM, 2, true>), dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, st,
                                Y + yb * d, X, rows, d, 2 * plan2.S, part, db + yb, qb, ynorm + yb, maxima, scale, k,
-                               bnd, col_val + yb * k, col_idx + yb * k, redo, redo_count);
+                               bnd, col_val + yb * k, col_idx + yb * k, redo, wide.redo_thr, redo_count);
             prof_end(st);
             HM_LAUNCH_CHECK("l2sq_col_finalize");
-            if (int rc = rescan_exact(st, Y + yb * d, X, m, d, db + yb, qb, scale, k, redo, redo_count, col_val + yb * k,
-                                      col_idx + yb * k, 1, 0, rpv, rpi))
+            if (int rc = wide_resolve(st, split, two_level, Y + yb * d, SY + yb * ld, X, SX, m, d, sd, ld, qb32,
+                                      db + yb, qb, scale, k, redo, redo_count, col_val + yb * k, col_idx + yb * k, 1,
+                                      0, wide, rpv, rpi))
                 return rc;
         }
     }
@@ -1165,7 +1299,8 @@ int run_bidir(hipStream_t st, const float* X, const float* Y, int64_t m, int64_t
         const unsigned long long *maxima, const float *qb32, const float *db32, const float *p32, const float *ge32, \
         ::hm::Entry *part, ::hm::Entry *colpart, unsigned int *colthr, double *cval, int *cidx, double *blockstats, \
         int *redo, int *redo_count, double *row_val, int *row_idx, double *col_val, int *col_idx, double *stats,   \
-        float *xsplit, float *ysplit, double *rpv, int *rpi
+        float *xsplit, float *ysplit, double *rpv, int *rpi, const ::hm::WideBufs &wide
 #define L2SQ_RUN_PASS                                                                                               \
     st, X, Y, m, n, d, k, scale, flags, qb, db, xnorm, ynorm, maxima, qb32, db32, p32, ge32, part, colpart, colthr, \
-        cval, cidx, blockstats, redo, redo_count, row_val, row_idx, col_val, col_idx, stats, xsplit, ysplit, rpv, rpi
+        cval, cidx, blockstats, redo, redo_count, row_val, row_idx, col_val, col_idx, stats, xsplit, ysplit, rpv, rpi, \
+        wide

@@ -18,6 +18,61 @@ int run_k(L2SQ_RUN_ARGS) {
 }
 
 }  // namespace
+
+int wide_resolve(hipStream_t st, bool split, bool two_level, const float* A, const float* Asw, const float* B,
+                 const float* Bsw, int64_t nb, int d, int sd, int ld, const float* cand32, const double* abias,
+                 const double* bbias, double scale, int k, const int* redo, const int* redo_count,
+                 double* out_val, int* out_idx, int cols, int cbase, const WideBufs& w, double* rpv, int* rpi) {
+    int count = 0;
+    HM_HIP(hipMemcpyAsync(&count, redo_count, sizeof(int), hipMemcpyDeviceToHost, st));
+    HM_HIP(hipStreamSynchronize(st));
+    prof_count(cols ? "l2sq_wide_columns" : "l2sq_wide_rows", count);
+    if (count <= 0) return HM_OK;
+    hipLaunchKernelGGL(zero_words, dim3(1), dim3(64), 0, st, reinterpret_cast<unsigned long long*>(w.redo2_count), 1);
+    HM_LAUNCH_CHECK("zero_words");
+    const int gld = split ? ld : d;  // row stride of the gathered sweep rows
+    prof_begin(st, "l2sq_wide");
+    for (int q0 = 0; q0 < count; q0 += WIDE_ROWS) {
+        const int Q = count - q0 < WIDE_ROWS ? count - q0 : WIDE_ROWS;
+        const int Qpad = (int)panel_rows(Q);
+        hipLaunchKernelGGL(l2sq_wide_gather, dim3(2048), dim3(256), 0, st, Asw, gld, redo, q0, Q, Qpad, w.redo_thr,
+                           w.rows, w.thr, w.cnt);
+        HM_LAUNCH_CHECK("l2sq_wide_gather");
+        const DirPlan plan = plan_dir(Qpad, nb, 0, 256);
+        dim3 grid((unsigned)(Qpad / BX), (unsigned)plan.S);
+        const int vec4 = split || (d % 4) == 0;
+#define HM_WIDE(TL, PR)                                                                                             \
+    hipLaunchKernelGGL((l2sq_sweep<8, TL, false, PR, true>), grid, dim3(256), 0, st, w.rows, Bsw, (int64_t)0,        \
+                       (int64_t)Q, nb, sd, gld, (const float*)nullptr, cand32, (const float*)nullptr,               \
+                       (const float*)nullptr, (float)scale, plan.seg_len, (Entry*)nullptr, (Entry*)nullptr,          \
+                       (unsigned int*)nullptr, (double*)nullptr, vec4, 0, w.thr, w.cnt, w.buf)
+        if (split) {
+            if (two_level) HM_WIDE(true, 1);
+            else HM_WIDE(false, 1);
+        } else {
+            if (two_level) HM_WIDE(true, 0);
+            else HM_WIDE(false, 0);
+        }
+#undef HM_WIDE
+        HM_LAUNCH_CHECK("l2sq_sweep (wide)");
+        const unsigned eg = (unsigned)((Q + 3) / 4);
+        if (k <= 2)
+            hipLaunchKernelGGL((l2sq_wide_exact<2>), dim3(eg), dim3(256), 0, st, A, B, d, abias, bbias, scale, k, redo,
+                               q0, Q, w.cnt, w.buf, cols, cbase, out_val, out_idx, w.redo2, w.redo2_count);
+        else if (k <= 8)
+            hipLaunchKernelGGL((l2sq_wide_exact<8>), dim3(eg), dim3(256), 0, st, A, B, d, abias, bbias, scale, k, redo,
+                               q0, Q, w.cnt, w.buf, cols, cbase, out_val, out_idx, w.redo2, w.redo2_count);
+        else
+            hipLaunchKernelGGL((l2sq_wide_exact<32>), dim3(eg), dim3(256), 0, st, A, B, d, abias, bbias, scale, k,
+                               redo, q0, Q, w.cnt, w.buf, cols, cbase, out_val, out_idx, w.redo2, w.redo2_count);
+        HM_LAUNCH_CHECK("l2sq_wide_exact");
+    }
+    prof_end(st);
+    // rows with more than WIDE_CAP candidates near their k-th value: exact scan over all candidates
+    return rescan_exact(st, A, B, nb, d, abias, bbias, scale, k, w.redo2, w.redo2_count, out_val, out_idx, cols, cbase,
+                        rpv, rpi);
+}
+
 }  // namespace hm
 
 using namespace hm;
@@ -34,8 +89,9 @@ extern "C" size_t hm_pricing_l2sq_workspace_bytes(int64_t m, int64_t n, int32_t 
     float *xs, *ys;
     double* rpv;
     int* rpi;
+    WideBufs wide;
     layout(s, m, n, d, k, flags, &a, &b, &c, &e, &f, &g, &mx, &part, &colpart, &thr, &cv, &ci, &bs, &redo, &rc, &xs,
-           &ys, &rpv, &rpi);
+           &ys, &rpv, &rpi, &wide);
     return s.used;
 }
 
@@ -67,8 +123,9 @@ extern "C" int hm_pricing_l2sq(void* stream, const float* X, const float* Y, con
     float *xsplit, *ysplit;
     double* rpv;
     int* rpi;
+    WideBufs wide;
     layout(a, m, n, d, k, flags, &xnorm, &ynorm, &qb32, &p32, &db32, &ge32, &maxima, &part, &colpart, &colthr, &cval,
-           &cidx, &blockstats, &redo, &redo_count, &xsplit, &ysplit, &rpv, &rpi);
+           &cidx, &blockstats, &redo, &redo_count, &xsplit, &ysplit, &rpv, &rpi, &wide);
     hipLaunchKernelGGL(zero_words, dim3(1), dim3(64), 0, st, maxima, 4);
     HM_LAUNCH_CHECK("zero_words");
     // X side: ||x||, qb32, p32 (maxima[0..1] = max||x||, max|qb|); Y side: ||y||, db32, ge32 = q + db
@@ -80,5 +137,5 @@ extern "C" int hm_pricing_l2sq(void* stream, const float* X, const float* Y, con
     HM_LAUNCH_CHECK("l2sq_prep_rows");
     return run_k(st, X, Y, m, n, d, k, scale, flags, qb, db, xnorm, ynorm, maxima, qb32, db32, p32, ge32, part,
                  colpart, colthr, cval, cidx, blockstats, redo, redo_count, row_val, row_idx, col_val, col_idx, stats,
-                 xsplit, ysplit, rpv, rpi);
+                 xsplit, ysplit, rpv, rpi, wide);
 }

@@ -55,6 +55,17 @@ def _to_device(value, device, dtype):
     return torch.as_tensor(np.asarray(value), dtype=dtype, device=device)
 
 
+def _shuffled_features(value, perm, device, consume: bool):
+    """Rows of ``value`` in shuffle order as contiguous fp32 on ``device``. With ``consume`` a contiguous fp32
+    tensor already on the device is reordered in place (the caller's tensor then holds the shuffled rows), like the
+    reference's in-place feature reorder (prewarm.py:177-214): only one temporary copy is alive at a time."""
+    if consume and torch.is_tensor(value) and value.device == device and value.dtype == torch.float32 \
+            and value.is_contiguous():
+        value.copy_(value[perm])
+        return value
+    return _to_device(value, device, torch.float32)[perm].contiguous()
+
+
 @torch.no_grad()
 def solve_problem(problem: Problem, options: SolverOptions, *, max_iterations: int = 100,
                   random_seed: int = 42) -> Result:
@@ -75,8 +86,9 @@ def solve_problem(problem: Problem, options: SolverOptions, *, max_iterations: i
              else _to_device(problem.source_mass, device, torch.float64))[si]
         b = (torch.full((m,), 1.0 / m, dtype=torch.float64, device=device) if problem.target_mass is None
              else _to_device(problem.target_mass, device, torch.float64))[ti]
-        x = _to_device(problem.source_points, device, torch.float32)[si].contiguous()
-        y = _to_device(problem.target_points, device, torch.float32)[ti].contiguous()
+        consume = bool(options.consume_input_features)
+        x = _shuffled_features(problem.source_points, si, device, consume)
+        y = _shuffled_features(problem.target_points, ti, device, consume)
         full = Cost.create(x, y, problem.cost_type)
         sizes = level_sizes(n, m, options.coarsest_size_threshold, options.split_count)
         levels, previous, triggers = [], None, []

@@ -48,19 +48,28 @@ def _workspace(nbytes: int, device) -> torch.Tensor:
     return torch.empty(max(int(nbytes), 256), dtype=torch.uint8, device=device)
 
 
-SWEEP_PRECISIONS = ("fp32", "bf16x3")
+SWEEP_PRECISIONS = ("auto", "fp32", "bf16x3")
+SPLIT_MIN_D = 256  # "auto" sweeps on split-bf16 MFMA from this feature count on
+
+
+def sweep_precision(precision: str, d: int) -> str:
+    if precision not in SWEEP_PRECISIONS:
+        raise ValueError(f"precision must be one of {SWEEP_PRECISIONS}")
+    if precision == "auto":
+        return "bf16x3" if d >= SPLIT_MIN_D else "fp32"
+    return precision
 
 
 def pricing_l2sq(x, y, nx, ny, qb, dbb, k, *, dot_scale=2.0, rows=True, cols=True, stats=True, linf=False,
-                 precision="fp32"):
+                 precision="auto"):
     """Raw l2^2 pricing: returns (row_vals, row_idx, col_vals, col_idx, stats5) with None for skipped parts.
 
     ``stats5`` = (num, den, count, max sigma+, max|cost|); max|cost| is 0 unless ``linf``. ``precision`` picks the
-    candidate sweep: ``"fp32"`` MFMA or ``"bf16x3"`` split-bf16 MFMA (three products); both feed the same exact
-    fp64 re-evaluation, so the outputs are identical and only the speed (and the rescan rate) differs.
+    candidate sweep: ``"fp32"`` MFMA, ``"bf16x3"`` split-bf16 MFMA (three products) or ``"auto"`` (split-bf16 from
+    d = SPLIT_MIN_D on); all feed the same exact fp64 re-evaluation, so the outputs are identical and only the
+    speed (and the rescan rate) differs.
     """
-    if precision not in SWEEP_PRECISIONS:
-        raise ValueError(f"precision must be one of {SWEEP_PRECISIONS}")
+    precision = sweep_precision(precision, int(x.shape[1]))
     lib = _lib.load()
     x, y, nx, ny, qb, dbb = map(_c, (x, y, nx, ny, qb, dbb))
     m, n, d = x.shape[0], y.shape[0], x.shape[1]

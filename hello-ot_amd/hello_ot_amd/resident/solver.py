@@ -95,6 +95,11 @@ def solve_leaf(cost: Cost, a, b, level_index: int, options, max_iterations: int)
     return support, dual, LevelResult(level_index, "coarsest", n, m, level.initialization, stats, elapsed), level
 
 
+def _progress(options, message: str) -> None:
+    if options.verbose == "detailed":
+        print(f"[hello-mi355x] {message}", file=sys.stderr, flush=True)
+
+
 def initialize(cost: Cost, a, b, previous, known_side, options):
     """Dual propagation + directional assignment + northwest basis (gpu_resident/solver.py:38-64)."""
     started = time.perf_counter()
@@ -113,11 +118,13 @@ def initialize(cost: Cost, a, b, previous, known_side, options):
         xv, xi, _, _, _ = cost.scan(dual, k, direction="source")
         dual[:n] = -xv[:, 0]               # c-transform: f_i = min_j (c_ij - g_j)
         propagation = time.perf_counter() - started
+        _progress(options, f"init {n}x{m}: source c-transform scan {propagation:.3f}s")
         _, _, yv, yi, _ = cost.scan(dual, k, direction="target")
     elif known_side == "source":
         _, _, yv, yi, _ = cost.scan(dual, k, direction="target")
         dual[n:] = -yv[:, 0]
         propagation = time.perf_counter() - started
+        _progress(options, f"init {n}x{m}: target c-transform scan {propagation:.3f}s")
         xv, xi, _, _, _ = cost.scan(dual, k, direction="source")
     else:
         propagation = 0.0
@@ -127,6 +134,7 @@ def initialize(cost: Cost, a, b, previous, known_side, options):
     support = Support.initial(candidates, a, b)
     _sync()
     total = time.perf_counter() - started
+    _progress(options, f"init {n}x{m}: {len(support.keys)} initial edges {total:.3f}s")
     stats = InitializationStats(total, propagation, assigned, total - assigned, known_side, k, len(candidates),
                                 None, len(support.keys) - len(candidates), len(support.keys))
     return support, dual, stats
@@ -150,6 +158,8 @@ def refine(cost: Cost, a, b, previous, known_side, options, level_index, max_ite
         t0 = time.perf_counter()
         dual, lp = support.solve_lp(cost, a, b, dual, tol)
         lp_seconds = time.perf_counter() - t0
+        _progress(options, f"level={level_index} iteration={index} lp {lp_seconds:.3f}s support={before} "
+                           f"pdhg_iters={lp.iterations}")
         t0 = time.perf_counter()
         xv, xi, yv, yi, metrics = cost.scan(dual, options.pricing_topk, certificate=True)
         scan_seconds = time.perf_counter() - t0
@@ -177,9 +187,8 @@ def refine(cost: Cost, a, b, previous, known_side, options, level_index, max_ite
             BudgetedPruningStats(prune_seconds, after, len(support.keys), budget, after > budget),
             ActiveSupportStats(before, after, len(support.keys), peak),
             ConvergenceStats(metrics["l2"], tol, converged, metrics["l2"], metrics["linf"], metrics["max"], "l2")))
-        if options.verbose == "detailed":
-            print(f"[hello-mi355x] level={level_index} iteration={index} support={before} "
-                  f"dual_l2={metrics['l2']:.3e} lp_iters={lp.iterations}", file=sys.stderr)
+        _progress(options, f"level={level_index} iteration={index} scan {scan_seconds:.3f}s "
+                           f"dual_l2={metrics['l2']:.3e} added={added_count} support={len(support.keys)}")
         if converged:
             break
     converged = bool(history and history[-1].convergence.passed)

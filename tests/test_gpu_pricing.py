@@ -118,6 +118,36 @@ def test_l2sq_chunked_sides_and_ties(cuda, m, n, d, k, integer, precision):
     _assert_stats(st, ost, STATS_RTOL[precision])
 
 
+@pytest.mark.parametrize("precision", ["fp32", "bf16x3"])
+@pytest.mark.parametrize("copies", [400, 1500])
+def test_l2sq_dense_near_ties_resolved_exactly(cuda, precision, copies):
+    # `copies` target rows sit within 1e-4 of one point the queries also sit near: every query row has hundreds
+    # of candidates inside twice the sweep's error bound. 400 are resolved by the wide pass (under its 512-candidate
+    # capacity), 1500 overflow it into the exact full rescan; both must give the oracle's exact lists.
+    rng = np.random.default_rng(copies)
+    m, n, d, k = 40, 2000, 300, 8
+    base = rng.standard_normal(d).astype(np.float32)
+    X = (base + 1e-3 * rng.standard_normal((m, d))).astype(np.float32)
+    Y = (3.0 * rng.standard_normal((n, d))).astype(np.float32)
+    Y[:copies] = (base + 1e-4 * rng.standard_normal((copies, d))).astype(np.float32)
+    p = (X.astype(np.float64) ** 2).sum(1)
+    q = (Y.astype(np.float64) ** 2).sum(1)
+    qb, db = -p, -q
+    orv, ori, ocv, oci, ost = oracle.l2sq_scan(X, Y, p, q, qb, db, k, 2.0)
+    rv, ri, cv, ci, st = pricing_l2sq(*_to(cuda, X, Y, p, q, qb, db), k, linf=True, precision=precision)
+    np.testing.assert_array_equal(ri.cpu().numpy(), ori)
+    np.testing.assert_array_equal(rv.cpu().numpy(), orv)
+    np.testing.assert_array_equal(ci.cpu().numpy(), oci)
+    np.testing.assert_array_equal(cv.cpu().numpy(), ocv)
+    # Certificate: every pair has sigma within the sweep's error bound of 0 here (exactly, all sigma < 0), so a few
+    # fp32 scores round positive; their mass stays far below the tolerance scale of the relative dual
+    # infeasibility sqrt(num) / (1 + sqrt(den)). The cost sum and the (exact) maximum violation must agree.
+    gpu = st.cpu().numpy()
+    np.testing.assert_allclose(gpu[1], ost[1], rtol=STATS_RTOL[precision])
+    assert gpu[3] == ost[3]
+    assert np.sqrt(gpu[0]) / (1.0 + np.sqrt(gpu[1])) < 1e-4
+
+
 def test_l2sq_all_equal_scores_take_lowest_indices(cuda):
     # every pair ties exactly: integer-valued identical points -> every row's top-k is columns 0..k-1
     m, n, d, k = 70, 500, 4, 8
