@@ -30,6 +30,7 @@ import numpy as np  # noqa: E402
 import torch  # noqa: E402
 
 PEAK_FP32_MFMA = 157.3e12   # MI355X dense fp32 matrix FLOP/s
+PEAK_BF16_MFMA = 2.5e15     # MI355X dense bf16 matrix FLOP/s
 PEAK_HBM = 8.0e12           # MI355X HBM3E bytes/s
 PEAK_VALU_OPS = 256 * 64 * 2.4e9  # non-packed fp32 VALU lane-ops/s (256 CU x 64 lanes/clk x 2.4 GHz)
 
@@ -37,6 +38,21 @@ TRAFFIC_PROFILE = ROOT / "profiles" / "l2sq_sweep_c5_chunk8192.md"
 
 C5_N = 1_280_000
 C5_D = 8192
+
+
+def roofline(precision, achieved):
+    """Roofline of the sweep kernel. `achieved` is the algorithmic rate, 2*d flop per pair over the sweep's mean
+    launch time. The split-bf16 sweep executes three bf16 products per feature (hi*hi + hi*lo + lo*hi), so its
+    MFMA work is 3 x the algorithmic flops, held against the bf16 matrix peak; the fp32 sweep's work is the
+    algorithmic flops against the fp32 matrix peak."""
+    if precision == "bf16x3":
+        executed, peak, unit_work = 3.0 * achieved, PEAK_BF16_MFMA, "3 bf16 products x 2*d flop per pair"
+    else:
+        executed, peak, unit_work = achieved, PEAK_FP32_MFMA, "2*d flop per pair"
+    return {"bound": "mfma", "achieved": executed / 1e12, "peak": peak / 1e12, "unit": "TFLOP/s",
+            "frac": executed / peak, "traffic": sweep_traffic(), "traffic_source": TRAFFIC_PROFILE.name,
+            "kernel": "l2sq_sweep", "sweep": precision, "work_per_pair": unit_work,
+            "algorithmic_tflops": achieved / 1e12, "algorithmic_flops_per_pair": 2 * C5_D}
 
 
 def sweep_traffic():
@@ -113,16 +129,17 @@ def c5_inputs(dev, chunk):
     return X, Y, p, q, f, g
 
 
-def bench_c5(dev, chunk, steps, warmup):
+def bench_c5(dev, chunk, steps, warmup, inputs=None, precision="auto"):
     from hello_ot_amd import _lib
     from hello_ot_amd.kernels.generic_scan import pricing_l2sq
 
-    X, Y, p, q, f, g = c5_inputs(dev, chunk)
+    X, Y, p, q, f, g = c5_inputs(dev, chunk) if inputs is None else inputs
     qb, db = f - p, g - q
     k = 2
 
     def step():
-        return pricing_l2sq(X, Y, p, q, qb, db, k, dot_scale=2.0, rows=True, cols=True, stats=True, linf=True)
+        return pricing_l2sq(X, Y, p, q, qb, db, k, dot_scale=2.0, rows=True, cols=True, stats=True, linf=True,
+                            precision=precision)
 
     log(f"[bench] C5 chunk {chunk} x {C5_N}, d={C5_D}, k={k}: warmup {warmup}, steps {steps}")
     for _ in range(warmup):
@@ -148,8 +165,7 @@ def bench_c5(dev, chunk, steps, warmup):
         "finalize_ms_avg": fin_ms / max(fins, 1), "rescan_ms_total": res_ms,
         "positive_pairs": float(st[2]), "max_violation": float(st[3]),
     }
-    del X, Y, p, q, f, g, qb, db, out
-    torch.cuda.empty_cache()
+    del qb, db, out
     return sec, pairs, achieved, info
 
 
@@ -216,7 +232,8 @@ def bench_c2(dev, steps=3):
     qb, db = f - p, g - q
     out = {}
     for name, kw in (("rows", dict(rows=True, cols=False, stats=False)),
-                     ("bidir_stats", dict(rows=True, cols=True, stats=True, linf=True))):
+                     ("bidir_stats", dict(rows=True, cols=True, stats=True, linf=True)),
+                     ("bidir_stats_bf16x3", dict(rows=True, cols=True, stats=True, linf=True, precision="bf16x3"))):
         fn = lambda: pricing_l2sq(X, Y, p, q, qb, db, k, **kw)  # noqa: E731
         fn()
         sync()
@@ -441,8 +458,21 @@ def main():
         print(json.dumps({"metric": "C5 solve seconds to relative dual infeasibility 1e-6 (l2^2, d=8192)",
                           **bench_c5_solve(dev, args.c5_solve)}), flush=True)
         return
-    sec, pairs, achieved, info = bench_c5(dev, args.chunk, args.steps, args.warmup)
+    from hello_ot_amd.kernels.generic_scan import sweep_precision
+
+    inputs = c5_inputs(dev, args.chunk)
+    precision = sweep_precision("auto", C5_D)
+    sec, pairs, achieved, info = bench_c5(dev, args.chunk, args.steps, args.warmup, inputs, precision)
     extras = {}
+    if not args.no_extras and precision != "fp32":
+        # the same step on the fp32 MFMA sweep (identical outputs), against the fp32 matrix peak
+        log("[bench] C5 step on the fp32 sweep ...")
+        s32, _, a32, i32 = bench_c5(dev, args.chunk, args.steps, 0, inputs, "fp32")
+        extras["c5_step_fp32_sweep"] = {"pairs_per_s": pairs / s32, "ms_per_step": s32 * 1e3,
+                                        "sweep_ms_avg": i32["sweep_ms_avg"], "sweep_tflops": a32 / 1e12,
+                                        "sweep_mfma_frac": a32 / PEAK_FP32_MFMA}
+    del inputs
+    torch.cuda.empty_cache()
     if not args.no_extras:
         log("[bench] C2 ...")
         extras["c2_scan_131072x131072_d64_k8"] = bench_c2(dev)
@@ -467,15 +497,12 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
+        "dtype": "bf16x3+f64" if precision == "bf16x3" else "f32+f64",
         "data": "synthetic 64-component Gaussian mixtures (C5 recipe), generated on device",
         "config": {"workload": f"C5 pricing step: {args.chunk} query rows x 1,280,000 resident rows, d=8192, k=2, "
                                "rows+cols top-k + certificate", "chunk": args.chunk, "n_resident": C5_N,
                    "d": C5_D, "k": 2},
-        "roofline": {"bound": "mfma", "achieved": achieved / 1e12, "peak": PEAK_FP32_MFMA / 1e12,
-                     "unit": "TFLOP/s", "frac": achieved / PEAK_FP32_MFMA, "traffic": sweep_traffic(),
-                     "traffic_source": TRAFFIC_PROFILE.name,
-                     "kernel": "l2sq_sweep", "flops_per_pair": 2 * C5_D},
+        "roofline": roofline(precision, achieved),
         "cpu_baseline": cpu,
         "detail": info,
         "extras": extras,

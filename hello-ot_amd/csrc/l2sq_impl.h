@@ -57,11 +57,15 @@ constexpr int64_t CHUNK_MAX = 65536;          // X rows per internal chunk
 constexpr int FUSE_MIN_D = 256;               // columns ride on the row sweep from this d on (below it the
                                               // per-tile column epilogue outweighs the MFMA work: two sweeps)
 constexpr int64_t SWEEP_WGS = 1024;           // target workgroups per sweep launch (sets the Y segments)
+constexpr int64_t SWEEP_CUS = 256;            // CUs of an MI355X: one sweep workgroup each at a time
 constexpr int64_t RESCAN_SLICE = 512;         // candidates per exact-rescan item (one wave)
 constexpr int64_t RESCAN_ITEMS = 65536;       // (row, slice) items whose partial lists fit the rescan scratch
 constexpr size_t COLPART_CAP = size_t(12) << 30;  // bytes of per-chunk column partial lists
-constexpr int WIDE_ROWS = 8192;               // queued rows per wide pass
-constexpr int WIDE_CAP = 512;                 // candidates a queued row may collect in the wide pass
+constexpr int64_t WIDE_BUF = int64_t(1) << 22;  // candidate ids per wide-pass batch (rows x capacity)
+constexpr int WIDE_ROWS = 8192;               // queued rows per batch of the first wide round (capacity 512)
+constexpr int WIDE_CAP1 = 512;                // candidates a row may collect in the first wide round
+constexpr int WIDE_CAP2 = 16384;              // ... in the second round (rows that overflowed the first)
+constexpr int WIDE_SLICE = 128;               // collected candidates per exact-evaluation item (one wave)
 
 // fp32 unit roundoff doubled (covers truncating accumulation) and the classic gamma_n bound.
 inline double gamma_fp32(double n) {
@@ -180,21 +184,52 @@ __global__ void l2sq_split_bf16(const float* __restrict__ X, int64_t rows, int64
 // -------------------------------------------------------------------------------------------------
 // sweep over X rows [xb, xe) of one chunk
 // -------------------------------------------------------------------------------------------------
+// Workgroup -> (X panel, Y segment). Workgroups reach the 8 XCDs round-robin in launch order, so XCD x runs
+// workgroups x, x + 8, x + 16, .... Up to 64 panels the order is panel-major (workgroup L = panel + P * seg): with
+// all panels in flight each panel stays on one XCD and the segments in flight are few. With more panels, the 32
+// workgroups an XCD runs at a time (one per CU) form a block of 8 panels x 4 segments and the 8 XCDs' blocks
+// step through the segment groups of the same panel groups, so the panels in flight stay few and their features
+// stay in the last-level cache across Y tiles (measured at d = 8192: 15% faster for 500 panels, 8% slower for
+// 64). Grid: sweep_grid(P, S) workgroups; the padding ones exit at once.
+constexpr int MAP_PANELS = 64;  // panel-major order up to this many panels
+constexpr int MAP_BP = 8, MAP_BS = 4;  // block of one XCD's 32 concurrent workgroups
+__host__ __device__ inline void sweep_block(int64_t L, int P, int S, int64_t& panel, int64_t& seg) {
+    if (P <= MAP_PANELS) {
+        panel = L % P;
+        seg = L / P;
+        return;
+    }
+    const int64_t x = L & 7, t = L >> 3;
+    const int64_t B = (t >> 5) * 8 + x, i = t & 31;
+    const int64_t SG = (S + MAP_BS - 1) / MAP_BS;
+    panel = (B / SG) * MAP_BP + (i % MAP_BP);
+    seg = (B % SG) * MAP_BS + (i / MAP_BP);
+}
+
+inline unsigned sweep_grid(int64_t P, int64_t S) {
+    if (P <= MAP_PANELS) return (unsigned)(P * S);
+    const int64_t blocks = ((P + MAP_BP - 1) / MAP_BP) * ((S + MAP_BS - 1) / MAP_BS);
+    return (unsigned)((blocks + 7) / 8 * 8 * 32);
+}
+
 // PREC 0: X / Y are the fp32 features (row stride ld = d), products on v_mfma_f32_32x32x2f32.
 // PREC 1: X / Y are their split-bf16 copies (l2sq_split_bf16: d = features padded to 32, row stride ld, groups
 //         of 8 hi then 8 lo bf16 per 32 bytes, rows padded to whole 128-row panels); dot = hi*hi + hi*lo + lo*hi
 //         on v_mfma_f32_32x32x16_bf16.
 // APPEND (the wide pass of queued rows): no lists, columns or certificate; every candidate j of row r with
-// w >= wthr[r] is appended to wbuf[r * WIDE_CAP + ...] (wcnt[r] counts all of them, also past the capacity).
+// w >= wthr[r] is appended to wbuf[r * wcap + ...] (wcnt[r] counts all of them, also past the capacity).
 template <int K1, bool TWO_LEVEL, bool COLS, int PREC, bool APPEND = false>
 __global__ __launch_bounds__(256) void l2sq_sweep(
     const float* __restrict__ X, const float* __restrict__ Y, int64_t xb, int64_t xe, int64_t n, int d, int ld,
     const float* __restrict__ qb32, const float* __restrict__ db32, const float* __restrict__ p32,
-    const float* __restrict__ ge32, float scale, int64_t seg_len, Entry* __restrict__ part,
+    const float* __restrict__ ge32, float scale, int64_t seg_len, int P, int S, Entry* __restrict__ part,
     Entry* __restrict__ colpart, unsigned int* __restrict__ colthr, double* __restrict__ blockstats, int VEC4,
     int STATS, const float* __restrict__ wthr = nullptr, int* __restrict__ wcnt = nullptr,
-    int* __restrict__ wbuf = nullptr) {
+    int* __restrict__ wbuf = nullptr, int wcap = 0) {
     static_assert(!(APPEND && COLS), "the wide pass keeps no column lists");
+    int64_t panel, seg;
+    sweep_block(blockIdx.x, P, S, panel, seg);
+    if (panel >= P || seg >= S) return;  // grid padding (uniform per workgroup, before any barrier)
     __shared__ float sT[2 * STAGE];  // two LDS stages of (X tile, Y tile), 32 features each
     __shared__ float sDB[BY];
     __shared__ float sGE[BY];
@@ -207,8 +242,7 @@ __global__ __launch_bounds__(256) void l2sq_sweep(
     const int h = lane >> 5;    // which half of the 2-wide MFMA k slot
     const int r = lane & 31;    // X row within the wave's 32-row block
     const int64_t rows = xe - xb;
-    const int64_t x0 = xb + (int64_t)blockIdx.x * BX;
-    const int64_t seg = blockIdx.y;
+    const int64_t x0 = xb + panel * BX;
     const int64_t y_begin = seg * seg_len;
     const int64_t y_end = (y_begin + seg_len < n) ? (y_begin + seg_len) : n;
     const int64_t my_row = x0 + wave * 32 + r;
@@ -430,7 +464,7 @@ __global__ __launch_bounds__(256) void l2sq_sweep(
                     if (APPEND) {
                         if (ok && w >= wt) {
                             const int pos = atomicAdd(&wcnt[my_row], 1);
-                            if (pos < WIDE_CAP) wbuf[my_row * (int64_t)WIDE_CAP + pos] = (int)j;
+                            if (pos < wcap) wbuf[my_row * (int64_t)wcap + pos] = (int)j;
                         }
                     } else if (ok && w > lv[K1 - 1]) {
                         float cv = w;
@@ -493,7 +527,7 @@ __global__ __launch_bounds__(256) void l2sq_sweep(
                     insert_e<K1>(cw, cidx, pv, pi2);
             }
             if (half == 0 && j < y_end) {
-                Entry* dst = colpart + ((int64_t)blockIdx.x * n + j) * K1;
+                Entry* dst = colpart + (panel * n + j) * K1;
 #pragma unroll
                 for (int s = 0; s < K1; ++s) dst[s] = Entry{cw[s], cidx[s]};
                 if (cidx[K1 - 1] >= 0) atomicMax(&colthr[j], float_key(cw[K1 - 1]));
@@ -528,7 +562,7 @@ __global__ __launch_bounds__(256) void l2sq_sweep(
                 o[e] = sRed[0][e];
                 for (int w = 1; w < 4; ++w) o[e] = (e >= 3) ? fmax(o[e], sRed[w][e]) : o[e] + sRed[w][e];
             }
-            double* dst = blockstats + ((int64_t)blockIdx.y * gridDim.x + blockIdx.x) * 5;
+            double* dst = blockstats + (seg * P + panel) * 5;
             for (int e = 0; e < 5; ++e) dst[e] = o[e];
         }
     }
@@ -806,81 +840,117 @@ __global__ void l2sq_wide_gather(const float* __restrict__ src, int ld, const in
     }
 }
 
-// Wide pass, step 3: one wave per queued row evaluates the collected candidates with the fixed-order fp64 dot
-// (four at a time, as the rescan) and keeps the exact top-k under the tie rule; a row whose candidates overflowed
-// the buffer goes to the exact full rescan instead.
+// Wide pass, step 3: item (row q, slice of its collected candidates) is one wave; it evaluates WIDE_SLICE
+// candidates with the fixed-order fp64 dot (four at a time, as the rescan) and keeps their exact top-k under the
+// tie rule in pv / pi. A row whose candidates overflowed the capacity yields empty lists (it goes to the next
+// round, see l2sq_wide_merge).
 template <int K>
-__global__ __launch_bounds__(256) void l2sq_wide_exact(const float* __restrict__ A, const float* __restrict__ B, int d,
-                                                       const double* __restrict__ abias, const double* __restrict__ bbias,
-                                                       double scale, int k, const int* __restrict__ redo, int q0, int Q,
-                                                       const int* __restrict__ cnt, const int* __restrict__ buf,
-                                                       int COLS, int cbase, double* __restrict__ out_val,
-                                                       int* __restrict__ out_idx, int* __restrict__ redo2,
-                                                       int* __restrict__ redo2_count) {
+__global__ __launch_bounds__(256) void l2sq_wide_slices(const float* __restrict__ A, const float* __restrict__ B, int d,
+                                                        const double* __restrict__ abias,
+                                                        const double* __restrict__ bbias, double scale, int k,
+                                                        const int* __restrict__ queue, int q0, int Q,
+                                                        const int* __restrict__ cnt, const int* __restrict__ buf,
+                                                        int cap, int spr, int COLS, int cbase, double* __restrict__ pv,
+                                                        int* __restrict__ pi) {
     const int lane = threadIdx.x & 63;
-    const int q = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (q >= Q) return;  // uniform per wave
-    const int64_t row = redo[q0 + q];
-    const int c = cnt[q];
-    if (c > WIDE_CAP) {
-        if (lane == 0) redo2[atomicAdd(redo2_count, 1)] = (int)row;
+    const int64_t items = (int64_t)Q * spr;
+    for (int64_t item = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); item < items; item += (int64_t)gridDim.x * 4) {
+        const int q = (int)(item / spr);
+        const int sl = (int)(item % spr);
+        const int c = cnt[q];
+        const int t0 = sl * WIDE_SLICE;
+        const int t1 = c > cap ? t0 : (c < t0 + WIDE_SLICE ? c : t0 + WIDE_SLICE);
+        const int64_t row = queue[q0 + q];
+        const float* ar = A + row * (int64_t)d;
+        const int* cand = buf + (int64_t)q * cap;
+        double v[K];
+        int id[K];
+#pragma unroll
+        for (int s = 0; s < K; ++s) { v[s] = -INFINITY; id[s] = -1; }
+        for (int t = t0; t < t1; t += 4) {
+            const int j0 = cand[t];
+            const int j1 = t + 1 < t1 ? cand[t + 1] : j0;
+            const int j2 = t + 2 < t1 ? cand[t + 2] : j0;
+            const int j3 = t + 3 < t1 ? cand[t + 3] : j0;
+            const float* b0 = B + (int64_t)j0 * d;
+            const float* b1 = B + (int64_t)j1 * d;
+            const float* b2 = B + (int64_t)j2 * d;
+            const float* b3 = B + (int64_t)j3 * d;
+            double a0 = 0.0, a1 = 0.0, a2 = 0.0, a3 = 0.0;
+#pragma unroll 4
+            for (int f = lane; f < d; f += 64) {
+                const double x = (double)ar[f];
+                a0 = a0 + x * (double)b0[f];
+                a1 = a1 + x * (double)b1[f];
+                a2 = a2 + x * (double)b2[f];
+                a3 = a3 + x * (double)b3[f];
+            }
+            const double dots[4] = {wave_tree_sum(a0), wave_tree_sum(a1), wave_tree_sum(a2), wave_tree_sum(a3)};
+            const int js[4] = {j0, j1, j2, j3};
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                if (t + u < t1) {
+                    const int j = js[u];
+                    const double sdot = scale * dots[u];
+                    const double sig = COLS ? (sdot + bbias[j]) + abias[row] : (sdot + abias[row]) + bbias[j];
+                    if (sig == sig) put_sorted<K>(v, id, k, sig, cbase + j);
+                }
+            }
+        }
+#pragma unroll
+        for (int s = 0; s < K; ++s)
+            if (s < k && lane == s) {
+                pv[item * k + s] = v[s];
+                pi[item * k + s] = id[s];
+            }
+    }
+}
+
+// Wide pass, step 4: one thread per row merges its slices' lists into the output, or passes a row whose
+// candidates overflowed the capacity (and its threshold) on to the next round's queue.
+template <int K>
+__global__ void l2sq_wide_merge(const double* __restrict__ pv, const int* __restrict__ pi, int Q, int spr, int k,
+                                const int* __restrict__ cnt, int cap, const int* __restrict__ queue,
+                                const float* __restrict__ thr, int q0, double* __restrict__ out_val,
+                                int* __restrict__ out_idx, int* __restrict__ next, float* __restrict__ next_thr,
+                                int* __restrict__ next_count) {
+    const int q = blockIdx.x * blockDim.x + threadIdx.x;
+    if (q >= Q) return;
+    const int64_t row = queue[q0 + q];
+    if (cnt[q] > cap) {
+        const int slot = atomicAdd(next_count, 1);
+        next[slot] = (int)row;
+        next_thr[slot] = thr[q];
         return;
     }
     double v[K];
     int id[K];
 #pragma unroll
     for (int s = 0; s < K; ++s) { v[s] = -INFINITY; id[s] = -1; }
-    const float* ar = A + row * (int64_t)d;
-    const int* cand = buf + (int64_t)q * WIDE_CAP;
-    for (int t = 0; t < c; t += 4) {
-        const int j0 = cand[t];
-        const int j1 = t + 1 < c ? cand[t + 1] : j0;
-        const int j2 = t + 2 < c ? cand[t + 2] : j0;
-        const int j3 = t + 3 < c ? cand[t + 3] : j0;
-        const float* b0 = B + (int64_t)j0 * d;
-        const float* b1 = B + (int64_t)j1 * d;
-        const float* b2 = B + (int64_t)j2 * d;
-        const float* b3 = B + (int64_t)j3 * d;
-        double a0 = 0.0, a1 = 0.0, a2 = 0.0, a3 = 0.0;
-#pragma unroll 4
-        for (int f = lane; f < d; f += 64) {
-            const double x = (double)ar[f];
-            a0 = a0 + x * (double)b0[f];
-            a1 = a1 + x * (double)b1[f];
-            a2 = a2 + x * (double)b2[f];
-            a3 = a3 + x * (double)b3[f];
-        }
-        const double dots[4] = {wave_tree_sum(a0), wave_tree_sum(a1), wave_tree_sum(a2), wave_tree_sum(a3)};
-        const int js[4] = {j0, j1, j2, j3};
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            if (t + u < c) {
-                const int j = js[u];
-                const double sdot = scale * dots[u];
-                const double sig = COLS ? (sdot + bbias[j]) + abias[row] : (sdot + abias[row]) + bbias[j];
-                if (sig == sig) put_sorted<K>(v, id, k, sig, cbase + j);
-            }
-        }
+    for (int sl = 0; sl < spr; ++sl) {
+        const int64_t base = ((int64_t)q * spr + sl) * k;
+        for (int s = 0; s < k; ++s)
+            if (pi[base + s] >= 0) put_sorted<K>(v, id, k, pv[base + s], pi[base + s]);
     }
 #pragma unroll
     for (int s = 0; s < K; ++s)
-        if (s < k && lane == s) {
-            out_val[row * k + s] = v[s];
-            out_idx[row * k + s] = id[s];
-        }
+        if (s < k) { out_val[row * k + s] = v[s]; out_idx[row * k + s] = id[s]; }
 }
 
 }  // namespace
 
 // Scratch of the wide pass (workspace slices; layout() sizes them).
 struct WideBufs {
-    float* redo_thr;   // [m + n] thresholds of queued rows, by queue slot
+    float* redo_thr;   // [m + n] thresholds of the rows a finalize queued, by queue slot
     float* rows;       // [panel_rows(WIDE_ROWS) * ld] gathered sweep rows
     float* thr;        // [panel_rows(WIDE_ROWS)]
     int* cnt;          // [panel_rows(WIDE_ROWS)]
-    int* buf;          // [WIDE_ROWS * WIDE_CAP] candidate ids
-    int* redo2;        // [m + n] rows that overflowed WIDE_CAP
-    int* redo2_count;  // [2]
+    int* buf;          // [WIDE_BUF] candidate ids
+    int* redo2;        // [m + n] rows that overflowed the first round, with
+    float* redo2_thr;  // [m + n] their thresholds
+    int* redo3;        // [m + n] rows that overflowed the second round (exact full rescan)
+    float* redo3_thr;  // [m + n]
+    int* counts;       // [4]: redo2 and redo3 lengths
 };
 
 // Resolves the rows a finalize queued (defined in pricing_l2sq.hip): the wide pass over them, then the exact full
@@ -983,16 +1053,30 @@ inline int64_t chunk_rows(int64_t m, int64_t n, int kl, bool fused) {
 
 // Y segments per sweep launch: enough workgroups to fill the chip (SWEEP_WGS), and for k > 2 at least 8 so each
 // row has 16 partial lists; at most a quarter of the tiles and 64.
+// Y segments per sweep launch: enough workgroups to fill the chip (SWEEP_WGS), and for k > 2 at least 8 so each
+// row has 16 partial lists; at most a quarter of the tiles and `cap`. Among up to twice that many segments the
+// first whose workgroups fill whole rounds of the CUs (within 3%) is taken: a partial last round idles CUs.
 inline int choose_segments(int64_t m, int64_t n, int k, int cap = 64) {
     const int64_t panels = (m + BX - 1) / BX;
     const int64_t tiles = (n + BY - 1) / BY;
     int64_t s = (SWEEP_WGS + panels - 1) / panels;
     if (k > 2 && s < 8) s = 8;
-    const int64_t max_s = tiles / 4 > 0 ? tiles / 4 : 1;
+    int64_t max_s = tiles / 4 > 0 ? tiles / 4 : 1;
+    if (max_s > cap) max_s = cap;
     if (s > max_s) s = max_s;
-    if (s > cap) s = cap;
     if (s < 1) s = 1;
-    return (int)s;
+    int64_t best = s;
+    double best_waste = 1e30;
+    for (int64_t t = s; t <= max_s && t <= 2 * s; ++t) {
+        const int64_t wgs = panels * t;  // padding workgroups of the blocked order exit at once
+        const double waste = (double)((wgs + SWEEP_CUS - 1) / SWEEP_CUS * SWEEP_CUS) / (double)wgs - 1.0;
+        if (waste < best_waste - 1e-12) {
+            best = t;
+            best_waste = waste;
+        }
+        if (waste <= 0.03) break;
+    }
+    return (int)best;
 }
 
 inline DirPlan plan_dir(int64_t rows, int64_t cols, int k, int cap = 64) {
@@ -1079,9 +1163,12 @@ void layout(A& a, int64_t m, int64_t n, int d, int k, uint32_t flags, double** x
     wide->rows = a.template take<float>((size_t)wq * (split ? ldw : (size_t)d));
     wide->thr = a.template take<float>((size_t)wq);
     wide->cnt = a.template take<int>((size_t)wq);
-    wide->buf = a.template take<int>((size_t)WIDE_ROWS * WIDE_CAP);
+    wide->buf = a.template take<int>((size_t)WIDE_BUF);
     wide->redo2 = a.template take<int>((size_t)(m + n));
-    wide->redo2_count = a.template take<int>(2);
+    wide->redo2_thr = a.template take<float>((size_t)(m + n));
+    wide->redo3 = a.template take<int>((size_t)(m + n));
+    wide->redo3_thr = a.template take<float>((size_t)(m + n));
+    wide->counts = a.template take<int>(4);
 }
 
 // Exact rescan of the rows queued by a finalize: reads the queue length back (one host synchronisation), then
@@ -1176,7 +1263,7 @@ int run_bidir(hipStream_t st, const float* X, const float* Y, int64_t m, int64_t
         const int64_t xe = xb + ch < m ? xb + ch : m;
         const int64_t rows = xe - xb;
         const int64_t panels = (rows + BX - 1) / BX;
-        dim3 grid((unsigned)panels, (unsigned)plan.S);
+        const dim3 grid(sweep_grid(panels, plan.S));
         if (fused) {
             // column thresholds start at -inf for every chunk (its lists only rank its own X rows)
             const unsigned neg_inf_key = 0x007fffffu;  // float_key(-INFINITY)
@@ -1188,12 +1275,12 @@ int run_bidir(hipStream_t st, const float* X, const float* Y, int64_t m, int64_t
     do {                                                                                                             \
         if (split)                                                                                                   \
             hipLaunchKernelGGL((l2sq_sweep<K1, TL, CL, 1>), grid, dim3(256), 0, st, SX, SY, xb, xe, n, sd, ld, qb32, \
-                               db32, p32, ge32, (float)scale, plan.seg_len, part, colpart, colthr, blockstats, 1,     \
-                               (int)want_stats);                                                                     \
+                               db32, p32, ge32, (float)scale, plan.seg_len, (int)panels, plan.S, part, colpart,      \
+                               colthr, blockstats, 1, (int)want_stats);                                              \
         else                                                                                                         \
             hipLaunchKernelGGL((l2sq_sweep<K1, TL, CL, 0>), grid, dim3(256), 0, st, X, Y, xb, xe, n, d, d, qb32,     \
-                               db32, p32, ge32, (float)scale, plan.seg_len, part, colpart, colthr, blockstats,        \
-                               (int)vec4, (int)want_stats);                                                          \
+                               db32, p32, ge32, (float)scale, plan.seg_len, (int)panels, plan.S, part, colpart,      \
+                               colthr, blockstats, (int)vec4, (int)want_stats);                                      \
     } while (0)
         prof_begin(st, "l2sq_sweep");
         if (two_level) {
@@ -1207,7 +1294,7 @@ int run_bidir(hipStream_t st, const float* X, const float* Y, int64_t m, int64_t
 #undef HM_SWEEP
         HM_LAUNCH_CHECK("l2sq_sweep");
         if (want_stats) {
-            hipLaunchKernelGGL(l2sq_reduce_stats, dim3(1), dim3(256), 0, st, blockstats, (int64_t)grid.x * grid.y,
+            hipLaunchKernelGGL(l2sq_reduce_stats, dim3(1), dim3(256), 0, st, blockstats, (int64_t)panels * plan.S,
                                stats, linf, chunk_index > 0 ? 1 : 0);
             HM_LAUNCH_CHECK("l2sq_reduce_stats");
         }
@@ -1251,17 +1338,18 @@ int run_bidir(hipStream_t st, const float* X, const float* Y, int64_t m, int64_t
         for (int64_t yb = 0; yb < n; yb += ch2) {
             const int64_t ye = yb + ch2 < n ? yb + ch2 : n;
             const int64_t rows = ye - yb;
-            dim3 grid((unsigned)((rows + BX - 1) / BX), (unsigned)plan2.S);
+            const int64_t panels2 = (rows + BX - 1) / BX;
+            const dim3 grid(sweep_grid(panels2, plan2.S));
 #define HM_SWEEP2(TL)                                                                                                \
     do {                                                                                                             \
         if (split)                                                                                                   \
             hipLaunchKernelGGL((l2sq_sweep<K1, TL, false, 1>), grid, dim3(256), 0, st, SY, SX, yb, ye, m, sd, ld,    \
-                               db32, qb32, ge32, p32, (float)scale, plan2.seg_len, part, colpart, colthr, blockstats, \
-                               1, 0);                                                                                \
+                               db32, qb32, ge32, p32, (float)scale, plan2.seg_len, (int)panels2, plan2.S, part,      \
+                               colpart, colthr, blockstats, 1, 0);                                                   \
         else                                                                                                         \
             hipLaunchKernelGGL((l2sq_sweep<K1, TL, false, 0>), grid, dim3(256), 0, st, Y, X, yb, ye, m, d, d, db32,  \
-                               qb32, ge32, p32, (float)scale, plan2.seg_len, part, colpart, colthr, blockstats,      \
-                               (int)vec4, 0);                                                                        \
+                               qb32, ge32, p32, (float)scale, plan2.seg_len, (int)panels2, plan2.S, part, colpart,   \
+                               colthr, blockstats, (int)vec4, 0);                                                    \
     } while (0)
             prof_begin(st, "l2sq_sweep");
             if (two_level) HM_SWEEP2(true);

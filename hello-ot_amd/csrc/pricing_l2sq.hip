@@ -19,33 +19,39 @@ int run_k(L2SQ_RUN_ARGS) {
 
 }  // namespace
 
-int wide_resolve(hipStream_t st, bool split, bool two_level, const float* A, const float* Asw, const float* B,
-                 const float* Bsw, int64_t nb, int d, int sd, int ld, const float* cand32, const double* abias,
-                 const double* bbias, double scale, int k, const int* redo, const int* redo_count,
-                 double* out_val, int* out_idx, int cols, int cbase, const WideBufs& w, double* rpv, int* rpi) {
-    int count = 0;
-    HM_HIP(hipMemcpyAsync(&count, redo_count, sizeof(int), hipMemcpyDeviceToHost, st));
+namespace {
+
+int read_count(hipStream_t st, const int* count_dev, int* out) {
+    HM_HIP(hipMemcpyAsync(out, count_dev, sizeof(int), hipMemcpyDeviceToHost, st));
     HM_HIP(hipStreamSynchronize(st));
-    prof_count(cols ? "l2sq_wide_columns" : "l2sq_wide_rows", count);
-    if (count <= 0) return HM_OK;
-    hipLaunchKernelGGL(zero_words, dim3(1), dim3(64), 0, st, reinterpret_cast<unsigned long long*>(w.redo2_count), 1);
-    HM_LAUNCH_CHECK("zero_words");
+    return HM_OK;
+}
+
+// One round of the wide pass over `count` queued rows: per batch, gather the rows' sweep copies, re-sweep them
+// against all candidates collecting ids with w >= threshold (up to `cap` per row), evaluate the collected ids
+// exactly in slices, merge; rows past `cap` go to (next, next_thr, next_count).
+int wide_round(hipStream_t st, bool split, bool two_level, const float* A, const float* Asw, const float* B,
+               const float* Bsw, int64_t nb, int d, int sd, int ld, const float* cand32, const double* abias,
+               const double* bbias, double scale, int k, const int* queue, const float* queue_thr, int count,
+               int cap, double* out_val, int* out_idx, int cols, int cbase, const WideBufs& w, double* rpv, int* rpi,
+               int* next, float* next_thr, int* next_count) {
     const int gld = split ? ld : d;  // row stride of the gathered sweep rows
-    prof_begin(st, "l2sq_wide");
-    for (int q0 = 0; q0 < count; q0 += WIDE_ROWS) {
-        const int Q = count - q0 < WIDE_ROWS ? count - q0 : WIDE_ROWS;
+    const int batch = (int)(WIDE_BUF / cap) < WIDE_ROWS ? (int)(WIDE_BUF / cap) : WIDE_ROWS;
+    const int spr = cap / WIDE_SLICE;
+    const int vec4 = split || (d % 4) == 0;
+    for (int q0 = 0; q0 < count; q0 += batch) {
+        const int Q = count - q0 < batch ? count - q0 : batch;
         const int Qpad = (int)panel_rows(Q);
-        hipLaunchKernelGGL(l2sq_wide_gather, dim3(2048), dim3(256), 0, st, Asw, gld, redo, q0, Q, Qpad, w.redo_thr,
+        hipLaunchKernelGGL(l2sq_wide_gather, dim3(2048), dim3(256), 0, st, Asw, gld, queue, q0, Q, Qpad, queue_thr,
                            w.rows, w.thr, w.cnt);
         HM_LAUNCH_CHECK("l2sq_wide_gather");
         const DirPlan plan = plan_dir(Qpad, nb, 0, 256);
-        dim3 grid((unsigned)(Qpad / BX), (unsigned)plan.S);
-        const int vec4 = split || (d % 4) == 0;
+        const dim3 grid(sweep_grid(Qpad / BX, plan.S));
 #define HM_WIDE(TL, PR)                                                                                             \
     hipLaunchKernelGGL((l2sq_sweep<8, TL, false, PR, true>), grid, dim3(256), 0, st, w.rows, Bsw, (int64_t)0,        \
                        (int64_t)Q, nb, sd, gld, (const float*)nullptr, cand32, (const float*)nullptr,               \
-                       (const float*)nullptr, (float)scale, plan.seg_len, (Entry*)nullptr, (Entry*)nullptr,          \
-                       (unsigned int*)nullptr, (double*)nullptr, vec4, 0, w.thr, w.cnt, w.buf)
+                       (const float*)nullptr, (float)scale, plan.seg_len, Qpad / BX, plan.S, (Entry*)nullptr,        \
+                       (Entry*)nullptr, (unsigned int*)nullptr, (double*)nullptr, vec4, 0, w.thr, w.cnt, w.buf, cap)
         if (split) {
             if (two_level) HM_WIDE(true, 1);
             else HM_WIDE(false, 1);
@@ -55,21 +61,56 @@ int wide_resolve(hipStream_t st, bool split, bool two_level, const float* A, con
         }
 #undef HM_WIDE
         HM_LAUNCH_CHECK("l2sq_sweep (wide)");
-        const unsigned eg = (unsigned)((Q + 3) / 4);
-        if (k <= 2)
-            hipLaunchKernelGGL((l2sq_wide_exact<2>), dim3(eg), dim3(256), 0, st, A, B, d, abias, bbias, scale, k, redo,
-                               q0, Q, w.cnt, w.buf, cols, cbase, out_val, out_idx, w.redo2, w.redo2_count);
-        else if (k <= 8)
-            hipLaunchKernelGGL((l2sq_wide_exact<8>), dim3(eg), dim3(256), 0, st, A, B, d, abias, bbias, scale, k, redo,
-                               q0, Q, w.cnt, w.buf, cols, cbase, out_val, out_idx, w.redo2, w.redo2_count);
-        else
-            hipLaunchKernelGGL((l2sq_wide_exact<32>), dim3(eg), dim3(256), 0, st, A, B, d, abias, bbias, scale, k,
-                               redo, q0, Q, w.cnt, w.buf, cols, cbase, out_val, out_idx, w.redo2, w.redo2_count);
+        const int64_t items = (int64_t)Q * spr;
+        const unsigned eg = (unsigned)((items + 3) / 4 < 8192 ? (items + 3) / 4 : 8192);
+        const unsigned mg = (unsigned)((Q + 255) / 256);
+#define HM_WIDE_EXACT(KK)                                                                                           \
+    do {                                                                                                            \
+        hipLaunchKernelGGL((l2sq_wide_slices<KK>), dim3(eg), dim3(256), 0, st, A, B, d, abias, bbias, scale, k,       \
+                           queue, q0, Q, w.cnt, w.buf, cap, spr, cols, cbase, rpv, rpi);                            \
+        hipLaunchKernelGGL((l2sq_wide_merge<KK>), dim3(mg), dim3(256), 0, st, rpv, rpi, Q, spr, k, w.cnt, cap, queue, \
+                           w.thr, q0, out_val, out_idx, next, next_thr, next_count);                                \
+    } while (0)
+        if (k <= 2) HM_WIDE_EXACT(2);
+        else if (k <= 8) HM_WIDE_EXACT(8);
+        else HM_WIDE_EXACT(32);
+#undef HM_WIDE_EXACT
         HM_LAUNCH_CHECK("l2sq_wide_exact");
     }
+    return HM_OK;
+}
+
+}  // namespace
+
+int wide_resolve(hipStream_t st, bool split, bool two_level, const float* A, const float* Asw, const float* B,
+                 const float* Bsw, int64_t nb, int d, int sd, int ld, const float* cand32, const double* abias,
+                 const double* bbias, double scale, int k, const int* redo, const int* redo_count,
+                 double* out_val, int* out_idx, int cols, int cbase, const WideBufs& w, double* rpv, int* rpi) {
+    static_assert(WIDE_CAP1 % WIDE_SLICE == 0 && WIDE_CAP2 % WIDE_SLICE == 0, "whole slices per row");
+    static_assert((WIDE_BUF / WIDE_CAP1) * (WIDE_CAP1 / WIDE_SLICE) <= RESCAN_ITEMS &&
+                      (WIDE_BUF / WIDE_CAP2) * (WIDE_CAP2 / WIDE_SLICE) <= RESCAN_ITEMS,
+                  "slice lists of a batch fit the rescan scratch");
+    int count = 0;
+    if (int rc = read_count(st, redo_count, &count)) return rc;
+    prof_count(cols ? "l2sq_wide_columns" : "l2sq_wide_rows", count);
+    if (count <= 0) return HM_OK;
+    hipLaunchKernelGGL(zero_words, dim3(1), dim3(64), 0, st, reinterpret_cast<unsigned long long*>(w.counts), 2);
+    HM_LAUNCH_CHECK("zero_words");
+    prof_begin(st, "l2sq_wide");
+    int rc = wide_round(st, split, two_level, A, Asw, B, Bsw, nb, d, sd, ld, cand32, abias, bbias, scale, k, redo,
+                        w.redo_thr, count, WIDE_CAP1, out_val, out_idx, cols, cbase, w, rpv, rpi, w.redo2, w.redo2_thr,
+                        w.counts);
+    int count2 = 0;
+    if (!rc) rc = read_count(st, w.counts, &count2);
+    if (!rc && count2 > 0)
+        rc = wide_round(st, split, two_level, A, Asw, B, Bsw, nb, d, sd, ld, cand32, abias, bbias, scale, k, w.redo2,
+                        w.redo2_thr, count2, WIDE_CAP2, out_val, out_idx, cols, cbase, w, rpv, rpi, w.redo3,
+                        w.redo3_thr, w.counts + 1);
     prof_end(st);
-    // rows with more than WIDE_CAP candidates near their k-th value: exact scan over all candidates
-    return rescan_exact(st, A, B, nb, d, abias, bbias, scale, k, w.redo2, w.redo2_count, out_val, out_idx, cols, cbase,
+    if (rc) return rc;
+    // rows with more than WIDE_CAP2 candidates near their k-th value: exact scan over all candidates
+    if (count2 <= 0) return HM_OK;
+    return rescan_exact(st, A, B, nb, d, abias, bbias, scale, k, w.redo3, w.counts + 1, out_val, out_idx, cols, cbase,
                         rpv, rpi);
 }
 

@@ -47,8 +47,11 @@ int hm_abi_version(void); /* 1 */
  * Kernel timing. No reference counterpart: the reference returns a zeroed timing slot
  * (generic_scan.py:577-597, "collect_timing"). When enabled, every hot-path launch is bracketed by HIP
  * events on its own stream; hm_profile_query waits for the pending events and returns the accumulated
- * milliseconds and launch count for one kernel name: "l2sq_sweep", "l2sq_finalize", "l2sq_rescan",
- * "norm_sweep", "sddmm_l2sq_csr", "pdhg_iteration" (edge pass + node pass of one PDHG iteration).
+ * milliseconds and launch count for one kernel name: "l2sq_sweep", "l2sq_finalize", "l2sq_col_finalize",
+ * "l2sq_wide" (wide pass of uncertified rows), "l2sq_rescan" (exact full rescan), "norm_sweep",
+ * "sddmm_l2sq_csr", "pdhg_iteration" (passes of one PDHG iteration). Counters without timing report their
+ * total in `launches` (total_ms = 0): "l2sq_wide_rows" / "l2sq_wide_columns" (rows / columns sent to the wide
+ * pass) and "l2sq_rescan_rows" / "l2sq_rescan_columns" (rows / columns rescanned in full).
  */
 void hm_profile_enable(int on);
 void hm_profile_reset(void);
@@ -71,9 +74,12 @@ int hm_profile_query(const char* name, double* total_ms, int64_t* launches);
  *   row_val[m*k] fp64, row_idx[m*k] int32  -- per X row, best k columns (HM_ROWS)
  *   col_val[n*k] fp64, col_idx[n*k] int32  -- per Y row, best k X rows    (HM_COLS)
  *   stats[5] fp64 = (num = sum sigma+^2, den = sum c^2, count #{sigma>0}, max sigma+, max|c| (HM_LINF))
- * Values are exact fp64 re-evaluations (fixed-order fp64 dot) of candidates found by an fp32 MFMA sweep
- * with a rigorous error bound; rows whose bound cannot separate the k-th candidate are rescanned exactly
- * on the device. Certificate sums come from the fp32 sweep (relative error ~1e-6).
+ * Values are exact fp64 re-evaluations (fixed-order fp64 dot) of candidates found by an MFMA sweep (fp32, or
+ * split-bf16 with HM_BF16X3) with a rigorous error bound b. A row whose kept candidates cannot be separated
+ * from the dropped ones by 2b goes through a wide pass (its candidates with approximate score >= k-th - 2b are
+ * collected by a second sweep and evaluated exactly) and, past 512 such candidates, an exact full rescan.
+ * Certificate sums come from the sweep's approximate scores. The call synchronises the stream once per
+ * finalize to read the number of queued rows back.
  */
 size_t hm_pricing_l2sq_workspace_bytes(int64_t m, int64_t n, int32_t d, int32_t k, uint32_t flags);
 int hm_pricing_l2sq(void* stream, const float* X, const float* Y, const double* p, const double* q,
