@@ -64,6 +64,7 @@ SIGNATURES = {
     "hm_pair_costs_l2sq": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _I64, _I32, _D, _P]),
     "hm_pair_costs_norm": (ctypes.c_int, [_P, _P, _P, _P, _P, _I64, _I32, _I32, _P]),
     "hm_pair_costs_norm_fp32": (ctypes.c_int, [_P, _P, _P, _P, _P, _I64, _I32, _I32, _P]),
+    "hm_sparsify_support": (ctypes.c_int, [_I64, _I64, _I64, _P, _P, _P, _P, _I64, _D, _P]),
     "hm_pdhg_workspace_bytes": (_SZ, [_I64, _I64, _I64]),
     "hm_pdhg_solve": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, ctypes.POINTER(PdhgParams),
                                      _P, _P, ctypes.POINTER(PdhgResult), _P, _SZ]),

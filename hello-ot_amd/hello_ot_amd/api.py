@@ -94,6 +94,7 @@ def solve_problem(problem: Problem, options: SolverOptions, *, max_iterations: i
         levels, previous, triggers = [], None, []
         coarsest_refinement = None
         support = dual = None
+        sparsified = []
         for level_index in reversed(range(len(sizes))):
             nn, mm = sizes[level_index]
             cost = full.sliced(nn, mm)
@@ -108,6 +109,7 @@ def solve_problem(problem: Problem, options: SolverOptions, *, max_iterations: i
                 if triggered:
                     triggers.append(level_index)
             levels.append(level)
+            sparsified.extend(support.sparsification_log or [])
             previous = dual
         rows, cols = support.rows_cols()
         objective = float(full.pairs(rows, cols) @ support.values)
@@ -133,6 +135,10 @@ def solve_problem(problem: Problem, options: SolverOptions, *, max_iterations: i
         "total_scan_time": sum(i.full_scan_time for l in levels if l.kind == "refined" for i in l.solve.iterations),
         "cost_perturbation": {"policy": options.cost_perturbation, "activated": False,
                               "reentry_trigger_levels": triggers},
+        "support_sparsification": {"events": len(sparsified),
+                                   "cycle_updates": sum(r.cycle_updates for r in sparsified),
+                                   "removed_edges": sum(r.input_nnz - r.output_nnz for r in sparsified),
+                                   "wall_time": sum(r.wall_time for r in sparsified)},
     }
     result = Result(objective, solution, stage, wall, peak, None, metadata, ())
     if options.verbose != "off":

@@ -52,6 +52,13 @@ def active_support_budget(beta: float, n_source: int, n_target: int) -> int:
     return int(math.ceil(float(beta) * (int(n_source) + int(n_target))))
 
 
+def primal_support_cap(beta: float, gamma: int, n_source: int, n_target: int) -> int:
+    """Positive edges an LP solution may keep: the budget minus room for a basis (V - 1) and gamma * V new
+    violations (refinement/support_budget.py:56-67)."""
+    vertices = int(n_source) + int(n_target)
+    return active_support_budget(beta, n_source, n_target) - (vertices - 1) - int(gamma) * vertices
+
+
 @dataclass(frozen=True)
 class SolverOptions:
     split_count: int = 4
@@ -124,4 +131,4 @@ class SolverOptions:
 
 
 __all__ = ["POSITIVE_SUPPORT_TOLERANCE", "SolverOptions", "active_support_budget", "normalize_pricing_topk",
-           "validate_support_budget_factor"]
+           "primal_support_cap", "validate_support_budget_factor"]

@@ -21,7 +21,7 @@ import time
 import numpy as np
 import torch
 
-from ..config import active_support_budget
+from ..config import active_support_budget, primal_support_cap
 from ..types import (ActiveSupportStats, BudgetedPruningStats, CoarsestSolveStats, ConvergenceStats,
                      DualViolationStats, HelloSolveError, InitializationStats, IterationStats, LevelResult,
                      RefinementResult, RefinementSummary, SolveLPStats)
@@ -148,18 +148,24 @@ def refine(cost: Cost, a, b, previous, known_side, options, level_index, max_ite
     n, m = cost.shape
     tol = options.tolerance
     budget = active_support_budget(options.support_budget_factor, n, m)
+    cap = primal_support_cap(options.support_budget_factor, options.pricing_topk, n, m)
     peak = len(support.keys)
     previous_pruned, reentered, triggered = None, False, False
     history = []
+    sparsifications = []
     lp = None
     for index in range(max_iterations):
         it_started = time.perf_counter()
         before = len(support.keys)
         t0 = time.perf_counter()
-        dual, lp = support.solve_lp(cost, a, b, dual, tol)
+        dual, lp = support.solve_lp(cost, a, b, dual, tol, primal_cap=cap)
         lp_seconds = time.perf_counter() - t0
+        if support.last_sparsification is not None:
+            sparsifications.append(support.last_sparsification)
         _progress(options, f"level={level_index} iteration={index} lp {lp_seconds:.3f}s support={before} "
-                           f"pdhg_iters={lp.iterations}")
+                           f"pdhg_iters={lp.iterations}"
+                           + (f" sparsified {support.last_sparsification.input_nnz}->"
+                              f"{support.last_sparsification.output_nnz}" if support.last_sparsification else ""))
         t0 = time.perf_counter()
         xv, xi, yv, yi, metrics = cost.scan(dual, options.pricing_topk, certificate=True)
         scan_seconds = time.perf_counter() - t0
@@ -196,6 +202,7 @@ def refine(cost: Cost, a, b, previous, known_side, options, level_index, max_ite
                                 peak, "converged" if converged else "max_refinement_iterations", converged)
     level = LevelResult(level_index, "refined", n, m, init_stats, RefinementResult(tuple(history), summary),
                         time.perf_counter() - started)
+    support.sparsification_log = sparsifications
     return support, dual, level, triggered
 
 

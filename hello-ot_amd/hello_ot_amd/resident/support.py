@@ -12,6 +12,7 @@ import torch
 
 from ..config import POSITIVE_SUPPORT_TOLERANCE
 from ..lp import NativeRestrictedOTPDLP
+from .sparsify import sparsify_transport_support
 
 
 def normalize_masses(a: torch.Tensor, b: torch.Tensor):
@@ -48,6 +49,8 @@ class Support:
     structural: torch.Tensor
     n: int
     m: int
+    last_sparsification: object = None
+    sparsification_log: list | None = None
 
     @classmethod
     def initial(cls, candidates: torch.Tensor, a: torch.Tensor, b: torch.Tensor) -> "Support":
@@ -95,8 +98,12 @@ class Support:
         self.keys, self.values, self.structural = self.keys[keep], self.values[keep], self.structural[keep]
         return removed_keys
 
-    def solve_lp(self, cost, a: torch.Tensor, b: torch.Tensor, dual: torch.Tensor, tolerance: float):
-        """Restricted LP on the support, warm-started from the current flows and duals."""
+    def solve_lp(self, cost, a: torch.Tensor, b: torch.Tensor, dual: torch.Tensor, tolerance: float,
+                 primal_cap: int | None = None):
+        """Restricted LP on the support, warm-started from the current flows and duals. When the solution keeps
+        more than ``primal_cap`` positive edges, its support is sparsified by cycle cancelling (cost never
+        increases) and the duals are shifted down by half the new primal-dual gap per unit mass, as the reference
+        does (gpu_resident/support.py:121-137). ``self.last_sparsification`` holds that step's result or None."""
         rows, cols = self.rows_cols()
         costs = cost.pairs(rows, cols)
         solver = NativeRestrictedOTPDLP(device=a.device, evaluation_frequency=200)
@@ -106,7 +113,23 @@ class Support:
             raise RuntimeError(f"GPU restricted LP failed: {result.termination_reason}")
         self.values = result.x
         result.obj_val = float(costs @ result.x)
-        return result.y, result
+        dual = result.y
+        self.last_sparsification = None
+        if primal_cap is not None and int(torch.count_nonzero(self.values > POSITIVE_SUPPORT_TOLERANCE)) > primal_cap:
+            sparse = sparsify_transport_support(rows.cpu().numpy(), cols.cpu().numpy(), self.values.cpu().numpy(),
+                                                costs.cpu().numpy(), n_source=self.n, n_target=self.m,
+                                                target_nnz=primal_cap)
+            self.values = torch.as_tensor(sparse.values, device=a.device)
+            self.last_sparsification = sparse
+            result.x = self.values
+            result.obj_val = float(costs @ self.values)
+            rhs = torch.cat((a, b))
+            shift = ((rhs @ dual - result.obj_val) / a.sum()).clamp_min(0)
+            dual = dual - 0.5 * shift
+            result.y = dual
+            result.dual_obj_val = float(rhs @ dual)
+            result.gap = abs(result.obj_val - result.dual_obj_val) / (1 + abs(result.obj_val) + abs(result.dual_obj_val))
+        return dual, result
 
 
 __all__ = ["Support", "normalize_masses", "northwest"]

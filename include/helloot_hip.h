@@ -174,6 +174,28 @@ int hm_pdhg_solve(void* stream, const int64_t* rows, const int64_t* cols, const 
                   int64_t n_target, int64_t e, const hm_pdhg_params* params /* host */, double* x_out,
                   double* y_out, hm_pdhg_result* result /* host */, void* workspace, size_t workspace_bytes);
 
+/* ---------------------------------------------------------------------------------------------------- */
+/* Support sparsification (host)                                                                          */
+/* ---------------------------------------------------------------------------------------------------- */
+
+/*
+ * Cycle cancelling on a restricted-OT primal until at most target_nnz edges carry flow > zero_tolerance, never
+ * increasing the cost c^T x and keeping every row and column sum. Replaces
+ * restricted_ot/support_sparsification.py:52 (sparsify_transport_support, engine "cpp_lct") ->
+ * _support_sparsifier_ext.sparsify_transport_support (support_sparsifier_lct.cpp:378-555), which the
+ * GPU-resident solver calls when the LP's positive support exceeds its cap (gpu_resident/support.py:124-137).
+ *   rows[e], cols[e] int64 endpoints (HOST arrays), values[e] fp64 flows (HOST, in/out), costs[e] fp64 (HOST).
+ *   A spanning forest of the positive edges is built in edge order; the remaining positive edges enter in edge
+ *   order, each pushing flow around its tree cycle in the direction that does not increase the cost until an
+ *   edge reaches zero (a link-cut tree keeps each cycle O(log) amortised). The exact count is re-taken whenever
+ *   enough cycles have been cancelled to reach target_nnz, and the work stops once it is reached.
+ *   stats[3] (HOST): output nnz, cycles cancelled, tree operations. Flows <= zero_tolerance come back as 0.
+ * Runs on the calling thread; touches no device memory.
+ */
+int hm_sparsify_support(int64_t n_source, int64_t n_target, int64_t e, const int64_t* rows, const int64_t* cols,
+                        double* values, const double* costs, int64_t target_nnz, double zero_tolerance,
+                        int64_t* stats);
+
 #ifdef __cplusplus
 }
 #endif

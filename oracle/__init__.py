@@ -12,7 +12,9 @@ package, and only as the checker (or the timed CPU baseline); the product path n
 * sparse norm pair costs (``_native/norm_cost_scan/norm_cost_scan_kernel.cu:233-245``),
 * the Halpern-PDHG restricted-OT LP (``_native/cpp/solver.cpp:39-378``).
 
-``oracle/_ref/`` optionally holds the reference's own CPU modules (``_scan``, ``_lp``) compiled from
+``sparsify_support`` restates the support sparsifier (``support_sparsifier_lct.cpp:378-555``) in plain Python.
+
+``oracle/_ref/`` optionally holds the reference's own CPU modules (``_scan``, ``_lp``, ``_sparsify``) compiled from
 ``/root/reference`` by ``make -C oracle ref``; they pin the restatement where they build.
 
 Parity status per function (how each is pinned) is listed in ``parity_pins()``.
@@ -197,6 +199,117 @@ def pdhg_solve(rows, cols, costs, source_mass, target_mass, *, warm_start_primal
     }
 
 
+def sparsify_support(rows, cols, values, costs, n_source: int, n_target: int, target_nnz: int,
+                     zero_tolerance: float = 1e-15):
+    """Cycle cancelling on a restricted-OT primal (small inputs; plain Python with breadth-first tree paths).
+
+    Restates the reference's sparsifier (restricted_ot/support_sparsification.py:52 ->
+    support_sparsifier_lct.cpp:378-555): a spanning forest of the positive edges in edge order (union-find);
+    every other positive edge, in edge order, pushes flow around the cycle it closes with the tree path from its
+    source to its target -- edges at even positions of that path (counted from the source) lose what the entering
+    edge gains, odd positions gain it -- in the direction whose cost c_e - C_even + C_odd is not positive, by the
+    largest step keeping flows >= 0. If the entering edge stays positive, the first path edge (from the source)
+    at the minimum leaves the forest; otherwise the entering edge drops to zero. The exact positive count is
+    re-taken after every (count - target) cancelled cycles, and the loop stops once count <= target.
+    Returns (values, output nnz, cycles cancelled)."""
+    rows = np.asarray(rows, np.int64)
+    cols = np.asarray(cols, np.int64)
+    vals = np.array(values, dtype=np.float64)
+    costs = np.asarray(costs, np.float64)
+    vals[vals <= zero_tolerance] = 0.0
+    V = n_source + n_target
+    parent = list(range(V))
+
+    def find(a):
+        while parent[a] != a:
+            parent[a] = parent[parent[a]]
+            a = parent[a]
+        return a
+
+    rank = [0] * V
+    adj = {v: {} for v in range(V)}   # vertex -> {neighbour: edge id} of the forest
+    tree, entering = [], []
+    for k in range(len(rows)):
+        if vals[k] <= 0.0:
+            continue
+        a, b = find(int(rows[k])), find(n_source + int(cols[k]))
+        if a == b:
+            entering.append(k)
+            continue
+        if rank[a] < rank[b]:
+            a, b = b, a
+        parent[b] = a
+        rank[a] += rank[a] == rank[b]
+        tree.append(k)
+        adj[int(rows[k])][n_source + int(cols[k])] = k
+        adj[n_source + int(cols[k])][int(rows[k])] = k
+    nnz = int(np.count_nonzero(vals > zero_tolerance))
+    cycles = 0
+    if nnz <= target_nnz or not entering:
+        return vals, nnz, 0
+
+    def tree_path(u, v):
+        prev = {u: None}
+        queue = [u]
+        for x in queue:
+            if x == v:
+                break
+            for y, k in adj[x].items():
+                if y not in prev:
+                    prev[y] = (x, k)
+                    queue.append(y)
+        path = []
+        while v != u:
+            x, k = prev[v]
+            path.append(k)
+            v = x
+        return path[::-1]   # edges from u to v
+
+    tree_set = set(tree)
+    check_at = nnz - target_nnz
+    for pos, k in enumerate(entering):
+        if cycles >= check_at:
+            count = (len(entering) - pos) + sum(1 for t in tree_set if vals[t] > zero_tolerance)
+            if count <= target_nnz:
+                break
+            check_at = cycles + (count - target_nnz)
+        flow = vals[k]
+        if flow <= zero_tolerance:
+            continue
+        s, t = int(rows[k]), n_source + int(cols[k])
+        path = tree_path(s, t)
+        even, odd = path[0::2], path[1::2]
+        gain = costs[k] - sum(costs[e] for e in even) + sum(costs[e] for e in odd)
+        direction = 1.0 if gain <= 0.0 else -1.0
+        losing = even if direction > 0 else odd
+        step, leaving = np.inf, None
+        for e in losing:
+            if vals[e] < step:
+                step, leaving = vals[e], e
+        if direction < 0 and flow < step:
+            step = flow
+        step = max(0.0, step)
+        for e in even:
+            vals[e] -= direction * step
+        for e in odd:
+            vals[e] += direction * step
+        flow += direction * step
+        if flow > zero_tolerance:
+            vals[leaving] = 0.0
+            a, b = int(rows[leaving]), n_source + int(cols[leaving])
+            del adj[a][b], adj[b][a]
+            tree_set.discard(leaving)
+            adj[s][t] = k
+            adj[t][s] = k
+            tree_set.add(k)
+            vals[k] = flow
+        else:
+            vals[k] = 0.0
+        cycles += 1
+    vals[vals <= zero_tolerance] = 0.0
+    return vals, int(np.count_nonzero(vals)), cycles
+
+
 # ---------------------------------------------------------------------------------------------------
 # Reference CPU modules compiled from /root/reference (optional; absent on the GPU box unless built here).
 # ---------------------------------------------------------------------------------------------------
@@ -221,6 +334,11 @@ def ref_lp():
     return _load_ref("_lp")
 
 
+def ref_sparsify():
+    """The reference's support sparsifier (_native/support_sparsifier/*.cpp), or None if not built."""
+    return _load_ref("_sparsify")
+
+
 def parity_pins() -> dict:
     """How each oracle function is pinned (documentation for the test suite)."""
     return {
@@ -234,10 +352,14 @@ def parity_pins() -> dict:
         "pair_costs_norm": "numpy float64 norms at 1e-13 and exact integer-valued cases",
         "pdhg_solve": "reference _lp.solve_once (solver.cpp) with one thread, bit-identical iterates; "
                       "KATs tests/torch_restricted_ot_pdlp_test.py:16-80 (obj 0.1); scipy linprog optimum",
+        "sparsify_support": "reference _sparsify.sparsify_transport_support (support_sparsifier_lct.cpp) on random "
+                            "supports (same flows to 1e-12, same counts); invariants: row/column sums, cost never "
+                            "increases, flows >= 0, count <= target",
     }
 
 
 __all__ = [
     "build", "lib", "dot64", "l2sq_matrices", "norm_matrices", "topk", "stats", "l2sq_scan", "norm_scan",
-    "sddmm_l2sq", "pair_costs_norm", "pdhg_solve", "ref_scan", "ref_lp", "parity_pins",
+    "sddmm_l2sq", "pair_costs_norm", "pdhg_solve", "sparsify_support", "ref_scan", "ref_lp", "ref_sparsify",
+    "parity_pins",
 ]

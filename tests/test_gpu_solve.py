@@ -86,3 +86,26 @@ def test_brenier_c1_recovers_the_analytic_plan(cuda):
     big = sol.values > 0.5 / n
     assert big.sum() == n
     np.testing.assert_array_equal(sol.cols[big], inverse[sol.rows[big]])
+
+
+def test_solve_with_the_smallest_support_budget_sparsifies(cuda):
+    """beta = gamma + 2 (the smallest budget HELLO accepts) caps an LP's positive edges at m + n + 1, below what
+    PDHG leaves on these supports: the refinement must sparsify by cycle cancelling
+    (gpu_resident/support.py:124-137) and still reach the exact optimum."""
+    n = m = 200
+    rng = np.random.default_rng(11)
+    X = rng.random((n, 4)).astype(np.float32)
+    Y = rng.random((m, 4)).astype(np.float32)
+    a, b = rng.uniform(0.5, 1.5, n), rng.uniform(0.5, 1.5, m)
+    a, b = a / a.sum(), b / b.sum()
+    opts = SolverOptions(coarsest_size_threshold=60, support_budget_factor=4.0, verbose="off",
+                         cost_perturbation="off")
+    r = solve(X, Y, source_mass=a, target_mass=b, cost="l1", options=opts)
+    events = r.metadata["support_sparsification"]
+    assert events["events"] >= 1 and events["removed_edges"] > 0
+    assert all(l.solve.summary.converged for l in r.solve_stage.levels if l.kind == "refined")
+    exact = _exact(_cost_matrix(X, Y, "l1"), a, b)
+    assert abs(r.objective - exact) <= 2e-5 * abs(exact)
+    sol = r.solution.to_cpu()
+    np.testing.assert_allclose(np.bincount(sol.rows, weights=sol.values, minlength=n), a, atol=5e-6)
+    np.testing.assert_allclose(np.bincount(sol.cols, weights=sol.values, minlength=m), b, atol=5e-6)

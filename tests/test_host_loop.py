@@ -110,3 +110,11 @@ def test_candidate_keys_filter_and_dedupe():
     pos = candidate_keys(xv, xi, yv, yi, dual, 2, 3, positive=True)
     # rows: 0.5-0.2 > 0 -> (0,1); 0.5-0.7 < 0; -1+2 > 0 -> (1,0); columns: 0+0.1 > 0 -> (1,0)
     assert pos.tolist() == [1, 3]
+
+
+def test_primal_support_cap_reserves_basis_and_violations():
+    from hello_ot_amd.config import active_support_budget, primal_support_cap
+
+    # refinement/support_budget.py:56-67: budget - (V - 1) - gamma * V
+    assert primal_support_cap(10.0, 2, 300, 500) == active_support_budget(10.0, 300, 500) - 799 - 1600
+    assert primal_support_cap(4.0, 2, 200, 200) == 401
