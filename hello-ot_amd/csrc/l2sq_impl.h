@@ -24,6 +24,8 @@
 //   5. columns:  each chunk's exact column lists are merged into the output (tie rule kept).
 #pragma once
 
+#include <type_traits>
+
 #include "common.h"
 
 namespace hm {
@@ -144,21 +146,40 @@ inline unsigned prep_grid(int64_t rows) {
 
 // -------------------------------------------------------------------------------------------------
 // split-bf16 copy: x = hi + lo + e with hi = bf16(x), lo = bf16(x - hi) (round to nearest even), |e| <= 2^-16|x|.
-// Row r of the copy holds ld features (split_ld) as ld / 8 groups of 32 bytes: 8 hi, then 8 lo values; padding
-// features and the padding rows up to a whole 128-row panel are zero.
+// The copy is stored in the operand order of v_mfma_f32_32x32x16_bf16. Rows form blocks of 32 (block stride
+// 32 * ld words, ld = split_ld). A block is a run of 4 KiB chunks of 32 features. A chunk holds four 1 KiB operand
+// tiles: K-step s (16 features) and part p (hi / lo) at (2s + p) KiB. Within a tile, the 16 bytes at lane
+// 32h + r are features 8h .. 8h+7 of the K-step for row r, as 8 bf16. Padding features (to split_features) and
+// padding rows (to a whole 128-row panel) are zero.
+//
+// With this layout a lane's operand of one K-step is one coalesced 16-byte load. A Y tile's chunk is four
+// contiguous 4 KiB runs that go to LDS unchanged: conflict-free reads, no padding.
 // -------------------------------------------------------------------------------------------------
 __device__ inline unsigned short bf16_rne(float x) {
     const unsigned int u = __float_as_uint(x);
     return (unsigned short)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
 }
 
-__global__ void l2sq_split_bf16(const float* __restrict__ X, int64_t rows, int64_t padded_rows, int d, int ld,
+// 16-byte unit (hi part) of row `row`, chunk c, group g4 = 2s + h of a split copy with ld words per row; the lo
+// part follows 64 units later
+__host__ __device__ inline int64_t split_unit(int64_t row, int c, int g4, int ld) {
+    return ((row >> 5) * 32 * (int64_t)ld + (int64_t)c * 1024) / 4 + (g4 >> 1) * 128 + (g4 & 1) * 32 + (row & 31);
+}
+
+// item (32-row block, chunk c, group g4, row r): consecutive threads write consecutive 16-byte units
+__global__ void l2sq_split_bf16(const float* __restrict__ X, int64_t rows, int64_t padded_rows, int d, int sd, int ld,
                                 unsigned short* __restrict__ out) {
-    const int64_t groups = padded_rows * (ld / 8);
-    for (int64_t gidx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; gidx < groups;
+    const int nch = sd / KC;
+    const int64_t items = (padded_rows >> 5) * nch * 128;
+    uint4* out4 = reinterpret_cast<uint4*>(out);
+    for (int64_t gidx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; gidx < items;
          gidx += (int64_t)gridDim.x * blockDim.x) {
-        const int64_t row = gidx / (ld / 8);
-        const int k0 = (int)(gidx % (ld / 8)) * 8;
+        const int r = (int)(gidx & 31);
+        const int g4 = (int)((gidx >> 5) & 3);
+        const int64_t t = gidx >> 7;
+        const int c = (int)(t % nch);
+        const int64_t row = (t / nch) * 32 + r;
+        const int k0 = (c * 4 + g4) * 8;
         unsigned short hi[8], lo[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
@@ -175,9 +196,9 @@ __global__ void l2sq_split_bf16(const float* __restrict__ X, int64_t rows, int64
         b.y = lo[2] | ((unsigned int)lo[3] << 16);
         b.z = lo[4] | ((unsigned int)lo[5] << 16);
         b.w = lo[6] | ((unsigned int)lo[7] << 16);
-        uint4* dst = reinterpret_cast<uint4*>(out + row * (int64_t)ld * 2 + (int64_t)k0 * 2);
-        dst[0] = a;
-        dst[1] = b;
+        const int64_t u = split_unit(row, c, g4, ld);
+        out4[u] = a;
+        out4[u + 64] = b;
     }
 }
 
@@ -212,13 +233,182 @@ inline unsigned sweep_grid(int64_t P, int64_t S) {
     return (unsigned)((blocks + 7) / 8 * 8 * 32);
 }
 
-// PREC 0: X / Y are the fp32 features (row stride ld = d), products on v_mfma_f32_32x32x2f32.
-// PREC 1: X / Y are their split-bf16 copies (l2sq_split_bf16: d = features padded to 32, row stride ld, groups
-//         of 8 hi then 8 lo bf16 per 32 bytes, rows padded to whole 128-row panels); dot = hi*hi + hi*lo + lo*hi
-//         on v_mfma_f32_32x32x16_bf16.
+// Lane state of a sweep: the row's partial top-K1 list, its per-row constants and certificate partial sums.
+template <int K1>
+struct SweepRow {
+    float lv[K1];
+    int li[K1];
+    int64_t row;   // global X row of this lane
+    bool ok;       // row < xe
+    float qbi;     // row bias (scores of the column lists)
+    float wt;      // wide-pass threshold
+    float pi;      // certificate row term
+    double num64, den64, cnt64;
+    float mx, cmax;
+};
+
+template <int K1, bool APPEND>
+__device__ __forceinline__ void sweep_row_init(SweepRow<K1>& s, int64_t row, int64_t xe, int STATS,
+                                               const float* __restrict__ qb32, const float* __restrict__ p32,
+                                               const float* __restrict__ wthr) {
+#pragma unroll
+    for (int i = 0; i < K1; ++i) { s.lv[i] = -INFINITY; s.li[i] = -1; }
+    s.row = row;
+    s.ok = row < xe;
+    s.qbi = (s.ok && !APPEND) ? qb32[row] : 0.0f;
+    s.wt = (APPEND && s.ok) ? wthr[row] : INFINITY;
+    s.pi = (STATS && s.ok) ? p32[row] : 0.0f;
+    s.num64 = s.den64 = s.cnt64 = 0.0;
+    s.mx = s.cmax = 0.0f;
+}
+
+// Per-tile epilogue of both sweeps. tot[b][q] is the fp32 dot of this lane's X row with Y row
+// ytile + b*32 + 8*(q/4) + 4*h + q%4 (the lane (h, r) layout of the 32x32 MFMA accumulators). It ranks
+// w = scale*dot + db into the row list (or appends for the wide pass), adds the certificate terms and, with COLS,
+// passes the tile's scores scale*dot + qb through LDS so that each Y row keeps its best K1 over the workgroup's
+// 128 X rows. Ends with a barrier: the next tile may rewrite sDB / sGE / sC.
+template <int K1, bool COLS, bool APPEND>
+__device__ __forceinline__ void sweep_epilogue(const v16f (&tot)[NB], SweepRow<K1>& s, int tid, int wave, int h,
+                                               int r, int64_t ytile, int64_t y_end, int64_t x0, int64_t panel,
+                                               int64_t n, float scale, int STATS, const float* sDB, const float* sGE,
+                                               float* sC, Entry* __restrict__ colpart,
+                                               unsigned int* __restrict__ colthr, int* __restrict__ wcnt,
+                                               int* __restrict__ wbuf, int wcap) {
+    float tnum = 0.0f, tden = 0.0f;
+    unsigned int tcnt = 0;
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+#pragma unroll
+        for (int a = 0; a < 4; ++a) {
+            const int jl0 = b * 32 + 8 * a + 4 * h;
+            const float4 dbv = *reinterpret_cast<const float4*>(&sDB[jl0]);
+            float4 gev = make_float4(0, 0, 0, 0);
+            if (STATS) gev = *reinterpret_cast<const float4*>(&sGE[jl0]);
+            const float dbs[4] = {dbv.x, dbv.y, dbv.z, dbv.w};
+            const float ges[4] = {gev.x, gev.y, gev.z, gev.w};
+#pragma unroll
+            for (int cc = 0; cc < 4; ++cc) {
+                const int q = 4 * a + cc;
+                const float t = tot[b][q];
+                const float w = fmaf(scale, t, dbs[cc]);
+                const int64_t j = ytile + jl0 + cc;
+                const bool ok = s.ok && j < y_end;
+                if (APPEND) {
+                    if (ok && w >= s.wt) {
+                        const int pos = atomicAdd(&wcnt[s.row], 1);
+                        if (pos < wcap) wbuf[s.row * (int64_t)wcap + pos] = (int)j;
+                    }
+                } else if (ok && w > s.lv[K1 - 1]) {
+                    float cv = w;
+                    int ci = (int)j;
+#pragma unroll
+                    for (int i = 0; i < K1; ++i) {
+                        if (cv > s.lv[i]) {
+                            const float tv = s.lv[i];
+                            const int ti = s.li[i];
+                            s.lv[i] = cv;
+                            s.li[i] = ci;
+                            cv = tv;
+                            ci = ti;
+                        }
+                    }
+                }
+                if (STATS && ok) {
+                    const float sg = w + s.qbi;
+                    const float cost = (s.pi + ges[cc]) - w;
+                    tden = fmaf(cost, cost, tden);
+                    s.cmax = fmaxf(s.cmax, fabsf(cost));
+                    if (sg > 0.0f) {
+                        tnum = fmaf(sg, sg, tnum);
+                        s.mx = fmaxf(s.mx, sg);
+                        ++tcnt;
+                    }
+                }
+                if (COLS) sC[(jl0 + cc) * CST + wave * 32 + r] = s.ok ? fmaf(scale, t, s.qbi) : -INFINITY;
+            }
+        }
+    }
+    if (STATS) {
+        s.num64 += (double)tnum;
+        s.den64 += (double)tden;
+        s.cnt64 += (double)tcnt;
+    }
+    if (COLS) {
+        // each Y row of the tile: its best K1 over this workgroup's 128 X rows (two threads per row, folded).
+        // colthr[j] is the K1-th value of some full list of this chunk, a lower bound of the chunk's K1-th
+        // value: scores at or below it cannot enter the merged top-K1 and are skipped.
+        __syncthreads();
+        const int jl = tid >> 1, half = tid & 1;
+        const int64_t j = ytile + jl;
+        const float thr = j < y_end ? key_float(colthr[j]) : INFINITY;
+        float cw[K1];
+        int cidx[K1];
+#pragma unroll
+        for (int i = 0; i < K1; ++i) { cw[i] = -INFINITY; cidx[i] = -1; }
+        const float* src = &sC[jl * CST + half * 64];
+        const int base = (int)(x0 + half * 64);
+        for (int xx = 0; xx < 64; ++xx) {
+            const float v = src[xx];
+            if (v > thr && v > cw[K1 - 1]) insert_e<K1>(cw, cidx, v, base + xx);
+        }
+#pragma unroll
+        for (int i = 0; i < K1; ++i) {
+            const float pv = __shfl_xor(cw[i], 1, 64);
+            const int pi2 = __shfl_xor(cidx[i], 1, 64);
+            if (half == 0 && pi2 >= 0 && better_e(pv, pi2, cw[K1 - 1], cidx[K1 - 1])) insert_e<K1>(cw, cidx, pv, pi2);
+        }
+        if (half == 0 && j < y_end) {
+            Entry* dst = colpart + (panel * n + j) * K1;
+#pragma unroll
+            for (int i = 0; i < K1; ++i) dst[i] = Entry{cw[i], cidx[i]};
+            if (cidx[K1 - 1] >= 0) atomicMax(&colthr[j], float_key(cw[K1 - 1]));
+        }
+    }
+    __syncthreads();  // all epilogue reads of sDB/sGE/sC finish before the next tile rewrites them
+}
+
+// End of a sweep workgroup: lane lists -> part[(seg*rows + local row)*2 + h][K1], certificate partials reduced
+// over the workgroup into blockstats[(seg*P + panel)*5 ...].
+template <int K1, bool APPEND>
+__device__ __forceinline__ void sweep_finish(SweepRow<K1>& s, int tid, int lane, int wave, int h, int64_t seg,
+                                             int64_t rows, int64_t xb, int P, int64_t panel, int STATS,
+                                             Entry* __restrict__ part, double* __restrict__ blockstats,
+                                             double (*sRed)[5]) {
+    if (s.ok && !APPEND) {
+        Entry* out = part + ((seg * rows + (s.row - xb)) * 2 + h) * K1;
+#pragma unroll
+        for (int i = 0; i < K1; ++i) out[i] = Entry{s.lv[i], s.li[i]};
+    }
+    if (STATS) {
+        double v[5] = {s.num64, s.den64, s.cnt64, (double)s.mx, (double)s.cmax};
+#pragma unroll
+        for (int e = 0; e < 5; ++e) {
+            for (int o = 32; o >= 1; o >>= 1) {
+                const double t = __shfl_xor(v[e], o, 64);
+                v[e] = (e >= 3) ? fmax(v[e], t) : v[e] + t;
+            }
+        }
+        if (lane == 0) {
+#pragma unroll
+            for (int e = 0; e < 5; ++e) sRed[wave][e] = v[e];
+        }
+        __syncthreads();
+        if (tid == 0) {
+            double o[5];
+            for (int e = 0; e < 5; ++e) {
+                o[e] = sRed[0][e];
+                for (int w = 1; w < 4; ++w) o[e] = (e >= 3) ? fmax(o[e], sRed[w][e]) : o[e] + sRed[w][e];
+            }
+            double* dst = blockstats + (seg * P + panel) * 5;
+            for (int e = 0; e < 5; ++e) dst[e] = o[e];
+        }
+    }
+}
+
+// fp32 sweep: X / Y are the fp32 features (row stride ld = d), products on v_mfma_f32_32x32x2f32.
 // APPEND (the wide pass of queued rows): no lists, columns or certificate; every candidate j of row r with
 // w >= wthr[r] is appended to wbuf[r * wcap + ...] (wcnt[r] counts all of them, also past the capacity).
-template <int K1, bool TWO_LEVEL, bool COLS, int PREC, bool APPEND = false>
+template <int K1, bool TWO_LEVEL, bool COLS, bool APPEND = false>
 __global__ __launch_bounds__(256) void l2sq_sweep(
     const float* __restrict__ X, const float* __restrict__ Y, int64_t xb, int64_t xe, int64_t n, int d, int ld,
     const float* __restrict__ qb32, const float* __restrict__ db32, const float* __restrict__ p32,
@@ -245,39 +435,21 @@ __global__ __launch_bounds__(256) void l2sq_sweep(
     const int64_t x0 = xb + panel * BX;
     const int64_t y_begin = seg * seg_len;
     const int64_t y_end = (y_begin + seg_len < n) ? (y_begin + seg_len) : n;
-    const int64_t my_row = x0 + wave * 32 + r;
-    const bool row_ok = my_row < xe;
-
-    float lv[K1];
-    int li[K1];
-#pragma unroll
-    for (int s = 0; s < K1; ++s) { lv[s] = -INFINITY; li[s] = -1; }
-
-    const float qbi = (row_ok && !APPEND) ? qb32[my_row] : 0.0f;
-    const float wt = (APPEND && row_ok) ? wthr[my_row] : INFINITY;
-    const float pi = (STATS && row_ok) ? p32[my_row] : 0.0f;
-    double num64 = 0.0, den64 = 0.0, cnt64 = 0.0;
-    float mx = 0.0f, cmax = 0.0f;
+    SweepRow<K1> s;
+    sweep_row_init<K1, APPEND>(s, x0 + wave * 32 + r, xe, STATS, qb32, p32, wthr);
 
     const int nchunks = (d + KC - 1) / KC;
-    constexpr int BLK = PREC == 1 ? FLUSH_SPLIT : FLUSH_CHUNKS;  // chunks per fp32 accumulation block
 
     // global -> register staging for one chunk: 4 float4 of X and 4 of Y per thread (named registers: an array
-    // indexed before unrolling would be moved to LDS or scratch). The split copies are padded to whole 128-row
-    // panels and 32-feature chunks, so their loads need no bounds checks.
+    // indexed before unrolling would be moved to LDS or scratch)
     float4 gx0, gx1, gx2, gx3, gy0, gy1, gy2, gy3;  // set A: the chunk after the one being multiplied
     float4 hx0, hx1, hx2, hx3, hy0, hy1, hy2, hy3;  // set B: the chunk after that
-    const float* Xp = X + x0 * ld;  // this workgroup's X panel (uniform base; 32-bit lane offsets below)
-    auto load_one = [&](int i, int k0, int64_t ytile, const float* Yp, float4& ox, float4& oy) {
+    auto load_one = [&](int i, int k0, int64_t ytile, float4& ox, float4& oy) {
         const int lin = tid + 256 * i;
         const int row = lin >> 3, c4 = lin & 7;
         const int k = k0 + 4 * c4;
         const int64_t xr = x0 + row, yr = ytile + row;
-        if (PREC == 1) {
-            const unsigned off = (unsigned)row * (unsigned)ld + (unsigned)k;
-            ox = *reinterpret_cast<const float4*>(Xp + off);
-            oy = *reinterpret_cast<const float4*>(Yp + off);
-        } else if (VEC4) {
+        if (VEC4) {
             ox = (xr < xe && k < d) ? *reinterpret_cast<const float4*>(X + xr * ld + k) : make_float4(0, 0, 0, 0);
             oy = (yr < y_end && k < d) ? *reinterpret_cast<const float4*>(Y + yr * ld + k) : make_float4(0, 0, 0, 0);
         } else {
@@ -292,18 +464,16 @@ __global__ __launch_bounds__(256) void l2sq_sweep(
         }
     };
     auto load_a = [&](int c, int64_t ytile) {
-        const float* Yp = Y + ytile * ld;
-        load_one(0, c * KC, ytile, Yp, gx0, gy0);
-        load_one(1, c * KC, ytile, Yp, gx1, gy1);
-        load_one(2, c * KC, ytile, Yp, gx2, gy2);
-        load_one(3, c * KC, ytile, Yp, gx3, gy3);
+        load_one(0, c * KC, ytile, gx0, gy0);
+        load_one(1, c * KC, ytile, gx1, gy1);
+        load_one(2, c * KC, ytile, gx2, gy2);
+        load_one(3, c * KC, ytile, gx3, gy3);
     };
     auto load_b = [&](int c, int64_t ytile) {
-        const float* Yp = Y + ytile * ld;
-        load_one(0, c * KC, ytile, Yp, hx0, hy0);
-        load_one(1, c * KC, ytile, Yp, hx1, hy1);
-        load_one(2, c * KC, ytile, Yp, hx2, hy2);
-        load_one(3, c * KC, ytile, Yp, hx3, hy3);
+        load_one(0, c * KC, ytile, hx0, hy0);
+        load_one(1, c * KC, ytile, hx1, hy1);
+        load_one(2, c * KC, ytile, hx2, hy2);
+        load_one(3, c * KC, ytile, hx3, hy3);
     };
     auto rotate = [&]() {
         gx0 = hx0; gx1 = hx1; gx2 = hx2; gx3 = hx3;
@@ -340,44 +510,22 @@ __global__ __launch_bounds__(256) void l2sq_sweep(
     float outer[NB][16];
     // products of one 32-feature chunk held in an LDS stage
     auto compute = [&](const float* sx, const float* sy) {
-        if (PREC == 1) {
-            // two K-steps of 16 features; lane (h, r) supplies group 2s + h (8 features: hi, then lo)
+        // B operand: this lane's X row, features h*16 .. h*16+15 of the chunk
+        const float* bx = &sx[(wave * 32 + r) * STR + h * 16];
 #pragma unroll
-            for (int s2 = 0; s2 < 2; ++s2) {
-                const int gw = (2 * s2 + h) * 8;
-                const bf16x8 bh = *reinterpret_cast<const bf16x8*>(&sx[(wave * 32 + r) * STR + gw]);
-                const bf16x8 bl = *reinterpret_cast<const bf16x8*>(&sx[(wave * 32 + r) * STR + gw + 4]);
-                bf16x8 ah[NB], al[NB];
+        for (int g = 0; g < 4; ++g) {
+            const float4 bv = *reinterpret_cast<const float4*>(bx + 4 * g);
+            float4 av[NB];
+#pragma unroll
+            for (int b = 0; b < NB; ++b)
+                av[b] = *reinterpret_cast<const float4*>(&sy[(b * 32 + r) * STR + h * 16 + 4 * g]);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
 #pragma unroll
                 for (int b = 0; b < NB; ++b) {
-                    ah[b] = *reinterpret_cast<const bf16x8*>(&sy[(b * 32 + r) * STR + gw]);
-                    al[b] = *reinterpret_cast<const bf16x8*>(&sy[(b * 32 + r) * STR + gw + 4]);
-                }
-#pragma unroll
-                for (int b = 0; b < NB; ++b) acc[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah[b], bh, acc[b], 0, 0, 0);
-#pragma unroll
-                for (int b = 0; b < NB; ++b) acc[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah[b], bl, acc[b], 0, 0, 0);
-#pragma unroll
-                for (int b = 0; b < NB; ++b) acc[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al[b], bh, acc[b], 0, 0, 0);
-            }
-        } else {
-            // B operand: this lane's X row, features h*16 .. h*16+15 of the chunk
-            const float* bx = &sx[(wave * 32 + r) * STR + h * 16];
-#pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                const float4 bv = *reinterpret_cast<const float4*>(bx + 4 * g);
-                float4 av[NB];
-#pragma unroll
-                for (int b = 0; b < NB; ++b)
-                    av[b] = *reinterpret_cast<const float4*>(&sy[(b * 32 + r) * STR + h * 16 + 4 * g]);
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-#pragma unroll
-                    for (int b = 0; b < NB; ++b) {
-                        const float ae = e == 0 ? av[b].x : e == 1 ? av[b].y : e == 2 ? av[b].z : av[b].w;
-                        const float be = e == 0 ? bv.x : e == 1 ? bv.y : e == 2 ? bv.z : bv.w;
-                        acc[b] = __builtin_amdgcn_mfma_f32_32x32x2f32(ae, be, acc[b], 0, 0, 0);
-                    }
+                    const float ae = e == 0 ? av[b].x : e == 1 ? av[b].y : e == 2 ? av[b].z : av[b].w;
+                    const float be = e == 0 ? bv.x : e == 1 ? bv.y : e == 2 ? bv.z : bv.w;
+                    acc[b] = __builtin_amdgcn_mfma_f32_32x32x2f32(ae, be, acc[b], 0, 0, 0);
                 }
             }
         }
@@ -429,10 +577,10 @@ __global__ __launch_bounds__(256) void l2sq_sweep(
         };
         int c = 0;
         if (TWO_LEVEL) {
-            // fp32 blocks of BLK chunks folded into the outer sums (the error bound assumes this blocking)
-            for (; c + BLK <= nchunks; c += BLK) {
+            // fp32 blocks of FLUSH_CHUNKS chunks folded into the outer sums (the error bound assumes this blocking)
+            for (; c + FLUSH_CHUNKS <= nchunks; c += FLUSH_CHUNKS) {
 #pragma unroll
-                for (int u = 0; u < BLK; ++u) step(c + u);
+                for (int u = 0; u < FLUSH_CHUNKS; ++u) step(c + u);
 #pragma unroll
                 for (int b = 0; b < NB; ++b) {
 #pragma unroll
@@ -441,131 +589,279 @@ __global__ __launch_bounds__(256) void l2sq_sweep(
             }
         }
         for (; c < nchunks; ++c) step(c);
-        // epilogue: lane (h, r) holds D[m][n] for n = r (X row) and m = b*32 + 8*(q/4) + 4*h + q%4 (Y row)
-        float tnum = 0.0f, tden = 0.0f;
-        unsigned int tcnt = 0;
+        if (TWO_LEVEL) {
+#pragma unroll
+            for (int b = 0; b < NB; ++b) {
+#pragma unroll
+                for (int q = 0; q < 16; ++q) acc[b][q] = outer[b][q] + acc[b][q];
+            }
+        }
+        sweep_epilogue<K1, COLS, APPEND>(acc, s, tid, wave, h, r, ytile, y_end, x0, panel, n, scale, STATS, sDB, sGE,
+                                         sC, colpart, colthr, wcnt, wbuf, wcap);
+    }
+    sweep_finish<K1, APPEND>(s, tid, lane, wave, h, seg, rows, xb, P, panel, STATS, part, blockstats, sRed);
+}
+
+// -------------------------------------------------------------------------------------------------
+// split-bf16 sweep (X / Y: split copies in operand order, see l2sq_split_bf16; d = split_features, which is 1, 2
+// or 4 chunks, or a multiple of 4 chunks; ld = split_ld). dot = hi*hi + hi*lo + lo*hi on
+// v_mfma_f32_32x32x16_bf16, in fp32 blocks of 4 chunks (128 features) folded into outer sums kept in AGPRs.
+//
+// Data flow per chunk of 32 features:
+//   X: each wave's operands come straight from global memory into registers (a wave is the only reader of its 32
+//      rows), four register sets, chunk c in set c % 4, loaded two chunks ahead. With at most 4 chunks (no outer
+//      sums) the panel's X stays in registers for the whole segment.
+//   Y: the tile's chunk (16 KiB) is staged through registers into a ring of three LDS stages, three chunks ahead
+//      of the one multiplied.
+// One barrier per chunk, between its two K-steps: before it, the products of K-step 0 run while the operands of
+// K-step 1 are read from LDS and the loads ahead are issued; after it, the products of K-step 1 run while the
+// next chunk's K-step-0 operands are read (the barrier published that stage) and a staged chunk is written to the
+// stage the previous chunk used (the barrier retired its reads).
+// -------------------------------------------------------------------------------------------------
+struct XOps { float4 h0, l0, h1, l1; };                  // this lane's X operands of one chunk (K-steps 0 and 1)
+struct YOps { float4 h0, h1, h2, h3, l0, l1, l2, l3; };  // A operands of one K-step for the Y blocks 0..3
+struct YPart { float4 v0, v1, v2, v3; };                 // one thread's 16-byte share of each block of a Y chunk
+
+__device__ __forceinline__ float4 ld16(const float* base, unsigned byte_off) {
+    return *reinterpret_cast<const float4*>(reinterpret_cast<const char*>(base) + byte_off);
+}
+__device__ __forceinline__ bf16x8 as_bf16x8(const float4& v) { return __builtin_bit_cast(bf16x8, v); }
+
+// one K-step: acc[b] += Y_hi*X_hi, then Y_hi*X_lo, then Y_lo*X_hi
+__device__ __forceinline__ void split_kstep(v16f (&acc)[NB], const YOps& a, const float4& xh4, const float4& xl4) {
+    const bf16x8 xh = as_bf16x8(xh4), xl = as_bf16x8(xl4);
+    acc[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a.h0), xh, acc[0], 0, 0, 0);
+    acc[1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a.h1), xh, acc[1], 0, 0, 0);
+    acc[2] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a.h2), xh, acc[2], 0, 0, 0);
+    acc[3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a.h3), xh, acc[3], 0, 0, 0);
+    acc[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a.h0), xl, acc[0], 0, 0, 0);
+    acc[1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a.h1), xl, acc[1], 0, 0, 0);
+    acc[2] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a.h2), xl, acc[2], 0, 0, 0);
+    acc[3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a.h3), xl, acc[3], 0, 0, 0);
+    acc[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a.l0), xh, acc[0], 0, 0, 0);
+    acc[1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a.l1), xh, acc[1], 0, 0, 0);
+    acc[2] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a.l2), xh, acc[2], 0, 0, 0);
+    acc[3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a.l3), xh, acc[3], 0, 0, 0);
+}
+
+// fp32 values held in AGPRs (the outer sums): only these three operations touch them
+__device__ __forceinline__ float agpr_set(float v) {
+    float a;
+    asm("v_accvgpr_write_b32 %0, %1" : "=a"(a) : "v"(v));
+    return a;
+}
+__device__ __forceinline__ float agpr_get(float a) {
+    float v;
+    asm("v_accvgpr_read_b32 %0, %1" : "=v"(v) : "a"(a));
+    return v;
+}
+__device__ __forceinline__ float agpr_add(float a, float v) { return agpr_set(agpr_get(a) + v); }
+
+template <int U>
+__device__ __forceinline__ XOps& xset(XOps& a, XOps& b, XOps& c, XOps& d) {
+    if constexpr (U == 0) return a;
+    else if constexpr (U == 1) return b;
+    else if constexpr (U == 2) return c;
+    else return d;
+}
+
+// scheduling groups (masks of __builtin_amdgcn_sched_group_barrier)
+constexpr int SG_MFMA = 0x008, SG_VMEM_READ = 0x020, SG_DS_READ = 0x100, SG_DS_WRITE = 0x200;
+
+template <int K1, bool TWO_LEVEL, bool COLS, bool APPEND = false>
+__global__ __launch_bounds__(256) void l2sq_sweep_split(
+    const float* __restrict__ X, const float* __restrict__ Y, int64_t xb, int64_t xe, int64_t n, int d, int ld,
+    const float* __restrict__ qb32, const float* __restrict__ db32, const float* __restrict__ p32,
+    const float* __restrict__ ge32, float scale, int64_t seg_len, int P, int S, Entry* __restrict__ part,
+    Entry* __restrict__ colpart, unsigned int* __restrict__ colthr, double* __restrict__ blockstats, int STATS,
+    const float* __restrict__ wthr = nullptr, int* __restrict__ wcnt = nullptr, int* __restrict__ wbuf = nullptr,
+    int wcap = 0) {
+    static_assert(!(APPEND && COLS), "the wide pass keeps no column lists");
+    int64_t panel, seg;
+    sweep_block(blockIdx.x, P, S, panel, seg);
+    if (panel >= P || seg >= S) return;  // grid padding (uniform per workgroup, before any barrier)
+    __shared__ float4 sY[3 * 1024];  // LDS ring: 3 Y chunks of 4 blocks x 4 KiB
+    __shared__ float sDB[BY];
+    __shared__ float sGE[BY];
+    __shared__ float sC[COLS ? BY * CST : 1];
+    __shared__ double sRed[4][5];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int h = lane >> 5;
+    const int r = lane & 31;
+    const int64_t rows = xe - xb;
+    const int64_t x0 = xb + panel * BX;
+    const int64_t y_begin = seg * seg_len;
+    const int64_t y_end = (y_begin + seg_len < n) ? (y_begin + seg_len) : n;
+    SweepRow<K1> s;
+    sweep_row_init<K1, APPEND>(s, x0 + wave * 32 + r, xe, STATS, qb32, p32, wthr);
+
+    const int nchunks = d / KC;
+    const int64_t bstride = (int64_t)ld * 32;          // words per 32-row block
+    const float* Xw = X + ((x0 >> 5) + wave) * bstride;  // this wave's X block
+    const unsigned lane16 = (unsigned)lane * 16u;
+    const unsigned tid16 = (unsigned)tid * 16u;
+    const unsigned ystep = (unsigned)(bstride * 4);     // bytes between consecutive Y blocks
+
+    auto load_x = [&](XOps& o, int cc) {
+        const float* b = Xw + cc * 1024;
+        o.h0 = ld16(b, lane16);
+        o.l0 = ld16(b, 1024u + lane16);
+        o.h1 = ld16(b, 2048u + lane16);
+        o.l1 = ld16(b, 3072u + lane16);
+    };
+    // Y chunk position three ahead of the one multiplied (ta, ca); past the segment any in-bounds chunk will do,
+    // its data is never multiplied. Branch-free, so that a chunk step stays one scheduling region.
+    int64_t ta = y_begin;
+    int ca = 0;
+    auto load_ahead = [&](YPart& o) {
+        const bool past = ta >= y_end;
+        const float* b = Y + ((past ? y_begin : ta) >> 5) * bstride + (past ? 0 : ca) * 1024;
+        o.v0 = ld16(b, tid16);
+        o.v1 = ld16(b, ystep + tid16);
+        o.v2 = ld16(b, 2u * ystep + tid16);
+        o.v3 = ld16(b, 3u * ystep + tid16);
+        ++ca;
+        const bool wrap = ca == nchunks;
+        ca = wrap ? 0 : ca;
+        ta = wrap ? ta + BY : ta;
+    };
+    auto store_y = [&](int stage, const YPart& o) {
+        float4* dst = sY + stage * 1024 + tid;
+        dst[0] = o.v0;
+        dst[256] = o.v1;
+        dst[512] = o.v2;
+        dst[768] = o.v3;
+    };
+    auto read_ops = [&](YOps& o, int stage, int ks) {
+        const float4* src = sY + stage * 1024 + ks * 128 + lane;
+        o.h0 = src[0];
+        o.l0 = src[64];
+        o.h1 = src[256];
+        o.l1 = src[320];
+        o.h2 = src[512];
+        o.l2 = src[576];
+        o.h3 = src[768];
+        o.l3 = src[832];
+    };
+
+    XOps xs0, xs1, xs2, xs3;  // X operands: chunk c of the tile in set c % 4
+    YPart ya, yb;             // Y staging: ya is written to LDS this chunk, yb is loading
+    YOps o0, o1;              // Y operands of K-steps 0 and 1
+    int st0 = 0;              // LDS stage of the chunk being multiplied
+
+    load_ahead(ya);
+    store_y(0, ya);
+    load_ahead(ya);
+    store_y(1, ya);
+    load_ahead(ya);  // chunk 2, written during chunk 0
+    load_x(xs0, 0);
+    if (nchunks > 1) load_x(xs1, 1);
+    if (!TWO_LEVEL && nchunks > 2) {
+        load_x(xs2, 2);
+        load_x(xs3, 3);
+    }
+    __syncthreads();
+    read_ops(o0, 0, 0);
+
+    v16f acc[NB];
+    float outer[NB][16];  // AGPRs
+    auto step = [&](auto uc, int c) {
+        constexpr int U = decltype(uc)::value;
+        XOps& xs = xset<U>(xs0, xs1, xs2, xs3);
+        // K-step 0 (operands o0 and the X set of this chunk)
+        load_ahead(yb);
+        if (TWO_LEVEL) {
+            const int xc = c + 2 >= nchunks ? c + 2 - nchunks : c + 2;
+            load_x(xset<(U + 2) % 4>(xs0, xs1, xs2, xs3), xc);
+        }
+        read_ops(o1, st0, 1);
+        split_kstep(acc, o0, xs.h0, xs.l0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(SG_DS_READ, 2, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < (TWO_LEVEL ? 8 : 4); ++i) {
+            __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(SG_VMEM_READ, 1, 0);
+        }
+        if (!TWO_LEVEL) __builtin_amdgcn_sched_group_barrier(SG_MFMA, 4, 0);
+        __syncthreads();
+        // K-step 1; the next chunk's operands of K-step 0; chunk + 2 to the stage chunk - 1 used
+        const int st1 = st0 == 2 ? 0 : st0 + 1;
+        const int st2 = st1 == 2 ? 0 : st1 + 1;
+        read_ops(o0, st1, 0);
+        split_kstep(acc, o1, xs.h1, xs.l1);
+        store_y(st2, ya);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(SG_DS_READ, 2, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(SG_DS_WRITE, 1, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(SG_MFMA, 4, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        ya = yb;
+        st0 = st1;
+    };
+
+    for (int64_t ytile = y_begin; ytile < y_end; ytile += BY) {
 #pragma unroll
         for (int b = 0; b < NB; ++b) {
 #pragma unroll
-            for (int a = 0; a < 4; ++a) {
-                const int jl0 = b * 32 + 8 * a + 4 * h;
-                const float4 dbv = *reinterpret_cast<const float4*>(&sDB[jl0]);
-                float4 gev = make_float4(0, 0, 0, 0);
-                if (STATS) gev = *reinterpret_cast<const float4*>(&sGE[jl0]);
-                const float dbs[4] = {dbv.x, dbv.y, dbv.z, dbv.w};
-                const float ges[4] = {gev.x, gev.y, gev.z, gev.w};
+            for (int q = 0; q < 16; ++q) acc[b][q] = 0.0f;
+        }
+        // biases of this tile's Y rows (read in the epilogue, after at least one chunk barrier)
+        if (tid < BY) {
+            const int64_t j = ytile + tid;
+            sDB[tid] = j < y_end ? db32[j] : 0.0f;
+            sGE[tid] = (STATS && j < y_end) ? ge32[j] : 0.0f;
+        }
+        if (TWO_LEVEL) {
 #pragma unroll
-                for (int cc = 0; cc < 4; ++cc) {
-                    const int q = 4 * a + cc;
-                    const float tot = TWO_LEVEL ? (outer[b][q] + acc[b][q]) : acc[b][q];
-                    const float w = fmaf(scale, tot, dbs[cc]);
-                    const int64_t j = ytile + jl0 + cc;
-                    const bool ok = row_ok && j < y_end;
-                    if (APPEND) {
-                        if (ok && w >= wt) {
-                            const int pos = atomicAdd(&wcnt[my_row], 1);
-                            if (pos < wcap) wbuf[my_row * (int64_t)wcap + pos] = (int)j;
-                        }
-                    } else if (ok && w > lv[K1 - 1]) {
-                        float cv = w;
-                        int ci = (int)j;
+            for (int b = 0; b < NB; ++b) {
 #pragma unroll
-                        for (int s = 0; s < K1; ++s) {
-                            if (cv > lv[s]) {
-                                const float tv = lv[s];
-                                const int ti = li[s];
-                                lv[s] = cv;
-                                li[s] = ci;
-                                cv = tv;
-                                ci = ti;
-                            }
-                        }
+                for (int q = 0; q < 16; ++q) outer[b][q] = agpr_set(0.0f);
+            }
+            for (int cb = 0; cb < nchunks; cb += FLUSH_SPLIT) {
+                step(std::integral_constant<int, 0>{}, cb);
+                step(std::integral_constant<int, 1>{}, cb + 1);
+                step(std::integral_constant<int, 2>{}, cb + 2);
+                step(std::integral_constant<int, 3>{}, cb + 3);
+#pragma unroll
+                for (int b = 0; b < NB; ++b) {
+#pragma unroll
+                    for (int q = 0; q < 16; ++q) {
+                        outer[b][q] = agpr_add(outer[b][q], acc[b][q]);
+                        acc[b][q] = 0.0f;
                     }
-                    if (STATS && ok) {
-                        const float sg = w + qbi;
-                        const float cost = (pi + ges[cc]) - w;
-                        tden = fmaf(cost, cost, tden);
-                        cmax = fmaxf(cmax, fabsf(cost));
-                        if (sg > 0.0f) {
-                            tnum = fmaf(sg, sg, tnum);
-                            mx = fmaxf(mx, sg);
-                            ++tcnt;
-                        }
-                    }
-                    if (COLS) sC[(jl0 + cc) * CST + wave * 32 + r] = row_ok ? fmaf(scale, tot, qbi) : -INFINITY;
                 }
             }
-        }
-        if (STATS) {
-            num64 += (double)tnum;
-            den64 += (double)tden;
-            cnt64 += (double)tcnt;
-        }
-        if (COLS) {
-            // each Y row of the tile: its best K1 over this workgroup's 128 X rows (two threads per row, folded).
-            // colthr[j] is the K1-th value of some full list of this chunk, a lower bound of the chunk's K1-th
-            // value: scores at or below it cannot enter the merged top-K1 and are skipped.
-            __syncthreads();
-            const int jl = tid >> 1, half = tid & 1;
-            const int64_t j = ytile + jl;
-            const float thr = j < y_end ? key_float(colthr[j]) : INFINITY;
-            float cw[K1];
-            int cidx[K1];
 #pragma unroll
-            for (int s = 0; s < K1; ++s) { cw[s] = -INFINITY; cidx[s] = -1; }
-            const float* src = &sC[jl * CST + half * 64];
-            const int base = (int)(x0 + half * 64);
-            for (int xx = 0; xx < 64; ++xx) {
-                const float v = src[xx];
-                if (v > thr && v > cw[K1 - 1]) insert_e<K1>(cw, cidx, v, base + xx);
+            for (int b = 0; b < NB; ++b) {
+#pragma unroll
+                for (int q = 0; q < 16; ++q) acc[b][q] = agpr_get(outer[b][q]);
             }
-#pragma unroll
-            for (int s = 0; s < K1; ++s) {
-                const float pv = __shfl_xor(cw[s], 1, 64);
-                const int pi2 = __shfl_xor(cidx[s], 1, 64);
-                if (half == 0 && pi2 >= 0 && better_e(pv, pi2, cw[K1 - 1], cidx[K1 - 1]))
-                    insert_e<K1>(cw, cidx, pv, pi2);
-            }
-            if (half == 0 && j < y_end) {
-                Entry* dst = colpart + (panel * n + j) * K1;
-#pragma unroll
-                for (int s = 0; s < K1; ++s) dst[s] = Entry{cw[s], cidx[s]};
-                if (cidx[K1 - 1] >= 0) atomicMax(&colthr[j], float_key(cw[K1 - 1]));
+        } else {
+            step(std::integral_constant<int, 0>{}, 0);
+            if (nchunks > 1) step(std::integral_constant<int, 1>{}, 1);
+            if (nchunks > 2) {
+                step(std::integral_constant<int, 2>{}, 2);
+                step(std::integral_constant<int, 3>{}, 3);
             }
         }
-        __syncthreads();  // all epilogue reads of sDB/sGE/sC finish before the next tile rewrites them
+        sweep_epilogue<K1, COLS, APPEND>(acc, s, tid, wave, h, r, ytile, y_end, x0, panel, n, scale, STATS, sDB, sGE,
+                                         sC, colpart, colthr, wcnt, wbuf, wcap);
     }
-
-    // lane lists -> part[(seg*rows + local row)*2 + h][K1]
-    if (row_ok && !APPEND) {
-        Entry* out = part + ((seg * rows + (my_row - xb)) * 2 + h) * K1;
-#pragma unroll
-        for (int s = 0; s < K1; ++s) out[s] = Entry{lv[s], li[s]};
-    }
-    if (STATS) {
-        double v[5] = {num64, den64, cnt64, (double)mx, (double)cmax};
-#pragma unroll
-        for (int e = 0; e < 5; ++e) {
-            for (int o = 32; o >= 1; o >>= 1) {
-                const double t = __shfl_xor(v[e], o, 64);
-                v[e] = (e >= 3) ? fmax(v[e], t) : v[e] + t;
-            }
-        }
-        if (lane == 0) {
-#pragma unroll
-            for (int e = 0; e < 5; ++e) sRed[wave][e] = v[e];
-        }
-        __syncthreads();
-        if (tid == 0) {
-            double o[5];
-            for (int e = 0; e < 5; ++e) {
-                o[e] = sRed[0][e];
-                for (int w = 1; w < 4; ++w) o[e] = (e >= 3) ? fmax(o[e], sRed[w][e]) : o[e] + sRed[w][e];
-            }
-            double* dst = blockstats + (seg * P + panel) * 5;
-            for (int e = 0; e < 5; ++e) dst[e] = o[e];
-        }
-    }
+    sweep_finish<K1, APPEND>(s, tid, lane, wave, h, seg, rows, xb, P, panel, STATS, part, blockstats, sRed);
 }
 
 // deterministic reduction of per-block certificate partials (single block); later chunks accumulate
@@ -840,6 +1136,31 @@ __global__ void l2sq_wide_gather(const float* __restrict__ src, int ld, const in
     }
 }
 
+// The same for split copies (operand order): item (destination 32-row block, chunk, 16-byte unit of the row's
+// eight, row within the block); consecutive threads write consecutive units.
+__global__ void l2sq_wide_gather_split(const float* __restrict__ src, int ld, int sd, const int* __restrict__ redo,
+                                       int q0, int Q, int Qpad, const float* __restrict__ redo_thr,
+                                       float* __restrict__ dst, float* __restrict__ thr, int* __restrict__ cnt) {
+    const int nch = sd / KC;
+    const int64_t total = (int64_t)Qpad * nch * 8;
+    const uint4* s4 = reinterpret_cast<const uint4*>(src);
+    uint4* d4 = reinterpret_cast<uint4*>(dst);
+    for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += (int64_t)gridDim.x * blockDim.x) {
+        const int rr = (int)(e & 31);
+        const int j = (int)((e >> 5) & 7);  // (group g4 = 2s + h, part p) as 2 * g4 + p
+        const int64_t t = e >> 8;
+        const int c = (int)(t % nch);
+        const int64_t q = (t / nch) * 32 + rr;
+        const int g4 = j >> 1, p = j & 1;
+        const int64_t du = split_unit(q, c, g4, ld) + 64 * p;
+        d4[du] = q < Q ? s4[split_unit(redo[q0 + q], c, g4, ld) + 64 * p] : make_uint4(0, 0, 0, 0);
+    }
+    for (int q = blockIdx.x * blockDim.x + threadIdx.x; q < Qpad; q += gridDim.x * blockDim.x) {
+        thr[q] = q < Q ? redo_thr[q0 + q] : INFINITY;
+        cnt[q] = 0;
+    }
+}
+
 // Wide pass, step 3: item (row q, slice of its collected candidates) is one wave; it evaluates WIDE_SLICE
 // candidates with the fixed-order fp64 dot (four at a time, as the rescan) and keeps their exact top-k under the
 // tie rule in pv / pi. A row whose candidates overflowed the capacity yields empty lists (it goes to the next
@@ -1029,9 +1350,10 @@ inline bool fused_columns(int d, uint32_t flags) {
     return (flags & HM_COLS) && (flags & (HM_ROWS | HM_STATS)) && d >= FUSE_MIN_D;
 }
 
-// split copies: features padded to whole 32-feature chunks; a row stride that is a multiple of 2 KiB gets one
-// more chunk so the rows of a panel do not all start on the same memory channel
-inline int split_features(int d) { return (d + KC - 1) / KC * KC; }
+// split copies: features padded to 1, 2 or 4 chunks of 32, beyond that to whole groups of 4 chunks (the fp32
+// block of the sweep); a row stride that is a multiple of 2 KiB gets one more chunk so the 32-row blocks do not
+// all start on the same memory channel
+inline int split_features(int d) { return d <= 32 ? 32 : d <= 64 ? 64 : (d + 127) / 128 * 128; }
 inline int split_ld(int d) { return split_features(d) + (split_features(d) % 512 == 0 ? KC : 0); }
 inline int64_t panel_rows(int64_t rows) { return (rows + BX - 1) / BX * BX; }
 
@@ -1236,10 +1558,10 @@ int run_bidir(hipStream_t st, const float* X, const float* Y, int64_t m, int64_t
     const int64_t ch = cp.ch;
     const DirPlan plan = cp.plan;
     if (split) {
-        hipLaunchKernelGGL(l2sq_split_bf16, dim3(4096), dim3(256), 0, st, X, m, panel_rows(m), d, ld,
+        hipLaunchKernelGGL(l2sq_split_bf16, dim3(4096), dim3(256), 0, st, X, m, panel_rows(m), d, sd, ld,
                            reinterpret_cast<unsigned short*>(xsplit));
         HM_LAUNCH_CHECK("l2sq_split_bf16");
-        hipLaunchKernelGGL(l2sq_split_bf16, dim3(4096), dim3(256), 0, st, Y, n, panel_rows(n), d, ld,
+        hipLaunchKernelGGL(l2sq_split_bf16, dim3(4096), dim3(256), 0, st, Y, n, panel_rows(n), d, sd, ld,
                            reinterpret_cast<unsigned short*>(ysplit));
         HM_LAUNCH_CHECK("l2sq_split_bf16");
     }
@@ -1274,11 +1596,11 @@ int run_bidir(hipStream_t st, const float* X, const float* Y, int64_t m, int64_t
 #define HM_SWEEP(TL, CL)                                                                                             \
     do {                                                                                                             \
         if (split)                                                                                                   \
-            hipLaunchKernelGGL((l2sq_sweep<K1, TL, CL, 1>), grid, dim3(256), 0, st, SX, SY, xb, xe, n, sd, ld, qb32, \
-                               db32, p32, ge32, (float)scale, plan.seg_len, (int)panels, plan.S, part, colpart,      \
-                               colthr, blockstats, 1, (int)want_stats);                                              \
+            hipLaunchKernelGGL((l2sq_sweep_split<K1, TL, CL>), grid, dim3(256), 0, st, SX, SY, xb, xe, n, sd, ld,    \
+                               qb32, db32, p32, ge32, (float)scale, plan.seg_len, (int)panels, plan.S, part,         \
+                               colpart, colthr, blockstats, (int)want_stats);                                        \
         else                                                                                                         \
-            hipLaunchKernelGGL((l2sq_sweep<K1, TL, CL, 0>), grid, dim3(256), 0, st, X, Y, xb, xe, n, d, d, qb32,     \
+            hipLaunchKernelGGL((l2sq_sweep<K1, TL, CL>), grid, dim3(256), 0, st, X, Y, xb, xe, n, d, d, qb32,        \
                                db32, p32, ge32, (float)scale, plan.seg_len, (int)panels, plan.S, part, colpart,      \
                                colthr, blockstats, (int)vec4, (int)want_stats);                                      \
     } while (0)
@@ -1343,11 +1665,11 @@ int run_bidir(hipStream_t st, const float* X, const float* Y, int64_t m, int64_t
 #define HM_SWEEP2(TL)                                                                                                \
     do {                                                                                                             \
         if (split)                                                                                                   \
-            hipLaunchKernelGGL((l2sq_sweep<K1, TL, false, 1>), grid, dim3(256), 0, st, SY, SX, yb, ye, m, sd, ld,    \
+            hipLaunchKernelGGL((l2sq_sweep_split<K1, TL, false>), grid, dim3(256), 0, st, SY, SX, yb, ye, m, sd, ld, \
                                db32, qb32, ge32, p32, (float)scale, plan2.seg_len, (int)panels2, plan2.S, part,      \
-                               colpart, colthr, blockstats, 1, 0);                                                   \
+                               colpart, colthr, blockstats, 0);                                                      \
         else                                                                                                         \
-            hipLaunchKernelGGL((l2sq_sweep<K1, TL, false, 0>), grid, dim3(256), 0, st, Y, X, yb, ye, m, d, d, db32,  \
+            hipLaunchKernelGGL((l2sq_sweep<K1, TL, false>), grid, dim3(256), 0, st, Y, X, yb, ye, m, d, d, db32,     \
                                qb32, ge32, p32, (float)scale, plan2.seg_len, (int)panels2, plan2.S, part, colpart,   \
                                colthr, blockstats, (int)vec4, 0);                                                    \
     } while (0)

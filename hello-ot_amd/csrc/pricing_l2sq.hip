@@ -42,22 +42,26 @@ int wide_round(hipStream_t st, bool split, bool two_level, const float* A, const
     for (int q0 = 0; q0 < count; q0 += batch) {
         const int Q = count - q0 < batch ? count - q0 : batch;
         const int Qpad = (int)panel_rows(Q);
-        hipLaunchKernelGGL(l2sq_wide_gather, dim3(2048), dim3(256), 0, st, Asw, gld, queue, q0, Q, Qpad, queue_thr,
-                           w.rows, w.thr, w.cnt);
+        if (split)
+            hipLaunchKernelGGL(l2sq_wide_gather_split, dim3(2048), dim3(256), 0, st, Asw, gld, sd, queue, q0, Q, Qpad,
+                               queue_thr, w.rows, w.thr, w.cnt);
+        else
+            hipLaunchKernelGGL(l2sq_wide_gather, dim3(2048), dim3(256), 0, st, Asw, gld, queue, q0, Q, Qpad, queue_thr,
+                               w.rows, w.thr, w.cnt);
         HM_LAUNCH_CHECK("l2sq_wide_gather");
         const DirPlan plan = plan_dir(Qpad, nb, 0, 256);
         const dim3 grid(sweep_grid(Qpad / BX, plan.S));
-#define HM_WIDE(TL, PR)                                                                                             \
-    hipLaunchKernelGGL((l2sq_sweep<8, TL, false, PR, true>), grid, dim3(256), 0, st, w.rows, Bsw, (int64_t)0,        \
-                       (int64_t)Q, nb, sd, gld, (const float*)nullptr, cand32, (const float*)nullptr,               \
-                       (const float*)nullptr, (float)scale, plan.seg_len, Qpad / BX, plan.S, (Entry*)nullptr,        \
-                       (Entry*)nullptr, (unsigned int*)nullptr, (double*)nullptr, vec4, 0, w.thr, w.cnt, w.buf, cap)
+#define HM_WIDE(KERNEL, ...)                                                                                        \
+    hipLaunchKernelGGL(KERNEL, grid, dim3(256), 0, st, w.rows, Bsw, (int64_t)0, (int64_t)Q, nb, sd, gld,            \
+                       (const float*)nullptr, cand32, (const float*)nullptr, (const float*)nullptr, (float)scale,    \
+                       plan.seg_len, Qpad / BX, plan.S, (Entry*)nullptr, (Entry*)nullptr, (unsigned int*)nullptr,    \
+                       (double*)nullptr, __VA_ARGS__, w.thr, w.cnt, w.buf, cap)
         if (split) {
-            if (two_level) HM_WIDE(true, 1);
-            else HM_WIDE(false, 1);
+            if (two_level) HM_WIDE((l2sq_sweep_split<8, true, false, true>), 0);
+            else HM_WIDE((l2sq_sweep_split<8, false, false, true>), 0);
         } else {
-            if (two_level) HM_WIDE(true, 0);
-            else HM_WIDE(false, 0);
+            if (two_level) HM_WIDE((l2sq_sweep<8, true, false, true>), vec4, 0);
+            else HM_WIDE((l2sq_sweep<8, false, false, true>), vec4, 0);
         }
 #undef HM_WIDE
         HM_LAUNCH_CHECK("l2sq_sweep (wide)");
