@@ -118,7 +118,9 @@ def c5_inputs(dev, chunk):
     p, q = sqnorms(X), sqnorms(Y)
     # duals: g = 0 and f_i = min_j c_ij over 4096 sampled resident rows (a c-transform estimate), so a few
     # hundred pairs per row have sigma > 0, as in a refinement iteration
-    idx = torch.randperm(C5_N, device=dev)[:4096]
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(13)
+    idx = torch.randperm(C5_N, device=dev, generator=gen)[:4096]
     Ys = Y[idx]
     f = torch.empty(chunk, dtype=torch.float64, device=dev)
     for s in range(0, chunk, 4096):

@@ -266,8 +266,9 @@ __device__ __forceinline__ void sweep_row_init(SweepRow<K1>& s, int64_t row, int
 // ytile + b*32 + 8*(q/4) + 4*h + q%4 (the lane (h, r) layout of the 32x32 MFMA accumulators). It ranks
 // w = scale*dot + db into the row list (or appends for the wide pass), adds the certificate terms and, with COLS,
 // passes the tile's scores scale*dot + qb through LDS so that each Y row keeps its best K1 over the workgroup's
-// 128 X rows. Ends with a barrier: the next tile may rewrite sDB / sGE / sC.
-template <int K1, bool COLS, bool APPEND>
+// 128 X rows, CPASS Y rows at a time (sC holds CPASS * CST floats; 256 / CPASS threads scan each row and merge
+// their lists). Ends with a barrier: the next tile may rewrite sDB / sGE / sC.
+template <int K1, bool COLS, bool APPEND, int CPASS = BY>
 __device__ __forceinline__ void sweep_epilogue(const v16f (&tot)[NB], SweepRow<K1>& s, int tid, int wave, int h,
                                                int r, int64_t ytile, int64_t y_end, int64_t x0, int64_t panel,
                                                int64_t n, float scale, int STATS, const float* sDB, const float* sGE,
@@ -324,7 +325,6 @@ __device__ __forceinline__ void sweep_epilogue(const v16f (&tot)[NB], SweepRow<K
                         ++tcnt;
                     }
                 }
-                if (COLS) sC[(jl0 + cc) * CST + wave * 32 + r] = s.ok ? fmaf(scale, t, s.qbi) : -INFINITY;
             }
         }
     }
@@ -334,34 +334,57 @@ __device__ __forceinline__ void sweep_epilogue(const v16f (&tot)[NB], SweepRow<K
         s.cnt64 += (double)tcnt;
     }
     if (COLS) {
-        // each Y row of the tile: its best K1 over this workgroup's 128 X rows (two threads per row, folded).
-        // colthr[j] is the K1-th value of some full list of this chunk, a lower bound of the chunk's K1-th
-        // value: scores at or below it cannot enter the merged top-K1 and are skipped.
-        __syncthreads();
-        const int jl = tid >> 1, half = tid & 1;
-        const int64_t j = ytile + jl;
-        const float thr = j < y_end ? key_float(colthr[j]) : INFINITY;
-        float cw[K1];
-        int cidx[K1];
+        // each Y row of the tile: its best K1 over this workgroup's 128 X rows (TPR threads per row, merged by
+        // shuffles). colthr[j] is the K1-th value of some full list of this chunk, a lower bound of the chunk's
+        // K1-th value: scores at or below it cannot enter the merged top-K1 and are skipped.
+        static_assert(BY % CPASS == 0 && 256 % CPASS == 0 && CPASS % 32 == 0, "column pass shape");
+        constexpr int TPR = 256 / CPASS;  // threads per Y row
+        constexpr int XPT = BX / TPR;     // X rows each of them scans
 #pragma unroll
-        for (int i = 0; i < K1; ++i) { cw[i] = -INFINITY; cidx[i] = -1; }
-        const float* src = &sC[jl * CST + half * 64];
-        const int base = (int)(x0 + half * 64);
-        for (int xx = 0; xx < 64; ++xx) {
-            const float v = src[xx];
-            if (v > thr && v > cw[K1 - 1]) insert_e<K1>(cw, cidx, v, base + xx);
-        }
+        for (int pass = 0; pass < BY / CPASS; ++pass) {
+            if (pass > 0) __syncthreads();  // the previous pass's reads of sC are done
 #pragma unroll
-        for (int i = 0; i < K1; ++i) {
-            const float pv = __shfl_xor(cw[i], 1, 64);
-            const int pi2 = __shfl_xor(cidx[i], 1, 64);
-            if (half == 0 && pi2 >= 0 && better_e(pv, pi2, cw[K1 - 1], cidx[K1 - 1])) insert_e<K1>(cw, cidx, pv, pi2);
-        }
-        if (half == 0 && j < y_end) {
-            Entry* dst = colpart + (panel * n + j) * K1;
+            for (int b = 0; b < NB; ++b) {
+                if (b * 32 < pass * CPASS || b * 32 >= (pass + 1) * CPASS) continue;
 #pragma unroll
-            for (int i = 0; i < K1; ++i) dst[i] = Entry{cw[i], cidx[i]};
-            if (cidx[K1 - 1] >= 0) atomicMax(&colthr[j], float_key(cw[K1 - 1]));
+                for (int q = 0; q < 16; ++q) {
+                    const int jl = b * 32 + 8 * (q / 4) + 4 * h + (q % 4) - pass * CPASS;
+                    sC[jl * CST + wave * 32 + r] = s.ok ? fmaf(scale, tot[b][q], s.qbi) : -INFINITY;
+                }
+            }
+            __syncthreads();
+            const int jl = tid / TPR, part = tid % TPR;
+            const int64_t j = ytile + pass * CPASS + jl;
+            const float thr = j < y_end ? key_float(colthr[j]) : INFINITY;
+            float cw[K1];
+            int cidx[K1];
+#pragma unroll
+            for (int i = 0; i < K1; ++i) { cw[i] = -INFINITY; cidx[i] = -1; }
+            const float* src = &sC[jl * CST + part * XPT];
+            const int base = (int)(x0 + part * XPT);
+            for (int xx = 0; xx < XPT; ++xx) {
+                const float v = src[xx];
+                if (v > thr && v > cw[K1 - 1]) insert_e<K1>(cw, cidx, v, base + xx);
+            }
+#pragma unroll
+            for (int m = 1; m < TPR; m <<= 1) {
+                float pv[K1];
+                int pi2[K1];
+#pragma unroll
+                for (int i = 0; i < K1; ++i) {
+                    pv[i] = __shfl_xor(cw[i], m, 64);
+                    pi2[i] = __shfl_xor(cidx[i], m, 64);
+                }
+#pragma unroll
+                for (int i = 0; i < K1; ++i)
+                    if (pi2[i] >= 0 && better_e(pv[i], pi2[i], cw[K1 - 1], cidx[K1 - 1])) insert_e<K1>(cw, cidx, pv[i], pi2[i]);
+            }
+            if (part == 0 && j < y_end) {
+                Entry* dst = colpart + (panel * n + j) * K1;
+#pragma unroll
+                for (int i = 0; i < K1; ++i) dst[i] = Entry{cw[i], cidx[i]};
+                if (cidx[K1 - 1] >= 0) atomicMax(&colthr[j], float_key(cw[K1 - 1]));
+            }
         }
     }
     __syncthreads();  // all epilogue reads of sDB/sGE/sC finish before the next tile rewrites them
@@ -605,22 +628,26 @@ __global__ __launch_bounds__(256) void l2sq_sweep(
 // -------------------------------------------------------------------------------------------------
 // split-bf16 sweep (X / Y: split copies in operand order, see l2sq_split_bf16; d = split_features, which is 1, 2
 // or 4 chunks, or a multiple of 4 chunks; ld = split_ld). dot = hi*hi + hi*lo + lo*hi on
-// v_mfma_f32_32x32x16_bf16, in fp32 blocks of 4 chunks (128 features) folded into outer sums kept in AGPRs.
+// v_mfma_f32_32x32x16_bf16, in fp32 blocks of 4 chunks (128 features) folded into outer sums.
 //
 // Data flow per chunk of 32 features:
 //   X: each wave's operands come straight from global memory into registers (a wave is the only reader of its 32
-//      rows), four register sets, chunk c in set c % 4, loaded two chunks ahead. With at most 4 chunks (no outer
-//      sums) the panel's X stays in registers for the whole segment.
-//   Y: the tile's chunk (16 KiB) is staged through registers into a ring of three LDS stages, three chunks ahead
-//      of the one multiplied.
-// One barrier per chunk, between its two K-steps: before it, the products of K-step 0 run while the operands of
-// K-step 1 are read from LDS and the loads ahead are issued; after it, the products of K-step 1 run while the
-// next chunk's K-step-0 operands are read (the barrier published that stage) and a staged chunk is written to the
-// stage the previous chunk used (the barrier retired its reads).
+//      rows), four register sets, chunk c in set c % 4, loaded three chunks ahead. With at most 4 chunks (no
+//      outer sums) the panel's X stays in registers for the whole segment.
+//   Y: the tile's chunk (4 blocks x 4 KiB) goes straight from global memory to a ring of LDS stages
+//      (global_load_lds_dwordx4: each wave instruction writes 1 KiB), one stage fewer chunks ahead of the one
+//      multiplied than the ring has stages; no staging registers, no LDS stores.
+// One barrier per chunk, between its two K-steps. Before it, the products of K-step 0 run while the operands of
+// K-step 1 are read from LDS and the loads ahead are issued into the stage the previous chunk used (all its reads
+// retired at the previous barrier); each wave then waits for its own loads of the next chunk, so the barrier
+// publishes that stage. After it, the products of K-step 1 run while the next chunk's K-step-0 operands are read.
+// Outer sums: two accumulator sets alternate by block; the fold of the previous block (outer += acc, VALU) runs
+// a quarter per chunk among the current block's products.
 // -------------------------------------------------------------------------------------------------
+constexpr int SPLIT_STAGES = 5;  // LDS ring of Y chunks (16 KiB each)
+
 struct XOps { float4 h0, l0, h1, l1; };                  // this lane's X operands of one chunk (K-steps 0 and 1)
 struct YOps { float4 h0, h1, h2, h3, l0, l1, l2, l3; };  // A operands of one K-step for the Y blocks 0..3
-struct YPart { float4 v0, v1, v2, v3; };                 // one thread's 16-byte share of each block of a Y chunk
 
 __device__ __forceinline__ float4 ld16(const float* base, unsigned byte_off) {
     return *reinterpret_cast<const float4*>(reinterpret_cast<const char*>(base) + byte_off);
@@ -644,18 +671,13 @@ __device__ __forceinline__ void split_kstep(v16f (&acc)[NB], const YOps& a, cons
     acc[3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a.l3), xh, acc[3], 0, 0, 0);
 }
 
-// fp32 values held in AGPRs (the outer sums): only these three operations touch them
-__device__ __forceinline__ float agpr_set(float v) {
-    float a;
-    asm("v_accvgpr_write_b32 %0, %1" : "=a"(a) : "v"(v));
-    return a;
+template <int U>
+__device__ __forceinline__ float4* xset_stage(float4* a, float4* b, float4* c, float4* d) {
+    if constexpr (U == 0) return a;
+    else if constexpr (U == 1) return b;
+    else if constexpr (U == 2) return c;
+    else return d;
 }
-__device__ __forceinline__ float agpr_get(float a) {
-    float v;
-    asm("v_accvgpr_read_b32 %0, %1" : "=v"(v) : "a"(a));
-    return v;
-}
-__device__ __forceinline__ float agpr_add(float a, float v) { return agpr_set(agpr_get(a) + v); }
 
 template <int U>
 __device__ __forceinline__ XOps& xset(XOps& a, XOps& b, XOps& c, XOps& d) {
@@ -665,8 +687,42 @@ __device__ __forceinline__ XOps& xset(XOps& a, XOps& b, XOps& c, XOps& d) {
     else return d;
 }
 
+// 16 bytes per lane from global memory straight to LDS: lane l writes lds_byte + 16 l (M0 holds the wave-uniform
+// LDS address). Issued from assembly: the compiler would otherwise treat every later LDS read as a possible alias
+// of these writes and wait for all outstanding loads before it. The caller waits (wait_vmcnt) before the data is
+// read, and before the workgroup ends.
+__device__ __forceinline__ void load_lds16(const char* g, unsigned lds_byte) {
+    unsigned saved;  // M0 is restored, so the compiler's use of it (if any) is untouched
+    asm volatile(
+        "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off\n\ts_nop 0\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "v"(g), "s"(lds_byte));
+}
+
+// s_waitcnt that waits for the vector-memory counter only (gfx9 encoding: vmcnt in bits 3:0 and 15:14, expcnt
+// and lgkmcnt at their maxima)
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// Barrier of the split sweep's chunk loop: this wave's loads older than the last N have landed (the stage the
+// barrier publishes) and its LDS reads are done (the stage refilled after the barrier). No release fence: the
+// fence of __syncthreads would also wait for the loads still in flight to the other stages. The empty asm
+// statements keep the compiler from moving memory accesses across the barrier.
+template <int N>
+__device__ __forceinline__ void ring_barrier() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4));
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
 // scheduling groups (masks of __builtin_amdgcn_sched_group_barrier)
-constexpr int SG_MFMA = 0x008, SG_VMEM_READ = 0x020, SG_DS_READ = 0x100, SG_DS_WRITE = 0x200;
+constexpr int SG_VALU = 0x002, SG_MFMA = 0x008, SG_VMEM_READ = 0x020, SG_DS_READ = 0x100;
 
 template <int K1, bool TWO_LEVEL, bool COLS, bool APPEND = false>
 __global__ __launch_bounds__(256) void l2sq_sweep_split(
@@ -677,10 +733,18 @@ __global__ __launch_bounds__(256) void l2sq_sweep_split(
     const float* __restrict__ wthr = nullptr, int* __restrict__ wcnt = nullptr, int* __restrict__ wbuf = nullptr,
     int wcap = 0) {
     static_assert(!(APPEND && COLS), "the wide pass keeps no column lists");
+    // Ring of Y chunks: with outer sums (chunks per tile a multiple of 4) 4 stages, chunk c of a tile in stage
+    // c % 4, the same static index as its X set; the loads are then compiler builtins whose LDS writes the
+    // compiler can tell apart from the reads of the other stages. With at most 4 chunks per tile the stage index
+    // is dynamic and the loads are issued from assembly (there are no other loads in that loop to count).
+    constexpr int NS = TWO_LEVEL ? 4 : SPLIT_STAGES;
+    constexpr int AHEAD = NS - 1;                 // Y chunks in flight ahead of the one multiplied
+    constexpr int VMEM_STEP = TWO_LEVEL ? 8 : 4;  // vector-memory instructions a chunk issues (Y, then X)
     int64_t panel, seg;
     sweep_block(blockIdx.x, P, S, panel, seg);
     if (panel >= P || seg >= S) return;  // grid padding (uniform per workgroup, before any barrier)
-    __shared__ float4 sY[3 * 1024];  // LDS ring: 3 Y chunks of 4 blocks x 4 KiB
+    __shared__ float4 sY0[1024], sY1[1024], sY2[1024], sY3[1024];  // LDS ring (Y chunk: 4 blocks x 4 KiB)
+    __shared__ float4 sY4[NS > 4 ? 1024 : 1];
     __shared__ float sDB[BY];
     __shared__ float sGE[BY];
     __shared__ float sC[COLS ? BY * CST : 1];
@@ -704,6 +768,9 @@ __global__ __launch_bounds__(256) void l2sq_sweep_split(
     const unsigned lane16 = (unsigned)lane * 16u;
     const unsigned tid16 = (unsigned)tid * 16u;
     const unsigned ystep = (unsigned)(bstride * 4);     // bytes between consecutive Y blocks
+    auto ystage = [&](int st) -> float4* {
+        return st == 0 ? sY0 : st == 1 ? sY1 : st == 2 ? sY2 : st == 3 ? sY3 : sY4;
+    };
 
     auto load_x = [&](XOps& o, int cc) {
         const float* b = Xw + cc * 1024;
@@ -712,31 +779,30 @@ __global__ __launch_bounds__(256) void l2sq_sweep_split(
         o.h1 = ld16(b, 2048u + lane16);
         o.l1 = ld16(b, 3072u + lane16);
     };
-    // Y chunk position three ahead of the one multiplied (ta, ca); past the segment any in-bounds chunk will do,
-    // its data is never multiplied. Branch-free, so that a chunk step stays one scheduling region.
+    // Y chunk position AHEAD chunks past the one multiplied (ta, ca); past the segment any in-bounds chunk will
+    // do, its data is never multiplied. Branch-free, so that a chunk step stays one scheduling region.
     int64_t ta = y_begin;
     int ca = 0;
-    auto load_ahead = [&](YPart& o) {
+    auto load_ahead = [&](float4* stage) {
         const bool past = ta >= y_end;
-        const float* b = Y + ((past ? y_begin : ta) >> 5) * bstride + (past ? 0 : ca) * 1024;
-        o.v0 = ld16(b, tid16);
-        o.v1 = ld16(b, ystep + tid16);
-        o.v2 = ld16(b, 2u * ystep + tid16);
-        o.v3 = ld16(b, 3u * ystep + tid16);
+        const char* b = reinterpret_cast<const char*>(Y + ((past ? y_begin : ta) >> 5) * bstride + (past ? 0 : ca) * 1024);
+        // thread t's 16 bytes of block i go to stage + i*4 KiB + t*16; one wave instruction fills 1 KiB
+        float4* dst = stage + wave * 64;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            if (TWO_LEVEL)
+                __builtin_amdgcn_global_load_lds(b + i * ystep + tid16,
+                                                 (__attribute__((address_space(3))) void*)(dst + i * 256), 16, 0, 0);
+            else
+                load_lds16(b + i * ystep + tid16, __builtin_amdgcn_readfirstlane((unsigned)(uintptr_t)(dst + i * 256)));
+        }
         ++ca;
         const bool wrap = ca == nchunks;
         ca = wrap ? 0 : ca;
         ta = wrap ? ta + BY : ta;
     };
-    auto store_y = [&](int stage, const YPart& o) {
-        float4* dst = sY + stage * 1024 + tid;
-        dst[0] = o.v0;
-        dst[256] = o.v1;
-        dst[512] = o.v2;
-        dst[768] = o.v3;
-    };
-    auto read_ops = [&](YOps& o, int stage, int ks) {
-        const float4* src = sY + stage * 1024 + ks * 128 + lane;
+    auto read_ops = [&](YOps& o, const float4* stage, int ks) {
+        const float4* src = stage + ks * 128 + lane;
         o.h0 = src[0];
         o.l0 = src[64];
         o.h1 = src[256];
@@ -748,76 +814,98 @@ __global__ __launch_bounds__(256) void l2sq_sweep_split(
     };
 
     XOps xs0, xs1, xs2, xs3;  // X operands: chunk c of the tile in set c % 4
-    YPart ya, yb;             // Y staging: ya is written to LDS this chunk, yb is loading
     YOps o0, o1;              // Y operands of K-steps 0 and 1
     int st0 = 0;              // LDS stage of the chunk being multiplied
 
-    load_ahead(ya);
-    store_y(0, ya);
-    load_ahead(ya);
-    store_y(1, ya);
-    load_ahead(ya);  // chunk 2, written during chunk 0
+    load_ahead(sY0);
+    load_ahead(sY1);
+    load_ahead(sY2);
+    if (AHEAD > 3) load_ahead(sY3);
     load_x(xs0, 0);
     if (nchunks > 1) load_x(xs1, 1);
-    if (!TWO_LEVEL && nchunks > 2) {
-        load_x(xs2, 2);
-        load_x(xs3, 3);
-    }
+    if (nchunks > 2) load_x(xs2, 2);
+    if (!TWO_LEVEL && nchunks > 2) load_x(xs3, 3);
+    wait_vmcnt<0>();
     __syncthreads();
-    read_ops(o0, 0, 0);
+    read_ops(o0, sY0, 0);
 
-    v16f acc[NB];
-    float outer[NB][16];  // AGPRs
-    auto step = [&](auto uc, int c) {
+    v16f accA[NB], accB[NB];  // alternate 4-chunk blocks
+    float outer[NB][16];
+
+    // chunk c of the tile (X set U = c % 4) into `acc`; meanwhile a quarter of the other set is folded into the
+    // outer sums (FOLD) and cleared
+    auto step = [&](auto uc, auto fc, int c, v16f (&acc)[NB], v16f (&other)[NB]) {
         constexpr int U = decltype(uc)::value;
+        constexpr bool FOLD = decltype(fc)::value;
         XOps& xs = xset<U>(xs0, xs1, xs2, xs3);
-        // K-step 0 (operands o0 and the X set of this chunk)
-        load_ahead(yb);
-        if (TWO_LEVEL) {
-            const int xc = c + 2 >= nchunks ? c + 2 - nchunks : c + 2;
-            load_x(xset<(U + 2) % 4>(xs0, xs1, xs2, xs3), xc);
-        }
-        read_ops(o1, st0, 1);
+        // K-step 0; X three chunks ahead; then the Y chunk AHEAD further into the stage chunk - 1 used
+        const int st1 = st0 == NS - 1 ? 0 : st0 + 1;
+        float4* cur = TWO_LEVEL ? xset_stage<U>(sY0, sY1, sY2, sY3) : ystage(st0);
+        float4* nxt = TWO_LEVEL ? xset_stage<(U + 1) % 4>(sY0, sY1, sY2, sY3) : ystage(st1);
+        float4* fill = TWO_LEVEL ? xset_stage<(U + 3) % 4>(sY0, sY1, sY2, sY3) : ystage(st0 == 0 ? NS - 1 : st0 - 1);
+        read_ops(o1, cur, 1);
         split_kstep(acc, o0, xs.h0, xs.l0);
+        if (TWO_LEVEL) {
+            const int xc = c + 3 >= nchunks ? c + 3 - nchunks : c + 3;
+            load_x(xset<(U + 3) % 4>(xs0, xs1, xs2, xs3), xc);
+        }
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
             __builtin_amdgcn_sched_group_barrier(SG_DS_READ, 2, 0);
         }
+        if (TWO_LEVEL) {
 #pragma unroll
-        for (int i = 0; i < (TWO_LEVEL ? 8 : 4); ++i) {
-            __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
-            __builtin_amdgcn_sched_group_barrier(SG_VMEM_READ, 1, 0);
+            for (int i = 0; i < 4; ++i) {
+                __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(SG_VMEM_READ, 1, 0);
+            }
         }
-        if (!TWO_LEVEL) __builtin_amdgcn_sched_group_barrier(SG_MFMA, 4, 0);
-        __syncthreads();
-        // K-step 1; the next chunk's operands of K-step 0; chunk + 2 to the stage chunk - 1 used
-        const int st1 = st0 == 2 ? 0 : st0 + 1;
-        const int st2 = st1 == 2 ? 0 : st1 + 1;
-        read_ops(o0, st1, 0);
-        split_kstep(acc, o1, xs.h1, xs.l1);
-        store_y(st2, ya);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
-            __builtin_amdgcn_sched_group_barrier(SG_DS_READ, 2, 0);
-        }
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
-            __builtin_amdgcn_sched_group_barrier(SG_DS_WRITE, 1, 0);
-        }
-        __builtin_amdgcn_sched_group_barrier(SG_MFMA, 4, 0);
+        __builtin_amdgcn_sched_group_barrier(SG_MFMA, TWO_LEVEL ? 4 : 8, 0);
         __builtin_amdgcn_sched_barrier(0);
-        ya = yb;
+        // Issue order per chunk: X loads, then the Y loads; this wave's loads of the next chunk were issued at the
+        // end of the chunk AHEAD - 1 back, so at most the later chunks' instructions may still be in flight.
+        load_ahead(fill);
+        ring_barrier<(AHEAD - 1) * VMEM_STEP>();
+        // K-step 1; the next chunk's K-step-0 operands; a quarter of the fold
+        read_ops(o0, nxt, 0);
+        split_kstep(acc, o1, xs.h1, xs.l1);
+        if (FOLD) {
+#pragma unroll
+            for (int q = 0; q < 16; ++q) {
+                outer[U][q] += other[U][q];
+                other[U][q] = 0.0f;
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(SG_DS_READ, 2, 0);
+        }
+        if (FOLD) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(SG_VALU, 4, 0);
+            }
+        } else {
+            __builtin_amdgcn_sched_group_barrier(SG_MFMA, 8, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
         st0 = st1;
     };
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    using I2 = std::integral_constant<int, 2>;
+    using I3 = std::integral_constant<int, 3>;
+    using FOLD = std::true_type;
+    using NOFOLD = std::false_type;
 
     for (int64_t ytile = y_begin; ytile < y_end; ytile += BY) {
 #pragma unroll
         for (int b = 0; b < NB; ++b) {
 #pragma unroll
-            for (int q = 0; q < 16; ++q) acc[b][q] = 0.0f;
+            for (int q = 0; q < 16; ++q) { accA[b][q] = 0.0f; accB[b][q] = 0.0f; }
         }
         // biases of this tile's Y rows (read in the epilogue, after at least one chunk barrier)
         if (tid < BY) {
@@ -829,38 +917,42 @@ __global__ __launch_bounds__(256) void l2sq_sweep_split(
 #pragma unroll
             for (int b = 0; b < NB; ++b) {
 #pragma unroll
-                for (int q = 0; q < 16; ++q) outer[b][q] = agpr_set(0.0f);
+                for (int q = 0; q < 16; ++q) outer[b][q] = 0.0f;
             }
-            for (int cb = 0; cb < nchunks; cb += FLUSH_SPLIT) {
-                step(std::integral_constant<int, 0>{}, cb);
-                step(std::integral_constant<int, 1>{}, cb + 1);
-                step(std::integral_constant<int, 2>{}, cb + 2);
-                step(std::integral_constant<int, 3>{}, cb + 3);
-#pragma unroll
-                for (int b = 0; b < NB; ++b) {
-#pragma unroll
-                    for (int q = 0; q < 16; ++q) {
-                        outer[b][q] = agpr_add(outer[b][q], acc[b][q]);
-                        acc[b][q] = 0.0f;
-                    }
+            // blocks alternate between the two sets; the outer sums take the blocks in order
+            const int nblk = nchunks / FLUSH_SPLIT;
+            for (int kb = 0; kb < nblk; kb += 2) {
+                const int c = kb * FLUSH_SPLIT;
+                step(I0{}, FOLD{}, c, accA, accB);
+                step(I1{}, FOLD{}, c + 1, accA, accB);
+                step(I2{}, FOLD{}, c + 2, accA, accB);
+                step(I3{}, FOLD{}, c + 3, accA, accB);
+                if (kb + 1 < nblk) {
+                    step(I0{}, FOLD{}, c + 4, accB, accA);
+                    step(I1{}, FOLD{}, c + 5, accB, accA);
+                    step(I2{}, FOLD{}, c + 6, accB, accA);
+                    step(I3{}, FOLD{}, c + 7, accB, accA);
                 }
             }
+            // the last block's set; the other one was folded and cleared during it
+            const bool last_a = (nblk & 1) != 0;
 #pragma unroll
             for (int b = 0; b < NB; ++b) {
 #pragma unroll
-                for (int q = 0; q < 16; ++q) acc[b][q] = agpr_get(outer[b][q]);
+                for (int q = 0; q < 16; ++q) accA[b][q] = outer[b][q] + (last_a ? accA[b][q] : accB[b][q]);
             }
         } else {
-            step(std::integral_constant<int, 0>{}, 0);
-            if (nchunks > 1) step(std::integral_constant<int, 1>{}, 1);
+            step(I0{}, NOFOLD{}, 0, accA, accB);
+            if (nchunks > 1) step(I1{}, NOFOLD{}, 1, accA, accB);
             if (nchunks > 2) {
-                step(std::integral_constant<int, 2>{}, 2);
-                step(std::integral_constant<int, 3>{}, 3);
+                step(I2{}, NOFOLD{}, 2, accA, accB);
+                step(I3{}, NOFOLD{}, 3, accA, accB);
             }
         }
-        sweep_epilogue<K1, COLS, APPEND>(acc, s, tid, wave, h, r, ytile, y_end, x0, panel, n, scale, STATS, sDB, sGE,
-                                         sC, colpart, colthr, wcnt, wbuf, wcap);
+        sweep_epilogue<K1, COLS, APPEND>(accA, s, tid, wave, h, r, ytile, y_end, x0, panel, n, scale, STATS, sDB,
+                                         sGE, sC, colpart, colthr, wcnt, wbuf, wcap);
     }
+    wait_vmcnt<0>();  // the loads ahead into LDS land before the workgroup can end
     sweep_finish<K1, APPEND>(s, tid, lane, wave, h, seg, rows, xb, P, panel, STATS, part, blockstats, sRed);
 }
 
