@@ -51,12 +51,13 @@ def roofline(precision, achieved):
         executed, peak, unit_work = achieved, PEAK_FP32_MFMA, "2*d flop per pair"
     return {"bound": "mfma", "achieved": executed / 1e12, "peak": peak / 1e12, "unit": "TFLOP/s",
             "frac": executed / peak, "traffic": sweep_traffic(), "traffic_source": TRAFFIC_PROFILE.name,
-            "kernel": "l2sq_sweep", "sweep": precision, "work_per_pair": unit_work,
+            "kernel": "l2sq_sweep_split" if precision == "bf16x3" else "l2sq_sweep", "sweep": precision,
+            "work_per_pair": unit_work,
             "algorithmic_tflops": achieved / 1e12, "algorithmic_flops_per_pair": 2 * C5_D}
 
 
 def sweep_traffic():
-    """HBM bytes per l2sq_sweep launch at the C5 workload, from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE
+    """HBM bytes per split-sweep launch at the C5 workload, from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE
     summary (scaled by a plain copy kernel's counters); None when no such summary is present."""
     try:
         for line in TRAFFIC_PROFILE.read_text().splitlines():
