@@ -51,7 +51,7 @@ def roofline(precision, achieved):
         executed, peak, unit_work = achieved, PEAK_FP32_MFMA, "2*d flop per pair"
     return {"bound": "mfma", "achieved": executed / 1e12, "peak": peak / 1e12, "unit": "TFLOP/s",
             "frac": executed / peak, "traffic": sweep_traffic(), "traffic_source": TRAFFIC_PROFILE.name,
-            "kernel": "l2sq_sweep_split" if precision == "bf16x3" else "l2sq_sweep", "sweep": precision,
+            "kernel": "l2sq_sweep_split_w" if precision == "bf16x3" else "l2sq_sweep", "sweep": precision,
             "work_per_pair": unit_work,
             "algorithmic_tflops": achieved / 1e12, "algorithmic_flops_per_pair": 2 * C5_D}
 
@@ -132,7 +132,9 @@ def c5_inputs(dev, chunk):
     return X, Y, p, q, f, g
 
 
-def bench_c5(dev, chunk, steps, warmup, inputs=None, precision="auto"):
+def bench_c5(dev, chunk, steps, warmup, inputs=None, precision="auto", keep=None):
+    """One C5 pricing step timed over `steps` runs; with `keep` (a list) the last run's row and column outputs
+    are appended to it."""
     from hello_ot_amd import _lib
     from hello_ot_amd.kernels.generic_scan import pricing_l2sq
 
@@ -168,6 +170,8 @@ def bench_c5(dev, chunk, steps, warmup, inputs=None, precision="auto"):
         "finalize_ms_avg": fin_ms / max(fins, 1), "rescan_ms_total": res_ms,
         "positive_pairs": float(st[2]), "max_violation": float(st[3]),
     }
+    if keep is not None:
+        keep.extend(t.clone() for t in out[:4])
     del qb, db, out
     return sec, pairs, achieved, info
 
@@ -465,16 +469,22 @@ def main():
 
     inputs = c5_inputs(dev, args.chunk)
     precision = sweep_precision("auto", C5_D)
-    sec, pairs, achieved, info = bench_c5(dev, args.chunk, args.steps, args.warmup, inputs, precision)
+    split_out = []
+    sec, pairs, achieved, info = bench_c5(dev, args.chunk, args.steps, args.warmup, inputs, precision, split_out)
     extras = {}
     if not args.no_extras and precision != "fp32":
         # the same step on the fp32 MFMA sweep (identical outputs), against the fp32 matrix peak
         log("[bench] C5 step on the fp32 sweep ...")
-        s32, _, a32, i32 = bench_c5(dev, args.chunk, args.steps, 0, inputs, "fp32")
+        fp32_out = []
+        s32, _, a32, i32 = bench_c5(dev, args.chunk, args.steps, 0, inputs, "fp32", fp32_out)
+        # the exact fp64 re-check makes both sweeps' row and column lists (values and indices) identical
+        same = all(bool(torch.equal(a, b)) for a, b in zip(split_out, fp32_out))
         extras["c5_step_fp32_sweep"] = {"pairs_per_s": pairs / s32, "ms_per_step": s32 * 1e3,
                                         "sweep_ms_avg": i32["sweep_ms_avg"], "sweep_tflops": a32 / 1e12,
-                                        "sweep_mfma_frac": a32 / PEAK_FP32_MFMA}
-    del inputs
+                                        "sweep_mfma_frac": a32 / PEAK_FP32_MFMA,
+                                        "outputs_identical_to_split_sweep": same}
+        del fp32_out
+    del inputs, split_out
     torch.cuda.empty_cache()
     if not args.no_extras:
         log("[bench] C2 ...")

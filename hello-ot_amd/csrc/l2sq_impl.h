@@ -9,12 +9,13 @@
 // Pipeline, per internal chunk of at most CHUNK_MAX X rows (the column lists of a chunk stay bounded):
 //   1. prep (once): fp64 row norms ||x_i||, ||y_j||, their maxima, max|bias|; fp32 copies of the biases; with
 //                HM_BF16X3 the split-bf16 copies of X and Y.
-//   2. sweep:    MFMA tiles of Y * X^T, fp32 32x32x2 or split-bf16 32x32x16 (a workgroup owns 128 X rows and
-//                walks one segment of Y in 128-row tiles; lane (h, r) of a wave owns X row r of the wave's 32 and
-//                16 Y rows of each 32-row block). From the same accumulators:
+//   2. sweep:    MFMA tiles of Y * X^T, fp32 32x32x2 or split-bf16 32x32x16 (a workgroup owns a panel of 128 X
+//                rows, 256 in the split sweep for d > 128, and walks one segment of Y in 128-row tiles; lane (h, r)
+//                of a wave owns X row r of the wave's 32 and 16 Y rows of each 32-row block). From the same
+//                accumulators:
 //                  rows:    each lane keeps its best K1 of w = scale*dot32 + db32_j (ranks like sigma in j);
 //                  columns: the tile's scores scale*dot32 + qb32_i go through LDS and each Y row keeps its
-//                           best K1 over the workgroup's 128 X rows (one list per X panel);
+//                           best K1 over the panel's X rows (one list per X panel);
 //                  certificate sums in fp32 per tile, flushed to fp64.
 //   3. finalize: one wave per row (or column) merges the partial lists into the best KM, checks that every
 //                dropped value is below the k-th minus twice the rigorous error bound (otherwise the row is
@@ -46,7 +47,7 @@ namespace {
 typedef float v16f __attribute__((ext_vector_type(16)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
-constexpr int BX = 128;            // X rows per workgroup (4 waves x 32)
+constexpr int BX = 128;            // X rows per workgroup of the fp32 and short split sweeps (4 waves x 32)
 constexpr int NB = 4;              // 32-wide Y blocks per wave
 constexpr int BY = 32 * NB;        // Y rows per tile
 constexpr int KC = 32;             // features per LDS chunk
@@ -626,14 +627,13 @@ __global__ __launch_bounds__(256) void l2sq_sweep(
 }
 
 // -------------------------------------------------------------------------------------------------
-// split-bf16 sweep (X / Y: split copies in operand order, see l2sq_split_bf16; d = split_features, which is 1, 2
-// or 4 chunks, or a multiple of 4 chunks; ld = split_ld). dot = hi*hi + hi*lo + lo*hi on
-// v_mfma_f32_32x32x16_bf16, in fp32 blocks of 4 chunks (128 features) folded into outer sums.
+// split-bf16 sweep for d <= 128 (X / Y: split copies in operand order, see l2sq_split_bf16; d = split_features,
+// which is 1, 2 or 4 chunks; ld = split_ld). dot = hi*hi + hi*lo + lo*hi on v_mfma_f32_32x32x16_bf16 in one fp32
+// block; longer rows take l2sq_sweep_split_w.
 //
 // Data flow per chunk of 32 features:
-//   X: each wave's operands come straight from global memory into registers (a wave is the only reader of its 32
-//      rows), four register sets, chunk c in set c % 4, loaded three chunks ahead. With at most 4 chunks (no
-//      outer sums) the panel's X stays in registers for the whole segment.
+//   X: the panel's operands (at most 4 chunks) are loaded once into registers and stay for the whole segment (a
+//      wave is the only reader of its 32 rows).
 //   Y: the tile's chunk (4 blocks x 4 KiB) goes straight from global memory to a ring of LDS stages
 //      (global_load_lds_dwordx4: each wave instruction writes 1 KiB), one stage fewer chunks ahead of the one
 //      multiplied than the ring has stages; no staging registers, no LDS stores.
@@ -641,8 +641,6 @@ __global__ __launch_bounds__(256) void l2sq_sweep(
 // K-step 1 are read from LDS and the loads ahead are issued into the stage the previous chunk used (all its reads
 // retired at the previous barrier); each wave then waits for its own loads of the next chunk, so the barrier
 // publishes that stage. After it, the products of K-step 1 run while the next chunk's K-step-0 operands are read.
-// Outer sums: two accumulator sets alternate by block; the fold of the previous block (outer += acc, VALU) runs
-// a quarter per chunk among the current block's products.
 // -------------------------------------------------------------------------------------------------
 constexpr int SPLIT_STAGES = 5;  // LDS ring of Y chunks (16 KiB each)
 
@@ -724,7 +722,7 @@ __device__ __forceinline__ void ring_barrier() {
 // scheduling groups (masks of __builtin_amdgcn_sched_group_barrier)
 constexpr int SG_VALU = 0x002, SG_MFMA = 0x008, SG_VMEM_READ = 0x020, SG_DS_READ = 0x100;
 
-template <int K1, bool TWO_LEVEL, bool COLS, bool APPEND = false>
+template <int K1, bool COLS, bool APPEND = false>
 __global__ __launch_bounds__(256) void l2sq_sweep_split(
     const float* __restrict__ X, const float* __restrict__ Y, int64_t xb, int64_t xe, int64_t n, int d, int ld,
     const float* __restrict__ qb32, const float* __restrict__ db32, const float* __restrict__ p32,
@@ -733,18 +731,15 @@ __global__ __launch_bounds__(256) void l2sq_sweep_split(
     const float* __restrict__ wthr = nullptr, int* __restrict__ wcnt = nullptr, int* __restrict__ wbuf = nullptr,
     int wcap = 0) {
     static_assert(!(APPEND && COLS), "the wide pass keeps no column lists");
-    // Ring of Y chunks: with outer sums (chunks per tile a multiple of 4) 4 stages, chunk c of a tile in stage
-    // c % 4, the same static index as its X set; the loads are then compiler builtins whose LDS writes the
-    // compiler can tell apart from the reads of the other stages. With at most 4 chunks per tile the stage index
-    // is dynamic and the loads are issued from assembly (there are no other loads in that loop to count).
-    constexpr int NS = TWO_LEVEL ? 4 : SPLIT_STAGES;
-    constexpr int AHEAD = NS - 1;                 // Y chunks in flight ahead of the one multiplied
-    constexpr int VMEM_STEP = TWO_LEVEL ? 8 : 4;  // vector-memory instructions a chunk issues (Y, then X)
+    // Ring of Y chunks: the stage index is dynamic, so the loads are issued from assembly (there are no other
+    // loads in the chunk loop to count)
+    constexpr int NS = SPLIT_STAGES;
+    constexpr int AHEAD = NS - 1;  // Y chunks in flight ahead of the one multiplied
+    constexpr int VMEM_STEP = 4;   // vector-memory instructions a chunk issues
     int64_t panel, seg;
     sweep_block(blockIdx.x, P, S, panel, seg);
     if (panel >= P || seg >= S) return;  // grid padding (uniform per workgroup, before any barrier)
-    __shared__ float4 sY0[1024], sY1[1024], sY2[1024], sY3[1024];  // LDS ring (Y chunk: 4 blocks x 4 KiB)
-    __shared__ float4 sY4[NS > 4 ? 1024 : 1];
+    __shared__ float4 sY0[1024], sY1[1024], sY2[1024], sY3[1024], sY4[1024];  // LDS ring (Y chunk: 4 blocks x 4 KiB)
     __shared__ float sDB[BY];
     __shared__ float sGE[BY];
     __shared__ float sC[COLS ? BY * CST : 1];
@@ -789,13 +784,8 @@ __global__ __launch_bounds__(256) void l2sq_sweep_split(
         // thread t's 16 bytes of block i go to stage + i*4 KiB + t*16; one wave instruction fills 1 KiB
         float4* dst = stage + wave * 64;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            if (TWO_LEVEL)
-                __builtin_amdgcn_global_load_lds(b + i * ystep + tid16,
-                                                 (__attribute__((address_space(3))) void*)(dst + i * 256), 16, 0, 0);
-            else
-                load_lds16(b + i * ystep + tid16, __builtin_amdgcn_readfirstlane((unsigned)(uintptr_t)(dst + i * 256)));
-        }
+        for (int i = 0; i < 4; ++i)
+            load_lds16(b + i * ystep + tid16, __builtin_amdgcn_readfirstlane((unsigned)(uintptr_t)(dst + i * 256)));
         ++ca;
         const bool wrap = ca == nchunks;
         ca = wrap ? 0 : ca;
@@ -813,84 +803,57 @@ __global__ __launch_bounds__(256) void l2sq_sweep_split(
         o.l3 = src[832];
     };
 
-    XOps xs0, xs1, xs2, xs3;  // X operands: chunk c of the tile in set c % 4
+    XOps xs0, xs1, xs2, xs3;  // X operands of chunks 0..3
     YOps o0, o1;              // Y operands of K-steps 0 and 1
     int st0 = 0;              // LDS stage of the chunk being multiplied
 
     load_ahead(sY0);
     load_ahead(sY1);
     load_ahead(sY2);
-    if (AHEAD > 3) load_ahead(sY3);
+    load_ahead(sY3);
     load_x(xs0, 0);
     if (nchunks > 1) load_x(xs1, 1);
-    if (nchunks > 2) load_x(xs2, 2);
-    if (!TWO_LEVEL && nchunks > 2) load_x(xs3, 3);
+    if (nchunks > 2) {
+        load_x(xs2, 2);
+        load_x(xs3, 3);
+    }
     wait_vmcnt<0>();
     __syncthreads();
     read_ops(o0, sY0, 0);
 
-    v16f accA[NB], accB[NB];  // alternate 4-chunk blocks
-    float outer[NB][16];
+    v16f acc[NB];
 
-    // chunk c of the tile (X set U = c % 4) into `acc`; meanwhile a quarter of the other set is folded into the
-    // outer sums (FOLD) and cleared
-    auto step = [&](auto uc, auto fc, int c, v16f (&acc)[NB], v16f (&other)[NB]) {
+    // chunk c = U of the tile
+    auto step = [&](auto uc) {
         constexpr int U = decltype(uc)::value;
-        constexpr bool FOLD = decltype(fc)::value;
         XOps& xs = xset<U>(xs0, xs1, xs2, xs3);
-        // K-step 0; X three chunks ahead; then the Y chunk AHEAD further into the stage chunk - 1 used
+        // K-step 0, then the Y chunk AHEAD further into the stage chunk - 1 used
         const int st1 = st0 == NS - 1 ? 0 : st0 + 1;
-        float4* cur = TWO_LEVEL ? xset_stage<U>(sY0, sY1, sY2, sY3) : ystage(st0);
-        float4* nxt = TWO_LEVEL ? xset_stage<(U + 1) % 4>(sY0, sY1, sY2, sY3) : ystage(st1);
-        float4* fill = TWO_LEVEL ? xset_stage<(U + 3) % 4>(sY0, sY1, sY2, sY3) : ystage(st0 == 0 ? NS - 1 : st0 - 1);
+        float4* cur = ystage(st0);
+        float4* nxt = ystage(st1);
+        float4* fill = ystage(st0 == 0 ? NS - 1 : st0 - 1);
         read_ops(o1, cur, 1);
         split_kstep(acc, o0, xs.h0, xs.l0);
-        if (TWO_LEVEL) {
-            const int xc = c + 3 >= nchunks ? c + 3 - nchunks : c + 3;
-            load_x(xset<(U + 3) % 4>(xs0, xs1, xs2, xs3), xc);
-        }
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
             __builtin_amdgcn_sched_group_barrier(SG_DS_READ, 2, 0);
         }
-        if (TWO_LEVEL) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
-                __builtin_amdgcn_sched_group_barrier(SG_VMEM_READ, 1, 0);
-            }
-        }
-        __builtin_amdgcn_sched_group_barrier(SG_MFMA, TWO_LEVEL ? 4 : 8, 0);
+        __builtin_amdgcn_sched_group_barrier(SG_MFMA, 8, 0);
         __builtin_amdgcn_sched_barrier(0);
-        // Issue order per chunk: X loads, then the Y loads; this wave's loads of the next chunk were issued at the
-        // end of the chunk AHEAD - 1 back, so at most the later chunks' instructions may still be in flight.
+        // this wave's loads of the next chunk were issued AHEAD - 1 chunks back, so at most the later chunks'
+        // instructions may still be in flight
         load_ahead(fill);
         ring_barrier<(AHEAD - 1) * VMEM_STEP>();
-        // K-step 1; the next chunk's K-step-0 operands; a quarter of the fold
+        // K-step 1; the next chunk's K-step-0 operands
         read_ops(o0, nxt, 0);
         split_kstep(acc, o1, xs.h1, xs.l1);
-        if (FOLD) {
-#pragma unroll
-            for (int q = 0; q < 16; ++q) {
-                outer[U][q] += other[U][q];
-                other[U][q] = 0.0f;
-            }
-        }
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
             __builtin_amdgcn_sched_group_barrier(SG_DS_READ, 2, 0);
         }
-        if (FOLD) {
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
-                __builtin_amdgcn_sched_group_barrier(SG_VALU, 4, 0);
-            }
-        } else {
-            __builtin_amdgcn_sched_group_barrier(SG_MFMA, 8, 0);
-        }
+        __builtin_amdgcn_sched_group_barrier(SG_MFMA, 8, 0);
         __builtin_amdgcn_sched_barrier(0);
         st0 = st1;
     };
@@ -898,14 +861,12 @@ __global__ __launch_bounds__(256) void l2sq_sweep_split(
     using I1 = std::integral_constant<int, 1>;
     using I2 = std::integral_constant<int, 2>;
     using I3 = std::integral_constant<int, 3>;
-    using FOLD = std::true_type;
-    using NOFOLD = std::false_type;
 
     for (int64_t ytile = y_begin; ytile < y_end; ytile += BY) {
 #pragma unroll
         for (int b = 0; b < NB; ++b) {
 #pragma unroll
-            for (int q = 0; q < 16; ++q) { accA[b][q] = 0.0f; accB[b][q] = 0.0f; }
+            for (int q = 0; q < 16; ++q) acc[b][q] = 0.0f;
         }
         // biases of this tile's Y rows (read in the epilogue, after at least one chunk barrier)
         if (tid < BY) {
@@ -913,47 +874,406 @@ __global__ __launch_bounds__(256) void l2sq_sweep_split(
             sDB[tid] = j < y_end ? db32[j] : 0.0f;
             sGE[tid] = (STATS && j < y_end) ? ge32[j] : 0.0f;
         }
-        if (TWO_LEVEL) {
-#pragma unroll
-            for (int b = 0; b < NB; ++b) {
-#pragma unroll
-                for (int q = 0; q < 16; ++q) outer[b][q] = 0.0f;
-            }
-            // blocks alternate between the two sets; the outer sums take the blocks in order
-            const int nblk = nchunks / FLUSH_SPLIT;
-            for (int kb = 0; kb < nblk; kb += 2) {
-                const int c = kb * FLUSH_SPLIT;
-                step(I0{}, FOLD{}, c, accA, accB);
-                step(I1{}, FOLD{}, c + 1, accA, accB);
-                step(I2{}, FOLD{}, c + 2, accA, accB);
-                step(I3{}, FOLD{}, c + 3, accA, accB);
-                if (kb + 1 < nblk) {
-                    step(I0{}, FOLD{}, c + 4, accB, accA);
-                    step(I1{}, FOLD{}, c + 5, accB, accA);
-                    step(I2{}, FOLD{}, c + 6, accB, accA);
-                    step(I3{}, FOLD{}, c + 7, accB, accA);
-                }
-            }
-            // the last block's set; the other one was folded and cleared during it
-            const bool last_a = (nblk & 1) != 0;
-#pragma unroll
-            for (int b = 0; b < NB; ++b) {
-#pragma unroll
-                for (int q = 0; q < 16; ++q) accA[b][q] = outer[b][q] + (last_a ? accA[b][q] : accB[b][q]);
-            }
-        } else {
-            step(I0{}, NOFOLD{}, 0, accA, accB);
-            if (nchunks > 1) step(I1{}, NOFOLD{}, 1, accA, accB);
-            if (nchunks > 2) {
-                step(I2{}, NOFOLD{}, 2, accA, accB);
-                step(I3{}, NOFOLD{}, 3, accA, accB);
-            }
+        step(I0{});
+        if (nchunks > 1) step(I1{});
+        if (nchunks > 2) {
+            step(I2{});
+            step(I3{});
         }
-        sweep_epilogue<K1, COLS, APPEND>(accA, s, tid, wave, h, r, ytile, y_end, x0, panel, n, scale, STATS, sDB,
-                                         sGE, sC, colpart, colthr, wcnt, wbuf, wcap);
+        sweep_epilogue<K1, COLS, APPEND>(acc, s, tid, wave, h, r, ytile, y_end, x0, panel, n, scale, STATS, sDB, sGE,
+                                         sC, colpart, colthr, wcnt, wbuf, wcap);
     }
     wait_vmcnt<0>();  // the loads ahead into LDS land before the workgroup can end
     sweep_finish<K1, APPEND>(s, tid, lane, wave, h, seg, rows, xb, P, panel, STATS, part, blockstats, sRed);
+}
+
+// -------------------------------------------------------------------------------------------------
+// split-bf16 sweep over 256-row X panels, for d > 128 (outer sums; d a multiple of 4 chunks). Same copies,
+// products and Y ring as l2sq_sweep_split, with 8 waves (two per SIMD), each owning 32 X rows against the tile's
+// 128 Y rows: per chunk a CU fetches 48 KiB for twice the products of the 128-row panel's 32 KiB, and the 8
+// concurrent panels of an XCD hit its L2 far more often (83% against 53% of requests at d = 8192).
+//   X: each wave's operands come straight to registers, two sets, chunk c in set c % 2, loaded one chunk ahead.
+//   Y operands: read from LDS right before their pass (the other wave of the SIMD multiplies meanwhile), so that at
+//      most two halves of a K-step are live; every read of a chunk's stage precedes the barrier after which the
+//      stage may be refilled.
+//   Accumulators: one set of 4 blocks (32 Y rows x 32 X rows each) and their outer sums, all in the 256 registers
+//      a wave has at two waves per SIMD. Block y restarts at the chunks c = y (mod 4): its accumulator is folded
+//      into the outer sums (outer += acc) and its first product of the chunk starts from zero. So every fp32 block
+//      spans at most 4 chunks (128 features), a dot is the ordered fp32 sum of at most d / 128 + 1 blocks, and one
+//      block is folded per chunk.
+//   Row lists: lane (h, r) of wave w holds X row 32w + r; its partial list lives in `part` between tiles (each
+//      epilogue reads it, merges the tile and writes it back), so the chunk loop carries no lists.
+//   Columns: the tile's scores pass through LDS 32 Y rows at a time; 16 threads per Y row scan 16 X rows each
+//      (panel rows t, t + 16, ...: a stride that spreads the reads over the LDS banks).
+// -------------------------------------------------------------------------------------------------
+constexpr int BXW = 256;                // X rows per workgroup of the 256-row split sweep
+constexpr int WAVES_W = BXW / 32;       // waves per workgroup (32 X rows each)
+constexpr int THREADS_W = 64 * WAVES_W;
+constexpr int CSTW = BXW + 8;           // LDS row stride of its column-score pass (floats)
+
+template <int U>
+__device__ __forceinline__ XOps& xset2(XOps& a, XOps& b) {
+    if constexpr ((U & 1) == 0) return a;
+    else return b;
+}
+
+// Y operands of one K-step in two halves: the hi parts of the 4 Y blocks, and the lo parts
+struct YHalf { float4 b0, b1, b2, b3; };
+
+template <int Y>
+__device__ __forceinline__ const float4& yhalf_at(const YHalf& a) {
+    if constexpr (Y == 0) return a.b0;
+    else if constexpr (Y == 1) return a.b1;
+    else if constexpr (Y == 2) return a.b2;
+    else return a.b3;
+}
+
+// Products of one pass over the 4 Y blocks: acc[y] += Y_part(y) * X_part. With R >= 0 the pass takes the blocks
+// from R + 1 on, R last; with FOLD, block R is first folded into outer (outer += acc) and its product starts from
+// zero (the block restarts).
+template <int R, bool FOLD, int I>
+__device__ __forceinline__ void pass_one(v16f (&acc)[NB], float (&outer)[NB][16], const YHalf& yp, const bf16x8& xv) {
+    constexpr int y = R < 0 ? I : (R + 1 + I) % NB;
+    const bf16x8 yv = as_bf16x8(yhalf_at<y>(yp));
+    if constexpr (FOLD && y == R) {
+#pragma unroll
+        for (int q = 0; q < 16; ++q) outer[y][q] += acc[y][q];
+        const v16f zero = {};
+        acc[y] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(yv, xv, zero, 0, 0, 0);
+    } else {
+        acc[y] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(yv, xv, acc[y], 0, 0, 0);
+    }
+}
+
+template <int R, bool FOLD>
+__device__ __forceinline__ void split_pass(v16f (&acc)[NB], float (&outer)[NB][16], const YHalf& yp, const float4& x4) {
+    const bf16x8 xv = as_bf16x8(x4);
+    pass_one<R, FOLD, 0>(acc, outer, yp, xv);
+    pass_one<R, FOLD, 1>(acc, outer, yp, xv);
+    pass_one<R, FOLD, 2>(acc, outer, yp, xv);
+    pass_one<R, FOLD, 3>(acc, outer, yp, xv);
+}
+
+// Epilogue of the 256-row split sweep for one tile. tot[y][q] is the fp32 dot of the lane's X row with Y row
+// ytile + 32y + 8(q/4) + 4h + q%4. Rows: the lane's list (half h of segment seg) is read from `part` (or starts
+// empty at the segment's first tile), takes w = scale*dot + db in increasing j and is written back; APPEND
+// queues candidates instead. Columns as in sweep_epilogue, over the panel's 256 X rows.
+template <int K1, bool COLS, bool APPEND>
+__device__ __forceinline__ void sweep_epilogue_w(const float (&tot)[NB][16], int64_t row, bool ok, float qbi,
+                                                 float pi, float wt, bool first, int tid, int wave, int h, int r,
+                                                 int64_t ytile, int64_t y_end, int64_t x0, int64_t xb, int64_t rows,
+                                                 int64_t seg, int64_t panel, int64_t n, float scale, int STATS,
+                                                 const float* sDB, const float* sGE, float* sC,
+                                                 Entry* __restrict__ part, Entry* __restrict__ colpart,
+                                                 unsigned int* __restrict__ colthr, int* __restrict__ wcnt,
+                                                 int* __restrict__ wbuf, int wcap, double& num64, double& den64,
+                                                 double& cnt64, float& mx, float& cmax) {
+    float tnum = 0.0f, tden = 0.0f;
+    unsigned int tcnt = 0;
+    float lv[APPEND ? 1 : K1];
+    int li[APPEND ? 1 : K1];
+    Entry* lp = APPEND ? nullptr : part + ((seg * rows + (row - xb)) * 2 + h) * K1;
+    if (!APPEND) {
+#pragma unroll
+        for (int i = 0; i < K1; ++i) {
+            Entry e{-INFINITY, -1};
+            if (ok && !first) e = lp[i];
+            lv[i] = e.w;
+            li[i] = e.j;
+        }
+    }
+#pragma unroll
+    for (int y = 0; y < NB; ++y) {
+#pragma unroll
+        for (int a = 0; a < 4; ++a) {
+            const int jl0 = y * 32 + 8 * a + 4 * h;
+            const float4 dbv = *reinterpret_cast<const float4*>(&sDB[jl0]);
+            float4 gev = make_float4(0, 0, 0, 0);
+            if (STATS) gev = *reinterpret_cast<const float4*>(&sGE[jl0]);
+            const float dbs[4] = {dbv.x, dbv.y, dbv.z, dbv.w};
+            const float ges[4] = {gev.x, gev.y, gev.z, gev.w};
+#pragma unroll
+            for (int cc = 0; cc < 4; ++cc) {
+                const float w = fmaf(scale, tot[y][4 * a + cc], dbs[cc]);
+                const int64_t j = ytile + jl0 + cc;
+                const bool okj = ok && j < y_end;
+                if constexpr (APPEND) {
+                    if (okj && w >= wt) {
+                        const int pos = atomicAdd(&wcnt[row], 1);
+                        if (pos < wcap) wbuf[row * (int64_t)wcap + pos] = (int)j;
+                    }
+                } else if (okj && w > lv[K1 - 1]) {
+                    float cv = w;
+                    int ci = (int)j;
+#pragma unroll
+                    for (int i = 0; i < K1; ++i) {
+                        if (cv > lv[i]) {
+                            const float tv = lv[i];
+                            const int ti = li[i];
+                            lv[i] = cv;
+                            li[i] = ci;
+                            cv = tv;
+                            ci = ti;
+                        }
+                    }
+                }
+                if (STATS && okj) {
+                    const float sg = w + qbi;
+                    const float cost = (pi + ges[cc]) - w;
+                    tden = fmaf(cost, cost, tden);
+                    cmax = fmaxf(cmax, fabsf(cost));
+                    if (sg > 0.0f) {
+                        tnum = fmaf(sg, sg, tnum);
+                        mx = fmaxf(mx, sg);
+                        ++tcnt;
+                    }
+                }
+            }
+        }
+    }
+    if (!APPEND && ok) {
+#pragma unroll
+        for (int i = 0; i < K1; ++i) lp[i] = Entry{lv[i], li[i]};
+    }
+    if (STATS) {
+        num64 += (double)tnum;
+        den64 += (double)tden;
+        cnt64 += (double)tcnt;
+    }
+    if (COLS) {
+        // each Y row of the tile: its best K1 over the panel's 256 X rows (16 threads per row, merged by
+        // shuffles); colthr[j] bounds the chunk's K1-th value from below, as in sweep_epilogue
+#pragma unroll
+        for (int pass = 0; pass < NB; ++pass) {
+            if (pass > 0) __syncthreads();  // the previous pass's reads of sC are done
+#pragma unroll
+            for (int q = 0; q < 16; ++q) {
+                const int jl = 8 * (q / 4) + 4 * h + (q % 4);
+                sC[jl * CSTW + wave * 32 + r] = ok ? fmaf(scale, tot[pass][q], qbi) : -INFINITY;
+            }
+            __syncthreads();
+            const int jl = tid >> 4, part16 = tid & 15;
+            const int64_t j = ytile + pass * 32 + jl;
+            const float thr = j < y_end ? key_float(colthr[j]) : INFINITY;
+            float cw[K1];
+            int cidx[K1];
+#pragma unroll
+            for (int i = 0; i < K1; ++i) { cw[i] = -INFINITY; cidx[i] = -1; }
+            const float* src = &sC[jl * CSTW + part16];
+            const int base = (int)(x0 + part16);
+            for (int xx = 0; xx < BXW / 16; ++xx) {
+                const float v = src[16 * xx];
+                if (v > thr && v > cw[K1 - 1]) insert_e<K1>(cw, cidx, v, base + 16 * xx);
+            }
+#pragma unroll
+            for (int m = 1; m < 16; m <<= 1) {
+                float pv[K1];
+                int pi2[K1];
+#pragma unroll
+                for (int i = 0; i < K1; ++i) {
+                    pv[i] = __shfl_xor(cw[i], m, 64);
+                    pi2[i] = __shfl_xor(cidx[i], m, 64);
+                }
+#pragma unroll
+                for (int i = 0; i < K1; ++i)
+                    if (pi2[i] >= 0 && better_e(pv[i], pi2[i], cw[K1 - 1], cidx[K1 - 1])) insert_e<K1>(cw, cidx, pv[i], pi2[i]);
+            }
+            if (part16 == 0 && j < y_end) {
+                Entry* dst = colpart + (panel * n + j) * K1;
+#pragma unroll
+                for (int i = 0; i < K1; ++i) dst[i] = Entry{cw[i], cidx[i]};
+                if (cidx[K1 - 1] >= 0) atomicMax(&colthr[j], float_key(cw[K1 - 1]));
+            }
+        }
+    }
+    __syncthreads();  // all epilogue reads of sDB/sGE/sC finish before the next tile rewrites them
+}
+
+template <int K1, bool COLS, bool APPEND = false>
+__global__ __launch_bounds__(THREADS_W) void l2sq_sweep_split_w(
+    const float* __restrict__ X, const float* __restrict__ Y, int64_t xb, int64_t xe, int64_t n, int d, int ld,
+    const float* __restrict__ qb32, const float* __restrict__ db32, const float* __restrict__ p32,
+    const float* __restrict__ ge32, float scale, int64_t seg_len, int P, int S, Entry* __restrict__ part,
+    Entry* __restrict__ colpart, unsigned int* __restrict__ colthr, double* __restrict__ blockstats, int STATS,
+    const float* __restrict__ wthr = nullptr, int* __restrict__ wcnt = nullptr, int* __restrict__ wbuf = nullptr,
+    int wcap = 0) {
+    static_assert(!(APPEND && COLS), "the wide pass keeps no column lists");
+    constexpr int AHEAD = 3;      // Y chunks in flight ahead of the one multiplied (4-stage ring)
+    constexpr int VMEM_STEP = 6;  // vector-memory instructions a chunk issues (4 X, then 2 Y)
+    int64_t panel, seg;
+    sweep_block(blockIdx.x, P, S, panel, seg);
+    if (panel >= P || seg >= S) return;  // grid padding (uniform per workgroup, before any barrier)
+    __shared__ float4 sY0[1024], sY1[1024], sY2[1024], sY3[1024];  // LDS ring (Y chunk: 4 blocks x 4 KiB)
+    __shared__ float sDB[BY];
+    __shared__ float sGE[BY];
+    __shared__ float sC[COLS ? 32 * CSTW : 1];
+    __shared__ double sRed[WAVES_W][5];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int h = lane >> 5;
+    const int r = lane & 31;
+    const int64_t rows = xe - xb;
+    const int64_t x0 = xb + panel * BXW;
+    const int64_t y_begin = seg * seg_len;
+    const int64_t y_end = (y_begin + seg_len < n) ? (y_begin + seg_len) : n;
+    const int64_t row = x0 + wave * 32 + r;
+    const bool ok = row < xe;
+    const float qbi = (ok && !APPEND) ? qb32[row] : 0.0f;
+    const float pi = (STATS && ok) ? p32[row] : 0.0f;
+    const float wt = (APPEND && ok) ? wthr[row] : INFINITY;
+    double num64 = 0.0, den64 = 0.0, cnt64 = 0.0;
+    float mx = 0.0f, cmax = 0.0f;
+
+    const int nchunks = d / KC;
+    const int64_t bstride = (int64_t)ld * 32;          // words per 32-row block
+    const float* Xw = X + ((x0 >> 5) + wave) * bstride;  // this wave's X block
+    const unsigned lane16 = (unsigned)lane * 16u;
+    const unsigned t16 = (unsigned)(tid & 255) * 16u;
+    const unsigned bstep = (unsigned)(bstride * 4);     // bytes between consecutive 32-row blocks
+    const int bsel = tid >> 8;                          // Y blocks 0 and 2 (waves 0-3) or 1 and 3 (waves 4-7)
+
+    auto load_x = [&](XOps& o, int cc) {
+        const float* b = Xw + cc * 1024;
+        o.h0 = ld16(b, lane16);
+        o.l0 = ld16(b, 1024u + lane16);
+        o.h1 = ld16(b, 2048u + lane16);
+        o.l1 = ld16(b, 3072u + lane16);
+    };
+    // Y chunk AHEAD chunks past the one multiplied (ta, ca); past the segment any in-bounds chunk will do, its
+    // data is never multiplied. Thread t's 16 bytes of block 2i + bsel go to stage + (2i + bsel)*4 KiB +
+    // (t % 256)*16: one wave instruction fills 1 KiB.
+    int64_t ta = y_begin;
+    int ca = 0;
+    auto load_ahead = [&](float4* stage) {
+        const bool past = ta >= y_end;
+        const char* b = reinterpret_cast<const char*>(Y + ((past ? y_begin : ta) >> 5) * bstride + (past ? 0 : ca) * 1024);
+        float4* dst = stage + bsel * 256 + (wave & 3) * 64;
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+            __builtin_amdgcn_global_load_lds(b + (2 * i + bsel) * bstep + t16,
+                                             (__attribute__((address_space(3))) void*)(dst + i * 512), 16, 0, 0);
+        ++ca;
+        const bool wrap = ca == nchunks;
+        ca = wrap ? 0 : ca;
+        ta = wrap ? ta + BY : ta;
+    };
+    // half p (0: hi, 1: lo) of the operands of K-step ks of the Y chunk in `stage`
+    auto read_half = [&](YHalf& o, const float4* stage, int ks, int p) {
+        const float4* src = stage + ks * 128 + p * 64 + lane;
+        o.b0 = src[0];
+        o.b1 = src[256];
+        o.b2 = src[512];
+        o.b3 = src[768];
+    };
+
+    XOps xs0, xs1;  // X operands: chunk c in set c % 2
+    YHalf yh, yl;   // Y operands of the pass in flight (hi and lo halves of one K-step)
+    load_ahead(sY0);
+    load_ahead(sY1);
+    load_ahead(sY2);
+    load_x(xs0, 0);
+    wait_vmcnt<0>();
+    __syncthreads();
+
+    v16f acc[NB];
+    float outer[NB][16];
+#pragma unroll
+    for (int y = 0; y < NB; ++y) {
+#pragma unroll
+        for (int q = 0; q < 16; ++q) { acc[y][q] = 0.0f; outer[y][q] = 0.0f; }
+    }
+
+    // chunk c (U = c % 4: Y stage U, X set U % 2, restarting accumulator block U)
+    auto step = [&](auto uc, int c) {
+        constexpr int U = decltype(uc)::value;
+        XOps& xs = xset2<U>(xs0, xs1);
+        float4* cur = xset_stage<U>(sY0, sY1, sY2, sY3);
+        float4* fill = xset_stage<(U + 3) % 4>(sY0, sY1, sY2, sY3);
+        // the next chunk's X into the other set (last used by chunk c - 1)
+        load_x(xset2<U + 1>(xs0, xs1), c + 1 == nchunks ? 0 : c + 1);
+        // K-step 0 (block U restarts), then K-step 1's operands, all read before the barrier
+        read_half(yh, cur, 0, 0);
+        read_half(yl, cur, 0, 1);
+        split_pass<U, true>(acc, outer, yh, xs.h0);
+        split_pass<U, false>(acc, outer, yh, xs.l0);
+        __builtin_amdgcn_sched_barrier(0);
+        read_half(yh, cur, 1, 0);
+        split_pass<U, false>(acc, outer, yl, xs.h0);
+        __builtin_amdgcn_sched_barrier(0);
+        read_half(yl, cur, 1, 1);
+        // the Y chunk AHEAD further into the stage chunk - 1 used (all its reads retired at the previous barrier);
+        // this wave's loads of the next chunk's Y were issued AHEAD - 1 chunks back, so at most the later chunks'
+        // instructions may still be in flight at the barrier
+        load_ahead(fill);
+        ring_barrier<(AHEAD - 1) * VMEM_STEP>();
+        split_pass<-1, false>(acc, outer, yh, xs.h1);
+        split_pass<-1, false>(acc, outer, yh, xs.l1);
+        split_pass<-1, false>(acc, outer, yl, xs.h1);
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    using I2 = std::integral_constant<int, 2>;
+    using I3 = std::integral_constant<int, 3>;
+
+    for (int64_t ytile = y_begin; ytile < y_end; ytile += BY) {
+        // biases of this tile's Y rows (read in the epilogue, after at least one chunk barrier)
+        if (tid < BY) {
+            const int64_t j = ytile + tid;
+            sDB[tid] = j < y_end ? db32[j] : 0.0f;
+            sGE[tid] = (STATS && j < y_end) ? ge32[j] : 0.0f;
+        }
+        for (int c = 0; c < nchunks; c += 4) {
+            step(I0{}, c);
+            step(I1{}, c + 1);
+            step(I2{}, c + 2);
+            step(I3{}, c + 3);
+        }
+        // the blocks' last parts into the outer sums; the accumulators restart from zero for the next tile
+#pragma unroll
+        for (int y = 0; y < NB; ++y) {
+#pragma unroll
+            for (int q = 0; q < 16; ++q) {
+                outer[y][q] += acc[y][q];
+                acc[y][q] = 0.0f;
+            }
+        }
+        sweep_epilogue_w<K1, COLS, APPEND>(outer, row, ok, qbi, pi, wt, ytile == y_begin, tid, wave, h, r, ytile,
+                                           y_end, x0, xb, rows, seg, panel, n, scale, STATS, sDB, sGE, sC, part,
+                                           colpart, colthr, wcnt, wbuf, wcap, num64, den64, cnt64, mx, cmax);
+#pragma unroll
+        for (int y = 0; y < NB; ++y) {
+#pragma unroll
+            for (int q = 0; q < 16; ++q) outer[y][q] = 0.0f;
+        }
+    }
+    wait_vmcnt<0>();  // the loads ahead into LDS land before the workgroup can end
+    if (STATS) {
+        double v[5] = {num64, den64, cnt64, (double)mx, (double)cmax};
+#pragma unroll
+        for (int e = 0; e < 5; ++e) {
+            for (int o = 32; o >= 1; o >>= 1) {
+                const double t = __shfl_xor(v[e], o, 64);
+                v[e] = (e >= 3) ? fmax(v[e], t) : v[e] + t;
+            }
+        }
+        if (lane == 0) {
+#pragma unroll
+            for (int e = 0; e < 5; ++e) sRed[wave][e] = v[e];
+        }
+        __syncthreads();
+        if (tid == 0) {
+            double o[5];
+            for (int e = 0; e < 5; ++e) {
+                o[e] = sRed[0][e];
+                for (int w = 1; w < WAVES_W; ++w) o[e] = (e >= 3) ? fmax(o[e], sRed[w][e]) : o[e] + sRed[w][e];
+            }
+            double* dst = blockstats + (seg * P + panel) * 5;
+            for (int e = 0; e < 5; ++e) dst[e] = o[e];
+        }
+    }
 }
 
 // deterministic reduction of per-block certificate partials (single block); later chunks accumulate
@@ -1447,31 +1767,32 @@ inline bool fused_columns(int d, uint32_t flags) {
 // all start on the same memory channel
 inline int split_features(int d) { return d <= 32 ? 32 : d <= 64 ? 64 : (d + 127) / 128 * 128; }
 inline int split_ld(int d) { return split_features(d) + (split_features(d) % 512 == 0 ? KC : 0); }
-inline int64_t panel_rows(int64_t rows) { return (rows + BX - 1) / BX * BX; }
+inline int64_t panel_rows(int64_t rows, int bx = BX) { return (rows + bx - 1) / bx * bx; }
 
-// Rows per internal chunk of the swept side (m rows against n): balanced chunks of whole 128-row panels, and with
+// X rows per sweep workgroup: 256 for the split sweep with outer sums (l2sq_sweep_split_w), else 128
+inline int sweep_panel(int d, uint32_t flags) { return ((flags & HM_BF16X3) && d > KC * FLUSH_SPLIT) ? BXW : BX; }
+
+// Rows per internal chunk of the swept side (m rows against n): balanced chunks of whole bx-row panels, and with
 // fused columns the chunk's column partial lists (kl entries per panel and column) within COLPART_CAP.
-inline int64_t chunk_rows(int64_t m, int64_t n, int kl, bool fused) {
+inline int64_t chunk_rows(int64_t m, int64_t n, int kl, bool fused, int bx) {
     int64_t ch = CHUNK_MAX;
     if (fused) {
         const int64_t per_panel = n * (int64_t)kl * (int64_t)sizeof(Entry);
         int64_t panels = (int64_t)(COLPART_CAP / (size_t)per_panel);
         if (panels < 1) panels = 1;
-        if (panels * BX < ch) ch = panels * BX;
+        if (panels * bx < ch) ch = panels * bx;
     }
-    const int64_t whole = panel_rows(m);
+    const int64_t whole = panel_rows(m, bx);
     if (ch >= whole) return whole;
     const int64_t nch = (m + ch - 1) / ch;
-    return panel_rows((m + nch - 1) / nch);
+    return panel_rows((m + nch - 1) / nch, bx);
 }
 
 // Y segments per sweep launch: enough workgroups to fill the chip (SWEEP_WGS), and for k > 2 at least 8 so each
-// row has 16 partial lists; at most a quarter of the tiles and 64.
-// Y segments per sweep launch: enough workgroups to fill the chip (SWEEP_WGS), and for k > 2 at least 8 so each
 // row has 16 partial lists; at most a quarter of the tiles and `cap`. Among up to twice that many segments the
 // first whose workgroups fill whole rounds of the CUs (within 3%) is taken: a partial last round idles CUs.
-inline int choose_segments(int64_t m, int64_t n, int k, int cap = 64) {
-    const int64_t panels = (m + BX - 1) / BX;
+inline int choose_segments(int64_t m, int64_t n, int k, int cap, int bx) {
+    const int64_t panels = (m + bx - 1) / bx;
     const int64_t tiles = (n + BY - 1) / BY;
     int64_t s = (SWEEP_WGS + panels - 1) / panels;
     if (k > 2 && s < 8) s = 8;
@@ -1493,11 +1814,11 @@ inline int choose_segments(int64_t m, int64_t n, int k, int cap = 64) {
     return (int)best;
 }
 
-inline DirPlan plan_dir(int64_t rows, int64_t cols, int k, int cap = 64) {
+inline DirPlan plan_dir(int64_t rows, int64_t cols, int k, int cap, int bx) {
     DirPlan p;
     p.rows = rows;
     p.cols = cols;
-    p.S = choose_segments(rows, cols, k, cap);
+    p.S = choose_segments(rows, cols, k, cap, bx);
     const int64_t tiles = (cols + BY - 1) / BY;
     const int64_t tiles_per = (tiles + p.S - 1) / p.S;
     p.seg_len = tiles_per * BY;
@@ -1508,6 +1829,7 @@ inline DirPlan plan_dir(int64_t rows, int64_t cols, int k, int cap = 64) {
 // Everything the workspace layout and the driver derive from the call's shape.
 struct CallPlan {
     int kl, km;
+    int bx;  // X rows per sweep workgroup
     bool fused, swapped, row_pass;
     int64_t ch, ch2;  // chunk rows of the row pass and of the swapped pass
     DirPlan plan, plan2;
@@ -1519,20 +1841,21 @@ inline CallPlan plan_call(int64_t m, int64_t n, int d, int k, uint32_t flags) {
     c.fused = fused_columns(d, flags);
     c.swapped = (flags & HM_COLS) && !c.fused;
     c.row_pass = (flags & HM_ROWS) || c.fused || (flags & HM_STATS);
+    c.bx = sweep_panel(d, flags);
     static const int sizes[3] = {8, 16, 40};
     for (int t = 0; t < 3; ++t) {
         c.kl = sizes[t];
-        c.ch = chunk_rows(m, n, c.kl, c.fused);
-        c.plan = plan_dir(c.ch, n, k);
-        c.ch2 = c.swapped ? chunk_rows(n, m, c.kl, false) : 0;
-        c.plan2 = plan_dir(c.swapped ? c.ch2 : 1, m, k);
+        c.ch = chunk_rows(m, n, c.kl, c.fused, c.bx);
+        c.plan = plan_dir(c.ch, n, k, 64, c.bx);
+        c.ch2 = c.swapped ? chunk_rows(n, m, c.kl, false, c.bx) : 0;
+        c.plan2 = plan_dir(c.swapped ? c.ch2 : 1, m, k, 64, c.bx);
         if (c.kl >= c.km) break;
         // fewest partial lists any finalized row or column of this call merges
         int64_t nl = INT64_MAX;
         if (flags & HM_ROWS) nl = std::min<int64_t>(nl, 2 * (int64_t)c.plan.S);
         if (c.fused) {
             const int64_t last = m - (m - 1) / c.ch * c.ch;
-            nl = std::min<int64_t>(nl, std::min<int64_t>(c.ch / BX, (last + BX - 1) / BX));
+            nl = std::min<int64_t>(nl, std::min<int64_t>(c.ch / c.bx, (last + c.bx - 1) / c.bx));
         }
         if (c.swapped) nl = std::min<int64_t>(nl, 2 * (int64_t)c.plan2.S);
         if (nl == INT64_MAX || list_k_for(nl, k) <= c.kl) break;
@@ -1546,7 +1869,7 @@ void layout(A& a, int64_t m, int64_t n, int d, int k, uint32_t flags, double** x
             unsigned int** colthr, double** cval, int** cidx, double** blockstats, int** redo, int** redo_count,
             float** xsplit, float** ysplit, double** rpv, int** rpi, WideBufs* wide) {
     const CallPlan c = plan_call(m, n, d, k, flags);
-    const int64_t panels = c.ch / BX;
+    const int64_t panels = c.ch / c.bx;
     size_t part_entries = (size_t)c.plan.S * c.ch * 2 * c.kl;
     if (c.swapped && (size_t)c.plan2.S * c.ch2 * 2 * c.kl > part_entries)
         part_entries = (size_t)c.plan2.S * c.ch2 * 2 * c.kl;
@@ -1568,11 +1891,12 @@ void layout(A& a, int64_t m, int64_t n, int d, int k, uint32_t flags, double** x
     *redo_count = a.template take<int>(2);
     const bool split = (flags & HM_BF16X3) != 0;
     const size_t ldw = (size_t)split_ld(d);
-    *xsplit = a.template take<float>(split ? (size_t)panel_rows(m) * ldw : 1);
-    *ysplit = a.template take<float>(split ? (size_t)panel_rows(n) * ldw : 1);
+    // split copies cover whole 256-row panels: either side may be the swept one
+    *xsplit = a.template take<float>(split ? (size_t)panel_rows(m, BXW) * ldw : 1);
+    *ysplit = a.template take<float>(split ? (size_t)panel_rows(n, BXW) * ldw : 1);
     *rpv = a.template take<double>((size_t)RESCAN_ITEMS * k);
     *rpi = a.template take<int>((size_t)RESCAN_ITEMS * k);
-    const int64_t wq = panel_rows(WIDE_ROWS);
+    const int64_t wq = panel_rows(WIDE_ROWS, BXW);
     wide->redo_thr = a.template take<float>((size_t)(m + n));
     wide->rows = a.template take<float>((size_t)wq * (split ? ldw : (size_t)d));
     wide->thr = a.template take<float>((size_t)wq);
@@ -1649,11 +1973,12 @@ int run_bidir(hipStream_t st, const float* X, const float* Y, int64_t m, int64_t
     const float* SY = split ? ysplit : Y;
     const int64_t ch = cp.ch;
     const DirPlan plan = cp.plan;
+    const int bx = cp.bx;
     if (split) {
-        hipLaunchKernelGGL(l2sq_split_bf16, dim3(4096), dim3(256), 0, st, X, m, panel_rows(m), d, sd, ld,
+        hipLaunchKernelGGL(l2sq_split_bf16, dim3(4096), dim3(256), 0, st, X, m, panel_rows(m, BXW), d, sd, ld,
                            reinterpret_cast<unsigned short*>(xsplit));
         HM_LAUNCH_CHECK("l2sq_split_bf16");
-        hipLaunchKernelGGL(l2sq_split_bf16, dim3(4096), dim3(256), 0, st, Y, n, panel_rows(n), d, sd, ld,
+        hipLaunchKernelGGL(l2sq_split_bf16, dim3(4096), dim3(256), 0, st, Y, n, panel_rows(n, BXW), d, sd, ld,
                            reinterpret_cast<unsigned short*>(ysplit));
         HM_LAUNCH_CHECK("l2sq_split_bf16");
     }
@@ -1661,7 +1986,8 @@ int run_bidir(hipStream_t st, const float* X, const float* Y, int64_t m, int64_t
     // (gamma over the additions of a block, then over the blocks), plus for the split products the dropped
     // terms lo*lo + hi*e + e*hi + ... <= (3 * 2^-16 * (1 + 2^-7) + 3 * 2^-24) |x_k y_k|.
     const double fb = two_level ? (double)flush : (double)d;
-    const double nblk = two_level ? std::ceil((double)d / flush) : 1.0;
+    // (the 256-row split sweep restarts its 4 accumulator blocks at staggered chunks: one block more per dot)
+    const double nblk = two_level ? std::ceil((double)d / flush) + (split ? 1.0 : 0.0) : 1.0;
     const double terms = split ? 3.0 * fb * (1.0 + 1.0 / 8.0) : fb;
     const double ea = gamma_fp32(terms) + gamma_fp32(nblk) + gamma_fp32(terms) * gamma_fp32(nblk);
     const double split_rel = split ? 3.0 * std::ldexp(1.0, -16) * (1.0 + std::ldexp(1.0, -7)) + 3.0 * std::ldexp(1.0, -24)
@@ -1676,7 +2002,7 @@ int run_bidir(hipStream_t st, const float* X, const float* Y, int64_t m, int64_t
     for (int64_t xb = 0; row_pass && xb < m; xb += ch, ++chunk_index) {
         const int64_t xe = xb + ch < m ? xb + ch : m;
         const int64_t rows = xe - xb;
-        const int64_t panels = (rows + BX - 1) / BX;
+        const int64_t panels = (rows + bx - 1) / bx;
         const dim3 grid(sweep_grid(panels, plan.S));
         if (fused) {
             // column thresholds start at -inf for every chunk (its lists only rank its own X rows)
@@ -1687,8 +2013,12 @@ int run_bidir(hipStream_t st, const float* X, const float* Y, int64_t m, int64_t
         }
 #define HM_SWEEP(TL, CL)                                                                                             \
     do {                                                                                                             \
-        if (split)                                                                                                   \
-            hipLaunchKernelGGL((l2sq_sweep_split<K1, TL, CL>), grid, dim3(256), 0, st, SX, SY, xb, xe, n, sd, ld,    \
+        if (split && TL)                                                                                             \
+            hipLaunchKernelGGL((l2sq_sweep_split_w<K1, CL>), grid, dim3(THREADS_W), 0, st, SX, SY, xb, xe, n, sd,    \
+                               ld, qb32, db32, p32, ge32, (float)scale, plan.seg_len, (int)panels, plan.S, part,     \
+                               colpart, colthr, blockstats, (int)want_stats);                                        \
+        else if (split)                                                                                              \
+            hipLaunchKernelGGL((l2sq_sweep_split<K1, CL>), grid, dim3(256), 0, st, SX, SY, xb, xe, n, sd, ld, \
                                qb32, db32, p32, ge32, (float)scale, plan.seg_len, (int)panels, plan.S, part,         \
                                colpart, colthr, blockstats, (int)want_stats);                                        \
         else                                                                                                         \
@@ -1752,13 +2082,17 @@ int run_bidir(hipStream_t st, const float* X, const float* Y, int64_t m, int64_t
         for (int64_t yb = 0; yb < n; yb += ch2) {
             const int64_t ye = yb + ch2 < n ? yb + ch2 : n;
             const int64_t rows = ye - yb;
-            const int64_t panels2 = (rows + BX - 1) / BX;
+            const int64_t panels2 = (rows + bx - 1) / bx;
             const dim3 grid(sweep_grid(panels2, plan2.S));
 #define HM_SWEEP2(TL)                                                                                                \
     do {                                                                                                             \
-        if (split)                                                                                                   \
-            hipLaunchKernelGGL((l2sq_sweep_split<K1, TL, false>), grid, dim3(256), 0, st, SY, SX, yb, ye, m, sd, ld, \
-                               db32, qb32, ge32, p32, (float)scale, plan2.seg_len, (int)panels2, plan2.S, part,      \
+        if (split && TL)                                                                                             \
+            hipLaunchKernelGGL((l2sq_sweep_split_w<K1, false>), grid, dim3(THREADS_W), 0, st, SY, SX, yb, ye, m, sd, \
+                               ld, db32, qb32, ge32, p32, (float)scale, plan2.seg_len, (int)panels2, plan2.S, part,  \
+                               colpart, colthr, blockstats, 0);                                                      \
+        else if (split)                                                                                              \
+            hipLaunchKernelGGL((l2sq_sweep_split<K1, false>), grid, dim3(256), 0, st, SY, SX, yb, ye, m, sd,  \
+                               ld, db32, qb32, ge32, p32, (float)scale, plan2.seg_len, (int)panels2, plan2.S, part,  \
                                colpart, colthr, blockstats, 0);                                                      \
         else                                                                                                         \
             hipLaunchKernelGGL((l2sq_sweep<K1, TL, false>), grid, dim3(256), 0, st, Y, X, yb, ye, m, d, d, db32,     \

@@ -41,7 +41,8 @@ int wide_round(hipStream_t st, bool split, bool two_level, const float* A, const
     const int vec4 = split || (d % 4) == 0;
     for (int q0 = 0; q0 < count; q0 += batch) {
         const int Q = count - q0 < batch ? count - q0 : batch;
-        const int Qpad = (int)panel_rows(Q);
+        const int bx = (split && two_level) ? BXW : BX;  // X rows per sweep workgroup
+        const int Qpad = (int)panel_rows(Q, bx);
         if (split)
             hipLaunchKernelGGL(l2sq_wide_gather_split, dim3(2048), dim3(256), 0, st, Asw, gld, sd, queue, q0, Q, Qpad,
                                queue_thr, w.rows, w.thr, w.cnt);
@@ -49,19 +50,19 @@ int wide_round(hipStream_t st, bool split, bool two_level, const float* A, const
             hipLaunchKernelGGL(l2sq_wide_gather, dim3(2048), dim3(256), 0, st, Asw, gld, queue, q0, Q, Qpad, queue_thr,
                                w.rows, w.thr, w.cnt);
         HM_LAUNCH_CHECK("l2sq_wide_gather");
-        const DirPlan plan = plan_dir(Qpad, nb, 0, 256);
-        const dim3 grid(sweep_grid(Qpad / BX, plan.S));
-#define HM_WIDE(KERNEL, ...)                                                                                        \
-    hipLaunchKernelGGL(KERNEL, grid, dim3(256), 0, st, w.rows, Bsw, (int64_t)0, (int64_t)Q, nb, sd, gld,            \
+        const DirPlan plan = plan_dir(Qpad, nb, 0, 256, bx);
+        const dim3 grid(sweep_grid(Qpad / bx, plan.S));
+#define HM_WIDE(KERNEL, THREADS, ...)                                                                               \
+    hipLaunchKernelGGL(KERNEL, grid, dim3(THREADS), 0, st, w.rows, Bsw, (int64_t)0, (int64_t)Q, nb, sd, gld,        \
                        (const float*)nullptr, cand32, (const float*)nullptr, (const float*)nullptr, (float)scale,    \
-                       plan.seg_len, Qpad / BX, plan.S, (Entry*)nullptr, (Entry*)nullptr, (unsigned int*)nullptr,    \
+                       plan.seg_len, Qpad / bx, plan.S, (Entry*)nullptr, (Entry*)nullptr, (unsigned int*)nullptr,    \
                        (double*)nullptr, __VA_ARGS__, w.thr, w.cnt, w.buf, cap)
         if (split) {
-            if (two_level) HM_WIDE((l2sq_sweep_split<8, true, false, true>), 0);
-            else HM_WIDE((l2sq_sweep_split<8, false, false, true>), 0);
+            if (two_level) HM_WIDE((l2sq_sweep_split_w<8, false, true>), THREADS_W, 0);
+            else HM_WIDE((l2sq_sweep_split<8, false, true>), 256, 0);
         } else {
-            if (two_level) HM_WIDE((l2sq_sweep<8, true, false, true>), vec4, 0);
-            else HM_WIDE((l2sq_sweep<8, false, false, true>), vec4, 0);
+            if (two_level) HM_WIDE((l2sq_sweep<8, true, false, true>), 256, vec4, 0);
+            else HM_WIDE((l2sq_sweep<8, false, false, true>), 256, vec4, 0);
         }
 #undef HM_WIDE
         HM_LAUNCH_CHECK("l2sq_sweep (wide)");

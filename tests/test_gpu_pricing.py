@@ -61,6 +61,8 @@ def _assert_stats(gpu, ref, rtol=2e-5):
     (100, 200, 7, 17, 2.0),     # irregular k (reference tests k in {1,3,8,17,32})
     (50, 40, 100, 32, 2.0),     # k close to n
     (300, 500, 300, 3, 2.0),    # two-level fp32 accumulation (d > 256)
+    (300, 700, 200, 17, 2.0),   # split sweep with 256-row panels and 40-entry partial lists
+    (520, 3000, 640, 4, 1.0),   # 256-row panels (the last ragged), 20 chunks per tile, 24 tiles per row
     (1, 1, 1, 1, 2.0),          # smallest problem
     (5, 3, 16, 8, 2.0),         # k > n: sentinel slots
 ])
