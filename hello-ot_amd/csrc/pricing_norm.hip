@@ -43,6 +43,31 @@ __device__ inline float distance_reg(const float (&x)[DR], const float* __restri
     return (KIND == HM_COST_L2) ? (float)sqrt((double)acc) : acc;  // fp64 sqrt rounded once: correctly rounded
 }
 
+// distance with x in registers and exactly DR features (DR % 4 == 0, y 16-byte aligned): the same operations in the
+// same order as distance_reg, with y read from LDS as float4 and no per-feature bounds
+template <int KIND, int DR>
+__device__ inline float distance_exact(const float (&x)[DR], const float* __restrict__ y) {
+    static_assert(DR % 4 == 0, "whole float4 rows");
+    float yv[DR];
+#pragma unroll
+    for (int k = 0; k < DR; k += 4) {
+        const float4 t = *reinterpret_cast<const float4*>(y + k);
+        yv[k] = t.x;
+        yv[k + 1] = t.y;
+        yv[k + 2] = t.z;
+        yv[k + 3] = t.w;
+    }
+    float acc = 0.0f;
+#pragma unroll
+    for (int base = 0; base < DR; base += 32) {
+        float part = 0.0f;
+#pragma unroll
+        for (int k = base; k < base + 32 && k < DR; ++k) part = feature_op<KIND>(part, x[k] - yv[k]);
+        acc = (KIND == HM_COST_LINF) ? fmaxf(acc, part) : acc + part;
+    }
+    return (KIND == HM_COST_L2) ? (float)sqrt((double)acc) : acc;  // fp64 sqrt rounded once: correctly rounded
+}
+
 // distance with x streamed from global memory (any d)
 template <int KIND>
 __device__ inline float distance_mem(const float* __restrict__ x, const float* __restrict__ y, int d) {
@@ -66,14 +91,16 @@ __global__ void norm_prep(const float* __restrict__ Y, int64_t n, int d, const d
     atomicMax(&maxima[1], double_key(fabs(g[j])));
 }
 
-template <int KIND, int K, int DR>
+// EXACT: d == DR (a multiple of 4), so Y rows in LDS are whole float4s
+template <int KIND, int K, int DR, bool EXACT>
 __global__ __launch_bounds__(256) void norm_sweep(const float* __restrict__ X, const float* __restrict__ Y, int64_t m,
                                                   int64_t n, int d, const double* __restrict__ rb,
                                                   const double* __restrict__ cb,
                                                   const unsigned long long* __restrict__ ymaxima, int k,
                                                   int64_t seg_len, double* __restrict__ part_v, int* __restrict__ part_i,
                                                   double* __restrict__ blockstats, int STATS, int TRANSPOSED, int ntile) {
-    extern __shared__ float smem[];
+    extern __shared__ float4 smem4[];
+    float* smem = reinterpret_cast<float*>(smem4);
     float* sy = smem;                            // ntile * d
     float* scb = smem + (size_t)ntile * d;       // ntile (column duals as fp32)
     __shared__ double sRed[4][5];
@@ -122,7 +149,8 @@ __global__ __launch_bounds__(256) void norm_sweep(const float* __restrict__ X, c
             for (int jj = 0; jj < cnt; ++jj) {
                 const float* yj = sy + (size_t)jj * d;
                 float c;
-                if (DR > 0) c = distance_reg<KIND, (DR > 0 ? DR : 1)>(x, yj, d);
+                if constexpr (EXACT) c = distance_exact<KIND, DR>(x, yj);
+                else if (DR > 0) c = distance_reg<KIND, (DR > 0 ? DR : 1)>(x, yj, d);
                 else c = distance_mem<KIND>(X + row * d, yj, d);
                 const float s32 = (scb[jj] - c) + fi32;
                 if (s32 > thr) {
@@ -278,7 +306,7 @@ void norm_layout(A& a, int64_t m, int64_t n, int k, uint32_t flags, double** pv,
     *maxima = a.template take<unsigned long long>(4);
 }
 
-template <int KIND, int K, int DR>
+template <int KIND, int K, int DR, bool EXACT>
 int norm_direction_t(hipStream_t st, const float* X, const float* Y, int64_t m, int64_t n, int d, const double* rb,
                      const double* cb, const unsigned long long* ymaxima, int k, bool stats, bool transposed,
                      NormPlan plan, double* pv, int* pi, double* bs, double* out_v, int* out_i, double* stats_out,
@@ -289,7 +317,7 @@ int norm_direction_t(hipStream_t st, const float* X, const float* Y, int64_t m, 
     if ((size_t)ntile * (d + 1) > LDS_FLOATS) return fail(HM_EINVAL, "norm pricing supports d <= %d", LDS_FLOATS - 1);
     const size_t shmem = ((size_t)ntile * d + ntile) * sizeof(float);
     prof_begin(st, "norm_sweep");
-    hipLaunchKernelGGL((norm_sweep<KIND, K, DR>), grid, dim3(256), shmem, st, X, Y, m, n, d, rb, cb, ymaxima, k,
+    hipLaunchKernelGGL((norm_sweep<KIND, K, DR, EXACT>), grid, dim3(256), shmem, st, X, Y, m, n, d, rb, cb, ymaxima, k,
                        plan.seg_len, pv, pi, bs, (int)stats, (int)transposed, ntile);
     prof_end(st);
     HM_LAUNCH_CHECK("norm_sweep");
@@ -308,13 +336,16 @@ int norm_direction_d(hipStream_t st, const float* X, const float* Y, int64_t m, 
                      const double* cb, const unsigned long long* ymaxima, int k, bool stats, bool transposed,
                      NormPlan plan, double* pv, int* pi, double* bs, double* out_v, int* out_i, double* stats_out,
                      int linf) {
+    if (d == 8)
+        return norm_direction_t<KIND, K, 8, true>(st, X, Y, m, n, d, rb, cb, ymaxima, k, stats, transposed, plan, pv, pi,
+                                                  bs, out_v, out_i, stats_out, linf);
     if (d <= 8)
-        return norm_direction_t<KIND, K, 8>(st, X, Y, m, n, d, rb, cb, ymaxima, k, stats, transposed, plan, pv, pi, bs,
+        return norm_direction_t<KIND, K, 8, false>(st, X, Y, m, n, d, rb, cb, ymaxima, k, stats, transposed, plan, pv, pi, bs,
                                             out_v, out_i, stats_out, linf);
     if (d <= 64)
-        return norm_direction_t<KIND, K, 64>(st, X, Y, m, n, d, rb, cb, ymaxima, k, stats, transposed, plan, pv, pi, bs,
+        return norm_direction_t<KIND, K, 64, false>(st, X, Y, m, n, d, rb, cb, ymaxima, k, stats, transposed, plan, pv, pi, bs,
                                              out_v, out_i, stats_out, linf);
-    return norm_direction_t<KIND, K, 0>(st, X, Y, m, n, d, rb, cb, ymaxima, k, stats, transposed, plan, pv, pi, bs,
+    return norm_direction_t<KIND, K, 0, false>(st, X, Y, m, n, d, rb, cb, ymaxima, k, stats, transposed, plan, pv, pi, bs,
                                         out_v, out_i, stats_out, linf);
 }
 
