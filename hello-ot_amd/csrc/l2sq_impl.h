@@ -903,13 +903,15 @@ __global__ __launch_bounds__(256) void l2sq_sweep_split(
 //      block is folded per chunk.
 //   Row lists: lane (h, r) of wave w holds X row 32w + r; its partial list lives in `part` between tiles (each
 //      epilogue reads it, merges the tile and writes it back), so the chunk loop carries no lists.
-//   Columns: the tile's scores pass through LDS 32 Y rows at a time; 16 threads per Y row scan 16 X rows each
-//      (panel rows t, t + 16, ...: a stride that spreads the reads over the LDS banks).
+//   Columns: the tile's scores pass through LDS 64 Y rows at a time; 8 threads per Y row scan 32 X rows each
+//      (panel rows t, t + 8, ...: a stride that spreads the reads over the LDS banks) into lists of 64-bit keys
+//      (score order, then lower index), merged across the 8 by bitonic merges.
 // -------------------------------------------------------------------------------------------------
 constexpr int BXW = 256;                // X rows per workgroup of the 256-row split sweep
 constexpr int WAVES_W = BXW / 32;       // waves per workgroup (32 X rows each)
 constexpr int THREADS_W = 64 * WAVES_W;
 constexpr int CSTW = BXW + 8;           // LDS row stride of its column-score pass (floats)
+constexpr int CROWS_W = 64;             // Y rows per column-score pass
 
 template <int U>
 __device__ __forceinline__ XOps& xset2(XOps& a, XOps& b) {
@@ -952,6 +954,57 @@ __device__ __forceinline__ void split_pass(v16f (&acc)[NB], float (&outer)[NB][1
     pass_one<R, FOLD, 1>(acc, outer, yp, xv);
     pass_one<R, FOLD, 2>(acc, outer, yp, xv);
     pass_one<R, FOLD, 3>(acc, outer, yp, xv);
+}
+
+// Column candidates of the 256-row sweep as 64-bit keys: float_key of the score (with -0 taken as +0, so that
+// equal scores compare equal) above the complement of the X index, so that a larger key is a better entry (higher
+// score, then lower index: the order of better_e); the empty entry (-inf, -1) is the smallest key of all.
+constexpr unsigned long long CAND_EMPTY = (unsigned long long)0x007fffffu << 32;  // float_key(-inf), index -1
+__device__ __forceinline__ unsigned long long cand_key(float v, int i) {
+    return ((unsigned long long)float_key(v + 0.0f) << 32) | (unsigned int)~i;
+}
+__device__ __forceinline__ float cand_value(unsigned long long k) { return key_float((unsigned int)(k >> 32)); }
+__device__ __forceinline__ int cand_index(unsigned long long k) { return (int)~(unsigned int)k; }
+
+// insert kv into the descending list k[0..K) (the smallest entry drops out)
+template <int K>
+__device__ __forceinline__ void cand_insert(unsigned long long (&k)[K], unsigned long long kv) {
+#pragma unroll
+    for (int i = 0; i < K; ++i) {
+        const bool c = kv > k[i];
+        const unsigned long long t = k[i];
+        k[i] = c ? kv : t;
+        kv = c ? t : kv;
+    }
+}
+
+// k := the best K of k and the descending list of the lane `m` apart (xor): the elementwise maximum of k and the
+// other list reversed is a bitonic sequence holding the best K of both, which a bitonic sorter puts in order
+template <int K>
+__device__ __forceinline__ void cand_merge(unsigned long long (&k)[K], int m) {
+    static_assert((K & (K - 1)) == 0, "power-of-two list");
+    unsigned long long o[K];
+#pragma unroll
+    for (int i = 0; i < K; ++i) {
+        const unsigned long long v = k[K - 1 - i];
+        const unsigned int lo = __shfl_xor((unsigned int)v, m, 64);
+        const unsigned int hi = __shfl_xor((unsigned int)(v >> 32), m, 64);
+        o[i] = ((unsigned long long)hi << 32) | lo;
+    }
+#pragma unroll
+    for (int i = 0; i < K; ++i) k[i] = k[i] > o[i] ? k[i] : o[i];
+#pragma unroll
+    for (int s = K / 2; s >= 1; s >>= 1) {
+#pragma unroll
+        for (int i = 0; i < K; ++i) {
+            if ((i & s) == 0) {
+                const unsigned long long a = k[i], b = k[i + s];
+                const bool c = a > b;
+                k[i] = c ? a : b;
+                k[i + s] = c ? b : a;
+            }
+        }
+    }
 }
 
 // Epilogue of the 256-row split sweep for one tile. tot[y][q] is the fp32 dot of the lane's X row with Y row
@@ -1041,48 +1094,78 @@ __device__ __forceinline__ void sweep_epilogue_w(const float (&tot)[NB][16], int
         cnt64 += (double)tcnt;
     }
     if (COLS) {
-        // each Y row of the tile: its best K1 over the panel's 256 X rows (16 threads per row, merged by
-        // shuffles); colthr[j] bounds the chunk's K1-th value from below, as in sweep_epilogue
+        // each Y row of the tile: its best K1 over the panel's 256 X rows, 64 Y rows per pass (8 threads per row
+        // scanning 32 X rows each, then merged across the 8); colthr[j] bounds the chunk's K1-th value from below,
+        // as in sweep_epilogue
+        constexpr int TPR = THREADS_W / CROWS_W;  // threads per Y row
+        constexpr int XPT = BXW / TPR;            // X rows each of them scans (panel rows t, t + TPR, ...)
 #pragma unroll
-        for (int pass = 0; pass < NB; ++pass) {
+        for (int pass = 0; pass < NB * 32 / CROWS_W; ++pass) {
             if (pass > 0) __syncthreads();  // the previous pass's reads of sC are done
 #pragma unroll
-            for (int q = 0; q < 16; ++q) {
-                const int jl = 8 * (q / 4) + 4 * h + (q % 4);
-                sC[jl * CSTW + wave * 32 + r] = ok ? fmaf(scale, tot[pass][q], qbi) : -INFINITY;
+            for (int bb = 0; bb < CROWS_W / 32; ++bb) {
+#pragma unroll
+                for (int q = 0; q < 16; ++q) {
+                    const int jl = bb * 32 + 8 * (q / 4) + 4 * h + (q % 4);
+                    sC[jl * CSTW + wave * 32 + r] =
+                        ok ? fmaf(scale, tot[pass * (CROWS_W / 32) + bb][q], qbi) : -INFINITY;
+                }
             }
             __syncthreads();
-            const int jl = tid >> 4, part16 = tid & 15;
-            const int64_t j = ytile + pass * 32 + jl;
+            const int jl = tid / TPR, part8 = tid % TPR;
+            const int64_t j = ytile + pass * CROWS_W + jl;
             const float thr = j < y_end ? key_float(colthr[j]) : INFINITY;
-            float cw[K1];
-            int cidx[K1];
+            const float* src = &sC[jl * CSTW + part8];
+            const int base = (int)(x0 + part8);
+            Entry* dst = colpart + (panel * n + j) * K1;
+            if constexpr ((K1 & (K1 - 1)) == 0) {
+                // candidates as 64-bit keys (value order, then lower index): insertion while scanning, bitonic
+                // merges across the row's threads
+                unsigned long long key[K1];
 #pragma unroll
-            for (int i = 0; i < K1; ++i) { cw[i] = -INFINITY; cidx[i] = -1; }
-            const float* src = &sC[jl * CSTW + part16];
-            const int base = (int)(x0 + part16);
-            for (int xx = 0; xx < BXW / 16; ++xx) {
-                const float v = src[16 * xx];
-                if (v > thr && v > cw[K1 - 1]) insert_e<K1>(cw, cidx, v, base + 16 * xx);
-            }
-#pragma unroll
-            for (int m = 1; m < 16; m <<= 1) {
-                float pv[K1];
-                int pi2[K1];
-#pragma unroll
-                for (int i = 0; i < K1; ++i) {
-                    pv[i] = __shfl_xor(cw[i], m, 64);
-                    pi2[i] = __shfl_xor(cidx[i], m, 64);
+                for (int i = 0; i < K1; ++i) key[i] = CAND_EMPTY;
+                for (int xx = 0; xx < XPT; ++xx) {
+                    const float v = src[TPR * xx];
+                    if (v > thr) {
+                        const unsigned long long kv = cand_key(v, base + TPR * xx);
+                        if (kv > key[K1 - 1]) cand_insert<K1>(key, kv);
+                    }
                 }
 #pragma unroll
-                for (int i = 0; i < K1; ++i)
-                    if (pi2[i] >= 0 && better_e(pv[i], pi2[i], cw[K1 - 1], cidx[K1 - 1])) insert_e<K1>(cw, cidx, pv[i], pi2[i]);
-            }
-            if (part16 == 0 && j < y_end) {
-                Entry* dst = colpart + (panel * n + j) * K1;
+                for (int m = 1; m < TPR; m <<= 1) cand_merge<K1>(key, m);
+                if (part8 == 0 && j < y_end) {
 #pragma unroll
-                for (int i = 0; i < K1; ++i) dst[i] = Entry{cw[i], cidx[i]};
-                if (cidx[K1 - 1] >= 0) atomicMax(&colthr[j], float_key(cw[K1 - 1]));
+                    for (int i = 0; i < K1; ++i) dst[i] = Entry{cand_value(key[i]), cand_index(key[i])};
+                    if (cand_index(key[K1 - 1]) >= 0) atomicMax(&colthr[j], (unsigned int)(key[K1 - 1] >> 32));
+                }
+            } else {
+                float cw[K1];
+                int cidx[K1];
+#pragma unroll
+                for (int i = 0; i < K1; ++i) { cw[i] = -INFINITY; cidx[i] = -1; }
+                for (int xx = 0; xx < XPT; ++xx) {
+                    const float v = src[TPR * xx];
+                    if (v > thr && v > cw[K1 - 1]) insert_e<K1>(cw, cidx, v, base + TPR * xx);
+                }
+#pragma unroll
+                for (int m = 1; m < TPR; m <<= 1) {
+                    float pv[K1];
+                    int pi2[K1];
+#pragma unroll
+                    for (int i = 0; i < K1; ++i) {
+                        pv[i] = __shfl_xor(cw[i], m, 64);
+                        pi2[i] = __shfl_xor(cidx[i], m, 64);
+                    }
+#pragma unroll
+                    for (int i = 0; i < K1; ++i)
+                        if (pi2[i] >= 0 && better_e(pv[i], pi2[i], cw[K1 - 1], cidx[K1 - 1]))
+                            insert_e<K1>(cw, cidx, pv[i], pi2[i]);
+                }
+                if (part8 == 0 && j < y_end) {
+#pragma unroll
+                    for (int i = 0; i < K1; ++i) dst[i] = Entry{cw[i], cidx[i]};
+                    if (cidx[K1 - 1] >= 0) atomicMax(&colthr[j], float_key(cw[K1 - 1]));
+                }
             }
         }
     }
@@ -1106,7 +1189,7 @@ __global__ __launch_bounds__(THREADS_W) void l2sq_sweep_split_w(
     __shared__ float4 sY0[1024], sY1[1024], sY2[1024], sY3[1024];  // LDS ring (Y chunk: 4 blocks x 4 KiB)
     __shared__ float sDB[BY];
     __shared__ float sGE[BY];
-    __shared__ float sC[COLS ? 32 * CSTW : 1];
+    __shared__ float sC[COLS ? CROWS_W * CSTW : 1];
     __shared__ double sRed[WAVES_W][5];
 
     const int tid = threadIdx.x;

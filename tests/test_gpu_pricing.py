@@ -150,15 +150,17 @@ def test_l2sq_dense_near_ties_resolved_exactly(cuda, precision, copies):
     assert np.sqrt(gpu[0]) / (1.0 + np.sqrt(gpu[1])) < 1e-4
 
 
-def test_l2sq_all_equal_scores_take_lowest_indices(cuda):
-    # every pair ties exactly: integer-valued identical points -> every row's top-k is columns 0..k-1
-    m, n, d, k = 70, 500, 4, 8
+@pytest.mark.parametrize("m,d,precision", [(70, 4, "fp32"), (300, 256, "bf16x3")])
+def test_l2sq_all_equal_scores_take_lowest_indices(cuda, m, d, precision):
+    # every pair ties exactly: integer-valued identical points -> every row's top-k is columns 0..k-1 and every
+    # column's is rows 0..k-1 (at d = 256 through the 256-row split sweep's fused column lists)
+    n, k = 500, 8
     X = np.ones((m, d), np.float32)
     Y = np.ones((n, d), np.float32)
     p = (X.astype(np.float64) ** 2).sum(1)
     q = (Y.astype(np.float64) ** 2).sum(1)
     qb, db = -p, -q
-    rv, ri, cv, ci, st = pricing_l2sq(*_to(cuda, X, Y, p, q, qb, db), k)
+    rv, ri, cv, ci, st = pricing_l2sq(*_to(cuda, X, Y, p, q, qb, db), k, precision=precision)
     assert (ri.cpu().numpy() == np.arange(k)[None, :]).all()
     assert (ci.cpu().numpy() == np.arange(k)[None, :]).all()
     assert (rv.cpu().numpy() == 0.0).all()
