@@ -112,8 +112,23 @@ __global__ __launch_bounds__(256) void l2sq_prep_rows(const float* __restrict__ 
     double mx_norm = 0.0, mx_bias = 0.0;
     for (int64_t row = (int64_t)blockIdx.x * 4 + wave; row < m; row += (int64_t)gridDim.x * 4) {
         const float* x = X + row * (int64_t)d;
-        double s = 0.0;
-        for (int k = lane; k < d; k += 64) s += (double)x[k] * (double)x[k];
+        // the norm only bounds errors (it is inflated by 1e-12 below), so any summation order will do: float4
+        // loads and four independent sums when rows are whole float4s
+        double s0 = 0.0, s1 = 0.0, s2 = 0.0, s3 = 0.0;
+        int k0 = 0;
+        if ((d & 3) == 0) {
+            const float4* x4 = reinterpret_cast<const float4*>(x);
+            for (int k = lane; k < d / 4; k += 64) {
+                const float4 v = x4[k];
+                s0 += (double)v.x * (double)v.x;
+                s1 += (double)v.y * (double)v.y;
+                s2 += (double)v.z * (double)v.z;
+                s3 += (double)v.w * (double)v.w;
+            }
+            k0 = d;
+        }
+        for (int k = k0 + lane; k < d; k += 64) s0 += (double)x[k] * (double)x[k];
+        double s = (s0 + s1) + (s2 + s3);
         for (int o = 32; o >= 1; o >>= 1) s += __shfl_xor(s, o, 64);
         const double nrm = std::sqrt(s) * (1.0 + 1e-12);
         mx_norm = fmax(mx_norm, nrm);
@@ -167,39 +182,51 @@ __host__ __device__ inline int64_t split_unit(int64_t row, int c, int g4, int ld
     return ((row >> 5) * 32 * (int64_t)ld + (int64_t)c * 1024) / 4 + (g4 >> 1) * 128 + (g4 & 1) * 32 + (row & 31);
 }
 
-// item (32-row block, chunk c, group g4, row r): consecutive threads write consecutive 16-byte units
-__global__ void l2sq_split_bf16(const float* __restrict__ X, int64_t rows, int64_t padded_rows, int d, int sd, int ld,
-                                unsigned short* __restrict__ out) {
+// Item (32-row block, pair of chunks): the workgroup reads the block's 64 features per row into LDS (consecutive
+// threads on consecutive features of a row), then writes the 512 operand-order units of the two chunks
+// (consecutive threads on consecutive rows of a unit group): reads and writes both coalesced.
+__global__ __launch_bounds__(256) void l2sq_split_bf16(const float* __restrict__ X, int64_t rows, int64_t padded_rows,
+                                                       int d, int sd, int ld, unsigned short* __restrict__ out) {
+    __shared__ float tile[32][65];  // 32 rows x 64 features (one pad column: conflict-free row-wise reads)
     const int nch = sd / KC;
-    const int64_t items = (padded_rows >> 5) * nch * 128;
+    const int npair = (nch + 1) / 2;
+    const int64_t items = (padded_rows >> 5) * npair;
     uint4* out4 = reinterpret_cast<uint4*>(out);
-    for (int64_t gidx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; gidx < items;
-         gidx += (int64_t)gridDim.x * blockDim.x) {
-        const int r = (int)(gidx & 31);
-        const int g4 = (int)((gidx >> 5) & 3);
-        const int64_t t = gidx >> 7;
-        const int c = (int)(t % nch);
-        const int64_t row = (t / nch) * 32 + r;
-        const int k0 = (c * 4 + g4) * 8;
-        unsigned short hi[8], lo[8];
+    const int t = threadIdx.x;
+    for (int64_t it = blockIdx.x; it < items; it += gridDim.x) {
+        const int64_t blk = it / npair;
+        const int c0 = (int)(it % npair) * 2;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const float x = (row < rows && k0 + e < d) ? X[row * d + k0 + e] : 0.0f;
-            hi[e] = bf16_rne(x);
-            lo[e] = bf16_rne(x - __uint_as_float((unsigned int)hi[e] << 16));
+        for (int i = 0; i < 8; ++i) {
+            const int e = t + 256 * i;
+            const int rr = e >> 6, f = e & 63;
+            const int64_t row = blk * 32 + rr;
+            const int k = c0 * KC + f;
+            tile[rr][f] = (row < rows && k < d) ? X[row * d + k] : 0.0f;
         }
-        uint4 a, b;
-        a.x = hi[0] | ((unsigned int)hi[1] << 16);
-        a.y = hi[2] | ((unsigned int)hi[3] << 16);
-        a.z = hi[4] | ((unsigned int)hi[5] << 16);
-        a.w = hi[6] | ((unsigned int)hi[7] << 16);
-        b.x = lo[0] | ((unsigned int)lo[1] << 16);
-        b.y = lo[2] | ((unsigned int)lo[3] << 16);
-        b.z = lo[4] | ((unsigned int)lo[5] << 16);
-        b.w = lo[6] | ((unsigned int)lo[7] << 16);
-        const int64_t u = split_unit(row, c, g4, ld);
-        out4[u] = a;
-        out4[u + 64] = b;
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int u = t + 256 * i;  // (part, chunk of the pair, group g4, row r), r fastest
+            const int r = u & 31, g4 = (u >> 5) & 3, cc = (u >> 7) & 1, part = u >> 8;
+            if (c0 + cc < nch) {
+                const float* src = &tile[r][cc * KC + g4 * 8];
+                unsigned short v[8];
+#pragma unroll
+                for (int e2 = 0; e2 < 8; ++e2) {
+                    const float x = src[e2];
+                    const unsigned short hi = bf16_rne(x);
+                    v[e2] = part ? bf16_rne(x - __uint_as_float((unsigned int)hi << 16)) : hi;
+                }
+                uint4 w;
+                w.x = v[0] | ((unsigned int)v[1] << 16);
+                w.y = v[2] | ((unsigned int)v[3] << 16);
+                w.z = v[4] | ((unsigned int)v[5] << 16);
+                w.w = v[6] | ((unsigned int)v[7] << 16);
+                out4[split_unit(blk * 32 + r, c0 + cc, g4, ld) + (part ? 64 : 0)] = w;
+            }
+        }
+        __syncthreads();  // the tile is rewritten by the next item
     }
 }
 
@@ -1403,6 +1430,26 @@ struct BoundArgs {
 // The row side A (rows A[r], row bias abias[r], norm anorm[r]) pairs with candidates from side B (B[c],
 // bias bbias[c]); sigma = COLS ? (s*dot + bbias[c]) + abias[r] : (s*dot + abias[r]) + bbias[c], which keeps
 // the (dot + qb) + db association of the caller's (x, y) pair in both directions.
+// N dot64 products of the row `a` with rows c[0..N) of B in one pass over the features: the same order as
+// wave_dot64 for each (lane l sums features l, l + 64, ... in order, then the halving-stride tree)
+template <int N>
+__device__ __forceinline__ void multi_dot64(const float* __restrict__ a, const float* __restrict__ B, const int (&c)[4],
+                                            int d, int lane, double (&dots)[4]) {
+    const float* b[N];
+#pragma unroll
+    for (int t = 0; t < N; ++t) b[t] = B + (int64_t)c[t] * d;
+    double acc[N];
+#pragma unroll
+    for (int t = 0; t < N; ++t) acc[t] = 0.0;
+    for (int f = lane; f < d; f += 64) {
+        const double xa = (double)a[f];
+#pragma unroll
+        for (int t = 0; t < N; ++t) acc[t] = acc[t] + xa * (double)b[t][f];
+    }
+#pragma unroll
+    for (int t = 0; t < N; ++t) dots[t] = wave_tree_sum(acc[t]);
+}
+
 template <int KL, int KM, int G, bool COLS>
 __global__ __launch_bounds__(256) void l2sq_finalize(
     const float* __restrict__ A, const float* __restrict__ B, int64_t R, int d, int nlists,
@@ -1506,15 +1553,30 @@ __global__ __launch_bounds__(256) void l2sq_finalize(
     double sv = -INFINITY;
     int sj = -1;
     const float* ar = A + row * (int64_t)d;
+    // up to four candidates per pass over the row's features (each load of the row serves every dot of the pass;
+    // every dot keeps the dot64 order); `need` is uniform over the wave
+    for (int e0 = 0; e0 < need;) {
+        const int nb = need - e0 >= 4 ? 4 : (need - e0 >= 2 ? 2 : 1);
+        int c[4] = {-1, -1, -1, -1};
 #pragma unroll
-    for (int e = 0; e < KM; ++e) {
-        if (e < need) {
-            const int c = ti[e];
-            const double dot = wave_dot64(ar, B + (int64_t)c * d, d, lane);
-            const double sdot = scale * dot;
-            const double sig = COLS ? (sdot + bbias[c]) + abias[row] : (sdot + abias[row]) + bbias[c];
-            if (lane == e) { sv = sig; sj = c; }
+        for (int e = 0; e < KM; ++e) {
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+                if (e == e0 + t && t < nb) c[t] = ti[e];
         }
+        double dots[4];
+        if (nb == 4) multi_dot64<4>(ar, B, c, d, lane, dots);
+        else if (nb == 2) multi_dot64<2>(ar, B, c, d, lane, dots);
+        else multi_dot64<1>(ar, B, c, d, lane, dots);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            if (t < nb) {
+                const double sdot = scale * dots[t];
+                const double sig = COLS ? (sdot + bbias[c[t]]) + abias[row] : (sdot + abias[row]) + bbias[c[t]];
+                if (lane == e0 + t) { sv = sig; sj = c[t]; }
+            }
+        }
+        e0 += nb;
     }
     int er = 0;
     for (int src = 0; src < need; ++src) {
