@@ -261,6 +261,18 @@ inline unsigned sweep_grid(int64_t P, int64_t S) {
     return (unsigned)((blocks + 7) / 8 * 8 * 32);
 }
 
+// Shared row thresholds (per local row of a sweep launch; all keys start at float_key(-inf)): a lane whose partial
+// list of a row is full publishes its last entry, so the key is the K1-th value of some full list of that row.
+// Scores at or below it are not inserted into any of the row's lists: they are at most the largest last entry of
+// the row's full lists, which the finalize already takes as the bound of what the lists dropped. With no buffer
+// (nullptr) nothing is filtered.
+__device__ __forceinline__ float row_threshold_get(const unsigned int* rowthr, int64_t local) {
+    return rowthr ? key_float(rowthr[local]) : -INFINITY;
+}
+__device__ __forceinline__ void row_threshold_raise(unsigned int* rowthr, int64_t local, float last) {
+    if (rowthr) atomicMax(&rowthr[local], float_key(last));
+}
+
 // Lane state of a sweep: the row's partial top-K1 list, its per-row constants and certificate partial sums.
 template <int K1>
 struct SweepRow {
@@ -302,9 +314,13 @@ __device__ __forceinline__ void sweep_epilogue(const v16f (&tot)[NB], SweepRow<K
                                                int64_t n, float scale, int STATS, const float* sDB, const float* sGE,
                                                float* sC, Entry* __restrict__ colpart,
                                                unsigned int* __restrict__ colthr, int* __restrict__ wcnt,
-                                               int* __restrict__ wbuf, int wcap) {
+                                               int* __restrict__ wbuf, int wcap, unsigned int* __restrict__ rowthr,
+                                               int64_t xb) {
     float tnum = 0.0f, tden = 0.0f;
     unsigned int tcnt = 0;
+    // the row's shared threshold: scores at or below it cannot enter the row's merged lists (row_threshold_*)
+    const float rthr = (!APPEND && s.ok) ? row_threshold_get(rowthr, s.row - xb) : -INFINITY;
+    const float last0 = APPEND ? 0.0f : s.lv[K1 - 1];
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
 #pragma unroll
@@ -327,7 +343,7 @@ __device__ __forceinline__ void sweep_epilogue(const v16f (&tot)[NB], SweepRow<K
                         const int pos = atomicAdd(&wcnt[s.row], 1);
                         if (pos < wcap) wbuf[s.row * (int64_t)wcap + pos] = (int)j;
                     }
-                } else if (ok && w > s.lv[K1 - 1]) {
+                } else if (ok && w > s.lv[K1 - 1] && w > rthr) {
                     float cv = w;
                     int ci = (int)j;
 #pragma unroll
@@ -356,6 +372,8 @@ __device__ __forceinline__ void sweep_epilogue(const v16f (&tot)[NB], SweepRow<K
             }
         }
     }
+    if (!APPEND && s.ok && s.li[K1 - 1] >= 0 && s.lv[K1 - 1] != last0)
+        row_threshold_raise(rowthr, s.row - xb, s.lv[K1 - 1]);
     if (STATS) {
         s.num64 += (double)tnum;
         s.den64 += (double)tden;
@@ -466,7 +484,7 @@ __global__ __launch_bounds__(256) void l2sq_sweep(
     const float* __restrict__ ge32, float scale, int64_t seg_len, int P, int S, Entry* __restrict__ part,
     Entry* __restrict__ colpart, unsigned int* __restrict__ colthr, double* __restrict__ blockstats, int VEC4,
     int STATS, const float* __restrict__ wthr = nullptr, int* __restrict__ wcnt = nullptr,
-    int* __restrict__ wbuf = nullptr, int wcap = 0) {
+    int* __restrict__ wbuf = nullptr, int wcap = 0, unsigned int* __restrict__ rowthr = nullptr) {
     static_assert(!(APPEND && COLS), "the wide pass keeps no column lists");
     int64_t panel, seg;
     sweep_block(blockIdx.x, P, S, panel, seg);
@@ -648,7 +666,7 @@ __global__ __launch_bounds__(256) void l2sq_sweep(
             }
         }
         sweep_epilogue<K1, COLS, APPEND>(acc, s, tid, wave, h, r, ytile, y_end, x0, panel, n, scale, STATS, sDB, sGE,
-                                         sC, colpart, colthr, wcnt, wbuf, wcap);
+                                         sC, colpart, colthr, wcnt, wbuf, wcap, rowthr, xb);
     }
     sweep_finish<K1, APPEND>(s, tid, lane, wave, h, seg, rows, xb, P, panel, STATS, part, blockstats, sRed);
 }
@@ -756,7 +774,7 @@ __global__ __launch_bounds__(256) void l2sq_sweep_split(
     const float* __restrict__ ge32, float scale, int64_t seg_len, int P, int S, Entry* __restrict__ part,
     Entry* __restrict__ colpart, unsigned int* __restrict__ colthr, double* __restrict__ blockstats, int STATS,
     const float* __restrict__ wthr = nullptr, int* __restrict__ wcnt = nullptr, int* __restrict__ wbuf = nullptr,
-    int wcap = 0) {
+    int wcap = 0, unsigned int* __restrict__ rowthr = nullptr) {
     static_assert(!(APPEND && COLS), "the wide pass keeps no column lists");
     // Ring of Y chunks: the stage index is dynamic, so the loads are issued from assembly (there are no other
     // loads in the chunk loop to count)
@@ -908,7 +926,7 @@ __global__ __launch_bounds__(256) void l2sq_sweep_split(
             step(I3{});
         }
         sweep_epilogue<K1, COLS, APPEND>(acc, s, tid, wave, h, r, ytile, y_end, x0, panel, n, scale, STATS, sDB, sGE,
-                                         sC, colpart, colthr, wcnt, wbuf, wcap);
+                                         sC, colpart, colthr, wcnt, wbuf, wcap, rowthr, xb);
     }
     wait_vmcnt<0>();  // the loads ahead into LDS land before the workgroup can end
     sweep_finish<K1, APPEND>(s, tid, lane, wave, h, seg, rows, xb, P, panel, STATS, part, blockstats, sRed);
@@ -1047,7 +1065,8 @@ __device__ __forceinline__ void sweep_epilogue_w(const float (&tot)[NB][16], int
                                                  Entry* __restrict__ part, Entry* __restrict__ colpart,
                                                  unsigned int* __restrict__ colthr, int* __restrict__ wcnt,
                                                  int* __restrict__ wbuf, int wcap, double& num64, double& den64,
-                                                 double& cnt64, float& mx, float& cmax) {
+                                                 double& cnt64, float& mx, float& cmax,
+                                                 unsigned int* __restrict__ rowthr) {
     float tnum = 0.0f, tden = 0.0f;
     unsigned int tcnt = 0;
     float lv[APPEND ? 1 : K1];
@@ -1062,6 +1081,9 @@ __device__ __forceinline__ void sweep_epilogue_w(const float (&tot)[NB][16], int
             li[i] = e.j;
         }
     }
+    // the row's shared threshold: scores at or below it cannot enter the row's merged lists (row_threshold_*)
+    const float rthr = (!APPEND && ok) ? row_threshold_get(rowthr, row - xb) : -INFINITY;
+    const float last0 = APPEND ? 0.0f : lv[K1 - 1];
 #pragma unroll
     for (int y = 0; y < NB; ++y) {
 #pragma unroll
@@ -1082,7 +1104,7 @@ __device__ __forceinline__ void sweep_epilogue_w(const float (&tot)[NB][16], int
                         const int pos = atomicAdd(&wcnt[row], 1);
                         if (pos < wcap) wbuf[row * (int64_t)wcap + pos] = (int)j;
                     }
-                } else if (okj && w > lv[K1 - 1]) {
+                } else if (okj && w > lv[K1 - 1] && w > rthr) {
                     float cv = w;
                     int ci = (int)j;
 #pragma unroll
@@ -1114,6 +1136,7 @@ __device__ __forceinline__ void sweep_epilogue_w(const float (&tot)[NB][16], int
     if (!APPEND && ok) {
 #pragma unroll
         for (int i = 0; i < K1; ++i) lp[i] = Entry{lv[i], li[i]};
+        if (li[K1 - 1] >= 0 && lv[K1 - 1] != last0) row_threshold_raise(rowthr, row - xb, lv[K1 - 1]);
     }
     if (STATS) {
         num64 += (double)tnum;
@@ -1206,7 +1229,7 @@ __global__ __launch_bounds__(THREADS_W) void l2sq_sweep_split_w(
     const float* __restrict__ ge32, float scale, int64_t seg_len, int P, int S, Entry* __restrict__ part,
     Entry* __restrict__ colpart, unsigned int* __restrict__ colthr, double* __restrict__ blockstats, int STATS,
     const float* __restrict__ wthr = nullptr, int* __restrict__ wcnt = nullptr, int* __restrict__ wbuf = nullptr,
-    int wcap = 0) {
+    int wcap = 0, unsigned int* __restrict__ rowthr = nullptr) {
     static_assert(!(APPEND && COLS), "the wide pass keeps no column lists");
     constexpr int AHEAD = 3;      // Y chunks in flight ahead of the one multiplied (4-stage ring)
     constexpr int VMEM_STEP = 6;  // vector-memory instructions a chunk issues (4 X, then 2 Y)
@@ -1352,7 +1375,7 @@ __global__ __launch_bounds__(THREADS_W) void l2sq_sweep_split_w(
         }
         sweep_epilogue_w<K1, COLS, APPEND>(outer, row, ok, qbi, pi, wt, ytile == y_begin, tid, wave, h, r, ytile,
                                            y_end, x0, xb, rows, seg, panel, n, scale, STATS, sDB, sGE, sC, part,
-                                           colpart, colthr, wcnt, wbuf, wcap, num64, den64, cnt64, mx, cmax);
+                                           colpart, colthr, wcnt, wbuf, wcap, num64, den64, cnt64, mx, cmax, rowthr);
 #pragma unroll
         for (int y = 0; y < NB; ++y) {
 #pragma unroll
@@ -1829,6 +1852,7 @@ struct WideBufs {
     int* redo3;        // [m + n] rows that overflowed the second round (exact full rescan)
     float* redo3_thr;  // [m + n]
     int* counts;       // [4]: redo2 and redo3 lengths
+    unsigned int* rowthr;  // [rows of a sweep launch] the sweeps' shared row thresholds (row_threshold_*)
 };
 
 // Resolves the rows a finalize queued (defined in pricing_l2sq.hip): the wide pass over them, then the exact full
@@ -2052,6 +2076,7 @@ void layout(A& a, int64_t m, int64_t n, int d, int k, uint32_t flags, double** x
     wide->redo3 = a.template take<int>((size_t)(m + n));
     wide->redo3_thr = a.template take<float>((size_t)(m + n));
     wide->counts = a.template take<int>(4);
+    wide->rowthr = a.template take<unsigned int>((size_t)std::max<int64_t>(std::max<int64_t>(c.ch, c.ch2), 1));
 }
 
 // Exact rescan of the rows queued by a finalize: reads the queue length back (one host synchronisation), then
@@ -2119,6 +2144,7 @@ int run_bidir(hipStream_t st, const float* X, const float* Y, int64_t m, int64_t
     const int64_t ch = cp.ch;
     const DirPlan plan = cp.plan;
     const int bx = cp.bx;
+    unsigned int* rowthr = wide.rowthr;
     if (split) {
         hipLaunchKernelGGL(l2sq_split_bf16, dim3(4096), dim3(256), 0, st, X, m, panel_rows(m, BXW), d, sd, ld,
                            reinterpret_cast<unsigned short*>(xsplit));
@@ -2149,27 +2175,32 @@ int run_bidir(hipStream_t st, const float* X, const float* Y, int64_t m, int64_t
         const int64_t rows = xe - xb;
         const int64_t panels = (rows + bx - 1) / bx;
         const dim3 grid(sweep_grid(panels, plan.S));
+        const unsigned neg_inf_key = 0x007fffffu;  // float_key(-INFINITY)
         if (fused) {
             // column thresholds start at -inf for every chunk (its lists only rank its own X rows)
-            const unsigned neg_inf_key = 0x007fffffu;  // float_key(-INFINITY)
             hipLaunchKernelGGL(fill_u32, dim3((unsigned)((n + 255) / 256 < 4096 ? (n + 255) / 256 : 4096)), dim3(256), 0,
                                st, colthr, n, neg_inf_key);
             HM_LAUNCH_CHECK("fill_u32");
         }
+        // row thresholds start at -inf for every chunk (they index the chunk's rows)
+        hipLaunchKernelGGL(fill_u32, dim3((unsigned)((rows + 255) / 256 < 4096 ? (rows + 255) / 256 : 4096)), dim3(256), 0,
+                           st, rowthr, rows, neg_inf_key);
+        HM_LAUNCH_CHECK("fill_u32");
+#define NOWIDE (const float*)nullptr, (int*)nullptr, (int*)nullptr, 0
 #define HM_SWEEP(TL, CL)                                                                                             \
     do {                                                                                                             \
         if (split && TL)                                                                                             \
             hipLaunchKernelGGL((l2sq_sweep_split_w<K1, CL>), grid, dim3(THREADS_W), 0, st, SX, SY, xb, xe, n, sd,    \
                                ld, qb32, db32, p32, ge32, (float)scale, plan.seg_len, (int)panels, plan.S, part,     \
-                               colpart, colthr, blockstats, (int)want_stats);                                        \
+                               colpart, colthr, blockstats, (int)want_stats, NOWIDE, rowthr);                       \
         else if (split)                                                                                              \
             hipLaunchKernelGGL((l2sq_sweep_split<K1, CL>), grid, dim3(256), 0, st, SX, SY, xb, xe, n, sd, ld, \
                                qb32, db32, p32, ge32, (float)scale, plan.seg_len, (int)panels, plan.S, part,         \
-                               colpart, colthr, blockstats, (int)want_stats);                                        \
+                               colpart, colthr, blockstats, (int)want_stats, NOWIDE, rowthr);                       \
         else                                                                                                         \
             hipLaunchKernelGGL((l2sq_sweep<K1, TL, CL>), grid, dim3(256), 0, st, X, Y, xb, xe, n, d, d, qb32,        \
                                db32, p32, ge32, (float)scale, plan.seg_len, (int)panels, plan.S, part, colpart,      \
-                               colthr, blockstats, (int)vec4, (int)want_stats);                                      \
+                               colthr, blockstats, (int)vec4, (int)want_stats, NOWIDE, rowthr);                     \
     } while (0)
         prof_begin(st, "l2sq_sweep");
         if (two_level) {
@@ -2229,26 +2260,30 @@ int run_bidir(hipStream_t st, const float* X, const float* Y, int64_t m, int64_t
             const int64_t rows = ye - yb;
             const int64_t panels2 = (rows + bx - 1) / bx;
             const dim3 grid(sweep_grid(panels2, plan2.S));
+            hipLaunchKernelGGL(fill_u32, dim3((unsigned)((rows + 255) / 256 < 4096 ? (rows + 255) / 256 : 4096)),
+                               dim3(256), 0, st, rowthr, rows, 0x007fffffu /* float_key(-INFINITY) */);
+            HM_LAUNCH_CHECK("fill_u32");
 #define HM_SWEEP2(TL)                                                                                                \
     do {                                                                                                             \
         if (split && TL)                                                                                             \
             hipLaunchKernelGGL((l2sq_sweep_split_w<K1, false>), grid, dim3(THREADS_W), 0, st, SY, SX, yb, ye, m, sd, \
                                ld, db32, qb32, ge32, p32, (float)scale, plan2.seg_len, (int)panels2, plan2.S, part,  \
-                               colpart, colthr, blockstats, 0);                                                      \
+                               colpart, colthr, blockstats, 0, NOWIDE, rowthr);                                     \
         else if (split)                                                                                              \
             hipLaunchKernelGGL((l2sq_sweep_split<K1, false>), grid, dim3(256), 0, st, SY, SX, yb, ye, m, sd,  \
                                ld, db32, qb32, ge32, p32, (float)scale, plan2.seg_len, (int)panels2, plan2.S, part,  \
-                               colpart, colthr, blockstats, 0);                                                      \
+                               colpart, colthr, blockstats, 0, NOWIDE, rowthr);                                     \
         else                                                                                                         \
             hipLaunchKernelGGL((l2sq_sweep<K1, TL, false>), grid, dim3(256), 0, st, Y, X, yb, ye, m, d, d, db32,     \
                                qb32, ge32, p32, (float)scale, plan2.seg_len, (int)panels2, plan2.S, part, colpart,   \
-                               colthr, blockstats, (int)vec4, 0);                                                    \
+                               colthr, blockstats, (int)vec4, 0, NOWIDE, rowthr);                                   \
     } while (0)
             prof_begin(st, "l2sq_sweep");
             if (two_level) HM_SWEEP2(true);
             else HM_SWEEP2(false);
             prof_end(st);
 #undef HM_SWEEP2
+#undef NOWIDE
             HM_LAUNCH_CHECK("l2sq_sweep");
             hipLaunchKernelGGL(zero_words, dim3(1), dim3(64), 0, st, reinterpret_cast<unsigned long long*>(redo_count), 1);
             prof_begin(st, "l2sq_col_finalize");
