@@ -35,6 +35,7 @@ PEAK_HBM = 8.0e12           # MI355X HBM3E bytes/s
 PEAK_VALU_OPS = 256 * 64 * 2.4e9  # non-packed fp32 VALU lane-ops/s (256 CU x 64 lanes/clk x 2.4 GHz)
 
 TRAFFIC_PROFILE = ROOT / "profiles" / "l2sq_sweep_c5_chunk8192.md"
+COUNTER_PROFILE = ROOT / "profiles" / "l2sq_sweep_c5_counters.md"
 
 C5_N = 1_280_000
 C5_D = 8192
@@ -53,7 +54,8 @@ def roofline(precision, achieved):
             "frac": executed / peak, "traffic": sweep_traffic(), "traffic_source": TRAFFIC_PROFILE.name,
             "kernel": "l2sq_sweep_split_w" if precision == "bf16x3" else "l2sq_sweep", "sweep": precision,
             "work_per_pair": unit_work,
-            "algorithmic_tflops": achieved / 1e12, "algorithmic_flops_per_pair": 2 * C5_D}
+            "algorithmic_tflops": achieved / 1e12, "algorithmic_flops_per_pair": 2 * C5_D,
+            "counters": sweep_counters() if precision == "bf16x3" else None}
 
 
 def sweep_traffic():
@@ -66,6 +68,24 @@ def sweep_traffic():
     except OSError:
         pass
     return None
+
+
+def sweep_counters():
+    """The split sweep's sustained engine clock and MFMA-busy fraction at the C5 workload, from the committed
+    rocprofv3 shader-counter summary (GRBM_GUI_ACTIVE and SQ_VALU_MFMA_BUSY_CYCLES over the dispatch); None when
+    no such summary is present."""
+    out = {}
+    try:
+        for line in COUNTER_PROFILE.read_text().splitlines():
+            for key in ("sustained_clock_ghz", "mfma_busy_frac"):
+                if line.startswith(key + " ="):
+                    out[key] = float(line.split("=")[1])
+    except OSError:
+        return None
+    if not out:
+        return None
+    out["source"] = COUNTER_PROFILE.name
+    return out
 
 
 def log(msg):
