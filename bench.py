@@ -244,6 +244,34 @@ def cpu_baseline_c5(dev, sample_rows=4096, sample_cols=196608, threads=16):
 # extras: C2, C3, C4
 # ----------------------------------------------------------------------------------------------------------
 
+def bench_library_gemm(dev, warmup=10, steps=40):
+    """Reference point for the sweep's MFMA rate: the vendor library's plain bf16 GEMM (`torch.matmul`, which
+    calls hipBLASLt) on the sweep's product shape, the 8192-row query chunk times 131072 resident rows at
+    d = 8192, bf16 in and out, timed with events on torch's stream after a warm-up long enough to reach the
+    sustained clock. It computes one product per pair; the split sweep computes three plus the selection."""
+    m, n, d = 8192, 131072, C5_D
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(5)
+    A = torch.randn(m, d, device=dev, dtype=torch.bfloat16, generator=gen)
+    B = torch.randn(d, n, device=dev, dtype=torch.bfloat16, generator=gen)
+    C = torch.empty(m, n, device=dev, dtype=torch.bfloat16)
+    for _ in range(warmup):
+        torch.matmul(A, B, out=C)
+    sync()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        torch.matmul(A, B, out=C)
+    end.record()
+    sync()
+    sec = start.elapsed_time(end) / 1e3 / steps
+    flops = 2.0 * m * n * d
+    del A, B, C
+    torch.cuda.empty_cache()
+    return {"shape_m_n_d": [m, n, d], "ms": sec * 1e3, "tflops": flops / sec / 1e12,
+            "frac_of_bf16_peak": flops / sec / PEAK_BF16_MFMA}
+
+
 def bench_c2(dev, steps=3):
     from hello_ot_amd import _lib
     from hello_ot_amd.kernels.generic_scan import pricing_l2sq
@@ -507,6 +535,8 @@ def main():
     del inputs, split_out
     torch.cuda.empty_cache()
     if not args.no_extras:
+        log("[bench] hipBLASLt bf16 GEMM of the sweep's product shape ...")
+        extras["library_bf16_gemm_same_shape"] = bench_library_gemm(dev)
         log("[bench] C2 ...")
         extras["c2_scan_131072x131072_d64_k8"] = bench_c2(dev)
         log("[bench] C3 ...")
