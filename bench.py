@@ -487,6 +487,9 @@ def main():
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first run a plain 1 GiB device-to-device copy kernel three times (the reference point "
                          "for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE to bytes)")
+    ap.add_argument("--only", default="", metavar="LIST",
+                    help="instead of the default run, run only the listed secondary workloads (comma-separated: "
+                         "c2, c3, c4) and print their figures as one JSON line (for counter passes)")
     ap.add_argument("--c5-solve", type=int, default=0, metavar="ROWS",
                     help="instead of the default run, solve the C5 instance with ROWS points per side "
                          "(1280000 = the full instance) and print its JSON line")
@@ -509,6 +512,19 @@ def main():
         sync()
         log("[bench] copy calibration: 3 x 1 GiB read + 1 GiB written")
         del src, dst
+    if args.only:
+        names = [x.strip() for x in args.only.split(",") if x.strip()]
+        runs = {"c2": ("c2_scan_131072x131072_d64_k8", bench_c2), "c3": ("c3_sddmm_pdhg_262144_d256", bench_c3),
+                "c4": ("c4_norm_scan_524288_d8", bench_c4)}
+        bad = [x for x in names if x not in runs]
+        if bad:
+            raise SystemExit(f"--only: unknown workload(s) {bad}; choose from {sorted(runs)}")
+        extras = {}
+        for x in names:
+            log(f"[bench] {x} ...")
+            extras[runs[x][0]] = runs[x][1](dev)
+        print(json.dumps({"only": names, "extras": extras}), flush=True)
+        return
     if args.c5_solve:
         print(json.dumps({"metric": "C5 solve seconds to relative dual infeasibility 1e-6 (l2^2, d=8192)",
                           **bench_c5_solve(dev, args.c5_solve)}), flush=True)
