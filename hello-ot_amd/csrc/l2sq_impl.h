@@ -687,7 +687,7 @@ __global__ __launch_bounds__(256) void l2sq_sweep(
 // retired at the previous barrier); each wave then waits for its own loads of the next chunk, so the barrier
 // publishes that stage. After it, the products of K-step 1 run while the next chunk's K-step-0 operands are read.
 // -------------------------------------------------------------------------------------------------
-constexpr int SPLIT_STAGES = 5;  // LDS ring of Y chunks (16 KiB each)
+constexpr int SPLIT_STAGES = 3;  // LDS ring of Y chunks (16 KiB each): 49 KiB of LDS, two workgroups per CU
 
 struct XOps { float4 h0, l0, h1, l1; };                  // this lane's X operands of one chunk (K-steps 0 and 1)
 struct YOps { float4 h0, h1, h2, h3, l0, l1, l2, l3; };  // A operands of one K-step for the Y blocks 0..3
@@ -768,7 +768,7 @@ __device__ __forceinline__ void ring_barrier() {
 constexpr int SG_VALU = 0x002, SG_MFMA = 0x008, SG_VMEM_READ = 0x020, SG_DS_READ = 0x100;
 
 template <int K1, bool COLS, bool APPEND = false>
-__global__ __launch_bounds__(256) void l2sq_sweep_split(
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(COLS ? 1 : 2))) void l2sq_sweep_split(
     const float* __restrict__ X, const float* __restrict__ Y, int64_t xb, int64_t xe, int64_t n, int d, int ld,
     const float* __restrict__ qb32, const float* __restrict__ db32, const float* __restrict__ p32,
     const float* __restrict__ ge32, float scale, int64_t seg_len, int P, int S, Entry* __restrict__ part,
@@ -784,7 +784,7 @@ __global__ __launch_bounds__(256) void l2sq_sweep_split(
     int64_t panel, seg;
     sweep_block(blockIdx.x, P, S, panel, seg);
     if (panel >= P || seg >= S) return;  // grid padding (uniform per workgroup, before any barrier)
-    __shared__ float4 sY0[1024], sY1[1024], sY2[1024], sY3[1024], sY4[1024];  // LDS ring (Y chunk: 4 blocks x 4 KiB)
+    __shared__ float4 sY0[1024], sY1[1024], sY2[1024];  // LDS ring (Y chunk: 4 blocks x 4 KiB)
     __shared__ float sDB[BY];
     __shared__ float sGE[BY];
     __shared__ float sC[COLS ? BY * CST : 1];
@@ -809,7 +809,8 @@ __global__ __launch_bounds__(256) void l2sq_sweep_split(
     const unsigned tid16 = (unsigned)tid * 16u;
     const unsigned ystep = (unsigned)(bstride * 4);     // bytes between consecutive Y blocks
     auto ystage = [&](int st) -> float4* {
-        return st == 0 ? sY0 : st == 1 ? sY1 : st == 2 ? sY2 : st == 3 ? sY3 : sY4;
+        static_assert(NS == 3, "stage table");
+        return st == 0 ? sY0 : st == 1 ? sY1 : sY2;
     };
 
     auto load_x = [&](XOps& o, int cc) {
@@ -852,10 +853,9 @@ __global__ __launch_bounds__(256) void l2sq_sweep_split(
     YOps o0, o1;              // Y operands of K-steps 0 and 1
     int st0 = 0;              // LDS stage of the chunk being multiplied
 
+    static_assert(AHEAD == 2, "initial ring fill");
     load_ahead(sY0);
     load_ahead(sY1);
-    load_ahead(sY2);
-    load_ahead(sY3);
     load_x(xs0, 0);
     if (nchunks > 1) load_x(xs1, 1);
     if (nchunks > 2) {
