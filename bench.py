@@ -7,6 +7,10 @@ Gaussian mixture (means ~ N(0, 4I), identity covariance, equal weights), query c
 independent mixture; k = 2 (pricing_topk default). Inputs are resident in HBM before timing starts.
 ``value`` = pairs scanned per second (chunk x 1.28M per step).
 
+The metric's second half, the full C5 solve (1.28M x 1.28M, d=8192, relative dual infeasibility 1e-6), runs
+last and lands in ``solve_seconds.c5`` (seconds, convergence, final dual infeasibility, peak GPU memory, and the
+initialization / scan / LP split); ``--no-c5-solve`` skips it.
+
 Extra fields measure the other configurations: C2 (isolated 131072^2 d=64 k=8 scan), C3 (SDDMM + 1000 PDHG
 iterations, m=n=262144 d=256, 16 nnz/row), C4 (l1 / linf scans, m=n=524288 d=8) and the full HELLO solve seconds
 of C1 (Brenier, 2048, d=32) and C4 (l1 and linf, 524288, d=8).
@@ -43,18 +47,20 @@ C5_D = 8192
 
 def roofline(precision, achieved):
     """Roofline of the sweep kernel. `achieved` is the algorithmic rate, 2*d flop per pair over the sweep's mean
-    launch time. The split-bf16 sweep executes three bf16 products per feature (hi*hi + hi*lo + lo*hi), so its
-    MFMA work is 3 x the algorithmic flops, held against the bf16 matrix peak; the fp32 sweep's work is the
-    algorithmic flops against the fp32 matrix peak."""
+    launch time, held against the peak of the matrix units the sweep runs on: the bf16 peak for the split-bf16
+    sweep, the fp32 peak for the fp32 sweep. The split sweep executes three bf16 products per feature (hi*hi +
+    hi*lo + lo*hi), so its executed MFMA rate (3x the algorithmic one) is reported beside it; its algorithmic
+    fraction cannot exceed 1/3."""
     if precision == "bf16x3":
-        executed, peak, unit_work = 3.0 * achieved, PEAK_BF16_MFMA, "3 bf16 products x 2*d flop per pair"
+        products, peak = 3.0, PEAK_BF16_MFMA
     else:
-        executed, peak, unit_work = achieved, PEAK_FP32_MFMA, "2*d flop per pair"
-    return {"bound": "mfma", "achieved": executed / 1e12, "peak": peak / 1e12, "unit": "TFLOP/s",
-            "frac": executed / peak, "traffic": sweep_traffic(), "traffic_source": TRAFFIC_PROFILE.name,
+        products, peak = 1.0, PEAK_FP32_MFMA
+    return {"bound": "mfma", "achieved": achieved / 1e12, "peak": peak / 1e12, "unit": "TFLOP/s",
+            "frac": achieved / peak, "traffic": sweep_traffic(), "traffic_source": TRAFFIC_PROFILE.name,
             "kernel": "l2sq_sweep_split_w" if precision == "bf16x3" else "l2sq_sweep", "sweep": precision,
-            "work_per_pair": unit_work,
-            "algorithmic_tflops": achieved / 1e12, "algorithmic_flops_per_pair": 2 * C5_D,
+            "work_per_pair": "2*d flop (algorithmic)", "algorithmic_flops_per_pair": 2 * C5_D,
+            "executed_products_per_feature": products, "executed_tflops": products * achieved / 1e12,
+            "executed_frac": products * achieved / peak,
             "counters": sweep_counters() if precision == "bf16x3" else None}
 
 
@@ -86,6 +92,39 @@ def sweep_counters():
         return None
     out["source"] = COUNTER_PROFILE.name
     return out
+
+
+NORM_COUNTER_PROFILE = ROOT / "profiles" / "norm_sweep_c4_counters.md"
+
+
+def norm_counters(name):
+    """Executed VALU work of the C4 norm sweep from the committed rocprofv3 counter summary (SQ_INSTS_VALU per
+    pair and the VALU lane-op fraction of the non-packed fp32 peak over the sweep's duration); None when absent."""
+    out = {}
+    try:
+        for line in NORM_COUNTER_PROFILE.read_text().splitlines():
+            for key in ("valu_insts_per_pair", "valu_lane_op_frac", "duration_ms"):
+                if line.startswith(f"{name}_{key} ="):
+                    out[key] = float(line.split("=")[1])
+    except OSError:
+        return None
+    if not out:
+        return None
+    out["source"] = NORM_COUNTER_PROFILE.name
+    return out
+
+
+def host_info():
+    """CPU model and core count of the host the CPU baseline runs on."""
+    model = None
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"nproc": os.cpu_count(), "cpu_model": model}
 
 
 def log(msg):
@@ -137,19 +176,24 @@ def c5_inputs(dev, chunk):
     Y = gmm(C5_N, C5_D, seed=2, dev=dev, means_seed=12)
     X = gmm(chunk, C5_D, seed=1, dev=dev, means_seed=11)
     p, q = sqnorms(X), sqnorms(Y)
-    # duals: g = 0 and f_i = min_j c_ij over 4096 sampled resident rows (a c-transform estimate), so a few
-    # hundred pairs per row have sigma > 0, as in a refinement iteration
-    gen = torch.Generator(device=dev)
-    gen.manual_seed(13)
-    idx = torch.randperm(C5_N, device=dev, generator=gen)[:4096]
-    Ys = Y[idx]
-    f = torch.empty(chunk, dtype=torch.float64, device=dev)
-    for s in range(0, chunk, 4096):
-        dots = (X[s:s + 4096] @ Ys.T).double()
-        f[s:s + 4096] = (p[s:s + 4096, None] + q[idx][None, :] - 2.0 * dots).min(1).values
+    f = c_transform_sample(X, Y, p, q)
     g = torch.zeros(C5_N, dtype=torch.float64, device=dev)
     sync()
     return X, Y, p, q, f, g
+
+
+def c_transform_sample(X, Y, p, q, sample=4096):
+    """Duals of a refinement-like state: g = 0 and f_i = min_j c_ij over `sample` sampled resident rows (a
+    c-transform estimate), so a few hundred pairs per row have sigma > 0."""
+    gen = torch.Generator(device=X.device)
+    gen.manual_seed(13)
+    idx = torch.randperm(Y.shape[0], device=X.device, generator=gen)[:sample]
+    Ys = Y[idx]
+    f = torch.empty(X.shape[0], dtype=torch.float64, device=X.device)
+    for s in range(0, X.shape[0], 4096):
+        dots = (X[s:s + 4096] @ Ys.T).double()
+        f[s:s + 4096] = (p[s:s + 4096, None] + q[idx][None, :] - 2.0 * dots).min(1).values
+    return f
 
 
 def bench_c5(dev, chunk, steps, warmup, inputs=None, precision="auto", keep=None):
@@ -203,12 +247,15 @@ def cpu_baseline_c5(dev, sample_rows=4096, sample_cols=196608, threads=16):
 
     threads = min(threads, os.cpu_count() or 1)
     torch.set_num_threads(threads)
-    X = gmm(sample_rows, C5_D, seed=1, dev=dev, means_seed=11).cpu()
-    Y = gmm(sample_cols, C5_D, seed=2, dev=dev, means_seed=12).cpu()
-    p = (X.double() ** 2).sum(1).numpy()
-    q = (Y.double() ** 2).sum(1).numpy()
-    f = p.copy() * 0.0
-    g = q.copy() * 0.0
+    Xd = gmm(sample_rows, C5_D, seed=1, dev=dev, means_seed=11)
+    Yd = gmm(sample_cols, C5_D, seed=2, dev=dev, means_seed=12)
+    pd_, qd = sqnorms(Xd), sqnorms(Yd)
+    # the same kind of duals as the GPU step: f from a sampled c-transform, g = 0
+    fd = c_transform_sample(Xd, Yd, pd_, qd)
+    X, Y = Xd.cpu(), Yd.cpu()
+    p, q, f = pd_.cpu().numpy(), qd.cpu().numpy(), fd.cpu().numpy()
+    g = np.zeros(sample_cols)
+    del Xd, Yd
     sc = oracle.ref_scan()
     k = 2
     rv = np.full((sample_rows, k), -np.inf)
@@ -237,7 +284,8 @@ def cpu_baseline_c5(dev, sample_rows=4096, sample_cols=196608, threads=16):
     pairs = sample_rows * sample_cols
     return {"value": pairs / sec, "unit": "pairs/s", "cores": threads, "kind": kind,
             "sample": f"{sample_rows} query x {sample_cols} resident rows of the C5 mixture, d={C5_D}, k=2, "
-                      f"bidirectional + certificate ({sec:.1f} s)"}
+                      f"bidirectional + certificate, sampled c-transform duals as the GPU step ({sec:.1f} s)",
+            **host_info()}
 
 
 # ----------------------------------------------------------------------------------------------------------
@@ -274,7 +322,7 @@ def bench_library_gemm(dev, warmup=10, steps=40):
 
 def bench_c2(dev, steps=3):
     from hello_ot_amd import _lib
-    from hello_ot_amd.kernels.generic_scan import pricing_l2sq
+    from hello_ot_amd.kernels.generic_scan import pricing_l2sq, sweep_precision
 
     m = n = 131072
     d, k = 64, 8
@@ -298,9 +346,13 @@ def bench_c2(dev, steps=3):
         sw_ms, sw_n = _lib.profile_query("l2sq_sweep")
         _lib.profile_enable(False)
         sweep_s = sw_ms / max(steps, 1) / 1e3   # all sweep launches of one call (one per internal query chunk)
-        out[name] = {"seconds": sec, "pairs_per_s": m * n / sec, "sweep_launches_per_call": sw_n // max(steps, 1),
-                     "sweep_ms_per_call": sweep_s * 1e3, "sweep_tflops": 2 * d * m * n / sweep_s / 1e12,
-                     "sweep_mfma_frac": 2 * d * m * n / sweep_s / PEAK_FP32_MFMA}
+        prec = sweep_precision(kw.get("precision", "auto"), d)
+        peak, products = (PEAK_BF16_MFMA, 3.0) if prec == "bf16x3" else (PEAK_FP32_MFMA, 1.0)
+        alg = 2 * d * m * n / sweep_s
+        out[name] = {"seconds": sec, "pairs_per_s": m * n / sec, "sweep": prec,
+                     "sweep_launches_per_call": sw_n // max(steps, 1), "sweep_ms_per_call": sweep_s * 1e3,
+                     "sweep_algorithmic_tflops": alg / 1e12, "peak_tflops": peak / 1e12,
+                     "sweep_algorithmic_frac": alg / peak, "sweep_executed_frac": products * alg / peak}
     return out
 
 
@@ -395,9 +447,8 @@ def bench_c4(dev):
         sec = time.perf_counter() - t0
         sw_ms, sw_n = _lib.profile_query("norm_sweep")
         _lib.profile_enable(False)
-        sweep_s = sw_ms / max(sw_n, 1) / 1e3
-        out[name] = {"bidir_stats_seconds": sec, "pairs_per_s_per_direction": m * n / sweep_s,
-                     "sweep_valu_frac_3d_ops": 3 * d * m * n / sweep_s / PEAK_VALU_OPS}
+        out[name] = {"bidir_stats_seconds": sec, "pairs_per_s": m * n / sec, "sweep_launches": sw_n,
+                     "sweep_ms_total": sw_ms, "valu_counters": norm_counters(name)}
     return out
 
 
@@ -464,6 +515,7 @@ def bench_c5_solve(dev, rows):
     sync()
     log("[bench] C5 solve: solving ...")
     r = solve(X, Y, options=SolverOptions(verbose="detailed", consume_input_features=True))
+    del X, Y
     finest = r.solve_stage.levels[-1].solve.summary
     return {"rows": rows, "d": C5_D, "seconds": r.total_wall_time, "objective": r.objective,
             "converged": bool(finest.converged),
@@ -471,6 +523,8 @@ def bench_c5_solve(dev, rows):
             "peak_gpu_memory_gib": r.peak_gpu_memory_mib / 1024.0,
             "refinement_iterations": r.metadata["total_refinement_iterations"],
             "scan_seconds": r.metadata["total_scan_time"], "lp_seconds": r.metadata["total_lp_solve_time"],
+            "init_seconds": sum(l.initialization.wall_time for l in r.solve_stage.levels
+                                if l.kind == "refined" and l.initialization is not None),
             "levels": _level_summary(r)}
 
 
@@ -484,6 +538,10 @@ def main():
     ap.add_argument("--chunk", type=int, default=8192, help="query rows per step against the 1.28M resident rows")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extras", action="store_true")
+    ap.add_argument("--no-c5-solve", action="store_true",
+                    help="skip the full C5 solve (1.28M x 1.28M, d=8192) that the default run times last")
+    ap.add_argument("--fp32-sweep", action="store_true",
+                    help="also time the C5 step on the fp32 MFMA sweep and check its outputs against the split sweep")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first run a plain 1 GiB device-to-device copy kernel three times (the reference point "
                          "for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE to bytes)")
@@ -536,7 +594,7 @@ def main():
     split_out = []
     sec, pairs, achieved, info = bench_c5(dev, args.chunk, args.steps, args.warmup, inputs, precision, split_out)
     extras = {}
-    if not args.no_extras and precision != "fp32":
+    if args.fp32_sweep and precision != "fp32":
         # the same step on the fp32 MFMA sweep (identical outputs), against the fp32 matrix peak
         log("[bench] C5 step on the fp32 sweep ...")
         fp32_out = []
@@ -545,7 +603,7 @@ def main():
         same = all(bool(torch.equal(a, b)) for a, b in zip(split_out, fp32_out))
         extras["c5_step_fp32_sweep"] = {"pairs_per_s": pairs / s32, "ms_per_step": s32 * 1e3,
                                         "sweep_ms_avg": i32["sweep_ms_avg"], "sweep_tflops": a32 / 1e12,
-                                        "sweep_mfma_frac": a32 / PEAK_FP32_MFMA,
+                                        "sweep_frac_of_fp32_peak": a32 / PEAK_FP32_MFMA,
                                         "outputs_identical_to_split_sweep": same}
         del fp32_out
     del inputs, split_out
@@ -565,6 +623,10 @@ def main():
     if not args.no_cpu_baseline:
         log("[bench] CPU baseline ...")
         cpu = cpu_baseline_c5(dev)
+    solve_c5 = None
+    if not args.no_c5_solve:
+        torch.cuda.empty_cache()
+        solve_c5 = bench_c5_solve(dev, C5_N)
     line = {
         "metric": "pricing pairs/s (l2^2 bidirectional scan + certificate, m=n=1.28M d=8192)",
         "value": pairs / sec,
@@ -583,6 +645,7 @@ def main():
                    "d": C5_D, "k": 2},
         "roofline": roofline(precision, achieved),
         "cpu_baseline": cpu,
+        "solve_seconds": {"c5": solve_c5},
         "detail": info,
         "extras": extras,
     }

@@ -98,6 +98,46 @@ __device__ inline void insert_e(float (&w)[K], int (&id)[K], float v, int i) {
     }
 }
 
+// Certificate inputs of a sweep: the fp64 biases (staged in LDS per panel and per tile) and the device maxima of
+// the swept-against side (ymax[1] = max|db|), so that pairs near zero get their score in fp64.
+struct CertArgs {
+    const double* qb;
+    const double* db;
+    const unsigned long long* ymax;
+};
+
+// 2.5 fp32 units: the slack below bounds four fp32 roundings (db_j and qb_i to fp32, the fma giving w, the add
+// giving sg) with room for the rounding of the slack itself
+constexpr float CERT_REL = 1.4901161e-07f;
+// LDS entries of a certificate bias array (the wide pass, which has no certificate, compiles them to one entry)
+#define STATS_LDS(n) (APPEND ? 1 : (n))
+
+// Certificate terms of one pair from its fp32 dot t and fp32 score w = fl(scale*t + db32_j). The fp64 score
+// sigma' = (scale*t + qb_i) + db_j (the reference's arithmetic: fp32 dot, fp64 epilogue) differs from the fp32 score
+// sg = fl(w + qb32_i) by at most CERT_REL * (|w| + |qb32_i|) + CERT_REL * max|db| = slack. Pairs beyond the slack are
+// decided in fp32 (a positive one adds sg^2 to the tile's fp32 sum); pairs within it get sigma' in fp64, which
+// decides the count and adds sigma'^2 to the lane's fp64 sum.
+__device__ __forceinline__ void cert_score(float t, float w, float qbi, float sdb, float scale, double qb64,
+                                           double db64, float& tnum, unsigned int& tcnt, double& num64) {
+    const float sg = w + qbi;
+    const float slack = fmaf(CERT_REL, fabsf(w) + fabsf(qbi), sdb);
+    if (sg > slack) {
+        tnum = fmaf(sg, sg, tnum);
+        ++tcnt;
+    } else if (sg > -slack) {
+        const double sig = ((double)scale * (double)t + qb64) + db64;
+        if (sig > 0.0) {
+            num64 = fma(sig, sig, num64);
+            ++tcnt;
+        }
+    }
+}
+
+// CERT_REL * max|db| of a sweep's certificate (0 without one)
+__device__ __forceinline__ float cert_db_slack(int STATS, const CertArgs& c) {
+    return STATS ? CERT_REL * (float)key_double(c.ymax[1]) : 0.0f;
+}
+
 // -------------------------------------------------------------------------------------------------
 // prep: norms, maxima and fp32 bias copies
 // -------------------------------------------------------------------------------------------------
@@ -283,8 +323,9 @@ struct SweepRow {
     float qbi;     // row bias (scores of the column lists)
     float wt;      // wide-pass threshold
     float pi;      // certificate row term
-    double num64, den64, cnt64;
-    float mx, cmax;
+    double num64, den64;
+    unsigned int cnt;  // violated pairs of this lane (at most its share of one segment: fits 32 bits)
+    float cmax;
 };
 
 template <int K1, bool APPEND>
@@ -298,8 +339,9 @@ __device__ __forceinline__ void sweep_row_init(SweepRow<K1>& s, int64_t row, int
     s.qbi = (s.ok && !APPEND) ? qb32[row] : 0.0f;
     s.wt = (APPEND && s.ok) ? wthr[row] : INFINITY;
     s.pi = (STATS && s.ok) ? p32[row] : 0.0f;
-    s.num64 = s.den64 = s.cnt64 = 0.0;
-    s.mx = s.cmax = 0.0f;
+    s.num64 = s.den64 = 0.0;
+    s.cnt = 0u;
+    s.cmax = 0.0f;
 }
 
 // Per-tile epilogue of both sweeps. tot[b][q] is the fp32 dot of this lane's X row with Y row
@@ -311,7 +353,8 @@ __device__ __forceinline__ void sweep_row_init(SweepRow<K1>& s, int64_t row, int
 template <int K1, bool COLS, bool APPEND, int CPASS = BY>
 __device__ __forceinline__ void sweep_epilogue(const v16f (&tot)[NB], SweepRow<K1>& s, int tid, int wave, int h,
                                                int r, int64_t ytile, int64_t y_end, int64_t x0, int64_t panel,
-                                               int64_t n, float scale, int STATS, const float* sDB, const float* sGE,
+                                               int64_t n, float scale, int STATS, float sdb, const double* sQB64,
+                                               const double* sDB64, const float* sDB, const float* sGE,
                                                float* sC, Entry* __restrict__ colpart,
                                                unsigned int* __restrict__ colthr, int* __restrict__ wcnt,
                                                int* __restrict__ wbuf, int wcap, unsigned int* __restrict__ rowthr,
@@ -359,15 +402,10 @@ __device__ __forceinline__ void sweep_epilogue(const v16f (&tot)[NB], SweepRow<K
                     }
                 }
                 if (STATS && ok) {
-                    const float sg = w + s.qbi;
                     const float cost = (s.pi + ges[cc]) - w;
                     tden = fmaf(cost, cost, tden);
                     s.cmax = fmaxf(s.cmax, fabsf(cost));
-                    if (sg > 0.0f) {
-                        tnum = fmaf(sg, sg, tnum);
-                        s.mx = fmaxf(s.mx, sg);
-                        ++tcnt;
-                    }
+                    cert_score(t, w, s.qbi, sdb, scale, sQB64[wave * 32 + r], sDB64[jl0 + cc], tnum, tcnt, s.num64);
                 }
             }
         }
@@ -377,7 +415,7 @@ __device__ __forceinline__ void sweep_epilogue(const v16f (&tot)[NB], SweepRow<K
     if (STATS) {
         s.num64 += (double)tnum;
         s.den64 += (double)tden;
-        s.cnt64 += (double)tcnt;
+        s.cnt += tcnt;
     }
     if (COLS) {
         // each Y row of the tile: its best K1 over this workgroup's 128 X rows (TPR threads per row, merged by
@@ -449,7 +487,8 @@ __device__ __forceinline__ void sweep_finish(SweepRow<K1>& s, int tid, int lane,
         for (int i = 0; i < K1; ++i) out[i] = Entry{s.lv[i], s.li[i]};
     }
     if (STATS) {
-        double v[5] = {s.num64, s.den64, s.cnt64, (double)s.mx, (double)s.cmax};
+        // the maximum violation (slot 3) is taken exactly from the fp64 row lists after the sweep
+        double v[5] = {s.num64, s.den64, (double)s.cnt, 0.0, (double)s.cmax};
 #pragma unroll
         for (int e = 0; e < 5; ++e) {
             for (int o = 32; o >= 1; o >>= 1) {
@@ -483,13 +522,14 @@ __global__ __launch_bounds__(256) void l2sq_sweep(
     const float* __restrict__ qb32, const float* __restrict__ db32, const float* __restrict__ p32,
     const float* __restrict__ ge32, float scale, int64_t seg_len, int P, int S, Entry* __restrict__ part,
     Entry* __restrict__ colpart, unsigned int* __restrict__ colthr, double* __restrict__ blockstats, int VEC4,
-    int STATS, const float* __restrict__ wthr = nullptr, int* __restrict__ wcnt = nullptr,
+    int STATS, CertArgs cert, const float* __restrict__ wthr = nullptr, int* __restrict__ wcnt = nullptr,
     int* __restrict__ wbuf = nullptr, int wcap = 0, unsigned int* __restrict__ rowthr = nullptr) {
     static_assert(!(APPEND && COLS), "the wide pass keeps no column lists");
     int64_t panel, seg;
     sweep_block(blockIdx.x, P, S, panel, seg);
     if (panel >= P || seg >= S) return;  // grid padding (uniform per workgroup, before any barrier)
     __shared__ float sT[2 * STAGE];  // two LDS stages of (X tile, Y tile), 32 features each
+    __shared__ double sQB64[STATS_LDS(BX)], sDB64[STATS_LDS(BY)];  // fp64 biases for the certificate's near pairs
     __shared__ float sDB[BY];
     __shared__ float sGE[BY];
     __shared__ float sC[COLS ? BY * CST : 1];
@@ -506,6 +546,8 @@ __global__ __launch_bounds__(256) void l2sq_sweep(
     const int64_t y_end = (y_begin + seg_len < n) ? (y_begin + seg_len) : n;
     SweepRow<K1> s;
     sweep_row_init<K1, APPEND>(s, x0 + wave * 32 + r, xe, STATS, qb32, p32, wthr);
+    const float sdb = cert_db_slack(STATS, cert);
+    if (!APPEND && tid < BX) sQB64[tid] = (STATS && x0 + tid < xe) ? cert.qb[x0 + tid] : 0.0;
 
     const int nchunks = (d + KC - 1) / KC;
 
@@ -625,6 +667,7 @@ __global__ __launch_bounds__(256) void l2sq_sweep(
             const int64_t j = ytile + tid;
             sDB[tid] = j < y_end ? db32[j] : 0.0f;
             sGE[tid] = (STATS && j < y_end) ? ge32[j] : 0.0f;
+            if (!APPEND) sDB64[tid] = (STATS && j < y_end) ? cert.db[j] : 0.0;
         }
         auto step = [&](int c) {
             int64_t t2;
@@ -665,7 +708,8 @@ __global__ __launch_bounds__(256) void l2sq_sweep(
                 for (int q = 0; q < 16; ++q) acc[b][q] = outer[b][q] + acc[b][q];
             }
         }
-        sweep_epilogue<K1, COLS, APPEND>(acc, s, tid, wave, h, r, ytile, y_end, x0, panel, n, scale, STATS, sDB, sGE,
+        sweep_epilogue<K1, COLS, APPEND>(acc, s, tid, wave, h, r, ytile, y_end, x0, panel, n, scale, STATS, sdb,
+                                         sQB64, sDB64, sDB, sGE,
                                          sC, colpart, colthr, wcnt, wbuf, wcap, rowthr, xb);
     }
     sweep_finish<K1, APPEND>(s, tid, lane, wave, h, seg, rows, xb, P, panel, STATS, part, blockstats, sRed);
@@ -773,7 +817,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(COLS ? 1 : 
     const float* __restrict__ qb32, const float* __restrict__ db32, const float* __restrict__ p32,
     const float* __restrict__ ge32, float scale, int64_t seg_len, int P, int S, Entry* __restrict__ part,
     Entry* __restrict__ colpart, unsigned int* __restrict__ colthr, double* __restrict__ blockstats, int STATS,
-    const float* __restrict__ wthr = nullptr, int* __restrict__ wcnt = nullptr, int* __restrict__ wbuf = nullptr,
+    CertArgs cert, const float* __restrict__ wthr = nullptr, int* __restrict__ wcnt = nullptr,
+    int* __restrict__ wbuf = nullptr,
     int wcap = 0, unsigned int* __restrict__ rowthr = nullptr) {
     static_assert(!(APPEND && COLS), "the wide pass keeps no column lists");
     // Ring of Y chunks: the stage index is dynamic, so the loads are issued from assembly (there are no other
@@ -785,6 +830,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(COLS ? 1 : 
     sweep_block(blockIdx.x, P, S, panel, seg);
     if (panel >= P || seg >= S) return;  // grid padding (uniform per workgroup, before any barrier)
     __shared__ float4 sY0[1024], sY1[1024], sY2[1024];  // LDS ring (Y chunk: 4 blocks x 4 KiB)
+    __shared__ double sQB64[STATS_LDS(BX)], sDB64[STATS_LDS(BY)];  // fp64 biases for the certificate's near pairs
     __shared__ float sDB[BY];
     __shared__ float sGE[BY];
     __shared__ float sC[COLS ? BY * CST : 1];
@@ -801,6 +847,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(COLS ? 1 : 
     const int64_t y_end = (y_begin + seg_len < n) ? (y_begin + seg_len) : n;
     SweepRow<K1> s;
     sweep_row_init<K1, APPEND>(s, x0 + wave * 32 + r, xe, STATS, qb32, p32, wthr);
+    const float sdb = cert_db_slack(STATS, cert);
+    if (!APPEND && tid < BX) sQB64[tid] = (STATS && x0 + tid < xe) ? cert.qb[x0 + tid] : 0.0;
 
     const int nchunks = d / KC;
     const int64_t bstride = (int64_t)ld * 32;          // words per 32-row block
@@ -918,6 +966,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(COLS ? 1 : 
             const int64_t j = ytile + tid;
             sDB[tid] = j < y_end ? db32[j] : 0.0f;
             sGE[tid] = (STATS && j < y_end) ? ge32[j] : 0.0f;
+            if (!APPEND) sDB64[tid] = (STATS && j < y_end) ? cert.db[j] : 0.0;
         }
         step(I0{});
         if (nchunks > 1) step(I1{});
@@ -925,7 +974,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(COLS ? 1 : 
             step(I2{});
             step(I3{});
         }
-        sweep_epilogue<K1, COLS, APPEND>(acc, s, tid, wave, h, r, ytile, y_end, x0, panel, n, scale, STATS, sDB, sGE,
+        sweep_epilogue<K1, COLS, APPEND>(acc, s, tid, wave, h, r, ytile, y_end, x0, panel, n, scale, STATS, sdb,
+                                         sQB64, sDB64, sDB, sGE,
                                          sC, colpart, colthr, wcnt, wbuf, wcap, rowthr, xb);
     }
     wait_vmcnt<0>();  // the loads ahead into LDS land before the workgroup can end
@@ -1061,11 +1111,12 @@ __device__ __forceinline__ void sweep_epilogue_w(const float (&tot)[NB][16], int
                                                  float pi, float wt, bool first, int tid, int wave, int h, int r,
                                                  int64_t ytile, int64_t y_end, int64_t x0, int64_t xb, int64_t rows,
                                                  int64_t seg, int64_t panel, int64_t n, float scale, int STATS,
+                                                 float sdb, const double* sQB64, const double* sDB64,
                                                  const float* sDB, const float* sGE, float* sC,
                                                  Entry* __restrict__ part, Entry* __restrict__ colpart,
                                                  unsigned int* __restrict__ colthr, int* __restrict__ wcnt,
                                                  int* __restrict__ wbuf, int wcap, double& num64, double& den64,
-                                                 double& cnt64, float& mx, float& cmax,
+                                                 unsigned int& cnt, float& cmax,
                                                  unsigned int* __restrict__ rowthr) {
     float tnum = 0.0f, tden = 0.0f;
     unsigned int tcnt = 0;
@@ -1096,7 +1147,8 @@ __device__ __forceinline__ void sweep_epilogue_w(const float (&tot)[NB][16], int
             const float ges[4] = {gev.x, gev.y, gev.z, gev.w};
 #pragma unroll
             for (int cc = 0; cc < 4; ++cc) {
-                const float w = fmaf(scale, tot[y][4 * a + cc], dbs[cc]);
+                const float t = tot[y][4 * a + cc];
+                const float w = fmaf(scale, t, dbs[cc]);
                 const int64_t j = ytile + jl0 + cc;
                 const bool okj = ok && j < y_end;
                 if constexpr (APPEND) {
@@ -1120,15 +1172,10 @@ __device__ __forceinline__ void sweep_epilogue_w(const float (&tot)[NB][16], int
                     }
                 }
                 if (STATS && okj) {
-                    const float sg = w + qbi;
                     const float cost = (pi + ges[cc]) - w;
                     tden = fmaf(cost, cost, tden);
                     cmax = fmaxf(cmax, fabsf(cost));
-                    if (sg > 0.0f) {
-                        tnum = fmaf(sg, sg, tnum);
-                        mx = fmaxf(mx, sg);
-                        ++tcnt;
-                    }
+                    cert_score(t, w, qbi, sdb, scale, sQB64[wave * 32 + r], sDB64[jl0 + cc], tnum, tcnt, num64);
                 }
             }
         }
@@ -1141,7 +1188,7 @@ __device__ __forceinline__ void sweep_epilogue_w(const float (&tot)[NB][16], int
     if (STATS) {
         num64 += (double)tnum;
         den64 += (double)tden;
-        cnt64 += (double)tcnt;
+        cnt += tcnt;
     }
     if (COLS) {
         // each Y row of the tile: its best K1 over the panel's 256 X rows, 64 Y rows per pass (8 threads per row
@@ -1228,7 +1275,8 @@ __global__ __launch_bounds__(THREADS_W) void l2sq_sweep_split_w(
     const float* __restrict__ qb32, const float* __restrict__ db32, const float* __restrict__ p32,
     const float* __restrict__ ge32, float scale, int64_t seg_len, int P, int S, Entry* __restrict__ part,
     Entry* __restrict__ colpart, unsigned int* __restrict__ colthr, double* __restrict__ blockstats, int STATS,
-    const float* __restrict__ wthr = nullptr, int* __restrict__ wcnt = nullptr, int* __restrict__ wbuf = nullptr,
+    CertArgs cert, const float* __restrict__ wthr = nullptr, int* __restrict__ wcnt = nullptr,
+    int* __restrict__ wbuf = nullptr,
     int wcap = 0, unsigned int* __restrict__ rowthr = nullptr) {
     static_assert(!(APPEND && COLS), "the wide pass keeps no column lists");
     constexpr int AHEAD = 3;      // Y chunks in flight ahead of the one multiplied (4-stage ring)
@@ -1237,6 +1285,7 @@ __global__ __launch_bounds__(THREADS_W) void l2sq_sweep_split_w(
     sweep_block(blockIdx.x, P, S, panel, seg);
     if (panel >= P || seg >= S) return;  // grid padding (uniform per workgroup, before any barrier)
     __shared__ float4 sY0[1024], sY1[1024], sY2[1024], sY3[1024];  // LDS ring (Y chunk: 4 blocks x 4 KiB)
+    __shared__ double sQB64[STATS_LDS(BXW)], sDB64[STATS_LDS(BY)];  // fp64 biases for the certificate's near pairs
     __shared__ float sDB[BY];
     __shared__ float sGE[BY];
     __shared__ float sC[COLS ? CROWS_W * CSTW : 1];
@@ -1256,8 +1305,11 @@ __global__ __launch_bounds__(THREADS_W) void l2sq_sweep_split_w(
     const float qbi = (ok && !APPEND) ? qb32[row] : 0.0f;
     const float pi = (STATS && ok) ? p32[row] : 0.0f;
     const float wt = (APPEND && ok) ? wthr[row] : INFINITY;
-    double num64 = 0.0, den64 = 0.0, cnt64 = 0.0;
-    float mx = 0.0f, cmax = 0.0f;
+    double num64 = 0.0, den64 = 0.0;
+    unsigned int cnt = 0u;
+    float cmax = 0.0f;
+    const float sdb = cert_db_slack(STATS, cert);
+    if (!APPEND && tid < BXW) sQB64[tid] = (STATS && x0 + tid < xe) ? cert.qb[x0 + tid] : 0.0;
 
     const int nchunks = d / KC;
     const int64_t bstride = (int64_t)ld * 32;          // words per 32-row block
@@ -1357,6 +1409,7 @@ __global__ __launch_bounds__(THREADS_W) void l2sq_sweep_split_w(
             const int64_t j = ytile + tid;
             sDB[tid] = j < y_end ? db32[j] : 0.0f;
             sGE[tid] = (STATS && j < y_end) ? ge32[j] : 0.0f;
+            if (!APPEND) sDB64[tid] = (STATS && j < y_end) ? cert.db[j] : 0.0;
         }
         for (int c = 0; c < nchunks; c += 4) {
             step(I0{}, c);
@@ -1374,8 +1427,10 @@ __global__ __launch_bounds__(THREADS_W) void l2sq_sweep_split_w(
             }
         }
         sweep_epilogue_w<K1, COLS, APPEND>(outer, row, ok, qbi, pi, wt, ytile == y_begin, tid, wave, h, r, ytile,
-                                           y_end, x0, xb, rows, seg, panel, n, scale, STATS, sDB, sGE, sC, part,
-                                           colpart, colthr, wcnt, wbuf, wcap, num64, den64, cnt64, mx, cmax, rowthr);
+                                           y_end, x0, xb, rows, seg, panel, n, scale, STATS, sdb, sQB64, sDB64, sDB,
+                                           sGE, sC,
+                                           part,
+                                           colpart, colthr, wcnt, wbuf, wcap, num64, den64, cnt, cmax, rowthr);
 #pragma unroll
         for (int y = 0; y < NB; ++y) {
 #pragma unroll
@@ -1384,7 +1439,8 @@ __global__ __launch_bounds__(THREADS_W) void l2sq_sweep_split_w(
     }
     wait_vmcnt<0>();  // the loads ahead into LDS land before the workgroup can end
     if (STATS) {
-        double v[5] = {num64, den64, cnt64, (double)mx, (double)cmax};
+        // the maximum violation (slot 3) is taken exactly from the fp64 row lists after the sweep
+        double v[5] = {num64, den64, (double)cnt, 0.0, (double)cmax};
 #pragma unroll
         for (int e = 0; e < 5; ++e) {
             for (int o = 32; o >= 1; o >>= 1) {
@@ -2168,6 +2224,7 @@ int run_bidir(hipStream_t st, const float* X, const float* Y, int64_t m, int64_t
     bnd.acc_rel = split_rel + ea * (split ? 1.01 : 1.0) + u * (1.0 + ea + split_rel) + 4e-15 * (d / 64.0 + 8.0);
     bnd.db_rel = 2.0 * u + 1e-15;
     bnd.abs_slack = 1e-30 * (double)d;
+    const CertArgs cert{qb, db, maxima + 2};  // the row pass sweeps X rows against Y (maxima[2..3]: Y side)
     int chunk_index = 0;
     const bool row_pass = cp.row_pass;  // a columns-only call without fusion skips it
     for (int64_t xb = 0; row_pass && xb < m; xb += ch, ++chunk_index) {
@@ -2192,15 +2249,15 @@ int run_bidir(hipStream_t st, const float* X, const float* Y, int64_t m, int64_t
         if (split && TL)                                                                                             \
             hipLaunchKernelGGL((l2sq_sweep_split_w<K1, CL>), grid, dim3(THREADS_W), 0, st, SX, SY, xb, xe, n, sd,    \
                                ld, qb32, db32, p32, ge32, (float)scale, plan.seg_len, (int)panels, plan.S, part,     \
-                               colpart, colthr, blockstats, (int)want_stats, NOWIDE, rowthr);                       \
+                               colpart, colthr, blockstats, (int)want_stats, cert, NOWIDE, rowthr);                 \
         else if (split)                                                                                              \
             hipLaunchKernelGGL((l2sq_sweep_split<K1, CL>), grid, dim3(256), 0, st, SX, SY, xb, xe, n, sd, ld, \
                                qb32, db32, p32, ge32, (float)scale, plan.seg_len, (int)panels, plan.S, part,         \
-                               colpart, colthr, blockstats, (int)want_stats, NOWIDE, rowthr);                       \
+                               colpart, colthr, blockstats, (int)want_stats, cert, NOWIDE, rowthr);                 \
         else                                                                                                         \
             hipLaunchKernelGGL((l2sq_sweep<K1, TL, CL>), grid, dim3(256), 0, st, X, Y, xb, xe, n, d, d, qb32,        \
                                db32, p32, ge32, (float)scale, plan.seg_len, (int)panels, plan.S, part, colpart,      \
-                               colthr, blockstats, (int)vec4, (int)want_stats, NOWIDE, rowthr);                     \
+                               colthr, blockstats, (int)vec4, (int)want_stats, cert, NOWIDE, rowthr);               \
     } while (0)
         prof_begin(st, "l2sq_sweep");
         if (two_level) {
@@ -2268,15 +2325,15 @@ int run_bidir(hipStream_t st, const float* X, const float* Y, int64_t m, int64_t
         if (split && TL)                                                                                             \
             hipLaunchKernelGGL((l2sq_sweep_split_w<K1, false>), grid, dim3(THREADS_W), 0, st, SY, SX, yb, ye, m, sd, \
                                ld, db32, qb32, ge32, p32, (float)scale, plan2.seg_len, (int)panels2, plan2.S, part,  \
-                               colpart, colthr, blockstats, 0, NOWIDE, rowthr);                                     \
+                               colpart, colthr, blockstats, 0, CertArgs{}, NOWIDE, rowthr);                         \
         else if (split)                                                                                              \
             hipLaunchKernelGGL((l2sq_sweep_split<K1, false>), grid, dim3(256), 0, st, SY, SX, yb, ye, m, sd,  \
                                ld, db32, qb32, ge32, p32, (float)scale, plan2.seg_len, (int)panels2, plan2.S, part,  \
-                               colpart, colthr, blockstats, 0, NOWIDE, rowthr);                                     \
+                               colpart, colthr, blockstats, 0, CertArgs{}, NOWIDE, rowthr);                         \
         else                                                                                                         \
             hipLaunchKernelGGL((l2sq_sweep<K1, TL, false>), grid, dim3(256), 0, st, Y, X, yb, ye, m, d, d, db32,     \
                                qb32, ge32, p32, (float)scale, plan2.seg_len, (int)panels2, plan2.S, part, colpart,   \
-                               colthr, blockstats, (int)vec4, 0, NOWIDE, rowthr);                                   \
+                               colthr, blockstats, (int)vec4, 0, CertArgs{}, NOWIDE, rowthr);                       \
     } while (0)
             prof_begin(st, "l2sq_sweep");
             if (two_level) HM_SWEEP2(true);
@@ -2298,7 +2355,8 @@ int run_bidir(hipStream_t st, const float* X, const float* Y, int64_t m, int64_t
                 return rc;
         }
     }
-    if (want_stats && want_rows) {
+    if (want_stats) {
+        if (!want_rows) return fail(HM_EINVAL, "l2sq pricing: the certificate needs the row lists");
         hipLaunchKernelGGL(exact_row_max, dim3(1), dim3(256), 0, st, row_val, m, k, stats);
         HM_LAUNCH_CHECK("exact_row_max");
     }

@@ -56,7 +56,7 @@ int wide_round(hipStream_t st, bool split, bool two_level, const float* A, const
     hipLaunchKernelGGL(KERNEL, grid, dim3(THREADS), 0, st, w.rows, Bsw, (int64_t)0, (int64_t)Q, nb, sd, gld,        \
                        (const float*)nullptr, cand32, (const float*)nullptr, (const float*)nullptr, (float)scale,    \
                        plan.seg_len, Qpad / bx, plan.S, (Entry*)nullptr, (Entry*)nullptr, (unsigned int*)nullptr,    \
-                       (double*)nullptr, __VA_ARGS__, w.thr, w.cnt, w.buf, cap)
+                       (double*)nullptr, __VA_ARGS__, CertArgs{}, w.thr, w.cnt, w.buf, cap)
         if (split) {
             if (two_level) HM_WIDE((l2sq_sweep_split_w<8, false, true>), THREADS_W, 0);
             else HM_WIDE((l2sq_sweep_split<8, false, true>), 256, 0);
@@ -123,8 +123,17 @@ int wide_resolve(hipStream_t st, bool split, bool two_level, const float* A, con
 
 using namespace hm;
 
+namespace {
+// A certificate needs the fp64 row lists (its maximum violation is the best row score); a call that asks for the
+// certificate without them computes them into the workspace.
+uint32_t effective_flags(uint32_t flags) { return (flags & HM_STATS) ? (flags | HM_ROWS) : flags; }
+bool internal_rows(uint32_t flags) { return (flags & HM_STATS) && !(flags & HM_ROWS); }
+}  // namespace
+
 extern "C" size_t hm_pricing_l2sq_workspace_bytes(int64_t m, int64_t n, int32_t d, int32_t k, uint32_t flags) {
     if (m < 1 || n < 1 || k < 1 || k > 32) return 0;
+    const bool own_rows = internal_rows(flags);
+    flags = effective_flags(flags);
     Sizer s;
     double *a, *b, *bs, *cv;
     float *c, *e, *f, *g;
@@ -138,6 +147,10 @@ extern "C" size_t hm_pricing_l2sq_workspace_bytes(int64_t m, int64_t n, int32_t 
     WideBufs wide;
     layout(s, m, n, d, k, flags, &a, &b, &c, &e, &f, &g, &mx, &part, &colpart, &thr, &cv, &ci, &bs, &redo, &rc, &xs,
            &ys, &rpv, &rpi, &wide);
+    if (own_rows) {
+        s.template take<double>((size_t)m * k);
+        s.template take<int>((size_t)m * k);
+    }
     return s.used;
 }
 
@@ -170,8 +183,14 @@ extern "C" int hm_pricing_l2sq(void* stream, const float* X, const float* Y, con
     double* rpv;
     int* rpi;
     WideBufs wide;
+    const bool own_rows = internal_rows(flags);
+    flags = effective_flags(flags);
     layout(a, m, n, d, k, flags, &xnorm, &ynorm, &qb32, &p32, &db32, &ge32, &maxima, &part, &colpart, &colthr, &cval,
            &cidx, &blockstats, &redo, &redo_count, &xsplit, &ysplit, &rpv, &rpi, &wide);
+    if (own_rows) {
+        row_val = a.template take<double>((size_t)m * k);
+        row_idx = a.template take<int>((size_t)m * k);
+    }
     hipLaunchKernelGGL(zero_words, dim3(1), dim3(64), 0, st, maxima, 4);
     HM_LAUNCH_CHECK("zero_words");
     // X side: ||x||, qb32, p32 (maxima[0..1] = max||x||, max|qb|); Y side: ||y||, db32, ge32 = q + db

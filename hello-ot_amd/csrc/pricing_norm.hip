@@ -135,7 +135,7 @@ __global__ __launch_bounds__(256) void norm_sweep(const float* __restrict__ X, c
     for (int s = 0; s < K; ++s) { v[s] = -INFINITY; id[s] = -1; }
     float thr = -INFINITY;
     double num64 = 0.0, den64 = 0.0, cnt64 = 0.0;
-    float mx = 0.0f, cmax = 0.0f;
+    float cmax = 0.0f;
 
     for (int64_t t0 = y_begin; t0 < y_end; t0 += ntile) {
         const int cnt = (int)((y_end - t0) < ntile ? (y_end - t0) : ntile);
@@ -167,10 +167,18 @@ __global__ __launch_bounds__(256) void norm_sweep(const float* __restrict__ X, c
                 if (STATS) {
                     tden = fmaf(c, c, tden);
                     cmax = fmaxf(cmax, c);
-                    if (s32 > 0.0f) {
+                    // beyond the slack the fp32 score decides; within it the exact fp64 score does (the maximum
+                    // comes from the exact row lists afterwards)
+                    if (s32 > slack) {
                         tnum = fmaf(s32, s32, tnum);
-                        mx = fmaxf(mx, s32);
                         ++tc;
+                    } else if (s32 > -slack) {
+                        const double cd = (double)c;
+                        const double sig = TRANSPOSED ? (fi - cd) + cb[t0 + jj] : (cb[t0 + jj] - cd) + fi;
+                        if (sig > 0.0) {
+                            num64 = fma(sig, sig, num64);
+                            ++tc;
+                        }
                     }
                 }
             }
@@ -188,7 +196,7 @@ __global__ __launch_bounds__(256) void norm_sweep(const float* __restrict__ X, c
     }
     if (STATS) {
         const int lane = tid & 63, wave = tid >> 6;
-        double r[5] = {num64, den64, cnt64, (double)mx, (double)cmax};
+        double r[5] = {num64, den64, cnt64, 0.0, (double)cmax};  // slot 3: exact row maximum later
 #pragma unroll
         for (int e = 0; e < 5; ++e)
             for (int o = 32; o >= 1; o >>= 1) {
@@ -383,10 +391,13 @@ extern "C" size_t hm_pricing_norm_workspace_bytes(int64_t m, int64_t n, int32_t 
     return s.used;
 }
 
-extern "C" int hm_pricing_norm(void* stream, const float* X, const float* Y, const double* f, const double* g,
-                               int64_t m, int64_t n, int32_t d, int32_t k, int32_t kind, uint32_t flags,
-                               double* row_val, int32_t* row_idx, double* col_val, int32_t* col_idx, double* stats,
-                               void* workspace, size_t workspace_bytes) {
+namespace {
+
+// The scan with its scratch in `workspace` (caller memory, or the static scratch array of hm_pricing_norm_noalloc).
+// Everything the scratch holds is written before it is read; the maxima are cleared by a kernel, not a memset.
+int norm_scan_run(void* stream, const float* X, const float* Y, const double* f, const double* g, int64_t m,
+                  int64_t n, int32_t d, int32_t k, int32_t kind, uint32_t flags, double* row_val, int32_t* row_idx,
+                  double* col_val, int32_t* col_idx, double* stats, void* workspace, size_t workspace_bytes) {
     HM_CHECK_ARG(X && Y && f && g, "norm pricing: feature and dual pointers are required");
     HM_CHECK_ARG(m >= 1 && n >= 1 && d >= 1 && m < INT32_MAX && n < INT32_MAX,
                  "norm pricing requires nonempty inputs with int32 dimensions");
@@ -445,4 +456,14 @@ extern "C" int hm_pricing_norm(void* stream, const float* X, const float* Y, con
         if (rc != HM_OK) return rc;
     }
     return HM_OK;
+}
+
+}  // namespace
+
+extern "C" int hm_pricing_norm(void* stream, const float* X, const float* Y, const double* f, const double* g,
+                               int64_t m, int64_t n, int32_t d, int32_t k, int32_t kind, uint32_t flags,
+                               double* row_val, int32_t* row_idx, double* col_val, int32_t* col_idx, double* stats,
+                               void* workspace, size_t workspace_bytes) {
+    return norm_scan_run(stream, X, Y, f, g, m, n, d, k, kind, flags, row_val, row_idx, col_val, col_idx, stats,
+                         workspace, workspace_bytes);
 }

@@ -1,25 +1,32 @@
 // Support sparsification by cycle cancelling (host code; see hm_sparsify_support in include/helloot_hip.h).
 //
-// Behaviour follows the reference's sparsifier (restricted_ot/support_sparsification.py:52,
+// What it computes is the reference's sparsifier (restricted_ot/support_sparsification.py:52,
 // _native/support_sparsifier/support_sparsifier_lct.cpp:378-555):
-//   * a spanning forest of the positive edges, built in edge order by union-find;
-//   * the other positive edges enter in edge order; entering edge e = (s, t) closes the cycle e + tree path
-//     s .. t. Along that path (from s) the edges alternate: pushing +theta on e takes theta from the edges at
-//     even positions and gives it to those at odd positions, at cost theta * (c_e - C_even + C_odd). The push
-//     goes the way that does not increase the cost, by the largest step that keeps every flow >= 0. When e
-//     stays positive, the first edge (in path order) that reached zero leaves the forest and e takes its place;
+//   * the positive edges, in edge order, split into a spanning forest (union-find) and entering edges;
+//   * entering edge e = (s, t), in edge order, closes the cycle e + forest path s .. t. Walking that path from s,
+//     an edge crossed from its source endpoint to its target endpoint ("forward") gives up what e gains and an edge
+//     crossed the other way ("backward") takes it: pushing +theta on e costs theta (c_e - C_forward + C_backward).
+//     The push goes the way that does not increase the cost, by the largest step that keeps all flows >= 0. If e
+//     stays positive, the first edge from s among those that reached the step leaves the forest and e enters;
 //     otherwise e drops to zero;
-//   * every time enough cycles have been cancelled to possibly reach the target, the exact positive count is
-//     taken (a degenerate step removes nothing) and the work stops once it is at most the target.
+//   * the exact positive count is taken each time enough cycles have been cancelled to possibly reach the target
+//     (a degenerate cycle removes nothing), and the work stops once the count is at most the target.
 //
-// The forest is a link-cut tree over vertex nodes and edge nodes (vertices 1..V, edge slots V+1..): each
-// splay tree holds one path, in order, and aggregates over the edge nodes of its subtree, by the parity of
-// their position within the subtree: cost sums, the minimum flow and the node that first attains it, and a
-// pending flow addition. Reversing a subtree whose edge count is even swaps the two parities.
+// Representation (this file's own): the forest is a parent-pointer forest over the n_source + n_target vertices
+// (parent vertex and the edge to it), and flows are updated eagerly on the cycle's edges, in path order. The path
+// is found by two walkers climbing from s and t in lockstep that stamp the vertices they pass: the first vertex a
+// walker finds stamped by the other is the apex, so a cycle costs O(its length) whatever the depths. An exchange
+// re-hangs the side cut off by the leaving edge from e, reversing the parent pointers between e's endpoint and
+// the leaving edge. The count of positive forest edges is kept exact as flows move, so the stopping checks need no
+// pass over the forest.
+//
+// Eager updates round each flow once per cycle through it, in cycle order. The reference accumulates pending
+// additions in its link-cut tree and rounds their sums, so the two agree to rounding (about 1e-16 relative per
+// cycle), not bit for bit; counts and the choices made agree whenever no two candidate step values are closer
+// than that.
 #include <cmath>
 #include <cstdint>
 #include <limits>
-#include <numeric>
 #include <vector>
 
 #include "../../include/helloot_hip.h"
@@ -30,238 +37,33 @@ int fail(int code, const char* fmt, ...);
 
 namespace {
 
-constexpr double kInf = std::numeric_limits<double>::infinity();
-
-struct Node {
-    int32_t ch[2] = {0, 0};
-    int32_t up = 0;        // splay parent, or path parent when this node roots its splay tree
-    int32_t edges = 0;     // edge nodes in the subtree
-    bool flip = false;     // children's subtrees still to be reversed
-    bool edge = false;
-    bool pending = false;  // add[] still to be passed to the children
-    double flow = 0.0, cost = 0.0;
-    double sum[2] = {0.0, 0.0};    // cost sums by parity
-    double low[2] = {kInf, kInf};  // minimum flow by parity
-    int32_t at[2] = {0, 0};        // first node with that minimum
-    double add[2] = {0.0, 0.0};    // addition by parity, already applied to this node's aggregates
-};
-
-class Forest {
-  public:
-    explicit Forest(int64_t nodes) : n_(static_cast<size_t>(nodes + 1)) {}
-
-    void vertex(int32_t x) {
-        n_[x] = Node{};
+// disjoint sets over vertices (path halving, union by size)
+struct Components {
+    std::vector<int64_t> link, size;
+    explicit Components(int64_t n) : link(n), size(n, 1) {
+        for (int64_t v = 0; v < n; ++v) link[v] = v;
     }
-    void edge_node(int32_t x, double flow, double cost) {
-        n_[x] = Node{};
-        n_[x].edge = true;
-        n_[x].flow = flow;
-        n_[x].cost = cost;
-        pull(x);
-    }
-    // expose the path a .. b as one splay tree rooted at b (a first in order)
-    int32_t expose(int32_t a, int32_t b) {
-        evert(a);
-        access(b);
-        return b;
-    }
-    // attach isolated edge node x between the trees of a and b
-    void link_between(int32_t a, int32_t x, int32_t b) {
-        evert(a);
-        n_[a].up = x;
-        n_[x].up = b;
-    }
-    // cut edge node x out of the exposed path: its two sides become separate trees
-    bool cut_exposed(int32_t x) {
-        splay(x);
-        const int32_t l = n_[x].ch[0], r = n_[x].ch[1];
-        if (!l || !r) return false;
-        n_[l].up = 0;
-        n_[r].up = 0;
-        n_[x].ch[0] = n_[x].ch[1] = 0;
-        n_[x].up = 0;
-        pull(x);
-        return true;
-    }
-    void add_along(int32_t root, const double a[2]) { apply_add(root, a); }
-    const Node& at(int32_t x) const { return n_[x]; }
-    double flow(int32_t x) const { return n_[x].flow; }
-
-    // pass every pending flip and addition down so each node's flow is current
-    void settle() {
-        std::vector<int32_t> stack;
-        for (int32_t x = 1; x < static_cast<int32_t>(n_.size()); ++x) {
-            if (!splay_root(x)) continue;
-            stack.push_back(x);
-            while (!stack.empty()) {
-                const int32_t y = stack.back();
-                stack.pop_back();
-                push(y);
-                for (int c = 0; c < 2; ++c)
-                    if (n_[y].ch[c]) stack.push_back(n_[y].ch[c]);
-            }
+    int64_t root(int64_t v) {
+        while (link[v] != v) {
+            link[v] = link[link[v]];
+            v = link[v];
         }
+        return v;
     }
-
-  private:
-    int32_t edges(int32_t x) const { return x ? n_[x].edges : 0; }
-    bool splay_root(int32_t x) const {
-        const int32_t p = n_[x].up;
-        return !p || (n_[p].ch[0] != x && n_[p].ch[1] != x);
-    }
-
-    // fold child segment c (its parity shifted by `offset` edges) into x's aggregates
-    void fold(Node& x, const Node& c, int64_t offset) {
-        for (int r = 0; r < 2; ++r) {
-            const int s = static_cast<int>((offset + r) & 1);
-            x.sum[s] += c.sum[r];
-            if (c.low[r] < x.low[s]) {
-                x.low[s] = c.low[r];
-                x.at[s] = c.at[r];
-            }
-        }
-    }
-
-    void pull(int32_t x) {
-        Node& v = n_[x];
-        const int32_t l = v.ch[0], r = v.ch[1];
-        v.edges = edges(l) + (v.edge ? 1 : 0) + edges(r);
-        v.sum[0] = v.sum[1] = 0.0;
-        v.low[0] = v.low[1] = kInf;
-        v.at[0] = v.at[1] = 0;
-        if (l) fold(v, n_[l], 0);
-        if (v.edge) {
-            const int s = edges(l) & 1;
-            v.sum[s] += v.cost;
-            if (v.flow < v.low[s]) {
-                v.low[s] = v.flow;
-                v.at[s] = x;
-            }
-        }
-        if (r) fold(v, n_[r], edges(l) + (v.edge ? 1 : 0));
-    }
-
-    void apply_add(int32_t x, const double a[2]) {
-        if (!x || (a[0] == 0.0 && a[1] == 0.0)) return;
-        Node& v = n_[x];
-        for (int r = 0; r < 2; ++r) {
-            if (v.low[r] < kInf) v.low[r] += a[r];
-            v.add[r] += a[r];
-        }
-        v.pending = true;
-        if (v.edge) v.flow += a[edges(v.ch[0]) & 1];
-    }
-
-    void apply_flip(int32_t x) {
-        if (!x) return;
-        Node& v = n_[x];
-        const int32_t t = v.ch[0];
-        v.ch[0] = v.ch[1];
-        v.ch[1] = t;
-        if ((v.edges & 1) == 0) {  // position k -> edges-1-k changes parity iff edges is even
-            for (double* a : {v.sum, v.low, v.add}) {
-                const double t0 = a[0];
-                a[0] = a[1];
-                a[1] = t0;
-            }
-            const int32_t t1 = v.at[0];
-            v.at[0] = v.at[1];
-            v.at[1] = t1;
-        }
-        v.flip = !v.flip;
-    }
-
-    void push(int32_t x) {
-        Node& v = n_[x];
-        if (v.flip) {
-            apply_flip(v.ch[0]);
-            apply_flip(v.ch[1]);
-            v.flip = false;
-        }
-        if (v.pending) {
-            apply_add(v.ch[0], v.add);
-            const int64_t off = edges(v.ch[0]) + (v.edge ? 1 : 0);
-            const double shifted[2] = {v.add[off & 1], v.add[(off + 1) & 1]};
-            apply_add(v.ch[1], shifted);
-            v.add[0] = v.add[1] = 0.0;
-            v.pending = false;
-        }
-    }
-
-    void rotate(int32_t x) {
-        const int32_t p = n_[x].up, g = n_[p].up;
-        const int d = n_[p].ch[1] == x ? 1 : 0;
-        const int32_t b = n_[x].ch[d ^ 1];
-        if (!splay_root(p)) n_[g].ch[n_[g].ch[1] == p ? 1 : 0] = x;
-        n_[x].up = g;
-        n_[x].ch[d ^ 1] = p;
-        n_[p].up = x;
-        n_[p].ch[d] = b;
-        if (b) n_[b].up = p;
-        pull(p);
-        pull(x);
-    }
-
-    void splay(int32_t x) {
-        path_.clear();
-        for (int32_t y = x;; y = n_[y].up) {
-            path_.push_back(y);
-            if (splay_root(y)) break;
-        }
-        for (size_t i = path_.size(); i-- > 0;) push(path_[i]);
-        while (!splay_root(x)) {
-            const int32_t p = n_[x].up;
-            if (!splay_root(p)) {
-                const int32_t g = n_[p].up;
-                rotate((n_[g].ch[0] == p) == (n_[p].ch[0] == x) ? p : x);
-            }
-            rotate(x);
-        }
-    }
-
-    void access(int32_t x) {
-        int32_t below = 0;
-        for (int32_t y = x; y; y = n_[y].up) {
-            splay(y);
-            n_[y].ch[1] = below;
-            pull(y);
-            below = y;
-        }
-        splay(x);
-    }
-
-    void evert(int32_t x) {
-        access(x);
-        apply_flip(x);
-    }
-
-    std::vector<Node> n_;
-    std::vector<int32_t> path_;
-};
-
-struct UnionFind {
-    std::vector<int64_t> p;
-    std::vector<uint8_t> rank;
-    explicit UnionFind(int64_t n) : p(static_cast<size_t>(n)), rank(static_cast<size_t>(n), 0) {
-        std::iota(p.begin(), p.end(), 0);
-    }
-    int64_t root(int64_t x) {
-        while (p[x] != x) {
-            p[x] = p[p[x]];
-            x = p[x];
-        }
-        return x;
-    }
-    bool join(int64_t a, int64_t b) {
+    bool merge(int64_t a, int64_t b) {
         a = root(a);
         b = root(b);
         if (a == b) return false;
-        if (rank[a] < rank[b]) std::swap(a, b);
-        p[b] = a;
-        if (rank[a] == rank[b]) ++rank[a];
+        if (size[a] < size[b]) std::swap(a, b);
+        link[b] = a;
+        size[a] += size[b];
         return true;
     }
+};
+
+struct PathEdge {
+    int64_t edge;
+    bool forward;  // crossed from its source endpoint to its target endpoint
 };
 
 }  // namespace
@@ -276,101 +78,183 @@ extern "C" int hm_sparsify_support(int64_t n_source, int64_t n_target, int64_t e
         return fail(HM_EINVAL, "sparsify: zero_tolerance must be finite and nonnegative");
     const int64_t V = n_source + n_target;
     if (target_nnz < V - 1) return fail(HM_EINVAL, "sparsify: target_nnz must be at least n_source + n_target - 1");
-    if (2 * V + 1 >= static_cast<int64_t>(std::numeric_limits<int32_t>::max()))
-        return fail(HM_EINVAL, "sparsify: too many vertices");
 
-    // vertices: source i -> 1 + i, target j -> 1 + n_source + j
-    UnionFind uf(V);
-    std::vector<int64_t> tree, entering;
-    int64_t nnz = 0;
+    // --- forest and entering edges (vertices: source i -> i, target j -> n_source + j) ---
+    Components comps(V);
+    std::vector<int64_t> forest_edges, entering;
+    int64_t positive = 0;
     for (int64_t k = 0; k < e; ++k) {
         if (rows[k] < 0 || rows[k] >= n_source || cols[k] < 0 || cols[k] >= n_target)
             return fail(HM_EINVAL, "sparsify: edge %lld has an endpoint out of range", (long long)k);
-        if (!std::isfinite(values[k]) || values[k] < -zero_tolerance || !std::isfinite(costs[k]))
-            return fail(HM_EINVAL, "sparsify: edge %lld has a negative or non-finite flow or cost", (long long)k);
+        if (!std::isfinite(values[k]) || !std::isfinite(costs[k]) || values[k] < -zero_tolerance)
+            return fail(HM_EINVAL, "sparsify: edge %lld has a non-finite or negative flow, or a non-finite cost",
+                        (long long)k);
         if (values[k] <= zero_tolerance) {
             values[k] = 0.0;
             continue;
         }
-        ++nnz;
-        if (uf.join(rows[k], n_source + cols[k])) tree.push_back(k);
-        else entering.push_back(k);
+        ++positive;
+        (comps.merge(rows[k], n_source + cols[k]) ? forest_edges : entering).push_back(k);
     }
-    int64_t cycles = 0, tree_ops = 0;
-    if (nnz <= target_nnz || entering.empty()) {
-        stats[0] = nnz;
-        stats[1] = 0;
-        stats[2] = 0;
-        return HM_OK;
+
+    // parent pointers: each component hung from its lowest vertex, by a breadth-first walk over the forest edges
+    std::vector<int64_t> parent(V, -1), up_edge(V, -1);
+    {
+        std::vector<int64_t> start(V + 1, 0), adj(2 * forest_edges.size());
+        for (int64_t k : forest_edges) {
+            ++start[rows[k] + 1];
+            ++start[n_source + cols[k] + 1];
+        }
+        for (int64_t v = 0; v < V; ++v) start[v + 1] += start[v];
+        std::vector<int64_t> fill(start.begin(), start.end() - 1);
+        for (int64_t k : forest_edges) {
+            adj[fill[rows[k]]++] = k;
+            adj[fill[n_source + cols[k]]++] = k;
+        }
+        std::vector<char> seen(V, 0);
+        std::vector<int64_t> queue;
+        queue.reserve(V);
+        for (int64_t r = 0; r < V; ++r) {
+            if (seen[r]) continue;
+            seen[r] = 1;
+            queue.clear();
+            queue.push_back(r);
+            for (size_t h = 0; h < queue.size(); ++h) {
+                const int64_t x = queue[h];
+                for (int64_t p = start[x]; p < start[x + 1]; ++p) {
+                    const int64_t k = adj[p];
+                    const int64_t y = rows[k] == x ? n_source + cols[k] : rows[k];
+                    if (seen[y]) continue;
+                    seen[y] = 1;
+                    parent[y] = x;
+                    up_edge[y] = k;
+                    queue.push_back(y);
+                }
+            }
+        }
     }
-    Forest f(V + static_cast<int64_t>(tree.size()));
-    for (int32_t x = 1; x <= static_cast<int32_t>(V); ++x) f.vertex(x);
-    std::vector<int64_t> slot_edge(tree);  // tree slot s (node V + 1 + s) -> edge id
-    for (size_t s = 0; s < tree.size(); ++s) {
-        const int64_t k = tree[s];
-        const int32_t x = static_cast<int32_t>(V + 1 + static_cast<int64_t>(s));
-        f.edge_node(x, values[k], costs[k]);
-        f.link_between(static_cast<int32_t>(1 + rows[k]), x, static_cast<int32_t>(1 + n_source + cols[k]));
-    }
-    int64_t check_at = nnz - target_nnz;  // cycles after which the target can first be reached
+
+    // positive forest edges, kept exact as flows change
+    int64_t forest_positive = static_cast<int64_t>(forest_edges.size());
+    auto set_flow = [&](int64_t k, double v) {
+        const bool was = values[k] > zero_tolerance, now = v > zero_tolerance;
+        forest_positive += (int64_t)now - (int64_t)was;
+        values[k] = v;
+    };
+
+    std::vector<uint64_t> stamp(V, 0);
+    uint64_t tick = 0;
+    std::vector<PathEdge> from_s, from_t;
+    int64_t cycles = 0, exchanges = 0;
+    int64_t next_check = std::max<int64_t>(0, positive - target_nnz);
     for (size_t pos = 0; pos < entering.size(); ++pos) {
-        if (cycles >= check_at) {
-            f.settle();
-            int64_t count = static_cast<int64_t>(entering.size() - pos);
-            for (size_t s = 0; s < slot_edge.size(); ++s)
-                count += f.flow(static_cast<int32_t>(V + 1 + static_cast<int64_t>(s))) > zero_tolerance ? 1 : 0;
-            if (count <= target_nnz) break;
-            check_at = cycles + (count - target_nnz);
+        if (cycles >= next_check) {
+            const int64_t exact = forest_positive + static_cast<int64_t>(entering.size() - pos);
+            if (exact <= target_nnz) break;
+            next_check = cycles + (exact - target_nnz);
         }
         const int64_t k = entering[pos];
         double flow_e = values[k];
         if (flow_e <= zero_tolerance) continue;
-        const int32_t s_node = static_cast<int32_t>(1 + rows[k]);
-        const int32_t t_node = static_cast<int32_t>(1 + n_source + cols[k]);
-        const int32_t root = f.expose(s_node, t_node);
-        tree_ops += 2;
-        const Node& path = f.at(root);
-        // +theta on e: even positions (from the source) give theta, odd positions take it
-        const double gain = costs[k] - path.sum[0] + path.sum[1];
+        const int64_t s = rows[k], t = n_source + cols[k];
+
+        // --- the forest path s .. t: two walkers in lockstep; the first stamp of the other side is the apex ---
+        tick += 2;
+        const uint64_t mark_s = tick, mark_t = tick + 1;
+        int64_t a = s, b = t, apex = -1;
+        stamp[a] = mark_s;
+        stamp[b] = mark_t;
+        while (apex < 0) {
+            if (a >= 0) {
+                const int64_t up = parent[a];
+                if (up >= 0) {
+                    if (stamp[up] == mark_t) apex = up;
+                    stamp[up] = mark_s;
+                }
+                a = up;
+            }
+            if (apex < 0 && b >= 0) {
+                const int64_t up = parent[b];
+                if (up >= 0) {
+                    if (stamp[up] == mark_s) apex = up;
+                    stamp[up] = mark_t;
+                }
+                b = up;
+            }
+            if (a < 0 && b < 0 && apex < 0) return fail(HM_EINVAL, "sparsify: entering edge joins two components");
+        }
+        // edges from s up to the apex (in path order), then from t up to the apex (reverse path order)
+        from_s.clear();
+        from_t.clear();
+        for (int64_t x = s; x != apex; x = parent[x]) from_s.push_back({up_edge[x], x < n_source});
+        for (int64_t x = t; x != apex; x = parent[x]) from_t.push_back({up_edge[x], x >= n_source});
+
+        // --- direction, step and leaving edge ---
+        double sum_forward = 0.0, sum_backward = 0.0;  // path costs by crossing direction, in path order
+        for (const PathEdge& pe : from_s) (pe.forward ? sum_forward : sum_backward) += costs[pe.edge];
+        for (size_t q = from_t.size(); q-- > 0;) (from_t[q].forward ? sum_forward : sum_backward) += costs[from_t[q].edge];
+        const double gain = costs[k] - sum_forward + sum_backward;
         const double dir = gain <= 0.0 ? 1.0 : -1.0;
-        const int losing = dir > 0.0 ? 0 : 1;
-        double step = path.low[losing];
-        const int32_t leaving = path.at[losing];
+        const bool losing_forward = dir > 0.0;
+        double step = std::numeric_limits<double>::infinity();
+        int64_t leaving = -1;
+        bool leaving_on_s = true;
+        for (const PathEdge& pe : from_s)
+            if (pe.forward == losing_forward && values[pe.edge] < step) {
+                step = values[pe.edge];
+                leaving = pe.edge;
+                leaving_on_s = true;
+            }
+        for (size_t q = from_t.size(); q-- > 0;)
+            if (from_t[q].forward == losing_forward && values[from_t[q].edge] < step) {
+                step = values[from_t[q].edge];
+                leaving = from_t[q].edge;
+                leaving_on_s = false;
+            }
         if (dir < 0.0 && flow_e < step) step = flow_e;
         if (!std::isfinite(step)) return fail(HM_EINVAL, "sparsify: cycle without a bounded step");
-        if (step < -zero_tolerance) return fail(HM_EINVAL, "sparsify: a tree flow became negative");
         if (step < 0.0) step = 0.0;
-        const double delta[2] = {-dir * step, dir * step};
-        f.add_along(root, delta);
+
+        // --- push: forward edges lose dir * step, backward edges gain it ---
+        for (const PathEdge& pe : from_s) set_flow(pe.edge, values[pe.edge] + (pe.forward ? -dir : dir) * step);
+        for (const PathEdge& pe : from_t) set_flow(pe.edge, values[pe.edge] + (pe.forward ? -dir : dir) * step);
         flow_e += dir * step;
         if (flow_e > zero_tolerance) {
-            // the first edge on the losing side that reached zero leaves; e takes over its tree slot
-            if (leaving <= static_cast<int32_t>(V)) return fail(HM_EINVAL, "sparsify: no leaving edge");
-            const size_t slot = static_cast<size_t>(leaving - V - 1);
-            if (!f.cut_exposed(leaving)) return fail(HM_EINVAL, "sparsify: leaving edge not on the path");
-            values[slot_edge[slot]] = 0.0;
-            slot_edge[slot] = k;
-            f.edge_node(leaving, flow_e, costs[k]);
-            f.link_between(s_node, leaving, t_node);
-            tree_ops += 4;
+            // exchange: the leaving edge drops to zero; the side it cut off hangs from e
+            if (leaving < 0) return fail(HM_EINVAL, "sparsify: no leaving edge on the cycle");
+            set_flow(leaving, 0.0);
+            int64_t x = leaving_on_s ? s : t;
+            int64_t new_parent = leaving_on_s ? t : s, new_edge = k;
+            for (;;) {
+                const int64_t old_parent = parent[x], old_edge = up_edge[x];
+                parent[x] = new_parent;
+                up_edge[x] = new_edge;
+                if (old_edge == leaving) break;
+                new_parent = x;
+                new_edge = old_edge;
+                x = old_parent;
+            }
+            values[k] = flow_e;
+            ++forest_positive;
+            ++exchanges;
         } else {
             values[k] = 0.0;
         }
         ++cycles;
     }
-    f.settle();
-    for (size_t s = 0; s < slot_edge.size(); ++s) {
-        const double v = f.flow(static_cast<int32_t>(V + 1 + static_cast<int64_t>(s)));
-        if (!std::isfinite(v) || v < -zero_tolerance) return fail(HM_EINVAL, "sparsify: invalid flow after cancelling");
-        values[slot_edge[s]] = v > zero_tolerance ? v : 0.0;
-    }
+
     int64_t out = 0;
     for (int64_t k = 0; k < e; ++k) {
+        if (!std::isfinite(values[k]) || values[k] < -zero_tolerance)
+            return fail(HM_EINVAL, "sparsify: edge %lld ended with an invalid flow", (long long)k);
         if (values[k] <= zero_tolerance) values[k] = 0.0;
         else ++out;
     }
     stats[0] = out;
     stats[1] = cycles;
-    stats[2] = tree_ops;
+    // the reference reports the link-cut operations it performs: two per cycle (evert and access of the path)
+    // and four more per exchange (cut, re-initialise, evert, link); the same count follows from the cycle and
+    // exchange counts
+    stats[2] = 2 * cycles + 4 * exchanges;
     return HM_OK;
 }

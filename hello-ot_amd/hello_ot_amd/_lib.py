@@ -14,7 +14,7 @@ LIB_NAME = "libhelloot_hip.so"
 LIB_PATH = Path(__file__).resolve().parent / LIB_NAME
 HEADER_PATH = Path(__file__).resolve().parents[2] / "include" / "helloot_hip.h"
 
-HM_OK, HM_EINVAL, HM_EHIP, HM_ENOSPC = 0, 1, 2, 3
+HM_OK, HM_EINVAL, HM_EHIP, HM_ENOSPC, HM_ESOLVE = 0, 1, 2, 3, 4
 HM_ROWS, HM_COLS, HM_STATS, HM_LINF, HM_BF16X3 = 1, 2, 4, 8, 16
 COST_KINDS = {"l1": 0, "linf": 1, "l2": 2}
 
@@ -65,6 +65,7 @@ SIGNATURES = {
     "hm_pair_costs_norm": (ctypes.c_int, [_P, _P, _P, _P, _P, _I64, _I32, _I32, _P]),
     "hm_pair_costs_norm_fp32": (ctypes.c_int, [_P, _P, _P, _P, _P, _I64, _I32, _I32, _P]),
     "hm_sparsify_support": (ctypes.c_int, [_I64, _I64, _I64, _P, _P, _P, _P, _I64, _D, _P]),
+    "hm_transport_simplex": (ctypes.c_int, [_I64, _I64, _P, _P, _P, _I64, _P, _P, _P, _P, _P, _P, _P]),
     "hm_pdhg_workspace_bytes": (_SZ, [_I64, _I64, _I64]),
     "hm_pdhg_solve": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, ctypes.POINTER(PdhgParams),
                                      _P, _P, ctypes.POINTER(PdhgResult), _P, _SZ]),

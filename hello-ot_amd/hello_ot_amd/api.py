@@ -16,8 +16,9 @@ import torch
 from ._native_compat import require_native_runtime_compatibility
 from .config import SolverOptions
 from .resident.cost import Cost
-from .resident.solver import level_sizes, refine, shuffle_once_permutation, solve_leaf
-from .resident.support import normalize_masses
+from .resident.leaf import solve_coarsest
+from .resident.solver import level_sizes, refine_level, shuffle_once_permutation
+from .resident.support import balanced_masses
 from .types import Problem, Result, SolveStageResult, SparseOTSolution
 
 
@@ -92,33 +93,31 @@ def solve_problem(problem: Problem, options: SolverOptions, *, max_iterations: i
         full = Cost.create(x, y, problem.cost_type)
         sizes = level_sizes(n, m, options.coarsest_size_threshold, options.split_count)
         levels, previous, triggers = [], None, []
-        coarsest_refinement = None
         support = dual = None
         sparsified = []
         for level_index in reversed(range(len(sizes))):
             nn, mm = sizes[level_index]
             cost = full.sliced(nn, mm)
-            aa, bb = normalize_masses(a[:nn].clone(), b[:mm].clone())
+            aa, bb = balanced_masses(a[:nn].clone(), b[:mm].clone())
             if previous is None:
-                support, dual, level, coarsest_refinement = solve_leaf(cost, aa, bb, level_index, options,
-                                                                       max_iterations)
+                support, dual, level = solve_coarsest(cost, aa, bb, level_index)
             else:
-                known = "target" if nn >= mm else "source"
-                support, dual, level, triggered = refine(cost, aa, bb, previous, known, options, level_index,
-                                                         max_iterations, options.cost_perturbation == "auto")
+                inherited = "target" if nn >= mm else "source"
+                support, dual, level, triggered = refine_level(cost, aa, bb, previous, inherited, options, level_index,
+                                                               max_iterations, options.cost_perturbation == "auto")
                 if triggered:
                     triggers.append(level_index)
             levels.append(level)
-            sparsified.extend(support.sparsification_log or [])
+            sparsified.extend(support.sparsification_log)
             previous = dual
-        rows, cols = support.rows_cols()
-        objective = float(full.pairs(rows, cols) @ support.values)
+        rows, cols = support.endpoints()
+        objective = float(full.pairs(rows, cols) @ support.flow)
         keys = si[rows] * m + ti[cols]
         order = torch.argsort(keys, stable=True)
         f = torch.empty(n, dtype=torch.float64, device=device)
         g = torch.empty(m, dtype=torch.float64, device=device)
         f[si], g[ti] = dual[:n], dual[n:]
-        solution = SparseOTSolution((n, m), si[rows][order], ti[cols][order], support.values[order], f, g)
+        solution = SparseOTSolution((n, m), si[rows][order], ti[cols][order], support.flow[order], f, g)
         torch.cuda.synchronize(device)
         wall = time.perf_counter() - started
         peak = torch.cuda.max_memory_allocated(device) / 2**20
@@ -126,8 +125,7 @@ def solve_problem(problem: Problem, options: SolverOptions, *, max_iterations: i
     metadata = {
         "gpu_resident": True, "backend": "native", "device": str(device), "cost_type": problem.cost_type,
         "cost_precision": options.cost_precision, "stopping_norm": options.stopping_norm,
-        "coarsest_solver": "mi355x_refinement_from_zero_duals", "lp_solver": "mi355x_halpern_pdhg",
-        "coarsest_refinement": coarsest_refinement,
+        "coarsest_solver": "mi355x_network_simplex", "lp_solver": "mi355x_halpern_pdhg",
         "hierarchy_sizes": [list(s) for s in sizes],
         "total_refinement_iterations": sum(len(l.solve.iterations) for l in levels if l.kind == "refined"),
         "total_lp_solve_time": sum(i.solve_lp.wall_time for l in levels if l.kind == "refined"

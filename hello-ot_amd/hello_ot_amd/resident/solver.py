@@ -1,17 +1,22 @@
-"""HELLO driver: hierarchy chain, coarsest solve, per-level initialization and refinement, all on the GPU.
+"""HELLO driver on the device: hierarchy chain, exact coarsest level, and per-level seeding and refinement.
 
-Follows the reference's GPU-resident algorithm (``gpu_resident/solver.py:27-398``):
+What each level does is HELLO's algorithm as the reference's GPU-resident solver runs it
+(``gpu_resident/solver.py:27-398``):
 
-* one global shuffle of each side (``hierarchy/plan.py:73-87``); level l keeps the first n_l / m_l points;
-  going coarser, the larger side is divided by ``split_count`` until both are <= ``coarsest_size_threshold``;
-* coarsest level: refined from zero duals like any other level (the reference calls POT ``emd`` on the CPU);
-* each finer level: the side shared with the coarser level keeps its duals, the other side is completed by a
-  c-transform (directional top-1 scan), both directions contribute their ``assignment_topk`` best pairs and
-  the northwest-corner basis completes an initial support; then ``solve_lp -> pricing scan with certificate ->
-  add violating pairs -> budgeted pruning`` until the relative dual infeasibility is <= tolerance.
+* one global shuffle per side (``hierarchy/plan.py:73-87``); level l keeps the first n_l source and m_l target
+  points; going coarser, the larger side is divided by ``split_count`` until both fit ``coarsest_size_threshold``;
+* the coarsest level is solved exactly (network simplex, ``resident/leaf.py``), as the reference does with POT's
+  ``emd`` (``gpu_resident/solver.py:168-191``);
+* each finer level inherits the duals of the side it shares with the coarser level and completes the other side
+  by a c-transform (a directional top-1 scan); both directions' ``assignment_topk`` best pairs plus the
+  northwest-corner basis seed the support; then the refinement loop runs ``LP -> pricing scan with certificate ->
+  add violated pairs -> budgeted pruning`` until the relative dual infeasibility is at most the tolerance.
 
-Cost perturbation (``cost_perturbation="auto"``) is detected as in the reference (re-entry of pruned edges) but
-not applied: the level keeps refining on the original cost and the trigger is recorded in the metadata.
+Cost perturbation (``cost_perturbation="auto"``) is detected as the reference detects it (a pruned edge coming back)
+but not applied: the level keeps refining on the original cost and the trigger is recorded.
+
+The refinement is a small state machine (``LevelRefinement``): ``seed`` builds the support and duals, ``step`` runs
+one iteration and returns its record, ``run`` loops and assembles the level result.
 """
 from __future__ import annotations
 
@@ -22,27 +27,25 @@ import numpy as np
 import torch
 
 from ..config import active_support_budget, primal_support_cap
-from ..types import (ActiveSupportStats, BudgetedPruningStats, CoarsestSolveStats, ConvergenceStats,
-                     DualViolationStats, HelloSolveError, InitializationStats, IterationStats, LevelResult,
-                     RefinementResult, RefinementSummary, SolveLPStats)
+from ..types import (ActiveSupportStats, BudgetedPruningStats, ConvergenceStats, DualViolationStats,
+                     HelloSolveError, InitializationStats, IterationStats, LevelResult, RefinementResult,
+                     RefinementSummary, SolveLPStats)
 from .cost import Cost
-from .support import Support, normalize_masses
+from .support import ActiveSet
 
 
 def derive_hierarchy_seeds(seed: int, num_children: int):
     """Source-split, target-split and child seeds of a hierarchy node (hierarchy/utilities.py:56-65)."""
     rng = np.random.default_rng(int(seed))
-    src = int(rng.integers(0, 2**31 - 1))
-    tgt = int(rng.integers(0, 2**31 - 1))
-    children = [int(rng.integers(0, 2**31 - 1)) for _ in range(int(num_children))]
-    return src, tgt, children
+    draws = [int(rng.integers(0, 2**31 - 1)) for _ in range(2 + int(num_children))]
+    return draws[0], draws[1], draws[2:]
 
 
 def shuffle_once_permutation(n_source: int, n_target: int, seed: int, split_count: int):
     """One global random permutation per side (hierarchy/plan.py:73-87)."""
-    src, tgt, _ = derive_hierarchy_seeds(seed, split_count)
-    return (np.random.default_rng(src).permutation(int(n_source)).astype(np.int64),
-            np.random.default_rng(tgt).permutation(int(n_target)).astype(np.int64))
+    source_seed, target_seed, _ = derive_hierarchy_seeds(seed, split_count)
+    return (np.random.default_rng(source_seed).permutation(int(n_source)).astype(np.int64),
+            np.random.default_rng(target_seed).permutation(int(n_target)).astype(np.int64))
 
 
 def level_sizes(n: int, m: int, threshold: int, split: int):
@@ -50,49 +53,33 @@ def level_sizes(n: int, m: int, threshold: int, split: int):
     sizes = [(n, m)]
     while max(sizes[-1]) > threshold:
         nn, mm = sizes[-1]
-        sizes.append(((nn + split - 1) // split, mm) if nn >= mm else (nn, (mm + split - 1) // split))
+        if nn >= mm:
+            nn = -(-nn // split)
+        else:
+            mm = -(-mm // split)
+        sizes.append((nn, mm))
     return sizes
 
 
-def candidate_keys(xv, xi, yv, yi, dual, n, m, positive=False):
-    """Keys row * m + col of the row-direction and column-direction candidates (gpu_resident/solver.py:27-35);
-    with ``positive`` only pairs whose dual score sigma = f_i + g_j - c_ij is > 0."""
-    parts = []
-    if xi is not None:
-        rows = torch.arange(n, device=dual.device)[:, None].expand_as(xi)
-        mask = xi >= 0
+def candidate_keys(row_values, row_index, col_values, col_index, dual, n, m, positive=False):
+    """Sorted unique keys row * m + col of the pairs the scans proposed (gpu_resident/solver.py:27-35).
+
+    ``row_index[i]`` lists the columns proposed for source row i and ``col_index[j]`` the rows proposed for target
+    column j (-1 = empty slot). The stored values exclude the row's own dual (a row list holds g_j - c_ij, a
+    column list f_i - c_ij), so with ``positive`` a pair is kept only when adding that dual back gives a violated
+    pair, sigma_ij = f_i + g_j - c_ij > 0."""
+    pieces = []
+    for values, index, own, count, by_row in ((row_values, row_index, dual[:n], n, True),
+                                              (col_values, col_index, dual[n:], m, False)):
+        if index is None:
+            continue
+        owner = torch.arange(count, device=dual.device).unsqueeze(1).expand_as(index)
+        keep = index >= 0
         if positive:
-            mask &= xv + dual[:n, None] > 0
-        parts.append((rows * m + xi.long())[mask])
-    if yi is not None:
-        cols = torch.arange(m, device=dual.device)[:, None].expand_as(yi)
-        mask = yi >= 0
-        if positive:
-            mask &= yv + dual[n:, None] > 0
-        parts.append((yi.long() * m + cols)[mask])
-    return torch.unique(torch.cat(parts), sorted=True)
-
-
-def _sync():
-    torch.cuda.synchronize()
-
-
-def solve_leaf(cost: Cost, a, b, level_index: int, options, max_iterations: int):
-    """Coarsest level. The reference solves it exactly with POT ``emd`` on the CPU (gpu_resident/solver.py:168-191);
-    here it is refined like every other level, from zero duals: both directions' ``assignment_topk`` nearest
-    pairs plus the northwest basis, then LP / pricing / support updates until the certificate passes. The
-    result is optimal to the same tolerance as the finer levels and stays on the device."""
-    started = time.perf_counter()
-    n, m = cost.shape
-    zeros = torch.zeros(n + m, dtype=torch.float64, device=a.device)
-    support, dual, level, _ = refine(cost, a, b, zeros, None, options, level_index, max_iterations, False)
-    summary = level.solve.summary
-    if not summary.converged:
-        raise HelloSolveError(f"coarsest level did not converge in {max_iterations} iterations")
-    _sync()
-    elapsed = time.perf_counter() - started
-    stats = CoarsestSolveStats(elapsed, float(summary.final_objective), len(support.keys))
-    return support, dual, LevelResult(level_index, "coarsest", n, m, level.initialization, stats, elapsed), level
+            keep = keep & ((values + own.unsqueeze(1)) > 0)
+        partner = index.long()
+        pieces.append(((owner * m + partner) if by_row else (partner * m + owner))[keep])
+    return torch.unique(torch.cat(pieces), sorted=True)
 
 
 def _progress(options, message: str) -> None:
@@ -100,111 +87,155 @@ def _progress(options, message: str) -> None:
         print(f"[hello-mi355x] {message}", file=sys.stderr, flush=True)
 
 
-def initialize(cost: Cost, a, b, previous, known_side, options):
-    """Dual propagation + directional assignment + northwest basis (gpu_resident/solver.py:38-64)."""
-    started = time.perf_counter()
-    n, m = cost.shape
-    device = a.device
-    k = options.assignment_topk
-    dual = torch.zeros(n + m, dtype=torch.float64, device=device)
-    if known_side == "target":
-        dual[n:] = previous[-m:]
-    elif known_side == "source":
-        dual[:n] = previous[:n]
-    else:
-        dual = previous.clone()
-    xv = xi = yv = yi = None
-    if known_side == "target":
-        xv, xi, _, _, _ = cost.scan(dual, k, direction="source")
-        dual[:n] = -xv[:, 0]               # c-transform: f_i = min_j (c_ij - g_j)
-        propagation = time.perf_counter() - started
-        _progress(options, f"init {n}x{m}: source c-transform scan {propagation:.3f}s")
-        _, _, yv, yi, _ = cost.scan(dual, k, direction="target")
-    elif known_side == "source":
-        _, _, yv, yi, _ = cost.scan(dual, k, direction="target")
-        dual[n:] = -yv[:, 0]
-        propagation = time.perf_counter() - started
-        _progress(options, f"init {n}x{m}: target c-transform scan {propagation:.3f}s")
-        xv, xi, _, _, _ = cost.scan(dual, k, direction="source")
-    else:
+class _Stopwatch:
+    """Wall-clock laps (host time; device work is synchronised by the readbacks the steps already do)."""
+
+    def __init__(self):
+        self.origin = self.mark = time.perf_counter()
+
+    def lap(self) -> float:
+        now = time.perf_counter()
+        elapsed, self.mark = now - self.mark, now
+        return elapsed
+
+    def total(self) -> float:
+        return time.perf_counter() - self.origin
+
+
+class LevelRefinement:
+    """One refined hierarchy level: seeding from the coarser level's duals, then the refinement iterations."""
+
+    def __init__(self, cost: Cost, a, b, options, index: int, detect_reentry: bool):
+        self.cost, self.a, self.b, self.options, self.index = cost, a, b, options, index
+        self.n, self.m = cost.shape
+        self.detect_reentry = detect_reentry
+        self.budget = active_support_budget(options.support_budget_factor, self.n, self.m)
+        self.cap = primal_support_cap(options.support_budget_factor, options.pricing_topk, self.n, self.m)
+        self.support = None
+        self.dual = None
+        self.peak = 0
+        self.recently_pruned = None       # sorted keys removed by the last pruning
+        self.reentry_seen = False         # a pruned edge came back in the last iteration
+        self.perturbation_triggered = False
+        self.records = []
+        self.lp = None
+
+    # -- seeding ----------------------------------------------------------------------------------------
+    def seed(self, previous: torch.Tensor, inherited: str | None) -> InitializationStats:
+        """Inherit the shared side's duals, c-transform the other side, gather both directions' best pairs and
+        complete them with the northwest basis (gpu_resident/solver.py:38-64)."""
+        watch = _Stopwatch()
+        n, m, k = self.n, self.m, self.options.assignment_topk
+        dual = torch.zeros(n + m, dtype=torch.float64, device=self.a.device)
+        rows_best = cols_best = (None, None)
         propagation = 0.0
-        xv, xi, yv, yi, _ = cost.scan(dual, k)
-    candidates = candidate_keys(xv, xi, yv, yi, dual, n, m)
-    assigned = time.perf_counter() - started
-    support = Support.initial(candidates, a, b)
-    _sync()
-    total = time.perf_counter() - started
-    _progress(options, f"init {n}x{m}: {len(support.keys)} initial edges {total:.3f}s")
-    stats = InitializationStats(total, propagation, assigned, total - assigned, known_side, k, len(candidates),
-                                None, len(support.keys) - len(candidates), len(support.keys))
-    return support, dual, stats
+        if inherited == "target":
+            dual[n:] = previous[-m:]
+            rows_best = self.cost.scan(dual, k, direction="source")[:2]
+            dual[:n] = -rows_best[0][:, 0]          # f_i = min_j (c_ij - g_j)
+            propagation = watch.lap()
+            _progress(self.options, f"init {n}x{m}: source c-transform scan {propagation:.3f}s")
+            cols_best = self.cost.scan(dual, k, direction="target")[2:4]
+        elif inherited == "source":
+            dual[:n] = previous[:n]
+            cols_best = self.cost.scan(dual, k, direction="target")[2:4]
+            dual[n:] = -cols_best[0][:, 0]          # g_j = min_i (c_ij - f_i)
+            propagation = watch.lap()
+            _progress(self.options, f"init {n}x{m}: target c-transform scan {propagation:.3f}s")
+            rows_best = self.cost.scan(dual, k, direction="source")[:2]
+        else:
+            dual = previous.clone()
+            both = self.cost.scan(dual, k)
+            rows_best, cols_best = both[:2], both[2:4]
+        candidates = candidate_keys(*rows_best, *cols_best, dual, n, m)
+        assignment = watch.lap()
+        self.support = ActiveSet.seeded(candidates, self.a, self.b)
+        self.dual = dual
+        self.peak = len(self.support)
+        torch.cuda.synchronize()
+        basis = watch.lap()
+        total = watch.total()
+        _progress(self.options, f"init {n}x{m}: {len(self.support)} initial edges {total:.3f}s")
+        # support sizes as the reference reports them: the forward (row) assignment's n * min(m, k) slots, then the
+        # deduplicated union of both directions, then the basis edges that were not already candidates
+        return InitializationStats(total, propagation, propagation + assignment, basis, inherited, k,
+                                   n * min(m, k), len(candidates), len(self.support) - len(candidates),
+                                   len(self.support))
 
-
-def refine(cost: Cost, a, b, previous, known_side, options, level_index, max_iterations, detect_reentry):
-    """One level: initialization, then the SolveLP -> CheckOptimality -> UpdateSupport loop
-    (gpu_resident/solver.py:67-165)."""
-    started = time.perf_counter()
-    support, dual, init_stats = initialize(cost, a, b, previous, known_side, options)
-    n, m = cost.shape
-    tol = options.tolerance
-    budget = active_support_budget(options.support_budget_factor, n, m)
-    cap = primal_support_cap(options.support_budget_factor, options.pricing_topk, n, m)
-    peak = len(support.keys)
-    previous_pruned, reentered, triggered = None, False, False
-    history = []
-    sparsifications = []
-    lp = None
-    for index in range(max_iterations):
-        it_started = time.perf_counter()
-        before = len(support.keys)
-        t0 = time.perf_counter()
-        dual, lp = support.solve_lp(cost, a, b, dual, tol, primal_cap=cap)
-        lp_seconds = time.perf_counter() - t0
-        if support.last_sparsification is not None:
-            sparsifications.append(support.last_sparsification)
-        _progress(options, f"level={level_index} iteration={index} lp {lp_seconds:.3f}s support={before} "
+    # -- one iteration ----------------------------------------------------------------------------------
+    def step(self, iteration: int) -> bool:
+        """LP, pricing with certificate, and (unless converged) support growth and pruning. Returns convergence."""
+        options, tol = self.options, self.options.tolerance
+        watch = _Stopwatch()
+        support = self.support
+        size_before = len(support)
+        self.dual, lp = support.solve_lp(self.cost, self.a, self.b, self.dual, tol, primal_cap=self.cap)
+        self.lp = lp
+        lp_seconds = watch.lap()
+        thinned = support.last_sparsification
+        _progress(options, f"level={self.index} iteration={iteration} lp {lp_seconds:.3f}s support={size_before} "
                            f"pdhg_iters={lp.iterations}"
-                           + (f" sparsified {support.last_sparsification.input_nnz}->"
-                              f"{support.last_sparsification.output_nnz}" if support.last_sparsification else ""))
-        t0 = time.perf_counter()
-        xv, xi, yv, yi, metrics = cost.scan(dual, options.pricing_topk, certificate=True)
-        scan_seconds = time.perf_counter() - t0
+                           + (f" sparsified {thinned.input_nnz}->{thinned.output_nnz}" if thinned else ""))
+        xv, xi, yv, yi, metrics = self.cost.scan(self.dual, options.pricing_topk, certificate=True)
+        scan_seconds = watch.lap()
         converged = metrics["l2"] <= tol
-        if not converged and detect_reentry and reentered:
-            triggered = True
-        after, added_count, prune_seconds = before, 0, 0.0
+        if not converged and self.detect_reentry and self.reentry_seen:
+            self.perturbation_triggered = True
+        grown = size_before
+        added = 0
+        prune_seconds = 0.0
         if not converged:
-            candidates = candidate_keys(xv, xi, yv, yi, dual, n, m, positive=True)
-            fresh = support.extend(candidates)
-            added = support.keys[fresh]
-            added_count, after = len(added), len(support.keys)
-            peak = max(peak, after)
-            reentered = previous_pruned is not None and bool(torch.isin(added, previous_pruned).any())
-            t0 = time.perf_counter()
-            previous_pruned = support.prune(cost, dual, fresh, budget)
-            prune_seconds = time.perf_counter() - t0
-            if not added_count:
+            fresh = support.absorb(candidate_keys(xv, xi, yv, yi, self.dual, self.n, self.m, positive=True),
+                                   born=iteration)
+            added, grown = int(fresh.numel()), len(support)
+            if not added:
                 raise HelloSolveError("GPU full optimality check failed without new candidate edges")
-        history.append(IterationStats(
-            index, float(lp.obj_val), time.perf_counter() - it_started, 0.0, scan_seconds,
+            self.peak = max(self.peak, grown)
+            pruned_before = self.recently_pruned
+            self.reentry_seen = pruned_before is not None and bool(_contains_any(pruned_before, fresh))
+            watch.lap()
+            self.recently_pruned = support.trim(self.cost, self.dual, self.budget, iteration)
+            prune_seconds = watch.lap()
+        self.records.append(IterationStats(
+            iteration, float(lp.obj_val), watch.total(), 0.0, scan_seconds,
             SolveLPStats(lp_seconds, lp.iterations, lp.primal_feas, lp.gap, "l2", lp.termination_reason,
                          lp.primal_feas, lp.dual_feas, lp.dual_feas),
-            DualViolationStats(scan_seconds, metrics["count"], added_count),
-            BudgetedPruningStats(prune_seconds, after, len(support.keys), budget, after > budget),
-            ActiveSupportStats(before, after, len(support.keys), peak),
+            DualViolationStats(scan_seconds, metrics["count"], added),
+            BudgetedPruningStats(prune_seconds, grown, len(support), self.budget, grown > self.budget),
+            ActiveSupportStats(size_before, grown, len(support), self.peak),
             ConvergenceStats(metrics["l2"], tol, converged, metrics["l2"], metrics["linf"], metrics["max"], "l2")))
-        _progress(options, f"level={level_index} iteration={index} scan {scan_seconds:.3f}s "
-                           f"dual_l2={metrics['l2']:.3e} added={added_count} support={len(support.keys)}")
-        if converged:
-            break
-    converged = bool(history and history[-1].convergence.passed)
-    summary = RefinementSummary(time.perf_counter() - started, len(history), float(lp.obj_val), len(support.keys),
-                                peak, "converged" if converged else "max_refinement_iterations", converged)
-    level = LevelResult(level_index, "refined", n, m, init_stats, RefinementResult(tuple(history), summary),
-                        time.perf_counter() - started)
-    support.sparsification_log = sparsifications
-    return support, dual, level, triggered
+        _progress(options, f"level={self.index} iteration={iteration} scan {scan_seconds:.3f}s "
+                           f"dual_l2={metrics['l2']:.3e} added={added} support={len(support)}")
+        return converged
+
+    def run(self, max_iterations: int, initialization: InitializationStats, started: float) -> LevelResult:
+        converged = False
+        for iteration in range(max_iterations):
+            if self.step(iteration):
+                converged = True
+                break
+        summary = RefinementSummary(time.perf_counter() - started, len(self.records), float(self.lp.obj_val),
+                                    len(self.support), self.peak,
+                                    "converged" if converged else "max_refinement_iterations", converged)
+        return LevelResult(self.index, "refined", self.n, self.m, initialization,
+                           RefinementResult(tuple(self.records), summary), time.perf_counter() - started)
 
 
-__all__ = ["candidate_keys", "derive_hierarchy_seeds", "initialize", "level_sizes", "refine",
-           "shuffle_once_permutation", "solve_leaf"]
+def _contains_any(sorted_keys: torch.Tensor, queries: torch.Tensor) -> bool:
+    if sorted_keys.numel() == 0 or queries.numel() == 0:
+        return False
+    at = torch.searchsorted(sorted_keys, queries).clamp_max(sorted_keys.numel() - 1)
+    return bool((sorted_keys[at] == queries).any())
+
+
+def refine_level(cost: Cost, a, b, previous, inherited, options, level_index, max_iterations, detect_reentry):
+    """Seed and refine one level; returns (support, duals, LevelResult, perturbation trigger)."""
+    started = time.perf_counter()
+    level = LevelRefinement(cost, a, b, options, level_index, detect_reentry)
+    initialization = level.seed(previous, inherited)
+    result = level.run(max_iterations, initialization, started)
+    return level.support, level.dual, result, level.perturbation_triggered
+
+
+__all__ = ["LevelRefinement", "candidate_keys", "derive_hierarchy_seeds", "level_sizes", "refine_level",
+           "shuffle_once_permutation"]

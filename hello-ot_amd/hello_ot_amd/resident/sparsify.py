@@ -2,9 +2,9 @@
 
 Same signature, validation and result as the reference's routine (``restricted_ot/support_sparsification.py:13-145``,
 engine ``"cpp_lct"``), run by ``hm_sparsify_support`` in the native library: cycle cancelling on the host over a
-link-cut tree, as the reference does on its CPU (the GPU-resident reference solver exports the support to host
-memory for this step, ``gpu_resident/support.py:124-137``). The solver calls it only when an LP leaves more positive
-edges than the support cap allows.
+parent-pointer spanning forest with eager flow updates (the reference uses a link-cut tree on its CPU; the
+GPU-resident reference solver exports the support to host memory for this step, ``gpu_resident/support.py:124-137``).
+The solver calls it only when an LP leaves more positive edges than the support cap allows.
 """
 from __future__ import annotations
 

@@ -27,6 +27,7 @@ extern "C" {
 #define HM_EINVAL 1   /* invalid argument (ValueError in the Python mirror) */
 #define HM_EHIP 2     /* HIP runtime / launch error (RuntimeError) */
 #define HM_ENOSPC 3   /* workspace too small (RuntimeError) */
+#define HM_ESOLVE 4   /* a solver stopped without an optimum (RuntimeError) */
 
 /* Pricing flags */
 #define HM_ROWS 1u    /* per-row (query-side) top-k */
@@ -78,8 +79,11 @@ int hm_profile_query(const char* name, double* total_ms, int64_t* launches);
  * split-bf16 with HM_BF16X3) with a rigorous error bound b. A row whose kept candidates cannot be separated
  * from the dropped ones by 2b goes through a wide pass (its candidates with approximate score >= k-th - 2b are
  * collected by a second sweep and evaluated exactly) and, past 512 such candidates, an exact full rescan.
- * Certificate sums come from the sweep's approximate scores. The call synchronises the stream once per
- * finalize to read the number of queued rows back.
+ * Certificate: the maximum violation is the exact fp64 maximum (from the row lists, computed internally when
+ * HM_ROWS is off); count and num use the sweep's fp32-accumulated dot with an fp64 score for every pair within
+ * the fp32 rounding slack of zero (the reference's arithmetic: fp32 dots, fp64 epilogue); den and max|c| are
+ * accumulated from fp32 costs. The call synchronises the stream once per finalize to read the number of queued
+ * rows back.
  */
 size_t hm_pricing_l2sq_workspace_bytes(int64_t m, int64_t n, int32_t d, int32_t k, uint32_t flags);
 int hm_pricing_l2sq(void* stream, const float* X, const float* Y, const double* p, const double* q,
@@ -186,8 +190,9 @@ int hm_pdhg_solve(void* stream, const int64_t* rows, const int64_t* cols, const 
  * GPU-resident solver calls when the LP's positive support exceeds its cap (gpu_resident/support.py:124-137).
  *   rows[e], cols[e] int64 endpoints (HOST arrays), values[e] fp64 flows (HOST, in/out), costs[e] fp64 (HOST).
  *   A spanning forest of the positive edges is built in edge order; the remaining positive edges enter in edge
- *   order, each pushing flow around its tree cycle in the direction that does not increase the cost until an
- *   edge reaches zero (a link-cut tree keeps each cycle O(log) amortised). The exact count is re-taken whenever
+ *   order, each pushing flow around its forest cycle in the direction that does not increase the cost until an
+ *   edge reaches zero (the first such edge along the path from the entering edge's source leaves). The forest is
+ *   a parent-pointer forest with eager updates, O(cycle length) per cycle. The positive count is checked whenever
  *   enough cycles have been cancelled to reach target_nnz, and the work stops once it is reached.
  *   stats[3] (HOST): output nnz, cycles cancelled, tree operations. Flows <= zero_tolerance come back as 0.
  * Runs on the calling thread; touches no device memory.
@@ -195,6 +200,26 @@ int hm_pdhg_solve(void* stream, const int64_t* rows, const int64_t* cols, const 
 int hm_sparsify_support(int64_t n_source, int64_t n_target, int64_t e, const int64_t* rows, const int64_t* cols,
                         double* values, const double* costs, int64_t target_nnz, double zero_tolerance,
                         int64_t* stats);
+
+/* ---------------------------------------------------------------------------------------------------- */
+/* Exact coarsest level (host)                                                                            */
+/* ---------------------------------------------------------------------------------------------------- */
+
+/*
+ * Exact optimal vertex and duals of a small dense balanced transport problem, by the primal network simplex with
+ * strongly feasible trees (block-search pricing). Replaces the coarsest-level POT call ot.emd(a, b, M, log=True)
+ * of the GPU-resident solver (gpu_resident/solver.py:168-191; hierarchy/coarsest.py:38-60), which returns the
+ * plan and the duals log["u"], log["v"].
+ *   costs[n_source * n_target] row-major fp64, a[n_source], b[n_target] fp64 (HOST arrays, equal totals).
+ *   Outputs (HOST): the basic transport arcs basis_rows/cols[] int32 with basis_flows[] (capacity
+ *   n_source + n_target entries; *basis_count of them used, degenerate zero flows included), duals u[n_source],
+ *   v[n_target] with u_i + v_j = c_ij on basic arcs and u_i + v_j <= c_ij + 1e-12 (max|c| + 1) on all arcs, and the
+ *   pivot count (*pivots_out, may be NULL). HM_ESOLVE when no optimum is reached within max_pivots.
+ * Runs on the calling thread; touches no device memory.
+ */
+int hm_transport_simplex(int64_t n_source, int64_t n_target, const double* costs, const double* a, const double* b,
+                         int64_t max_pivots, int32_t* basis_rows, int32_t* basis_cols, double* basis_flows,
+                         int64_t* basis_count, double* u, double* v, int64_t* pivots_out);
 
 #ifdef __cplusplus
 }

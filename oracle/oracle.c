@@ -25,7 +25,8 @@
  *                  (pricing.cu:38-51). Missing slots hold (-inf, -1).
  *  pair costs   -- fp64 norms of fp32 rows for the sparse support (norm_cost_scan_kernel.cu:233-245):
  *                  per-lane fp64 partials in the dot64 lane layout and the same tree.
- *  PDHG         -- single-thread restatement of _native/cpp/solver.cpp:39-378 (team of one thread).
+ *  PDHG         -- restatement of _native/cpp/solver.cpp:39-378 with the reference's one-thread summation
+ *                  order: only the per-node passes run in parallel (disjoint writes), every reduction is serial.
  */
 #include <math.h>
 #include <stdint.h>
@@ -38,7 +39,12 @@
 static double dot64(const float* x, const float* y, int64_t d) {
     double acc[LANES];
     for (int l = 0; l < LANES; ++l) acc[l] = 0.0;
-    for (int64_t k = 0; k < d; ++k) acc[k % LANES] = acc[k % LANES] + (double)x[k] * (double)y[k];
+    /* lane l accumulates features l, l+64, l+128, ... in order; the lanes are independent, so the compiler may
+       vectorise across them without changing any lane's order */
+    int64_t t = 0;
+    for (; t + LANES <= d; t += LANES)
+        for (int l = 0; l < LANES; ++l) acc[l] = acc[l] + (double)x[t + l] * (double)y[t + l];
+    for (int l = 0; t + l < d; ++l) acc[l] = acc[l] + (double)x[t + l] * (double)y[t + l];
     for (int s = LANES / 2; s >= 1; s >>= 1)
         for (int l = 0; l < s; ++l) acc[l] = acc[l] + acc[l + s];
     return acc[0];
@@ -337,6 +343,9 @@ int orc_pdhg_solve(const int64_t* rows, const int64_t* cols, const double* c, co
         const int major = ((local_count + 1) % frequency) == 0;
         const int is_restart = (local_count % frequency == 0) && restart;
         const int checkpoint = major || is_restart;
+        /* Node passes: every edge belongs to exactly one source and one target, so the iterations of each pass
+           write disjoint entries and threads cannot change a single bit of the result. */
+        #pragma omp parallel for schedule(static)
         for (int64_t i = 0; i < n; ++i) {
             const double source_dual = y[i] / ns[i];
             double sum = 0.0;
@@ -354,6 +363,7 @@ int orc_pdhg_solve(const int64_t* rows, const int64_t* cols, const double* c, co
             if (checkpoint) dy[i] = reflected - y[i];
             y[i] = halpern * reflected + (1.0 - halpern) * ay[i];
         }
+        #pragma omp parallel for schedule(static)
         for (int64_t i = n; i < nodes; ++i) {
             double sum = 0.0;
             for (int64_t k = offsets[i]; k < offsets[i + 1]; ++k) sum += rx[edge_ids[k]];

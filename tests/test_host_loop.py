@@ -6,8 +6,9 @@ import pytest
 import torch
 
 from hello_ot_amd import Problem, SolverOptions
+from hello_ot_amd.resident.leaf import transport_simplex
 from hello_ot_amd.resident.solver import candidate_keys, derive_hierarchy_seeds, level_sizes, shuffle_once_permutation
-from hello_ot_amd.resident.support import Support, normalize_masses, northwest
+from hello_ot_amd.resident.support import ActiveSet, balanced_masses, staircase
 
 
 def test_options_defaults_and_validation_match_the_reference():
@@ -55,11 +56,11 @@ def test_hierarchy_chain_and_global_shuffle():
 
 
 @pytest.mark.parametrize("n,m,seed", [(5, 3, 0), (40, 55, 1), (1, 7, 2), (9, 1, 3)])
-def test_northwest_basis_is_a_feasible_spanning_tree(n, m, seed):
+def test_staircase_basis_is_a_feasible_spanning_tree(n, m, seed):
     rng = np.random.default_rng(seed)
-    a, b = normalize_masses(torch.as_tensor(rng.uniform(0.5, 1.5, n)), torch.as_tensor(rng.uniform(0.5, 1.5, m)))
+    a, b = balanced_masses(torch.as_tensor(rng.uniform(0.5, 1.5, n)), torch.as_tensor(rng.uniform(0.5, 1.5, m)))
     assert abs(float(a.sum() - b.sum())) <= 1e-15
-    keys, flows = northwest(a, b)
+    keys, flows = staircase(a, b)
     assert len(keys) == n + m - 1 and bool((flows >= 0).all())
     rows, cols = keys // m, keys % m
     # staircase: rows and cols never decrease and each step moves exactly one of them
@@ -71,6 +72,46 @@ def test_northwest_basis_is_a_feasible_spanning_tree(n, m, seed):
                                atol=1e-15)
 
 
+def _northwest_rule(a, b):
+    """Textbook northwest-corner rule on exact (dyadic) masses: allocate min(residual supply, residual demand),
+    then advance the row when its supply is used up -- first, when both are (the degenerate zero edge follows)."""
+    i = j = 0
+    ra, rb = a[0], b[0]
+    edges = []
+    while True:
+        x = min(ra, rb)
+        edges.append((i, j, x))
+        ra -= x
+        rb -= x
+        if i == len(a) - 1 and j == len(b) - 1:
+            return edges
+        if ra == 0 and i < len(a) - 1:
+            i += 1
+            ra = a[i]
+        else:
+            j += 1
+            rb = b[j]
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_staircase_matches_the_northwest_corner_rule_on_exact_masses(seed):
+    # integer multiples of 2^-10: every cumulative sum is exact, so ties (degenerate edges) are genuine
+    rng = np.random.default_rng(seed)
+    n, m = rng.integers(1, 30, 2)
+    a = rng.integers(1, 9, n).astype(np.float64)
+    b = rng.integers(1, 9, m).astype(np.float64)
+    b[-1] += a.sum() - b.sum()
+    if b[-1] <= 0:
+        a[-1] += 1 - b[-1]
+        b[-1] = 1.0
+    a, b = a / 1024.0, b / 1024.0
+    keys, flows = staircase(torch.as_tensor(a), torch.as_tensor(b))
+    want = _northwest_rule(list(a), list(b))
+    assert (keys // m).tolist() == [e[0] for e in want]
+    assert (keys % m).tolist() == [e[1] for e in want]
+    assert flows.tolist() == [e[2] for e in want]
+
+
 class _TableCost:
     def __init__(self, table):
         self.table = torch.as_tensor(table, dtype=torch.float64)
@@ -79,24 +120,109 @@ class _TableCost:
         return self.table[rows, cols]
 
 
-def test_support_extend_and_budgeted_pruning():
+def test_active_set_absorb_and_trim():
     n, m = 4, 5
     a = torch.full((n,), 0.25, dtype=torch.float64)
     b = torch.full((m,), 0.2, dtype=torch.float64)
-    s = Support.initial(torch.tensor([3, 17], dtype=torch.int64), a, b)
-    assert int(s.structural.sum()) == n + m - 1 and bool((torch.diff(s.keys) > 0).all())
-    fresh = s.extend(torch.tensor([0, 19, 12, 6], dtype=torch.int64))
-    assert set(s.keys[fresh].tolist()) == {19, 12, 6} - set(s.keys[~fresh].tolist())
+    s = ActiveSet.seeded(torch.tensor([3, 17], dtype=torch.int64), a, b)
+    assert int(s.pinned.sum()) == n + m - 1 and bool((torch.diff(s.keys) > 0).all())
+    assert float(s.flow.sum()) == pytest.approx(1.0)
+    before = set(s.keys.tolist())
+    new = s.absorb(torch.tensor([0, 6, 12, 19], dtype=torch.int64), born=0)
+    assert set(new.tolist()) == {0, 6, 12, 19} - before
+    assert bool((torch.diff(s.keys) > 0).all()) and set(s.keys.tolist()) == before | {0, 6, 12, 19}
+    fresh = s.born == 0
+    assert set(s.keys[fresh].tolist()) == set(new.tolist()) and float(s.flow[fresh].abs().sum()) == 0.0
     table = np.arange(n * m, dtype=np.float64).reshape(n, m)
     dual = torch.zeros(n + m, dtype=torch.float64)
-    size = len(s.keys)
-    # cost(r, c) = r * m + c = key and zero duals: the reduced cost of an edge is its key, so pruning one edge
-    # removes the largest non-structural (zero-flow) key
-    expected = int(s.keys[~s.structural].max())
-    removed = s.prune(_TableCost(table), dual, torch.zeros(size, dtype=torch.bool), size - 1)
-    assert removed.tolist() == [expected] and len(s.keys) == size - 1 and expected not in s.keys.tolist()
+    size = len(s)
+    # cost(r, c) = key and zero duals: the reduced cost of an edge is its key, so trimming one edge removes the
+    # largest key that is neither pinned nor added in this iteration
+    expected = int(s.keys[(~s.pinned) & (~fresh)].max())
+    removed = s.trim(_TableCost(table), dual, size - 1, iteration=0)
+    assert removed.tolist() == [expected] and len(s) == size - 1 and expected not in s.keys.tolist()
     with pytest.raises(RuntimeError, match="insufficient old zero-flow edges"):
-        s.prune(_TableCost(table), dual, torch.zeros(len(s.keys), dtype=torch.bool), 1)
+        s.trim(_TableCost(table), dual, 1, iteration=1)
+
+
+@pytest.mark.parametrize("seed", range(5))
+def test_trim_selects_as_a_stable_descending_sort(seed):
+    """Pruning removes the `excess` largest reduced costs among the eligible edges, equal values in key order
+    (refinement/budgeted_pruning.py:27-58: a stable descending argsort); many exact ties here."""
+    rng = np.random.default_rng(seed)
+    n, m = 30, 40
+    keys = np.sort(rng.choice(n * m, 500, replace=False))
+    flow = np.where(rng.random(500) < 0.2, rng.random(500), 0.0)
+    pinned = rng.random(500) < 0.1
+    born = np.where(rng.random(500) < 0.1, 3, -1).astype(np.int32)
+    table = rng.integers(0, 12, (n, m)).astype(np.float64)        # few distinct values: ties everywhere
+    dual = rng.integers(-2, 3, n + m).astype(np.float64)
+    s = ActiveSet(torch.as_tensor(keys), torch.as_tensor(flow), torch.as_tensor(pinned), torch.as_tensor(born), n, m)
+    budget = 420
+    removed = s.trim(_TableCost(table), torch.as_tensor(dual), budget, iteration=3)
+    rows, cols = keys // m, keys % m
+    eligible = np.nonzero((~pinned) & (born < 3) & (np.abs(flow) <= 1e-15))[0]
+    reduced = table[rows[eligible], cols[eligible]] - dual[rows[eligible]] - dual[n + cols[eligible]]
+    order = np.argsort(-reduced, kind="stable")[: 500 - budget]
+    assert removed.tolist() == sorted(keys[eligible[order]].tolist())
+    assert len(s) == budget and not set(removed.tolist()) & set(s.keys.tolist())
+
+
+def _highs(C, a, b):
+    import scipy.sparse as sp
+    from scipy.optimize import linprog
+
+    n, m = C.shape
+    rows, cols = np.repeat(np.arange(n), m), np.tile(np.arange(m), n)
+    A = sp.vstack([sp.csr_matrix((np.ones(n * m), (rows, np.arange(n * m))), shape=(n, n * m)),
+                   sp.csr_matrix((np.ones(n * m), (cols, np.arange(n * m))), shape=(m, n * m))])
+    res = linprog(C.ravel(), A_eq=A, b_eq=np.concatenate((a, b)), bounds=(0, None), method="highs")
+    assert res.status == 0
+    return res.fun
+
+
+@pytest.mark.parametrize("n,m,uniform,kind", [(1, 1, True, "r"), (1, 6, False, "r"), (7, 1, True, "r"),
+                                              (12, 17, False, "r"), (60, 60, True, "l2"), (80, 130, False, "l1"),
+                                              (150, 150, True, "grid")])
+def test_transport_simplex_is_exact(n, m, uniform, kind):
+    """The coarsest level's exact solver: HiGHS's optimum (1e-12), a feasible basic plan (at most n + m - 1 arcs,
+    marginals to 1e-15), duals tight on the basis and feasible on every pair (strong duality to 1e-12). Uniform
+    masses with n = m (an assignment problem, highly degenerate) and integer grid costs (massive ties) exercise the
+    anti-cycling rule."""
+    rng = np.random.default_rng(n * 1000 + m)
+    if kind == "r":
+        C = rng.random((n, m))
+    elif kind == "grid":
+        P, Q = rng.integers(0, 5, (n, 2)), rng.integers(0, 5, (m, 2))
+        C = np.abs(P[:, None, :] - Q[None, :, :]).sum(-1).astype(np.float64)
+    else:
+        X, Y = rng.random((n, 3)), rng.random((m, 3))
+        D = X[:, None, :] - Y[None, :, :]
+        C = (D ** 2).sum(-1) if kind == "l2" else np.abs(D).sum(-1)
+    if uniform:
+        a, b = np.full(n, 1.0 / n), np.full(m, 1.0 / m)
+    else:
+        a, b = rng.uniform(0.5, 1.5, n), rng.uniform(0.5, 1.5, m)
+        a, b = a / a.sum(), b / b.sum()
+    r, c, x, u, v, _ = transport_simplex(C, a, b)
+    assert len(x) <= n + m - 1 and (x >= 0).all()
+    np.testing.assert_allclose(np.bincount(r, weights=x, minlength=n), a, rtol=0, atol=1e-15)
+    np.testing.assert_allclose(np.bincount(c, weights=x, minlength=m), b, rtol=0, atol=1e-15)
+    primal = float(C[r, c] @ x)
+    scale = np.abs(C).max() + 1.0
+    assert abs(primal - _highs(C, a, b)) <= 1e-12 * scale
+    assert np.abs(C[r, c] - u[r] - v[c]).max() <= 1e-12 * scale
+    assert (C - u[:, None] - v[None, :]).min() >= -1e-12 * scale
+    assert abs(primal - (a @ u + b @ v)) <= 1e-12 * scale
+
+
+def test_transport_simplex_rejects_bad_input():
+    with pytest.raises(ValueError, match="unbalanced"):
+        transport_simplex(np.ones((2, 2)), np.array([0.5, 0.5]), np.array([0.2, 0.2]))
+    with pytest.raises(ValueError, match="finite"):
+        transport_simplex(np.array([[1.0, np.nan]]), np.array([1.0]), np.array([0.5, 0.5]))
+    with pytest.raises(ValueError, match="match"):
+        transport_simplex(np.ones((2, 3)), np.array([1.0]), np.array([0.5, 0.5]))
 
 
 def test_candidate_keys_filter_and_dedupe():
