@@ -23,6 +23,11 @@ bool profiling();
 void prof_begin(hipStream_t st, const char* name);
 void prof_end(hipStream_t st);
 void prof_count(const char* name, int64_t count);  // adds to a name's count (queued rescans, ...)
+// while alive, this thread's launches record no timing events and no counts
+struct ProfileOff {
+    ProfileOff();
+    ~ProfileOff();
+};
 
 #define HM_CHECK_ARG(cond, ...)                                  \
     do {                                                         \

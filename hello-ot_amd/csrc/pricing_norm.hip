@@ -10,6 +10,8 @@
 // One thread owns one X row (features in registers); Y tiles of 256 rows are staged in LDS and read by
 // broadcast. Column lists come from a second sweep with the roles swapped (the score keeps the original
 // association). Certificate sums are accumulated in fp32 per tile and flushed to fp64.
+#include <mutex>
+
 #include "common.h"
 
 namespace hm {
@@ -458,6 +460,29 @@ int norm_scan_run(void* stream, const float* X, const float* Y, const double* f,
     return HM_OK;
 }
 
+// Scratch of the allocation-free entry point: one array per GPU, for the life of the process. Host code reaches it
+// only through the device address hipGetSymbolAddress returns (looked up once per device, under a lock).
+constexpr size_t NORM_SCRATCH_BYTES = size_t(64) << 20;
+__device__ __align__(256) unsigned char scratch[NORM_SCRATCH_BYTES];
+constexpr int SCRATCH_DEVICES = 64;
+std::mutex scratch_lock;
+void* scratch_address[SCRATCH_DEVICES] = {};
+
+int scratch_for_current_device(void** out) {
+    int dev = -1;
+    HM_HIP(hipGetDevice(&dev));
+    if (dev < 0 || dev >= SCRATCH_DEVICES) return fail(HM_EINVAL, "norm pricing (no-alloc): device %d out of range", dev);
+    std::lock_guard<std::mutex> hold(scratch_lock);
+    if (scratch_address[dev] == nullptr) {
+        void* p = nullptr;
+        HM_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        if (p == nullptr) return fail(HM_EHIP, "norm pricing (no-alloc): no device address for the scratch array");
+        scratch_address[dev] = p;
+    }
+    *out = scratch_address[dev];
+    return HM_OK;
+}
+
 }  // namespace
 
 extern "C" int hm_pricing_norm(void* stream, const float* X, const float* Y, const double* f, const double* g,
@@ -466,4 +491,23 @@ extern "C" int hm_pricing_norm(void* stream, const float* X, const float* Y, con
                                void* workspace, size_t workspace_bytes) {
     return norm_scan_run(stream, X, Y, f, g, m, n, d, k, kind, flags, row_val, row_idx, col_val, col_idx, stats,
                          workspace, workspace_bytes);
+}
+
+extern "C" size_t hm_pricing_norm_noalloc_max_bytes(void) { return NORM_SCRATCH_BYTES; }
+
+extern "C" int hm_pricing_norm_noalloc(void* stream, const float* X, const float* Y, const double* f,
+                                       const double* g, int64_t m, int64_t n, int32_t d, int32_t k, int32_t kind,
+                                       uint32_t flags, double* row_val, int32_t* row_idx, double* col_val,
+                                       int32_t* col_idx, double* stats) {
+    HM_CHECK_ARG(m >= 1 && n >= 1 && k >= 1 && k <= 32, "norm pricing requires nonempty inputs and 1 <= k <= 32");
+    const size_t need = hm_pricing_norm_workspace_bytes(m, n, d, k, flags);
+    if (need > NORM_SCRATCH_BYTES)
+        return fail(HM_ENOSPC, "norm pricing (no-alloc): this call needs %zu bytes of scratch, above the %zu-byte static "
+                               "scratch array; call hm_pricing_norm with a workspace instead",
+                    need, NORM_SCRATCH_BYTES);
+    void* scratch_ptr = nullptr;
+    if (int rc = scratch_for_current_device(&scratch_ptr)) return rc;
+    const ProfileOff no_events;  // timing events would be created on demand
+    return norm_scan_run(stream, X, Y, f, g, m, n, d, k, kind, flags, row_val, row_idx, col_val, col_idx, stats,
+                         scratch_ptr, NORM_SCRATCH_BYTES);
 }

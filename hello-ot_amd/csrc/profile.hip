@@ -49,10 +49,15 @@ void collect_locked() {
 
 }  // namespace
 
+// launches of an allocation-free entry point record no timing events (events are created on demand)
+thread_local int g_quiet = 0;
+ProfileOff::ProfileOff() { ++g_quiet; }
+ProfileOff::~ProfileOff() { --g_quiet; }
+
 bool profiling() { return g_on; }
 
 void prof_begin(hipStream_t st, const char* name) {
-    if (!g_on) return;
+    if (!g_on || g_quiet) return;
     std::lock_guard<std::mutex> lock(g_mu);
     g_open = name;
     g_open_event = get_event();
@@ -60,7 +65,7 @@ void prof_begin(hipStream_t st, const char* name) {
 }
 
 void prof_end(hipStream_t st) {
-    if (!g_on) return;
+    if (!g_on || g_quiet) return;
     std::lock_guard<std::mutex> lock(g_mu);
     if (!g_open_event) return;
     hipEvent_t e = get_event();
@@ -71,7 +76,7 @@ void prof_end(hipStream_t st) {
 }
 
 void prof_count(const char* name, int64_t count) {
-    if (!g_on) return;
+    if (!g_on || g_quiet) return;
     std::lock_guard<std::mutex> lock(g_mu);
     g_totals[name].second += count;
 }

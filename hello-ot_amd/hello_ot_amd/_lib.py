@@ -60,6 +60,9 @@ SIGNATURES = {
     "hm_pricing_norm_workspace_bytes": (_SZ, [_I64, _I64, _I32, _I32, _U32]),
     "hm_pricing_norm": (ctypes.c_int, [_P, _P, _P, _P, _P, _I64, _I64, _I32, _I32, _I32, _U32,
                                        _P, _P, _P, _P, _P, _P, _SZ]),
+    "hm_pricing_norm_noalloc_max_bytes": (_SZ, []),
+    "hm_pricing_norm_noalloc": (ctypes.c_int, [_P, _P, _P, _P, _P, _I64, _I64, _I32, _I32, _I32, _U32,
+                                               _P, _P, _P, _P, _P]),
     "hm_sddmm_l2sq_csr": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I32, _D, _P]),
     "hm_pair_costs_l2sq": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _I64, _I32, _D, _P]),
     "hm_pair_costs_norm": (ctypes.c_int, [_P, _P, _P, _P, _P, _I64, _I32, _I32, _P]),

@@ -105,6 +105,22 @@ int hm_pricing_norm(void* stream, const float* X, const float* Y, const double* 
                     double* row_val, int32_t* row_idx, double* col_val, int32_t* col_idx, double* stats,
                     void* workspace, size_t workspace_bytes);
 
+/*
+ * hm_pricing_norm without a workspace and without any allocation. No counterpart in the reference: this entry
+ * point is for callers that cannot allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). Its scratch is a file-scope device array of hm_pricing_norm_noalloc_max_bytes()
+ * bytes (64 MiB) per GPU, held until the process ends; calls whose hm_pricing_norm_workspace_bytes exceeds it fail
+ * with HM_ENOSPC (524288 x 524288 at d = 8, k = 2 needs 12 MiB). The scratch of the CURRENT device is used, so the
+ * stream must belong to it. Every call on a GPU shares that GPU's array: calls that overlap on one GPU (other host
+ * threads, other streams) race. Nothing in the array has to start at zero (the call clears what it accumulates,
+ * with a kernel). Kernel timing (hm_profile_enable) records no events for these launches. Same outputs as
+ * hm_pricing_norm.
+ */
+size_t hm_pricing_norm_noalloc_max_bytes(void);
+int hm_pricing_norm_noalloc(void* stream, const float* X, const float* Y, const double* f, const double* g,
+                            int64_t m, int64_t n, int32_t d, int32_t k, int32_t kind, uint32_t flags,
+                            double* row_val, int32_t* row_idx, double* col_val, int32_t* col_idx, double* stats);
+
 /* ---------------------------------------------------------------------------------------------------- */
 /* (b) SDDMM cost evaluation on the active support                                                       */
 /* ---------------------------------------------------------------------------------------------------- */
