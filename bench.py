@@ -98,12 +98,13 @@ NORM_COUNTER_PROFILE = ROOT / "profiles" / "norm_sweep_c4_counters.md"
 
 
 def norm_counters(name):
-    """Executed VALU work of the C4 norm sweep from the committed rocprofv3 counter summary (SQ_INSTS_VALU per
-    pair and the VALU lane-op fraction of the non-packed fp32 peak over the sweep's duration); None when absent."""
+    """Executed VALU work of the C4 norm sweep from the committed rocprofv3 counter summary (SQ_INSTS_VALU wave
+    instructions per pair over both sweeps of a call, and VALU instructions issued per SIMD per cycle); None when
+    absent."""
     out = {}
     try:
         for line in NORM_COUNTER_PROFILE.read_text().splitlines():
-            for key in ("valu_insts_per_pair", "valu_lane_op_frac", "duration_ms"):
+            for key in ("valu_insts_per_pair", "valu_issue_per_simd_cycle", "duration_ms"):
                 if line.startswith(f"{name}_{key} ="):
                     out[key] = float(line.split("=")[1])
     except OSError:

@@ -103,7 +103,8 @@ __device__ inline void insert_e(float (&w)[K], int (&id)[K], float v, int i) {
 struct CertArgs {
     const double* qb;
     const double* db;
-    const unsigned long long* ymax;
+    const unsigned long long* ymax;  // [max ||y||, max |db|] of the swept-against side
+    const double* xnorm;             // ||x_i|| of the swept rows (global row index)
 };
 
 // 2.5 fp32 units: the slack below bounds four fp32 roundings (db_j and qb_i to fp32, the fma giving w, the add
@@ -114,17 +115,32 @@ constexpr float CERT_REL = 1.4901161e-07f;
 
 // Certificate terms of one pair from its fp32 dot t and fp32 score w = fl(scale*t + db32_j). The fp64 score
 // sigma' = (scale*t + qb_i) + db_j (the reference's arithmetic: fp32 dot, fp64 epilogue) differs from the fp32 score
-// sg = fl(w + qb32_i) by at most CERT_REL * (|w| + |qb32_i|) + CERT_REL * max|db| = slack. Pairs beyond the slack are
-// decided in fp32 (a positive one adds sg^2 to the tile's fp32 sum); pairs within it get sigma' in fp64, which
-// decides the count and adds sigma'^2 to the lane's fp64 sum.
-__device__ __forceinline__ void cert_score(float t, float w, float qbi, float sdb, float scale, double qb64,
-                                           double db64, float& tnum, unsigned int& tcnt, double& num64) {
+// sg = fl(w + qb32_i) by at most CERT_REL * (|w| + |qb32_i| + max|db|), and |w| <= scale ||x_i|| max||y|| (1 + 1e-2)
+// + max|db| bounds every |w| of row i, so the row's slack (row_cert_slack) covers all its pairs. Pairs beyond the
+// slack are decided in fp32 (a positive one adds sg^2 to the tile's fp32 sum); pairs within it get sigma' in fp64,
+// which decides the count and adds sigma'^2 to the lane's fp64 sum.
+//
+// cert_fast is the per-pair part, without branches: the cost terms, the fp32 decision, and `near` set for a pair
+// within the slack. A tile with a near pair on some lane runs cert_near over its pairs afterwards (rare: the slack is
+// a few fp32 units of the row's largest score).
+__device__ __forceinline__ void cert_fast(bool ok, float w, float ge, float pi, float qbi, float slack, float& tden,
+                                          float& cmax, float& tnum, unsigned int& tcnt, bool& near) {
+    const float cost = (pi + ge) - w;
+    const float cm = ok ? cost : 0.0f;
+    tden = fmaf(cm, cm, tden);
+    cmax = fmaxf(cmax, fabsf(cm));
     const float sg = w + qbi;
-    const float slack = fmaf(CERT_REL, fabsf(w) + fabsf(qbi), sdb);
-    if (sg > slack) {
-        tnum = fmaf(sg, sg, tnum);
-        ++tcnt;
-    } else if (sg > -slack) {
+    const bool pos = ok && sg > slack;
+    const float sp = pos ? sg : 0.0f;
+    tnum = fmaf(sp, sp, tnum);
+    tcnt += pos ? 1u : 0u;
+    near = near || (ok && fabsf(sg) <= slack);
+}
+
+__device__ __forceinline__ void cert_near(bool ok, float t, float w, float qbi, float slack, float scale, double qb64,
+                                          double db64, unsigned int& tcnt, double& num64) {
+    const float sg = w + qbi;
+    if (ok && fabsf(sg) <= slack) {
         const double sig = ((double)scale * (double)t + qb64) + db64;
         if (sig > 0.0) {
             num64 = fma(sig, sig, num64);
@@ -133,9 +149,12 @@ __device__ __forceinline__ void cert_score(float t, float w, float qbi, float sd
     }
 }
 
-// CERT_REL * max|db| of a sweep's certificate (0 without one)
-__device__ __forceinline__ float cert_db_slack(int STATS, const CertArgs& c) {
-    return STATS ? CERT_REL * (float)key_double(c.ymax[1]) : 0.0f;
+// slack of row `row` (0 without a certificate or past the chunk)
+__device__ __forceinline__ float row_cert_slack(int STATS, const CertArgs& c, int64_t row, bool ok, float scale) {
+    if (!STATS || !ok) return 0.0f;
+    const double ymax = key_double(c.ymax[0]), dmax = key_double(c.ymax[1]);
+    const double wmax = 1.01 * (double)scale * c.xnorm[row] * ymax + dmax;
+    return (float)(CERT_REL * (wmax + fabs(c.qb[row]) + dmax) * (1.0 + 1e-3));
 }
 
 // -------------------------------------------------------------------------------------------------
@@ -353,7 +372,7 @@ __device__ __forceinline__ void sweep_row_init(SweepRow<K1>& s, int64_t row, int
 template <int K1, bool COLS, bool APPEND, int CPASS = BY>
 __device__ __forceinline__ void sweep_epilogue(const v16f (&tot)[NB], SweepRow<K1>& s, int tid, int wave, int h,
                                                int r, int64_t ytile, int64_t y_end, int64_t x0, int64_t panel,
-                                               int64_t n, float scale, int STATS, float sdb, const double* sQB64,
+                                               int64_t n, float scale, int STATS, float slack, const double* sQB64,
                                                const double* sDB64, const float* sDB, const float* sGE,
                                                float* sC, Entry* __restrict__ colpart,
                                                unsigned int* __restrict__ colthr, int* __restrict__ wcnt,
@@ -361,6 +380,10 @@ __device__ __forceinline__ void sweep_epilogue(const v16f (&tot)[NB], SweepRow<K
                                                int64_t xb) {
     float tnum = 0.0f, tden = 0.0f;
     unsigned int tcnt = 0;
+    bool near = false;  // a pair of this tile within the certificate slack (cert_fast)
+    // Y rows of the tile inside the segment; pair (lane half h, offset c) is inside when 4h < ylim - c, a compare
+    // against a wave-uniform bound
+    const int ylim = (int)(y_end - ytile < (int64_t)(NB * 32) ? y_end - ytile : (int64_t)(NB * 32));
     // the row's shared threshold: scores at or below it cannot enter the row's merged lists (row_threshold_*)
     const float rthr = (!APPEND && s.ok) ? row_threshold_get(rowthr, s.row - xb) : -INFINITY;
     const float last0 = APPEND ? 0.0f : s.lv[K1 - 1];
@@ -380,7 +403,7 @@ __device__ __forceinline__ void sweep_epilogue(const v16f (&tot)[NB], SweepRow<K
                 const float t = tot[b][q];
                 const float w = fmaf(scale, t, dbs[cc]);
                 const int64_t j = ytile + jl0 + cc;
-                const bool ok = s.ok && j < y_end;
+                const bool ok = s.ok && 4 * h < ylim - (b * 32 + 8 * a + cc);
                 if (APPEND) {
                     if (ok && w >= s.wt) {
                         const int pos = atomicAdd(&wcnt[s.row], 1);
@@ -401,12 +424,22 @@ __device__ __forceinline__ void sweep_epilogue(const v16f (&tot)[NB], SweepRow<K
                         }
                     }
                 }
-                if (STATS && ok) {
-                    const float cost = (s.pi + ges[cc]) - w;
-                    tden = fmaf(cost, cost, tden);
-                    s.cmax = fmaxf(s.cmax, fabsf(cost));
-                    cert_score(t, w, s.qbi, sdb, scale, sQB64[wave * 32 + r], sDB64[jl0 + cc], tnum, tcnt, s.num64);
-                }
+                if (STATS) cert_fast(ok, w, ges[cc], s.pi, s.qbi, slack, tden, s.cmax, tnum, tcnt, near);
+            }
+        }
+    }
+    if (STATS && near) {
+        // reload the biases rather than keep the fast path's values alive in registers through the tile
+        asm volatile("" ::: "memory");
+        const double qb64 = sQB64[wave * 32 + r];
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+#pragma unroll
+            for (int q = 0; q < 16; ++q) {
+                const int jl = b * 32 + 8 * (q / 4) + 4 * h + (q % 4);
+                const float t = tot[b][q];
+                cert_near(s.ok && 4 * h < ylim - (jl - 4 * h), t, fmaf(scale, t, sDB[jl]), s.qbi, slack, scale, qb64,
+                          sDB64[jl], tcnt, s.num64);
             }
         }
     }
@@ -546,7 +579,7 @@ __global__ __launch_bounds__(256) void l2sq_sweep(
     const int64_t y_end = (y_begin + seg_len < n) ? (y_begin + seg_len) : n;
     SweepRow<K1> s;
     sweep_row_init<K1, APPEND>(s, x0 + wave * 32 + r, xe, STATS, qb32, p32, wthr);
-    const float sdb = cert_db_slack(STATS, cert);
+    const float slack = row_cert_slack(STATS, cert, s.row, s.ok, scale);
     if (!APPEND && tid < BX) sQB64[tid] = (STATS && x0 + tid < xe) ? cert.qb[x0 + tid] : 0.0;
 
     const int nchunks = (d + KC - 1) / KC;
@@ -708,7 +741,7 @@ __global__ __launch_bounds__(256) void l2sq_sweep(
                 for (int q = 0; q < 16; ++q) acc[b][q] = outer[b][q] + acc[b][q];
             }
         }
-        sweep_epilogue<K1, COLS, APPEND>(acc, s, tid, wave, h, r, ytile, y_end, x0, panel, n, scale, STATS, sdb,
+        sweep_epilogue<K1, COLS, APPEND>(acc, s, tid, wave, h, r, ytile, y_end, x0, panel, n, scale, STATS, slack,
                                          sQB64, sDB64, sDB, sGE,
                                          sC, colpart, colthr, wcnt, wbuf, wcap, rowthr, xb);
     }
@@ -847,7 +880,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(COLS ? 1 : 
     const int64_t y_end = (y_begin + seg_len < n) ? (y_begin + seg_len) : n;
     SweepRow<K1> s;
     sweep_row_init<K1, APPEND>(s, x0 + wave * 32 + r, xe, STATS, qb32, p32, wthr);
-    const float sdb = cert_db_slack(STATS, cert);
+    const float slack = row_cert_slack(STATS, cert, s.row, s.ok, scale);
     if (!APPEND && tid < BX) sQB64[tid] = (STATS && x0 + tid < xe) ? cert.qb[x0 + tid] : 0.0;
 
     const int nchunks = d / KC;
@@ -974,7 +1007,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(COLS ? 1 : 
             step(I2{});
             step(I3{});
         }
-        sweep_epilogue<K1, COLS, APPEND>(acc, s, tid, wave, h, r, ytile, y_end, x0, panel, n, scale, STATS, sdb,
+        sweep_epilogue<K1, COLS, APPEND>(acc, s, tid, wave, h, r, ytile, y_end, x0, panel, n, scale, STATS, slack,
                                          sQB64, sDB64, sDB, sGE,
                                          sC, colpart, colthr, wcnt, wbuf, wcap, rowthr, xb);
     }
@@ -1111,7 +1144,7 @@ __device__ __forceinline__ void sweep_epilogue_w(const float (&tot)[NB][16], int
                                                  float pi, float wt, bool first, int tid, int wave, int h, int r,
                                                  int64_t ytile, int64_t y_end, int64_t x0, int64_t xb, int64_t rows,
                                                  int64_t seg, int64_t panel, int64_t n, float scale, int STATS,
-                                                 float sdb, const double* sQB64, const double* sDB64,
+                                                 float slack, const double* sQB64, const double* sDB64,
                                                  const float* sDB, const float* sGE, float* sC,
                                                  Entry* __restrict__ part, Entry* __restrict__ colpart,
                                                  unsigned int* __restrict__ colthr, int* __restrict__ wcnt,
@@ -1120,6 +1153,10 @@ __device__ __forceinline__ void sweep_epilogue_w(const float (&tot)[NB][16], int
                                                  unsigned int* __restrict__ rowthr) {
     float tnum = 0.0f, tden = 0.0f;
     unsigned int tcnt = 0;
+    bool near = false;  // a pair of this tile within the certificate slack (cert_fast)
+    // Y rows of the tile inside the segment; pair (lane half h, offset c) is inside when 4h < ylim - c, a compare
+    // against a wave-uniform bound
+    const int ylim = (int)(y_end - ytile < (int64_t)(NB * 32) ? y_end - ytile : (int64_t)(NB * 32));
     float lv[APPEND ? 1 : K1];
     int li[APPEND ? 1 : K1];
     Entry* lp = APPEND ? nullptr : part + ((seg * rows + (row - xb)) * 2 + h) * K1;
@@ -1150,7 +1187,7 @@ __device__ __forceinline__ void sweep_epilogue_w(const float (&tot)[NB][16], int
                 const float t = tot[y][4 * a + cc];
                 const float w = fmaf(scale, t, dbs[cc]);
                 const int64_t j = ytile + jl0 + cc;
-                const bool okj = ok && j < y_end;
+                const bool okj = ok && 4 * h < ylim - (y * 32 + 8 * a + cc);
                 if constexpr (APPEND) {
                     if (okj && w >= wt) {
                         const int pos = atomicAdd(&wcnt[row], 1);
@@ -1171,12 +1208,22 @@ __device__ __forceinline__ void sweep_epilogue_w(const float (&tot)[NB][16], int
                         }
                     }
                 }
-                if (STATS && okj) {
-                    const float cost = (pi + ges[cc]) - w;
-                    tden = fmaf(cost, cost, tden);
-                    cmax = fmaxf(cmax, fabsf(cost));
-                    cert_score(t, w, qbi, sdb, scale, sQB64[wave * 32 + r], sDB64[jl0 + cc], tnum, tcnt, num64);
-                }
+                if (STATS) cert_fast(okj, w, ges[cc], pi, qbi, slack, tden, cmax, tnum, tcnt, near);
+            }
+        }
+    }
+    if (STATS && near) {
+        // reload the biases rather than keep the fast path's values alive in registers through the tile
+        asm volatile("" ::: "memory");
+        const double qb64 = sQB64[wave * 32 + r];
+#pragma unroll
+        for (int y = 0; y < NB; ++y) {
+#pragma unroll
+            for (int q = 0; q < 16; ++q) {
+                const int jl = y * 32 + 8 * (q / 4) + 4 * h + (q % 4);
+                const float t = tot[y][q];
+                cert_near(ok && 4 * h < ylim - (jl - 4 * h), t, fmaf(scale, t, sDB[jl]), qbi, slack, scale, qb64, sDB64[jl],
+                          tcnt, num64);
             }
         }
     }
@@ -1308,7 +1355,7 @@ __global__ __launch_bounds__(THREADS_W) void l2sq_sweep_split_w(
     double num64 = 0.0, den64 = 0.0;
     unsigned int cnt = 0u;
     float cmax = 0.0f;
-    const float sdb = cert_db_slack(STATS, cert);
+    const float slack = row_cert_slack(STATS, cert, row, ok, scale);
     if (!APPEND && tid < BXW) sQB64[tid] = (STATS && x0 + tid < xe) ? cert.qb[x0 + tid] : 0.0;
 
     const int nchunks = d / KC;
@@ -1427,7 +1474,7 @@ __global__ __launch_bounds__(THREADS_W) void l2sq_sweep_split_w(
             }
         }
         sweep_epilogue_w<K1, COLS, APPEND>(outer, row, ok, qbi, pi, wt, ytile == y_begin, tid, wave, h, r, ytile,
-                                           y_end, x0, xb, rows, seg, panel, n, scale, STATS, sdb, sQB64, sDB64, sDB,
+                                           y_end, x0, xb, rows, seg, panel, n, scale, STATS, slack, sQB64, sDB64, sDB,
                                            sGE, sC,
                                            part,
                                            colpart, colthr, wcnt, wbuf, wcap, num64, den64, cnt, cmax, rowthr);
@@ -2224,7 +2271,7 @@ int run_bidir(hipStream_t st, const float* X, const float* Y, int64_t m, int64_t
     bnd.acc_rel = split_rel + ea * (split ? 1.01 : 1.0) + u * (1.0 + ea + split_rel) + 4e-15 * (d / 64.0 + 8.0);
     bnd.db_rel = 2.0 * u + 1e-15;
     bnd.abs_slack = 1e-30 * (double)d;
-    const CertArgs cert{qb, db, maxima + 2};  // the row pass sweeps X rows against Y (maxima[2..3]: Y side)
+    const CertArgs cert{qb, db, maxima + 2, xnorm};  // the row pass sweeps X rows against Y (maxima[2..3]: Y side)
     int chunk_index = 0;
     const bool row_pass = cp.row_pass;  // a columns-only call without fusion skips it
     for (int64_t xb = 0; row_pass && xb < m; xb += ch, ++chunk_index) {
