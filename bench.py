@@ -35,11 +35,15 @@ import torch  # noqa: E402
 
 PEAK_FP32_MFMA = 157.3e12   # MI355X dense fp32 matrix FLOP/s
 PEAK_BF16_MFMA = 2.5e15     # MI355X dense bf16 matrix FLOP/s
+PEAK_INT8_MFMA = 5.0e15     # MI355X dense int8 matrix OP/s
 PEAK_HBM = 8.0e12           # MI355X HBM3E bytes/s
 PEAK_VALU_OPS = 256 * 64 * 2.4e9  # non-packed fp32 VALU lane-ops/s (256 CU x 64 lanes/clk x 2.4 GHz)
 
-TRAFFIC_PROFILE = ROOT / "profiles" / "l2sq_sweep_c5_chunk8192.md"
-COUNTER_PROFILE = ROOT / "profiles" / "l2sq_sweep_c5_counters.md"
+# committed rocprofv3 summaries of each split sweep at the C5 step: (HBM traffic, shader counters)
+SWEEP_PROFILES = {"bf16x3": (ROOT / "profiles" / "l2sq_sweep_c5_chunk8192.md",
+                             ROOT / "profiles" / "l2sq_sweep_c5_counters.md"),
+                  "int8x3": (ROOT / "profiles" / "l2sq_sweep_i8_c5_chunk8192.md",
+                             ROOT / "profiles" / "l2sq_sweep_i8_c5_counters.md")}
 
 C5_N = 1_280_000
 C5_D = 8192
@@ -48,27 +52,33 @@ C5_D = 8192
 def roofline(precision, achieved):
     """Roofline of the sweep kernel. `achieved` is the algorithmic rate, 2*d flop per pair over the sweep's mean
     launch time, held against the peak of the matrix units the sweep runs on: the bf16 peak for the split-bf16
-    sweep, the fp32 peak for the fp32 sweep. The split sweep executes three bf16 products per feature (hi*hi +
-    hi*lo + lo*hi), so its executed MFMA rate (3x the algorithmic one) is reported beside it; its algorithmic
-    fraction cannot exceed 1/3."""
+    sweep, the int8 peak for the int8 sweep, the fp32 peak for the fp32 sweep. The split sweeps execute three
+    products per feature (hi*hi + hi*lo + lo*hi), so their executed MFMA rate (3x the algorithmic one) is reported
+    beside it; their algorithmic fraction cannot exceed 1/3."""
     if precision == "bf16x3":
         products, peak = 3.0, PEAK_BF16_MFMA
+    elif precision == "int8x3":
+        products, peak = 3.0, PEAK_INT8_MFMA
     else:
         products, peak = 1.0, PEAK_FP32_MFMA
+    kernel = {"bf16x3": "l2sq_sweep_split_w", "int8x3": "l2sq_sweep_i8_w"}.get(precision, "l2sq_sweep")
     return {"bound": "mfma", "achieved": achieved / 1e12, "peak": peak / 1e12, "unit": "TFLOP/s",
-            "frac": achieved / peak, "traffic": sweep_traffic(), "traffic_source": TRAFFIC_PROFILE.name,
-            "kernel": "l2sq_sweep_split_w" if precision == "bf16x3" else "l2sq_sweep", "sweep": precision,
+            "frac": achieved / peak, "traffic": sweep_traffic(precision),
+            "traffic_source": SWEEP_PROFILES[precision][0].name if precision in SWEEP_PROFILES else None,
+            "kernel": kernel, "sweep": precision,
             "work_per_pair": "2*d flop (algorithmic)", "algorithmic_flops_per_pair": 2 * C5_D,
             "executed_products_per_feature": products, "executed_tflops": products * achieved / 1e12,
             "executed_frac": products * achieved / peak,
-            "counters": sweep_counters() if precision == "bf16x3" else None}
+            "counters": sweep_counters(precision)}
 
 
-def sweep_traffic():
+def sweep_traffic(precision):
     """HBM bytes per split-sweep launch at the C5 workload, from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE
     summary (scaled by a plain copy kernel's counters); None when no such summary is present."""
     try:
-        for line in TRAFFIC_PROFILE.read_text().splitlines():
+        if precision not in SWEEP_PROFILES:
+            return None
+        for line in SWEEP_PROFILES[precision][0].read_text().splitlines():
             if line.startswith("traffic_bytes_per_launch"):
                 return float(line.split("=")[1])
     except OSError:
@@ -76,13 +86,16 @@ def sweep_traffic():
     return None
 
 
-def sweep_counters():
+def sweep_counters(precision):
     """The split sweep's sustained engine clock and MFMA-busy fraction at the C5 workload, from the committed
     rocprofv3 shader-counter summary (GRBM_GUI_ACTIVE and SQ_VALU_MFMA_BUSY_CYCLES over the dispatch); None when
     no such summary is present."""
     out = {}
+    if precision not in SWEEP_PROFILES:
+        return None
+    profile = SWEEP_PROFILES[precision][1]
     try:
-        for line in COUNTER_PROFILE.read_text().splitlines():
+        for line in profile.read_text().splitlines():
             for key in ("sustained_clock_ghz", "mfma_busy_frac"):
                 if line.startswith(key + " ="):
                     out[key] = float(line.split("=")[1])
@@ -90,7 +103,7 @@ def sweep_counters():
         return None
     if not out:
         return None
-    out["source"] = COUNTER_PROFILE.name
+    out["source"] = profile.name
     return out
 
 
@@ -541,6 +554,8 @@ def main():
     ap.add_argument("--no-extras", action="store_true")
     ap.add_argument("--no-c5-solve", action="store_true",
                     help="skip the full C5 solve (1.28M x 1.28M, d=8192) that the default run times last")
+    ap.add_argument("--sweep", default="auto", choices=("auto", "fp32", "bf16x3", "int8x3"),
+                    help="sweep precision of the C5 step (all give the same exact lists)")
     ap.add_argument("--fp32-sweep", action="store_true",
                     help="also time the C5 step on the fp32 MFMA sweep and check its outputs against the split sweep")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -591,7 +606,7 @@ def main():
     from hello_ot_amd.kernels.generic_scan import sweep_precision
 
     inputs = c5_inputs(dev, args.chunk)
-    precision = sweep_precision("auto", C5_D)
+    precision = sweep_precision(args.sweep, C5_D)
     split_out = []
     sec, pairs, achieved, info = bench_c5(dev, args.chunk, args.steps, args.warmup, inputs, precision, split_out)
     extras = {}
@@ -639,7 +654,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16x3+f64" if precision == "bf16x3" else "f32+f64",
+        "dtype": {"bf16x3": "bf16x3+f64", "int8x3": "int8x3+f64"}.get(precision, "f32+f64"),
         "data": "synthetic 64-component Gaussian mixtures (C5 recipe), generated on device",
         "config": {"workload": f"C5 pricing step: {args.chunk} query rows x 1,280,000 resident rows, d=8192, k=2, "
                                "rows+cols top-k + certificate", "chunk": args.chunk, "n_resident": C5_N,

@@ -45,6 +45,8 @@ struct DirPlan {
 namespace {
 
 typedef float v16f __attribute__((ext_vector_type(16)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+typedef int v4i __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
 constexpr int BX = 128;            // X rows per workgroup of the fp32 and short split sweeps (4 waves x 32)
@@ -157,6 +159,18 @@ __device__ __forceinline__ float row_cert_slack(int STATS, const CertArgs& c, in
     return (float)(CERT_REL * (wmax + fabs(c.qb[row]) + dmax) * (1.0 + 1e-3));
 }
 
+// int8 split (HM_INT8X3): the rows of a block of 32 are quantized to v_k = rint(x_k / s) with one scale
+// s = max |x_k| / I8_Q over the block, so |v_k| <= I8_Q, and v = 256 h + l splits into int8 limbs
+// h = (v + 128) >> 8 in [-127, 127] and l in [-128, 127]. A scale per block keeps the scales of a sweep tile's Y
+// blocks uniform over the wave.
+constexpr int I8_Q = 32639;  // 256 * 127 + 127
+// the scale of a block with largest magnitude amax; 1 for a zero block or one so small that 1 / s would overflow
+// (all its v are then 0, and the quantization error |x_k| < s / 2 still holds)
+__device__ __forceinline__ float i8_scale(float amax) {
+    const float s = amax / (float)I8_Q;
+    return (s >= 1e-37f && s < INFINITY) ? s : 1.0f;
+}
+
 // -------------------------------------------------------------------------------------------------
 // prep: norms, maxima and fp32 bias copies
 // -------------------------------------------------------------------------------------------------
@@ -165,15 +179,18 @@ __global__ __launch_bounds__(256) void l2sq_prep_rows(const float* __restrict__ 
                                                       const double* __restrict__ p, const double* __restrict__ qb,
                                                       const double* __restrict__ db_for_ge, double* __restrict__ norm,
                                                       float* __restrict__ qb32, float* __restrict__ p32,
-                                                      unsigned long long* __restrict__ maxima /*[norm, |qb|]*/) {
+                                                      unsigned long long* __restrict__ maxima /*[norm, |qb|]*/,
+                                                      float* __restrict__ qscale = nullptr,
+                                                      double* __restrict__ l1 = nullptr) {
     __shared__ double sM[4][2];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     double mx_norm = 0.0, mx_bias = 0.0;
     for (int64_t row = (int64_t)blockIdx.x * 4 + wave; row < m; row += (int64_t)gridDim.x * 4) {
         const float* x = X + row * (int64_t)d;
-        // the norm only bounds errors (it is inflated by 1e-12 below), so any summation order will do: float4
+        // the norms only bound errors (they are inflated by 1e-12 below), so any summation order will do: float4
         // loads and four independent sums when rows are whole float4s
-        double s0 = 0.0, s1 = 0.0, s2 = 0.0, s3 = 0.0;
+        double s0 = 0.0, s1 = 0.0, s2 = 0.0, s3 = 0.0, a1 = 0.0;
+        float amax = 0.0f;
         int k0 = 0;
         if ((d & 3) == 0) {
             const float4* x4 = reinterpret_cast<const float4*>(x);
@@ -183,12 +200,22 @@ __global__ __launch_bounds__(256) void l2sq_prep_rows(const float* __restrict__ 
                 s1 += (double)v.y * (double)v.y;
                 s2 += (double)v.z * (double)v.z;
                 s3 += (double)v.w * (double)v.w;
+                a1 += ((double)fabsf(v.x) + (double)fabsf(v.y)) + ((double)fabsf(v.z) + (double)fabsf(v.w));
+                amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
             }
             k0 = d;
         }
-        for (int k = k0 + lane; k < d; k += 64) s0 += (double)x[k] * (double)x[k];
+        for (int k = k0 + lane; k < d; k += 64) {
+            s0 += (double)x[k] * (double)x[k];
+            a1 += (double)fabsf(x[k]);
+            amax = fmaxf(amax, fabsf(x[k]));
+        }
         double s = (s0 + s1) + (s2 + s3);
-        for (int o = 32; o >= 1; o >>= 1) s += __shfl_xor(s, o, 64);
+        for (int o = 32; o >= 1; o >>= 1) {
+            s += __shfl_xor(s, o, 64);
+            a1 += __shfl_xor(a1, o, 64);
+            amax = fmaxf(amax, __shfl_xor(amax, o, 64));
+        }
         const double nrm = std::sqrt(s) * (1.0 + 1e-12);
         mx_norm = fmax(mx_norm, nrm);
         mx_bias = fmax(mx_bias, std::fabs(qb[row]));
@@ -197,6 +224,10 @@ __global__ __launch_bounds__(256) void l2sq_prep_rows(const float* __restrict__ 
             qb32[row] = (float)qb[row];
             // "ge" = q + db for the cost of the certificate, "p" = p for the row side
             p32[row] = db_for_ge ? (float)(p[row] + db_for_ge[row]) : (float)p[row];
+            if (qscale) {
+                qscale[row] = amax;  // the int8 copy turns it into its block's scale
+                l1[row] = a1 * (1.0 + 1e-12);
+            }
         }
     }
     if (lane == 0) {
@@ -286,6 +317,111 @@ __global__ __launch_bounds__(256) void l2sq_split_bf16(const float* __restrict__
             }
         }
         __syncthreads();  // the tile is rewritten by the next item
+    }
+}
+
+// -------------------------------------------------------------------------------------------------
+// int8 split copy (HM_INT8X3) in the operand order of v_mfma_i32_32x32x32_i8, with the split-bf16 copy's geometry
+// counted in 4-byte words: a block of 32 rows is a run of 4 KiB chunks, here of 64 features (two bytes per feature,
+// ld = i8_ld(d) words per row); a chunk holds four 1 KiB tiles, K-step s (32 features) and limb p (h, then l) at
+// (2s + p) KiB; within a tile the 16 bytes at lane 32h + r are features 16h .. 16h+15 of the K-step for row r.
+// Padding features and rows are zero. The sweeps' unit arithmetic (split_unit, the LDS ring) is unchanged.
+//
+// Error terms of a pair (x, y), in dot units. With xq = s v and e = x - xq, |e_k| <= 0.51 s (v is rint of the fp32
+// product x * fl(1/s), within 0.504 of x / s):
+//   |x.y - xq.yq| <= sum |e_x||y| + sum |xq||e_y| <= alpha_x beta_y + alpha_y beta_x,
+//       alpha = 0.51 s,  beta = ||x||_1 + 0.51 s d (at least ||x||_1 and ||xq||_1);
+//   the sweep drops the limb product: s_x s_y |sum l_x l_y| <= gamma_x gamma_y,  gamma = s ||l||_2;
+//   the fp32 conversion of the two int32 sums (four roundings of values at most sum (|v_x| + 256)(|v_y| + 256) s_x s_y
+//       in magnitude) <= 5 u rho_x rho_y,  rho = ||x||_2 + 257 s sqrt(d).
+// Terms per row (alpha, beta, gamma, rho) go to qterm; their maxima over the side to qmax (ordered keys).
+// -------------------------------------------------------------------------------------------------
+inline int i8_features(int d) { return (d + 255) / 256 * 256; }  // whole groups of 4 chunks (the sweep's unroll)
+inline int i8_words(int d) { return i8_features(d) / 2; }
+inline int i8_ld(int d) { return i8_words(d) + (i8_words(d) % 512 == 0 ? KC : 0); }
+
+// One workgroup per 32-row block (grid-stride): the block's scale from its rows' maxima (which `qscale` holds on
+// entry and receives the block scale in their place), then per chunk the block's 32 x 64 features pass through LDS
+// (coalesced reads) and thread t quantizes and writes unit t of the chunk (coalesced writes); ||l||_2^2 is summed
+// exactly.
+__global__ __launch_bounds__(256) void l2sq_split_i8(const float* __restrict__ X, int64_t rows, int64_t padded_rows,
+                                                     int d, int sd, int ld, float* __restrict__ qscale,
+                                                     const double* __restrict__ l1, const double* __restrict__ norm,
+                                                     unsigned int* __restrict__ out, double* __restrict__ qterm,
+                                                     unsigned long long* __restrict__ qmax) {
+    __shared__ float tile[32][65];
+    __shared__ unsigned int sl[4][32];
+    __shared__ float sScale;
+    const int nch = sd / KC;  // 64-feature chunks
+    const int t = threadIdx.x;
+    const int s = t >> 7, p = (t >> 6) & 1, h = (t >> 5) & 1, r = t & 31;  // unit t: tile 2s + p, lane 32h + r
+    const int64_t blocks = padded_rows >> 5;
+    double mq[4] = {0.0, 0.0, 0.0, 0.0};
+    uint4* out4 = reinterpret_cast<uint4*>(out);
+    for (int64_t blk = blockIdx.x; blk < blocks; blk += gridDim.x) {
+        const int64_t row = blk * 32 + r;
+        if (t < 64) {
+            float a = (t < 32 && row < rows) ? qscale[row] : 0.0f;
+            for (int o = 16; o >= 1; o >>= 1) a = fmaxf(a, __shfl_xor(a, o, 64));
+            if (t == 0) sScale = i8_scale(a);
+        }
+        __syncthreads();
+        const float sb = sScale;
+        if (t < 32 && row < rows) qscale[row] = sb;
+        const float inv = 1.0f / sb;
+        unsigned int lsq = 0u;
+        for (int c = 0; c < nch; ++c) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int e = t + 256 * i;
+                const int rr = e >> 6, f = e & 63;
+                const int64_t xr = blk * 32 + rr;
+                const int k = c * 64 + f;
+                tile[rr][f] = (xr < rows && k < d) ? X[xr * d + k] : 0.0f;
+            }
+            __syncthreads();
+            const float* src = &tile[r][s * 32 + h * 16];
+            unsigned int wv[4];
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                unsigned int word = 0u;
+#pragma unroll
+                for (int e2 = 0; e2 < 4; ++e2) {
+                    const int v = (int)rintf(src[4 * g + e2] * inv);
+                    const int hi = (v + 128) >> 8;
+                    const int lo = v - hi * 256;
+                    lsq += (unsigned int)(lo * lo);
+                    word |= (unsigned int)((p ? lo : hi) & 0xff) << (8 * e2);
+                }
+                wv[g] = word;
+            }
+            out4[(blk * 32 * (int64_t)ld + (int64_t)c * 1024) / 4 + t] = make_uint4(wv[0], wv[1], wv[2], wv[3]);
+            __syncthreads();  // the tile is rewritten by the next chunk
+        }
+        if (p == 0) sl[2 * s + h][r] = lsq;  // the p = 1 threads summed the same values
+        __syncthreads();
+        if (t < 32 && row < rows) {
+            const unsigned long long l2 = (unsigned long long)sl[0][t] + sl[1][t] + sl[2][t] + sl[3][t];
+            const double sc = (double)sb;
+            const double q[4] = {0.51 * sc, l1[row] + 0.51 * sc * d, sc * std::sqrt((double)l2) * (1.0 + 1e-12),
+                                 norm[row] + 257.0 * sc * std::sqrt((double)d) * (1.0 + 1e-12)};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                qterm[row * 4 + e] = q[e];
+                mq[e] = fmax(mq[e], q[e]);
+            }
+        }
+        __syncthreads();  // sl and sScale are rewritten by the next block
+    }
+    if (t < 64) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            for (int o = 32; o >= 1; o >>= 1) mq[e] = fmax(mq[e], __shfl_xor(mq[e], o, 64));
+        }
+        if (t == 0) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) atomicMax(&qmax[e], double_key(mq[e]));
+        }
     }
 }
 
@@ -1210,6 +1346,9 @@ __device__ __forceinline__ void sweep_epilogue_w(const float (&tot)[NB][16], int
                 }
                 if (STATS) cert_fast(okj, w, ges[cc], pi, qbi, slack, tden, cmax, tnum, tcnt, near);
             }
+            // one group of pairs at a time: the scheduler would otherwise hoist every group's LDS reads to the
+            // top of the epilogue and spill them
+            __builtin_amdgcn_sched_barrier(0);
         }
     }
     if (STATS && near) {
@@ -1512,6 +1651,213 @@ __global__ __launch_bounds__(THREADS_W) void l2sq_sweep_split_w(
     }
 }
 
+// int8 sweep over 256-row X panels (HM_INT8X3): the panels, Y ring, X operand sets and epilogue of
+// l2sq_sweep_split_w on the int8 copies (64 features per 4 KiB chunk) and v_mfma_i32_32x32x32_i8. Per K-step of
+// 32 features: A[y] += Yh*Xh, B[y] += Yh*Xl, B[y] += Yl*Xh, exact in int32 (|A|, |B| <= 32512 d < 2^31 for
+// d <= 65536), so the dot needs no blocking: after the tile's last chunk t = ((65536 A + 256 B) s_y) s_x in fp32.
+__device__ __forceinline__ void i8_pass(v16i (&acc)[NB], const YHalf& yp, const float4& x4) {
+    const v4i xv = __builtin_bit_cast(v4i, x4);
+    acc[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(v4i, yp.b0), xv, acc[0], 0, 0, 0);
+    acc[1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(v4i, yp.b1), xv, acc[1], 0, 0, 0);
+    acc[2] = __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(v4i, yp.b2), xv, acc[2], 0, 0, 0);
+    acc[3] = __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(v4i, yp.b3), xv, acc[3], 0, 0, 0);
+}
+
+template <int K1, bool COLS, bool APPEND = false>
+__global__ __launch_bounds__(THREADS_W) void l2sq_sweep_i8_w(
+    const float* __restrict__ X, const float* __restrict__ Y, int64_t xb, int64_t xe, int64_t n, int d, int ld,
+    const float* __restrict__ qb32, const float* __restrict__ db32, const float* __restrict__ p32,
+    const float* __restrict__ ge32, float scale, int64_t seg_len, int P, int S, Entry* __restrict__ part,
+    Entry* __restrict__ colpart, unsigned int* __restrict__ colthr, double* __restrict__ blockstats, int STATS,
+    CertArgs cert, const float* __restrict__ xqs, const float* __restrict__ yqs, const float* __restrict__ wthr = nullptr, int* __restrict__ wcnt = nullptr,
+    int* __restrict__ wbuf = nullptr,
+    int wcap = 0, unsigned int* __restrict__ rowthr = nullptr) {
+    static_assert(!(APPEND && COLS), "the wide pass keeps no column lists");
+    constexpr int AHEAD = 3;      // Y chunks in flight ahead of the one multiplied (4-stage ring)
+    constexpr int VMEM_STEP = 6;  // vector-memory instructions a chunk issues (4 X, then 2 Y)
+    int64_t panel, seg;
+    sweep_block(blockIdx.x, P, S, panel, seg);
+    if (panel >= P || seg >= S) return;  // grid padding (uniform per workgroup, before any barrier)
+    __shared__ float4 sY0[1024], sY1[1024], sY2[1024], sY3[1024];  // LDS ring (Y chunk: 4 blocks x 4 KiB)
+    __shared__ double sQB64[STATS_LDS(BXW)], sDB64[STATS_LDS(BY)];  // fp64 biases for the certificate's near pairs
+    __shared__ float sDB[BY];
+    __shared__ float sGE[BY];
+    __shared__ float sC[COLS ? CROWS_W * CSTW : 1];
+    __shared__ double sRed[WAVES_W][5];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int h = lane >> 5;
+    const int r = lane & 31;
+    const int64_t rows = xe - xb;
+    const int64_t x0 = xb + panel * BXW;
+    const int64_t y_begin = seg * seg_len;
+    const int64_t y_end = (y_begin + seg_len < n) ? (y_begin + seg_len) : n;
+    const int64_t row = x0 + wave * 32 + r;
+    const bool ok = row < xe;
+    const float qbi = (ok && !APPEND) ? qb32[row] : 0.0f;
+    const float pi = (STATS && ok) ? p32[row] : 0.0f;
+    const float wt = (APPEND && ok) ? wthr[row] : INFINITY;
+    double num64 = 0.0, den64 = 0.0;
+    unsigned int cnt = 0u;
+    float cmax = 0.0f;
+    const float slack = row_cert_slack(STATS, cert, row, ok, scale);
+    const float sx = ok ? xqs[row] : 0.0f;
+    if (!APPEND && tid < BXW) sQB64[tid] = (STATS && x0 + tid < xe) ? cert.qb[x0 + tid] : 0.0;
+
+    const int nchunks = d / KC;
+    const int64_t bstride = (int64_t)ld * 32;          // words per 32-row block
+    const float* Xw = X + ((x0 >> 5) + wave) * bstride;  // this wave's X block
+    const unsigned lane16 = (unsigned)lane * 16u;
+    const unsigned t16 = (unsigned)(tid & 255) * 16u;
+    const unsigned bstep = (unsigned)(bstride * 4);     // bytes between consecutive 32-row blocks
+    const int bsel = tid >> 8;                          // Y blocks 0 and 2 (waves 0-3) or 1 and 3 (waves 4-7)
+
+    auto load_x = [&](XOps& o, int cc) {
+        const float* b = Xw + cc * 1024;
+        o.h0 = ld16(b, lane16);
+        o.l0 = ld16(b, 1024u + lane16);
+        o.h1 = ld16(b, 2048u + lane16);
+        o.l1 = ld16(b, 3072u + lane16);
+    };
+    // Y chunk AHEAD chunks past the one multiplied (ta, ca); past the segment any in-bounds chunk will do, its
+    // data is never multiplied. Thread t's 16 bytes of block 2i + bsel go to stage + (2i + bsel)*4 KiB +
+    // (t % 256)*16: one wave instruction fills 1 KiB.
+    int64_t ta = y_begin;
+    int ca = 0;
+    auto load_ahead = [&](float4* stage) {
+        const bool past = ta >= y_end;
+        const char* b = reinterpret_cast<const char*>(Y + ((past ? y_begin : ta) >> 5) * bstride + (past ? 0 : ca) * 1024);
+        float4* dst = stage + bsel * 256 + (wave & 3) * 64;
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+            __builtin_amdgcn_global_load_lds(b + (2 * i + bsel) * bstep + t16,
+                                             (__attribute__((address_space(3))) void*)(dst + i * 512), 16, 0, 0);
+        ++ca;
+        const bool wrap = ca == nchunks;
+        ca = wrap ? 0 : ca;
+        ta = wrap ? ta + BY : ta;
+    };
+    // half p (0: hi, 1: lo) of the operands of K-step ks of the Y chunk in `stage`
+    auto read_half = [&](YHalf& o, const float4* stage, int ks, int p) {
+        const float4* src = stage + ks * 128 + p * 64 + lane;
+        o.b0 = src[0];
+        o.b1 = src[256];
+        o.b2 = src[512];
+        o.b3 = src[768];
+    };
+
+    XOps xs0, xs1;  // X operands: chunk c in set c % 2
+    YHalf yh, yl;   // Y operands of the pass in flight (hi and lo halves of one K-step)
+    load_ahead(sY0);
+    load_ahead(sY1);
+    load_ahead(sY2);
+    load_x(xs0, 0);
+    wait_vmcnt<0>();
+    __syncthreads();
+
+    v16i accA[NB], accB[NB];  // sum h_y h_x and sum (h_y l_x + l_y h_x) of the tile's dots
+
+    // chunk c (U = c % 4: Y stage U, X set U % 2)
+    auto step = [&](auto uc, int c) {
+        constexpr int U = decltype(uc)::value;
+        XOps& xs = xset2<U>(xs0, xs1);
+        float4* cur = xset_stage<U>(sY0, sY1, sY2, sY3);
+        float4* fill = xset_stage<(U + 3) % 4>(sY0, sY1, sY2, sY3);
+        // the next chunk's X into the other set (last used by chunk c - 1)
+        load_x(xset2<U + 1>(xs0, xs1), c + 1 == nchunks ? 0 : c + 1);
+        // K-step 0, then K-step 1's operands, all read before the barrier
+        read_half(yh, cur, 0, 0);
+        read_half(yl, cur, 0, 1);
+        i8_pass(accA, yh, xs.h0);
+        i8_pass(accB, yh, xs.l0);
+        __builtin_amdgcn_sched_barrier(0);
+        read_half(yh, cur, 1, 0);
+        i8_pass(accB, yl, xs.h0);
+        __builtin_amdgcn_sched_barrier(0);
+        read_half(yl, cur, 1, 1);
+        // the Y chunk AHEAD further into the stage chunk - 1 used (all its reads retired at the previous barrier);
+        // this wave's loads of the next chunk's Y were issued AHEAD - 1 chunks back, so at most the later chunks'
+        // instructions may still be in flight at the barrier
+        load_ahead(fill);
+        ring_barrier<(AHEAD - 1) * VMEM_STEP>();
+        i8_pass(accA, yh, xs.h1);
+        i8_pass(accB, yh, xs.l1);
+        i8_pass(accB, yl, xs.h1);
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    using I2 = std::integral_constant<int, 2>;
+    using I3 = std::integral_constant<int, 3>;
+
+    for (int64_t ytile = y_begin; ytile < y_end; ytile += BY) {
+        // biases of this tile's Y rows (read in the epilogue, after at least one chunk barrier)
+        if (tid < BY) {
+            const int64_t j = ytile + tid;
+            sDB[tid] = j < y_end ? db32[j] : 0.0f;
+            sGE[tid] = (STATS && j < y_end) ? ge32[j] : 0.0f;
+            if (!APPEND) sDB64[tid] = (STATS && j < y_end) ? cert.db[j] : 0.0;
+        }
+        // the accumulators start from zero here rather than after the previous epilogue, so that they are dead
+        // (their registers free) while the epilogue runs
+#pragma unroll
+        for (int y = 0; y < NB; ++y) {
+#pragma unroll
+            for (int q = 0; q < 16; ++q) { accA[y][q] = 0; accB[y][q] = 0; }
+        }
+        for (int c = 0; c < nchunks; c += 4) {
+            step(I0{}, c);
+            step(I1{}, c + 1);
+            step(I2{}, c + 2);
+            step(I3{}, c + 3);
+        }
+        // fp32 dots t = ((65536 A + 256 B) s_y) s_x, with s_y the scale of Y block y (uniform over the wave)
+        float outer[NB][16];
+#pragma unroll
+        for (int y = 0; y < NB; ++y) {
+            const float sy = ytile + 32 * y < n ? yqs[ytile + 32 * y] : 0.0f;
+#pragma unroll
+            for (int q = 0; q < 16; ++q) {
+                const float u = fmaf(65536.0f, (float)accA[y][q], 256.0f * (float)accB[y][q]);
+                outer[y][q] = (u * sy) * sx;
+            }
+        }
+        sweep_epilogue_w<K1, COLS, APPEND>(outer, row, ok, qbi, pi, wt, ytile == y_begin, tid, wave, h, r, ytile,
+                                           y_end, x0, xb, rows, seg, panel, n, scale, STATS, slack, sQB64, sDB64, sDB,
+                                           sGE, sC,
+                                           part,
+                                           colpart, colthr, wcnt, wbuf, wcap, num64, den64, cnt, cmax, rowthr);
+    }
+    wait_vmcnt<0>();  // the loads ahead into LDS land before the workgroup can end
+    if (STATS) {
+        // the maximum violation (slot 3) is taken exactly from the fp64 row lists after the sweep
+        double v[5] = {num64, den64, (double)cnt, 0.0, (double)cmax};
+#pragma unroll
+        for (int e = 0; e < 5; ++e) {
+            for (int o = 32; o >= 1; o >>= 1) {
+                const double t = __shfl_xor(v[e], o, 64);
+                v[e] = (e >= 3) ? fmax(v[e], t) : v[e] + t;
+            }
+        }
+        if (lane == 0) {
+#pragma unroll
+            for (int e = 0; e < 5; ++e) sRed[wave][e] = v[e];
+        }
+        __syncthreads();
+        if (tid == 0) {
+            double o[5];
+            for (int e = 0; e < 5; ++e) {
+                o[e] = sRed[0][e];
+                for (int w = 1; w < WAVES_W; ++w) o[e] = (e >= 3) ? fmax(o[e], sRed[w][e]) : o[e] + sRed[w][e];
+            }
+            double* dst = blockstats + (seg * P + panel) * 5;
+            for (int e = 0; e < 5; ++e) dst[e] = o[e];
+        }
+    }
+}
+
 // deterministic reduction of per-block certificate partials (single block); later chunks accumulate
 __global__ void l2sq_reduce_stats(const double* __restrict__ blockstats, int64_t blocks, double* __restrict__ stats,
                                   int linf, int accumulate) {
@@ -1549,6 +1895,10 @@ struct BoundArgs {
     double acc_rel;   // relative bound on |dot32 - dot| in units of ||x||*||y||, plus fp64 slack
     double db_rel;    // relative bound contribution of fp32 bias rounding, in units of max|bias|
     double abs_slack; // absolute slack (flushed denormals)
+    // int8 sweep: the finalized side's per-row error terms (alpha, beta, gamma, rho; l2sq_split_i8) and the
+    // candidate side's maxima of them; null otherwise
+    const double* qterm = nullptr;
+    const unsigned long long* qmax = nullptr;
 };
 
 // Lists of row r: L in [0, nlists), each of KL entries at base + (((L / G) * R + r) * G + L % G) * KL (sorted,
@@ -1648,7 +1998,14 @@ __global__ __launch_bounds__(256) void l2sq_finalize(
     const double bmax = key_double(bmaxima[0]);
     const double dmax = key_double(bmaxima[1]);
     const double nxy = scale * anorm[row] * bmax;
-    const double b = (nxy * bnd.acc_rel + dmax * bnd.db_rel + fabs(abias[row]) * 1e-15 + bnd.abs_slack) * (1.0 + 1e-6);
+    double b = (nxy * bnd.acc_rel + dmax * bnd.db_rel + fabs(abias[row]) * 1e-15 + bnd.abs_slack) * (1.0 + 1e-6);
+    if (bnd.qterm) {
+        // quantization, dropped limb product and conversion terms of the int8 sweep (l2sq_split_i8)
+        const double* qt = bnd.qterm + row * 4;
+        const double ma = key_double(bnd.qmax[0]), mb = key_double(bnd.qmax[1]);
+        const double mg = key_double(bnd.qmax[2]), mr = key_double(bnd.qmax[3]);
+        b += scale * (qt[0] * mb + qt[1] * ma + qt[2] * mg + 5.0 * 0x1p-24 * qt[3] * mr) * (1.0 + 1e-6);
+    }
     // Candidates outside the kept list were dropped by a full partial list (w <= tail) or by the merge
     // (w <= tw[KM-1]); they cannot reach the exact top-k when that bound is below wk - 2b.
     const bool merge_dropped = nreal > KM;
@@ -1819,11 +2176,13 @@ __global__ void l2sq_wide_gather(const float* __restrict__ src, int ld, const in
     }
 }
 
-// The same for split copies (operand order): item (destination 32-row block, chunk, 16-byte unit of the row's
-// eight, row within the block); consecutive threads write consecutive units.
+// The same for split copies (operand order, split-bf16 or int8): item (destination 32-row block, chunk, 16-byte unit
+// of the row's eight, row within the block); consecutive threads write consecutive units. With `qsrc` (int8) the
+// rows' scales are gathered too.
 __global__ void l2sq_wide_gather_split(const float* __restrict__ src, int ld, int sd, const int* __restrict__ redo,
                                        int q0, int Q, int Qpad, const float* __restrict__ redo_thr,
-                                       float* __restrict__ dst, float* __restrict__ thr, int* __restrict__ cnt) {
+                                       float* __restrict__ dst, float* __restrict__ thr, int* __restrict__ cnt,
+                                       const float* __restrict__ qsrc, float* __restrict__ qdst) {
     const int nch = sd / KC;
     const int64_t total = (int64_t)Qpad * nch * 8;
     const uint4* s4 = reinterpret_cast<const uint4*>(src);
@@ -1841,6 +2200,7 @@ __global__ void l2sq_wide_gather_split(const float* __restrict__ src, int ld, in
     for (int q = blockIdx.x * blockDim.x + threadIdx.x; q < Qpad; q += gridDim.x * blockDim.x) {
         thr[q] = q < Q ? redo_thr[q0 + q] : INFINITY;
         cnt[q] = 0;
+        if (qsrc) qdst[q] = q < Q ? qsrc[redo[q0 + q]] : 0.0f;
     }
 }
 
@@ -1946,6 +2306,7 @@ __global__ void l2sq_wide_merge(const double* __restrict__ pv, const int* __rest
 // Scratch of the wide pass (workspace slices; layout() sizes them).
 struct WideBufs {
     float* redo_thr;   // [m + n] thresholds of the rows a finalize queued, by queue slot
+    float* qs;         // [panel_rows(WIDE_ROWS)] int8 scales of the gathered rows (int8 sweep)
     float* rows;       // [panel_rows(WIDE_ROWS) * ld] gathered sweep rows
     float* thr;        // [panel_rows(WIDE_ROWS)]
     int* cnt;          // [panel_rows(WIDE_ROWS)]
@@ -1958,13 +2319,27 @@ struct WideBufs {
     unsigned int* rowthr;  // [rows of a sweep launch] the sweeps' shared row thresholds (row_threshold_*)
 };
 
+// Per-side data of the int8 sweep (HM_INT8X3; null otherwise): row scales, ||.||_1, the rows' error terms
+// (l2sq_split_i8) and the maxima of each side's terms (X side at qmax[0..3], Y side at qmax[4..7]).
+struct I8Bufs {
+    float* xqs = nullptr;
+    float* yqs = nullptr;
+    double* xl1 = nullptr;
+    double* yl1 = nullptr;
+    double* xterm = nullptr;
+    double* yterm = nullptr;
+    unsigned long long* qmax = nullptr;
+};
+
 // Resolves the rows a finalize queued (defined in pricing_l2sq.hip): the wide pass over them, then the exact full
 // rescan of rows that overflowed it. A / B are the fp32 row and candidate sides (row stride d), Asw / Bsw their
-// sweep copies (split-bf16 with row stride ld when `split`, else A / B), cand32 the candidates' fp32 biases.
+// sweep copies (split-bf16 or int8 with row stride ld when `split`, else A / B), cand32 the candidates' fp32 biases,
+// aqs / bqs the int8 scales of both sides (null unless the sweep is the int8 one).
 int wide_resolve(hipStream_t st, bool split, bool two_level, const float* A, const float* Asw, const float* B,
                  const float* Bsw, int64_t nb, int d, int sd, int ld, const float* cand32, const double* abias,
                  const double* bbias, double scale, int k, const int* redo, const int* redo_count,
-                 double* out_val, int* out_idx, int cols, int cbase, const WideBufs& w, double* rpv, int* rpi);
+                 double* out_val, int* out_idx, int cols, int cbase, const WideBufs& w, double* rpv, int* rpi,
+                 const float* aqs, const float* bqs);
 
 namespace {
 
@@ -2042,7 +2417,9 @@ inline int split_ld(int d) { return split_features(d) + (split_features(d) % 512
 inline int64_t panel_rows(int64_t rows, int bx = BX) { return (rows + bx - 1) / bx * bx; }
 
 // X rows per sweep workgroup: 256 for the split sweep with outer sums (l2sq_sweep_split_w), else 128
-inline int sweep_panel(int d, uint32_t flags) { return ((flags & HM_BF16X3) && d > KC * FLUSH_SPLIT) ? BXW : BX; }
+inline int sweep_panel(int d, uint32_t flags) {
+    return ((flags & HM_INT8X3) || ((flags & HM_BF16X3) && d > KC * FLUSH_SPLIT)) ? BXW : BX;
+}
 
 // Rows per internal chunk of the swept side (m rows against n): balanced chunks of whole bx-row panels, and with
 // fused columns the chunk's column partial lists (kl entries per panel and column) within COLPART_CAP.
@@ -2139,7 +2516,7 @@ template <class A>
 void layout(A& a, int64_t m, int64_t n, int d, int k, uint32_t flags, double** xnorm, double** ynorm, float** qb32,
             float** p32, float** db32, float** ge32, unsigned long long** maxima, Entry** part, Entry** colpart,
             unsigned int** colthr, double** cval, int** cidx, double** blockstats, int** redo, int** redo_count,
-            float** xsplit, float** ysplit, double** rpv, int** rpi, WideBufs* wide) {
+            float** xsplit, float** ysplit, double** rpv, int** rpi, WideBufs* wide, I8Bufs* q8) {
     const CallPlan c = plan_call(m, n, d, k, flags);
     const int64_t panels = c.ch / c.bx;
     size_t part_entries = (size_t)c.plan.S * c.ch * 2 * c.kl;
@@ -2161,8 +2538,9 @@ void layout(A& a, int64_t m, int64_t n, int d, int k, uint32_t flags, double** x
     *blockstats = a.template take<double>((size_t)5 * panels * c.plan.S);
     *redo = a.template take<int>((size_t)(m + n));
     *redo_count = a.template take<int>(2);
-    const bool split = (flags & HM_BF16X3) != 0;
-    const size_t ldw = (size_t)split_ld(d);
+    const bool i8 = (flags & HM_INT8X3) != 0;
+    const bool split = (flags & (HM_BF16X3 | HM_INT8X3)) != 0;
+    const size_t ldw = (size_t)(i8 ? i8_ld(d) : split_ld(d));
     // split copies cover whole 256-row panels: either side may be the swept one
     *xsplit = a.template take<float>(split ? (size_t)panel_rows(m, BXW) * ldw : 1);
     *ysplit = a.template take<float>(split ? (size_t)panel_rows(n, BXW) * ldw : 1);
@@ -2180,6 +2558,17 @@ void layout(A& a, int64_t m, int64_t n, int d, int k, uint32_t flags, double** x
     wide->redo3_thr = a.template take<float>((size_t)(m + n));
     wide->counts = a.template take<int>(4);
     wide->rowthr = a.template take<unsigned int>((size_t)std::max<int64_t>(std::max<int64_t>(c.ch, c.ch2), 1));
+    wide->qs = a.template take<float>((size_t)wq);
+    *q8 = I8Bufs{};
+    if (i8) {
+        q8->xqs = a.template take<float>((size_t)m);
+        q8->yqs = a.template take<float>((size_t)n);
+        q8->xl1 = a.template take<double>((size_t)m);
+        q8->yl1 = a.template take<double>((size_t)n);
+        q8->xterm = a.template take<double>((size_t)m * 4);
+        q8->yterm = a.template take<double>((size_t)n * 4);
+        q8->qmax = a.template take<unsigned long long>(8);
+    }
 }
 
 // Exact rescan of the rows queued by a finalize: reads the queue length back (one host synchronisation), then
@@ -2227,7 +2616,7 @@ int run_bidir(hipStream_t st, const float* X, const float* Y, int64_t m, int64_t
               const float* ge32, Entry* part, Entry* colpart, unsigned int* colthr, double* cval, int* cidx,
               double* blockstats, int* redo, int* redo_count, double* row_val, int* row_idx, double* col_val,
               int* col_idx, double* stats, float* xsplit, float* ysplit, double* rpv, int* rpi,
-              const WideBufs& wide) {
+              const WideBufs& wide, const I8Bufs& q8) {
     // K1: entries per partial list of the sweep; KM: candidates the finalize merges and keeps
     const CallPlan cp = plan_call(m, n, d, k, flags);
     if (cp.kl != K1 || cp.km != KM) return fail(HM_EINVAL, "l2sq pricing: list sizes %d/%d do not match the plan %d/%d", K1, KM, cp.kl, cp.km);
@@ -2236,19 +2625,32 @@ int run_bidir(hipStream_t st, const float* X, const float* Y, int64_t m, int64_t
     const bool swapped = cp.swapped;
     const bool want_stats = (flags & HM_STATS) != 0;
     const int linf = (flags & HM_LINF) ? 1 : 0;
-    const bool split = (flags & HM_BF16X3) != 0;
+    const bool i8 = (flags & HM_INT8X3) != 0;
+    const bool split = (flags & (HM_BF16X3 | HM_INT8X3)) != 0;  // the sweep reads operand-order copies
     const int flush = KC * (split ? FLUSH_SPLIT : FLUSH_CHUNKS);
-    const bool two_level = d > flush;
+    const bool two_level = i8 || d > flush;  // the int8 sweep is always the 256-row one
     const bool vec4 = split || (d % 4) == 0;
-    const int sd = split ? split_features(d) : d;  // swept features (4-byte words per row of the split copy)
-    const int ld = split ? split_ld(d) : d;         // sweep row stride in 4-byte words
+    // swept 4-byte words per row of the copy, and its row stride
+    const int sd = i8 ? i8_words(d) : split ? split_features(d) : d;
+    const int ld = i8 ? i8_ld(d) : split ? split_ld(d) : d;
     const float* SX = split ? xsplit : X;
     const float* SY = split ? ysplit : Y;
     const int64_t ch = cp.ch;
     const DirPlan plan = cp.plan;
     const int bx = cp.bx;
     unsigned int* rowthr = wide.rowthr;
-    if (split) {
+    if (i8) {
+        // the row scales and ||.||_1 come from the prep pass; the copies add ||l||_2 and the error terms
+        hipLaunchKernelGGL(zero_words, dim3(1), dim3(64), 0, st, q8.qmax, 8);
+        hipLaunchKernelGGL(l2sq_split_i8, dim3((unsigned)std::min<int64_t>(panel_rows(m, BXW) / 32, 8192)), dim3(256),
+                           0, st, X, m, panel_rows(m, BXW), d, sd, ld, q8.xqs, q8.xl1, xnorm,
+                           reinterpret_cast<unsigned int*>(xsplit), q8.xterm, q8.qmax);
+        HM_LAUNCH_CHECK("l2sq_split_i8");
+        hipLaunchKernelGGL(l2sq_split_i8, dim3((unsigned)std::min<int64_t>(panel_rows(n, BXW) / 32, 8192)), dim3(256),
+                           0, st, Y, n, panel_rows(n, BXW), d, sd, ld, q8.yqs, q8.yl1, ynorm,
+                           reinterpret_cast<unsigned int*>(ysplit), q8.yterm, q8.qmax + 4);
+        HM_LAUNCH_CHECK("l2sq_split_i8");
+    } else if (split) {
         hipLaunchKernelGGL(l2sq_split_bf16, dim3(4096), dim3(256), 0, st, X, m, panel_rows(m, BXW), d, sd, ld,
                            reinterpret_cast<unsigned short*>(xsplit));
         HM_LAUNCH_CHECK("l2sq_split_bf16");
@@ -2269,8 +2671,18 @@ int run_bidir(hipStream_t st, const float* X, const float* Y, int64_t m, int64_t
     const double u = std::ldexp(1.0, -24);
     BoundArgs bnd;
     bnd.acc_rel = split_rel + ea * (split ? 1.01 : 1.0) + u * (1.0 + ea + split_rel) + 4e-15 * (d / 64.0 + 8.0);
+    if (i8) bnd.acc_rel = 1.01 * u + 4e-15 * (d / 64.0 + 8.0);  // the rounding of w; the dot's terms come per row
     bnd.db_rel = 2.0 * u + 1e-15;
     bnd.abs_slack = 1e-30 * (double)d;
+    // finalizes of X rows (candidates Y) and of Y rows (candidates X); the int8 terms are indexed from `base` rows
+    auto bound_for = [&](bool y_rows, int64_t base) {
+        BoundArgs b = bnd;
+        if (i8) {
+            b.qterm = (y_rows ? q8.yterm : q8.xterm) + 4 * base;
+            b.qmax = y_rows ? q8.qmax : q8.qmax + 4;
+        }
+        return b;
+    };
     const CertArgs cert{qb, db, maxima + 2, xnorm};  // the row pass sweeps X rows against Y (maxima[2..3]: Y side)
     int chunk_index = 0;
     const bool row_pass = cp.row_pass;  // a columns-only call without fusion skips it
@@ -2293,7 +2705,11 @@ int run_bidir(hipStream_t st, const float* X, const float* Y, int64_t m, int64_t
 #define NOWIDE (const float*)nullptr, (int*)nullptr, (int*)nullptr, 0
 #define HM_SWEEP(TL, CL)                                                                                             \
     do {                                                                                                             \
-        if (split && TL)                                                                                             \
+        if (i8)                                                                                                      \
+            hipLaunchKernelGGL((l2sq_sweep_i8_w<K1, CL>), grid, dim3(THREADS_W), 0, st, SX, SY, xb, xe, n, sd, ld,   \
+                               qb32, db32, p32, ge32, (float)scale, plan.seg_len, (int)panels, plan.S, part,         \
+                               colpart, colthr, blockstats, (int)want_stats, cert, q8.xqs, q8.yqs, NOWIDE, rowthr); \
+        else if (split && TL)                                                                                        \
             hipLaunchKernelGGL((l2sq_sweep_split_w<K1, CL>), grid, dim3(THREADS_W), 0, st, SX, SY, xb, xe, n, sd,    \
                                ld, qb32, db32, p32, ge32, (float)scale, plan.seg_len, (int)panels, plan.S, part,     \
                                colpart, colthr, blockstats, (int)want_stats, cert, NOWIDE, rowthr);                 \
@@ -2328,12 +2744,13 @@ int run_bidir(hipStream_t st, const float* X, const float* Y, int64_t m, int64_t
             prof_begin(st, "l2sq_finalize");
             hipLaunchKernelGGL((l2sq_finalize<K1, KM, 2, false>), dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, st,
                                X + xb * d, Y, rows, d, 2 * plan.S, part, qb + xb, db, xnorm + xb, maxima + 2, scale, k,
-                               bnd, row_val + xb * k, row_idx + xb * k, redo, wide.redo_thr, redo_count);
+                               bound_for(false, xb), row_val + xb * k, row_idx + xb * k, redo, wide.redo_thr,
+                               redo_count);
             prof_end(st);
             HM_LAUNCH_CHECK("l2sq_finalize");
             if (int rc = wide_resolve(st, split, two_level, X + xb * d, SX + xb * ld, Y, SY, n, d, sd, ld, db32,
                                       qb + xb, db, scale, k, redo, redo_count, row_val + xb * k, row_idx + xb * k, 0,
-                                      0, wide, rpv, rpi))
+                                      0, wide, rpv, rpi, i8 ? q8.xqs + xb : nullptr, q8.yqs))
                 return rc;
         }
         if (fused) {
@@ -2341,13 +2758,13 @@ int run_bidir(hipStream_t st, const float* X, const float* Y, int64_t m, int64_t
             hipLaunchKernelGGL(zero_words, dim3(1), dim3(64), 0, st, reinterpret_cast<unsigned long long*>(redo_count), 1);
             prof_begin(st, "l2sq_col_finalize");
             hipLaunchKernelGGL((l2sq_finalize<K1, KM, 1, true>), dim3((unsigned)((n + 3) / 4)), dim3(256), 0, st, Y, X, n, d,
-                               (int)panels, colpart, db, qb, ynorm, maxima, scale, k, bnd, cval, cidx, redo,
-                               wide.redo_thr, redo_count);
+                               (int)panels, colpart, db, qb, ynorm, maxima, scale, k, bound_for(true, 0), cval, cidx,
+                               redo, wide.redo_thr, redo_count);
             prof_end(st);
             HM_LAUNCH_CHECK("l2sq_col_finalize");
             if (int rc = wide_resolve(st, split, two_level, Y, SY, X + xb * d, SX + xb * ld, rows, d, sd, ld,
                                       qb32 + xb, db, qb + xb, scale, k, redo, redo_count, cval, cidx, 1, (int)xb,
-                                      wide, rpv, rpi))
+                                      wide, rpv, rpi, q8.yqs, i8 ? q8.xqs + xb : nullptr))
                 return rc;
             hipLaunchKernelGGL(l2sq_merge_columns, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, col_val, col_idx,
                                cval, cidx, n, k, chunk_index == 0 ? 1 : 0);
@@ -2369,7 +2786,11 @@ int run_bidir(hipStream_t st, const float* X, const float* Y, int64_t m, int64_t
             HM_LAUNCH_CHECK("fill_u32");
 #define HM_SWEEP2(TL)                                                                                                \
     do {                                                                                                             \
-        if (split && TL)                                                                                             \
+        if (i8)                                                                                                      \
+            hipLaunchKernelGGL((l2sq_sweep_i8_w<K1, false>), grid, dim3(THREADS_W), 0, st, SY, SX, yb, ye, m, sd,    \
+                               ld, db32, qb32, ge32, p32, (float)scale, plan2.seg_len, (int)panels2, plan2.S, part,  \
+                               colpart, colthr, blockstats, 0, CertArgs{}, q8.yqs, q8.xqs, NOWIDE, rowthr);         \
+        else if (split && TL)                                                                                        \
             hipLaunchKernelGGL((l2sq_sweep_split_w<K1, false>), grid, dim3(THREADS_W), 0, st, SY, SX, yb, ye, m, sd, \
                                ld, db32, qb32, ge32, p32, (float)scale, plan2.seg_len, (int)panels2, plan2.S, part,  \
                                colpart, colthr, blockstats, 0, CertArgs{}, NOWIDE, rowthr);                         \
@@ -2393,12 +2814,13 @@ int run_bidir(hipStream_t st, const float* X, const float* Y, int64_t m, int64_t
             prof_begin(st, "l2sq_col_finalize");
             hipLaunchKernelGGL((l2sq_finalize<K1, KM, 2, true>), dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, st,
                                Y + yb * d, X, rows, d, 2 * plan2.S, part, db + yb, qb, ynorm + yb, maxima, scale, k,
-                               bnd, col_val + yb * k, col_idx + yb * k, redo, wide.redo_thr, redo_count);
+                               bound_for(true, yb), col_val + yb * k, col_idx + yb * k, redo, wide.redo_thr,
+                               redo_count);
             prof_end(st);
             HM_LAUNCH_CHECK("l2sq_col_finalize");
             if (int rc = wide_resolve(st, split, two_level, Y + yb * d, SY + yb * ld, X, SX, m, d, sd, ld, qb32,
                                       db + yb, qb, scale, k, redo, redo_count, col_val + yb * k, col_idx + yb * k, 1,
-                                      0, wide, rpv, rpi))
+                                      0, wide, rpv, rpi, i8 ? q8.yqs + yb : nullptr, q8.xqs))
                 return rc;
         }
     }
@@ -2420,8 +2842,8 @@ int run_bidir(hipStream_t st, const float* X, const float* Y, int64_t m, int64_t
         const unsigned long long *maxima, const float *qb32, const float *db32, const float *p32, const float *ge32, \
         ::hm::Entry *part, ::hm::Entry *colpart, unsigned int *colthr, double *cval, int *cidx, double *blockstats, \
         int *redo, int *redo_count, double *row_val, int *row_idx, double *col_val, int *col_idx, double *stats,   \
-        float *xsplit, float *ysplit, double *rpv, int *rpi, const ::hm::WideBufs &wide
+        float *xsplit, float *ysplit, double *rpv, int *rpi, const ::hm::WideBufs &wide, const ::hm::I8Bufs &q8
 #define L2SQ_RUN_PASS                                                                                               \
     st, X, Y, m, n, d, k, scale, flags, qb, db, xnorm, ynorm, maxima, qb32, db32, p32, ge32, part, colpart, colthr, \
         cval, cidx, blockstats, redo, redo_count, row_val, row_idx, col_val, col_idx, stats, xsplit, ysplit, rpv, rpi, \
-        wide
+        wide, q8

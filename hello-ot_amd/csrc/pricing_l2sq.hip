@@ -34,7 +34,8 @@ int wide_round(hipStream_t st, bool split, bool two_level, const float* A, const
                const float* Bsw, int64_t nb, int d, int sd, int ld, const float* cand32, const double* abias,
                const double* bbias, double scale, int k, const int* queue, const float* queue_thr, int count,
                int cap, double* out_val, int* out_idx, int cols, int cbase, const WideBufs& w, double* rpv, int* rpi,
-               int* next, float* next_thr, int* next_count) {
+               int* next, float* next_thr, int* next_count, const float* aqs, const float* bqs) {
+    const bool i8 = aqs != nullptr;  // the int8 sweep: the gathered rows carry their scales
     const int gld = split ? ld : d;  // row stride of the gathered sweep rows
     const int batch = (int)(WIDE_BUF / cap) < WIDE_ROWS ? (int)(WIDE_BUF / cap) : WIDE_ROWS;
     const int spr = cap / WIDE_SLICE;
@@ -45,7 +46,7 @@ int wide_round(hipStream_t st, bool split, bool two_level, const float* A, const
         const int Qpad = (int)panel_rows(Q, bx);
         if (split)
             hipLaunchKernelGGL(l2sq_wide_gather_split, dim3(2048), dim3(256), 0, st, Asw, gld, sd, queue, q0, Q, Qpad,
-                               queue_thr, w.rows, w.thr, w.cnt);
+                               queue_thr, w.rows, w.thr, w.cnt, aqs, w.qs);
         else
             hipLaunchKernelGGL(l2sq_wide_gather, dim3(2048), dim3(256), 0, st, Asw, gld, queue, q0, Q, Qpad, queue_thr,
                                w.rows, w.thr, w.cnt);
@@ -56,13 +57,15 @@ int wide_round(hipStream_t st, bool split, bool two_level, const float* A, const
     hipLaunchKernelGGL(KERNEL, grid, dim3(THREADS), 0, st, w.rows, Bsw, (int64_t)0, (int64_t)Q, nb, sd, gld,        \
                        (const float*)nullptr, cand32, (const float*)nullptr, (const float*)nullptr, (float)scale,    \
                        plan.seg_len, Qpad / bx, plan.S, (Entry*)nullptr, (Entry*)nullptr, (unsigned int*)nullptr,    \
-                       (double*)nullptr, __VA_ARGS__, CertArgs{}, w.thr, w.cnt, w.buf, cap)
-        if (split) {
-            if (two_level) HM_WIDE((l2sq_sweep_split_w<8, false, true>), THREADS_W, 0);
-            else HM_WIDE((l2sq_sweep_split<8, false, true>), 256, 0);
+                       (double*)nullptr, __VA_ARGS__, w.thr, w.cnt, w.buf, cap)
+        if (i8) {
+            HM_WIDE((l2sq_sweep_i8_w<8, false, true>), THREADS_W, 0, CertArgs{}, w.qs, bqs);
+        } else if (split) {
+            if (two_level) HM_WIDE((l2sq_sweep_split_w<8, false, true>), THREADS_W, 0, CertArgs{});
+            else HM_WIDE((l2sq_sweep_split<8, false, true>), 256, 0, CertArgs{});
         } else {
-            if (two_level) HM_WIDE((l2sq_sweep<8, true, false, true>), 256, vec4, 0);
-            else HM_WIDE((l2sq_sweep<8, false, false, true>), 256, vec4, 0);
+            if (two_level) HM_WIDE((l2sq_sweep<8, true, false, true>), 256, vec4, 0, CertArgs{});
+            else HM_WIDE((l2sq_sweep<8, false, false, true>), 256, vec4, 0, CertArgs{});
         }
 #undef HM_WIDE
         HM_LAUNCH_CHECK("l2sq_sweep (wide)");
@@ -90,7 +93,8 @@ int wide_round(hipStream_t st, bool split, bool two_level, const float* A, const
 int wide_resolve(hipStream_t st, bool split, bool two_level, const float* A, const float* Asw, const float* B,
                  const float* Bsw, int64_t nb, int d, int sd, int ld, const float* cand32, const double* abias,
                  const double* bbias, double scale, int k, const int* redo, const int* redo_count,
-                 double* out_val, int* out_idx, int cols, int cbase, const WideBufs& w, double* rpv, int* rpi) {
+                 double* out_val, int* out_idx, int cols, int cbase, const WideBufs& w, double* rpv, int* rpi,
+                 const float* aqs, const float* bqs) {
     static_assert(WIDE_CAP1 % WIDE_SLICE == 0 && WIDE_CAP2 % WIDE_SLICE == 0, "whole slices per row");
     static_assert((WIDE_BUF / WIDE_CAP1) * (WIDE_CAP1 / WIDE_SLICE) <= RESCAN_ITEMS &&
                       (WIDE_BUF / WIDE_CAP2) * (WIDE_CAP2 / WIDE_SLICE) <= RESCAN_ITEMS,
@@ -104,13 +108,13 @@ int wide_resolve(hipStream_t st, bool split, bool two_level, const float* A, con
     prof_begin(st, "l2sq_wide");
     int rc = wide_round(st, split, two_level, A, Asw, B, Bsw, nb, d, sd, ld, cand32, abias, bbias, scale, k, redo,
                         w.redo_thr, count, WIDE_CAP1, out_val, out_idx, cols, cbase, w, rpv, rpi, w.redo2, w.redo2_thr,
-                        w.counts);
+                        w.counts, aqs, bqs);
     int count2 = 0;
     if (!rc) rc = read_count(st, w.counts, &count2);
     if (!rc && count2 > 0)
         rc = wide_round(st, split, two_level, A, Asw, B, Bsw, nb, d, sd, ld, cand32, abias, bbias, scale, k, w.redo2,
                         w.redo2_thr, count2, WIDE_CAP2, out_val, out_idx, cols, cbase, w, rpv, rpi, w.redo3,
-                        w.redo3_thr, w.counts + 1);
+                        w.redo3_thr, w.counts + 1, aqs, bqs);
     prof_end(st);
     if (rc) return rc;
     // rows with more than WIDE_CAP2 candidates near their k-th value: exact scan over all candidates
@@ -145,8 +149,9 @@ extern "C" size_t hm_pricing_l2sq_workspace_bytes(int64_t m, int64_t n, int32_t 
     double* rpv;
     int* rpi;
     WideBufs wide;
+    I8Bufs q8;
     layout(s, m, n, d, k, flags, &a, &b, &c, &e, &f, &g, &mx, &part, &colpart, &thr, &cv, &ci, &bs, &redo, &rc, &xs,
-           &ys, &rpv, &rpi, &wide);
+           &ys, &rpv, &rpi, &wide, &q8);
     if (own_rows) {
         s.template take<double>((size_t)m * k);
         s.template take<int>((size_t)m * k);
@@ -164,6 +169,8 @@ extern "C" int hm_pricing_l2sq(void* stream, const float* X, const float* Y, con
                  (long long)m, (long long)n, d);
     HM_CHECK_ARG(k >= 1 && k <= 32, "l2sq pricing requires 1 <= k <= 32 (k=%d)", k);
     HM_CHECK_ARG(scale == 1.0 || scale == 2.0, "dot_scale must be exactly 1 or 2");
+    HM_CHECK_ARG(!((flags & HM_BF16X3) && (flags & HM_INT8X3)), "HM_BF16X3 and HM_INT8X3 exclude each other");
+    HM_CHECK_ARG(!(flags & HM_INT8X3) || d <= 65536, "the int8 sweep supports d <= 65536 (d=%d)", d);
     HM_CHECK_ARG(!(flags & HM_ROWS) || (row_val && row_idx), "HM_ROWS requires row outputs");
     HM_CHECK_ARG(!(flags & HM_COLS) || (col_val && col_idx), "HM_COLS requires column outputs");
     HM_CHECK_ARG(!(flags & HM_STATS) || stats, "HM_STATS requires a stats output");
@@ -183,10 +190,11 @@ extern "C" int hm_pricing_l2sq(void* stream, const float* X, const float* Y, con
     double* rpv;
     int* rpi;
     WideBufs wide;
+    I8Bufs q8;
     const bool own_rows = internal_rows(flags);
     flags = effective_flags(flags);
     layout(a, m, n, d, k, flags, &xnorm, &ynorm, &qb32, &p32, &db32, &ge32, &maxima, &part, &colpart, &colthr, &cval,
-           &cidx, &blockstats, &redo, &redo_count, &xsplit, &ysplit, &rpv, &rpi, &wide);
+           &cidx, &blockstats, &redo, &redo_count, &xsplit, &ysplit, &rpv, &rpi, &wide, &q8);
     if (own_rows) {
         row_val = a.template take<double>((size_t)m * k);
         row_idx = a.template take<int>((size_t)m * k);
@@ -194,13 +202,14 @@ extern "C" int hm_pricing_l2sq(void* stream, const float* X, const float* Y, con
     hipLaunchKernelGGL(zero_words, dim3(1), dim3(64), 0, st, maxima, 4);
     HM_LAUNCH_CHECK("zero_words");
     // X side: ||x||, qb32, p32 (maxima[0..1] = max||x||, max|qb|); Y side: ||y||, db32, ge32 = q + db
+    // with HM_INT8X3 also the int8 row scales and ||.||_1 of both sides
     hipLaunchKernelGGL(l2sq_prep_rows, dim3(prep_grid(m)), dim3(256), 0, st, X, m, d, p, qb,
-                       (const double*)nullptr, xnorm, qb32, p32, maxima);
+                       (const double*)nullptr, xnorm, qb32, p32, maxima, q8.xqs, q8.xl1);
     HM_LAUNCH_CHECK("l2sq_prep_rows");
     hipLaunchKernelGGL(l2sq_prep_rows, dim3(prep_grid(n)), dim3(256), 0, st, Y, n, d, q, db, db, ynorm,
-                       db32, ge32, maxima + 2);
+                       db32, ge32, maxima + 2, q8.yqs, q8.yl1);
     HM_LAUNCH_CHECK("l2sq_prep_rows");
     return run_k(st, X, Y, m, n, d, k, scale, flags, qb, db, xnorm, ynorm, maxima, qb32, db32, p32, ge32, part,
                  colpart, colthr, cval, cidx, blockstats, redo, redo_count, row_val, row_idx, col_val, col_idx, stats,
-                 xsplit, ysplit, rpv, rpi, wide);
+                 xsplit, ysplit, rpv, rpi, wide, q8);
 }

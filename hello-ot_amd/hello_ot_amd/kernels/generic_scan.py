@@ -48,15 +48,22 @@ def _workspace(nbytes: int, device) -> torch.Tensor:
     return torch.empty(max(int(nbytes), 256), dtype=torch.uint8, device=device)
 
 
-SWEEP_PRECISIONS = ("auto", "fp32", "bf16x3")
-SPLIT_MIN_D = 64  # "auto" sweeps on split-bf16 MFMA from this feature count on (measured faster at d = 64 and 8192)
+SWEEP_PRECISIONS = ("auto", "fp32", "bf16x3", "int8x3")
+SPLIT_MIN_D = 64    # "auto" sweeps on split-bf16 MFMA from this feature count on (faster than fp32 at d = 64)
+INT8_MIN_D = 256    # ... and on the int8 split from this one on (MI355X, whole calls: 1.05x at d = 256, 1.30x at
+                    # 1024, 1.46x at 4096; the C5 sweep 1.85x at 8192)
+INT8_MAX_D = 65536  # the int8 sweep's int32 sums hold up to this many features
 
 
 def sweep_precision(precision: str, d: int) -> str:
     if precision not in SWEEP_PRECISIONS:
         raise ValueError(f"precision must be one of {SWEEP_PRECISIONS}")
     if precision == "auto":
+        if INT8_MIN_D <= d <= INT8_MAX_D:
+            return "int8x3"
         return "bf16x3" if d >= SPLIT_MIN_D else "fp32"
+    if precision == "int8x3" and d > INT8_MAX_D:
+        raise ValueError(f"the int8 sweep supports d <= {INT8_MAX_D}")
     return precision
 
 
@@ -65,16 +72,18 @@ def pricing_l2sq(x, y, nx, ny, qb, dbb, k, *, dot_scale=2.0, rows=True, cols=Tru
     """Raw l2^2 pricing: returns (row_vals, row_idx, col_vals, col_idx, stats5) with None for skipped parts.
 
     ``stats5`` = (num, den, count, max sigma+, max|cost|); max|cost| is 0 unless ``linf``. ``precision`` picks the
-    candidate sweep: ``"fp32"`` MFMA, ``"bf16x3"`` split-bf16 MFMA (three products) or ``"auto"`` (split-bf16 from
-    d = SPLIT_MIN_D on); all feed the same exact fp64 re-evaluation, so the outputs are identical and only the
-    speed (and the rescan rate) differs.
+    candidate sweep: ``"fp32"`` MFMA, ``"bf16x3"`` split-bf16 MFMA (three products), ``"int8x3"`` int8 MFMA over a
+    16-bit fixed-point split (three exact int32 products, d <= 65536) or ``"auto"`` (split-bf16 from d = SPLIT_MIN_D
+    on); all feed the same exact fp64 re-evaluation, so the outputs are identical and only the speed (and the
+    rescan rate) differs.
     """
     precision = sweep_precision(precision, int(x.shape[1]))
     lib = _lib.load()
     x, y, nx, ny, qb, dbb = map(_c, (x, y, nx, ny, qb, dbb))
     m, n, d = x.shape[0], y.shape[0], x.shape[1]
     flags = (_lib.HM_ROWS if rows else 0) | (_lib.HM_COLS if cols else 0) | (_lib.HM_STATS if stats else 0) \
-        | (_lib.HM_LINF if (stats and linf) else 0) | (_lib.HM_BF16X3 if precision == "bf16x3" else 0)
+        | (_lib.HM_LINF if (stats and linf) else 0) | (_lib.HM_BF16X3 if precision == "bf16x3" else 0) \
+        | (_lib.HM_INT8X3 if precision == "int8x3" else 0)
     dev = x.device
     rv = torch.empty((m, k), dtype=torch.float64, device=dev) if rows else None
     ri = torch.empty((m, k), dtype=torch.int32, device=dev) if rows else None

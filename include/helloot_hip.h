@@ -35,6 +35,7 @@ extern "C" {
 #define HM_STATS 4u   /* certificate sums num, den, count, max */
 #define HM_LINF 8u    /* also max|cost| (collect_linf_stats) */
 #define HM_BF16X3 16u /* l2^2 sweep on split-bf16 MFMA (hi*hi + hi*lo + lo*hi) instead of fp32 MFMA; same outputs */
+#define HM_INT8X3 32u /* l2^2 sweep on int8 MFMA over a 16-bit fixed-point split (h*h + h*l + l*h); same outputs */
 
 /* Norm cost kinds (generic_scan.py cost_type: 0=l1, 1=linf, 2=l2) */
 #define HM_COST_L1 0

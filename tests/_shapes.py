@@ -86,11 +86,11 @@ def exact_col_topk(X, Y_cols, p, q_cols, qb, db_cols, k, scale=2.0):
 
 
 def fp64_certificate(X, Y, p, q, qb, db, scale=2.0, chunk=65536, envelope=2.0 ** -12):
-    """Certificate of all pairs from fp64 GEMMs on the device: exact sums den, max sigma+, max|c|, and for the count
-    and num the interval the sweep's fp32-grade scores must fall in, from the per-pair envelope
+    """Certificate of all pairs from fp64 GEMMs on the device: exact sums den, max sigma+, max|c|, and for the count,
+    num and den the interval the sweep's fp32-grade scores and costs must fall in, from the per-pair envelope
     E_ij = envelope * scale * sum_k |x_ik y_jk| (see ``assert_l2sq_certificate`` in test_gpu_pricing)."""
     X64, Xa = X.double(), X.abs()
-    num_lo = num_hi = den = 0.0
+    num_lo = num_hi = den = den_slack = 0.0
     count_lo = count_hi = 0
     mx = cmax = env_max = 0.0
     for s in range(0, Y.shape[0], chunk):
@@ -106,11 +106,12 @@ def fp64_certificate(X, Y, p, q, qb, db, scale=2.0, chunk=65536, envelope=2.0 **
         count_hi += int((sigma > -env).sum())
         env_max = max(env_max, float(env.max()))
         den += float((cost * cost).sum())
+        den_slack += float((2.0 * cost.abs() * env + env * env).sum())
         mx = max(mx, float(sigma.max().clamp_min(0.0)))
         cmax = max(cmax, float(cost.abs().max()))
         del sigma, cost, env
-    return {"count": (count_lo, count_hi), "num": (num_lo, num_hi), "den": den, "max": mx, "cmax": cmax,
-            "envelope": env_max}
+    return {"count": (count_lo, count_hi), "num": (num_lo, num_hi), "den": den, "den_slack": den_slack, "max": mx,
+            "cmax": cmax, "envelope": env_max}
 
 
 def random_csr(rng, m, n, per_row):

@@ -38,8 +38,8 @@ def _assert_sorted_valid(vals, idx, bound):
 
 
 def test_c5_pricing_step_full_shape(cuda):
-    """C5 step: both sweeps give identical exact lists; 16 rows and 16 columns equal the oracle's exact top-2;
-    the certificate totals agree with an fp64 GEMM over all 1.05e10 pairs."""
+    """C5 step: the three sweeps give identical exact lists; 16 rows and 16 columns equal the oracle's exact top-2;
+    the certificate totals (int8 and split-bf16 sweeps) agree with an fp64 GEMM over all 1.05e10 pairs."""
     m, n, d, k = 8192, 1_280_000, 8192, 2
     _say("C5: generating 1,280,000 x 8192 resident rows")
     Y = gmm(n, d, seed=2, dev=cuda, means_seed=12)
@@ -48,13 +48,14 @@ def test_c5_pricing_step_full_shape(cuda):
     f, g = sampled_c_transform(X, Y, p, q)
     qb, db = f - p, g - q
     outs = {}
-    for precision in ("bf16x3", "fp32"):
+    for precision in ("int8x3", "bf16x3", "fp32"):
         _say(f"C5: {precision} sweep")
         outs[precision] = pricing_l2sq(X, Y, p, q, qb, db, k, linf=True, precision=precision)
         torch.cuda.synchronize()
-    rv, ri, cv, ci, st = outs["bf16x3"]
-    for a, b in zip(outs["bf16x3"][:4], outs["fp32"][:4]):
-        assert torch.equal(a, b)
+    rv, ri, cv, ci, st = outs["int8x3"]
+    for other in ("bf16x3", "fp32"):
+        for a, b in zip(outs["int8x3"][:4], outs[other][:4]):
+            assert torch.equal(a, b), other
     _assert_sorted_valid(rv, ri, n)
     _assert_sorted_valid(cv, ci, m)
     rng = np.random.default_rng(5)
@@ -80,6 +81,7 @@ def test_c5_pricing_step_full_shape(cuda):
     np.testing.assert_allclose(got[3], bounds["max"], rtol=1e-10)
     bounds["max"] = float(got[3])
     assert_l2sq_certificate(st, bounds)
+    assert_l2sq_certificate(outs["bf16x3"][4], bounds)
 
 
 def _c4_inputs(dev, seed=4):
