@@ -2392,7 +2392,12 @@ __global__ void fill_u32(unsigned int* p, int64_t count, unsigned int v) {
 // host orchestration
 // -------------------------------------------------------------------------------------------------
 // Candidates per row the finalize merges and keeps (KM), and entries per partial list of the sweep (KL).
-inline int merge_k(int k) { return k <= 2 ? 8 : (k <= 8 ? 16 : 40); }
+// The int8 sweep's error bound is about three times the split-bf16 one (its quantization terms), so for k <= 2
+// it keeps 16: fewer rows whose kept candidates do not separate from the dropped ones go to the wide pass.
+inline int merge_k(int k, uint32_t flags) {
+    if ((flags & HM_INT8X3) && k <= 2) return 16;
+    return k <= 2 ? 8 : (k <= 8 ? 16 : 40);
+}
 
 // A partial list sees about 1/nlists of a row's candidates. Its last entry bounds what it dropped; that bound
 // stays far below the k-th best unless the list holds KL of the best k + 2, so KL = 8 while (k + 2) / nlists <= 2
@@ -2486,13 +2491,16 @@ struct CallPlan {
 
 inline CallPlan plan_call(int64_t m, int64_t n, int d, int k, uint32_t flags) {
     CallPlan c;
-    c.km = merge_k(k);
+    c.km = merge_k(k, flags);
     c.fused = fused_columns(d, flags);
     c.swapped = (flags & HM_COLS) && !c.fused;
     c.row_pass = (flags & HM_ROWS) || c.fused || (flags & HM_STATS);
     c.bx = sweep_panel(d, flags);
     static const int sizes[3] = {8, 16, 40};
-    for (int t = 0; t < 3; ++t) {
+    // the int8 sweep's wider bound also wants deeper partial lists once k > 2 (their last entries bound what
+    // they dropped)
+    const int t0 = ((flags & HM_INT8X3) && k > 2) ? 1 : 0;
+    for (int t = t0; t < 3; ++t) {
         c.kl = sizes[t];
         c.ch = chunk_rows(m, n, c.kl, c.fused, c.bx);
         c.plan = plan_dir(c.ch, n, k, 64, c.bx);
