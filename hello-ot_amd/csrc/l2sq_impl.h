@@ -218,12 +218,14 @@ __global__ __launch_bounds__(256) void l2sq_prep_rows(const float* __restrict__ 
         }
         const double nrm = std::sqrt(s) * (1.0 + 1e-12);
         mx_norm = fmax(mx_norm, nrm);
-        mx_bias = fmax(mx_bias, std::fabs(qb[row]));
+        if (qb) mx_bias = fmax(mx_bias, std::fabs(qb[row]));
         if (lane == 0) {
             norm[row] = nrm;
-            qb32[row] = (float)qb[row];
-            // "ge" = q + db for the cost of the certificate, "p" = p for the row side
-            p32[row] = db_for_ge ? (float)(p[row] + db_for_ge[row]) : (float)p[row];
+            if (qb) {  // (a resident side's preparation has no biases)
+                qb32[row] = (float)qb[row];
+                // "ge" = q + db for the cost of the certificate, "p" = p for the row side
+                p32[row] = db_for_ge ? (float)(p[row] + db_for_ge[row]) : (float)p[row];
+            }
             if (qscale) {
                 qscale[row] = amax;  // the int8 copy turns it into its block's scale
                 l1[row] = a1 * (1.0 + 1e-12);
@@ -242,6 +244,30 @@ __global__ __launch_bounds__(256) void l2sq_prep_rows(const float* __restrict__ 
         }
         atomicMax(&maxima[0], double_key(mx_norm));
         atomicMax(&maxima[1], double_key(mx_bias));
+    }
+}
+
+// The Y side's biases for a call against a resident side (whose norms were computed once): db32, ge32 = q + db,
+// and the maxima max ||y|| (copied from the resident side) and max |db|.
+__global__ __launch_bounds__(256) void l2sq_prep_bias(int64_t n, const double* __restrict__ q,
+                                                      const double* __restrict__ db,
+                                                      const unsigned long long* __restrict__ ynorm_max,
+                                                      float* __restrict__ db32, float* __restrict__ ge32,
+                                                      unsigned long long* __restrict__ maxima /*[norm, |db|]*/) {
+    __shared__ double sM[4];
+    double mx = 0.0;
+    for (int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; j < n; j += (int64_t)gridDim.x * blockDim.x) {
+        db32[j] = (float)db[j];
+        ge32[j] = (float)(q[j] + db[j]);
+        mx = fmax(mx, std::fabs(db[j]));
+    }
+    for (int o = 32; o >= 1; o >>= 1) mx = fmax(mx, __shfl_xor(mx, o, 64));
+    if ((threadIdx.x & 63) == 0) sM[threadIdx.x >> 6] = mx;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        mx = fmax(fmax(sM[0], sM[1]), fmax(sM[2], sM[3]));
+        atomicMax(&maxima[1], double_key(mx));
+        if (blockIdx.x == 0) atomicMax(&maxima[0], *ynorm_max);
     }
 }
 
@@ -2320,7 +2346,8 @@ struct WideBufs {
 };
 
 // Per-side data of the int8 sweep (HM_INT8X3; null otherwise): row scales, ||.||_1, the rows' error terms
-// (l2sq_split_i8) and the maxima of each side's terms (X side at qmax[0..3], Y side at qmax[4..7]).
+// (l2sq_split_i8) and the maxima of each side's terms (4 keys per side). With y_ready the Y side's sweep copy
+// and data come prepared (a resident side, hm_l2sq_resident_prepare) and are not rebuilt.
 struct I8Bufs {
     float* xqs = nullptr;
     float* yqs = nullptr;
@@ -2328,7 +2355,9 @@ struct I8Bufs {
     double* yl1 = nullptr;
     double* xterm = nullptr;
     double* yterm = nullptr;
-    unsigned long long* qmax = nullptr;
+    unsigned long long* qmax_x = nullptr;
+    unsigned long long* qmax_y = nullptr;
+    bool y_ready = false;
 };
 
 // Resolves the rows a finalize queued (defined in pricing_l2sq.hip): the wide pass over them, then the exact full
@@ -2524,15 +2553,17 @@ template <class A>
 void layout(A& a, int64_t m, int64_t n, int d, int k, uint32_t flags, double** xnorm, double** ynorm, float** qb32,
             float** p32, float** db32, float** ge32, unsigned long long** maxima, Entry** part, Entry** colpart,
             unsigned int** colthr, double** cval, int** cidx, double** blockstats, int** redo, int** redo_count,
-            float** xsplit, float** ysplit, double** rpv, int** rpi, WideBufs* wide, I8Bufs* q8) {
+            float** xsplit, float** ysplit, double** rpv, int** rpi, WideBufs* wide, I8Bufs* q8,
+            bool y_resident = false) {
     const CallPlan c = plan_call(m, n, d, k, flags);
     const int64_t panels = c.ch / c.bx;
     size_t part_entries = (size_t)c.plan.S * c.ch * 2 * c.kl;
     if (c.swapped && (size_t)c.plan2.S * c.ch2 * 2 * c.kl > part_entries)
         part_entries = (size_t)c.plan2.S * c.ch2 * 2 * c.kl;
     const bool fused = c.fused;
+    // with a resident Y side its norms, sweep copy and int8 data live in the resident buffer (resident_layout)
     *xnorm = a.template take<double>(m);
-    *ynorm = a.template take<double>(n);
+    *ynorm = y_resident ? nullptr : a.template take<double>(n);
     *qb32 = a.template take<float>(m);
     *p32 = a.template take<float>(m);
     *db32 = a.template take<float>(n);
@@ -2551,7 +2582,7 @@ void layout(A& a, int64_t m, int64_t n, int d, int k, uint32_t flags, double** x
     const size_t ldw = (size_t)(i8 ? i8_ld(d) : split_ld(d));
     // split copies cover whole 256-row panels: either side may be the swept one
     *xsplit = a.template take<float>(split ? (size_t)panel_rows(m, BXW) * ldw : 1);
-    *ysplit = a.template take<float>(split ? (size_t)panel_rows(n, BXW) * ldw : 1);
+    *ysplit = y_resident ? nullptr : a.template take<float>(split ? (size_t)panel_rows(n, BXW) * ldw : 1);
     *rpv = a.template take<double>((size_t)RESCAN_ITEMS * k);
     *rpi = a.template take<int>((size_t)RESCAN_ITEMS * k);
     const int64_t wq = panel_rows(WIDE_ROWS, BXW);
@@ -2570,12 +2601,41 @@ void layout(A& a, int64_t m, int64_t n, int d, int k, uint32_t flags, double** x
     *q8 = I8Bufs{};
     if (i8) {
         q8->xqs = a.template take<float>((size_t)m);
-        q8->yqs = a.template take<float>((size_t)n);
         q8->xl1 = a.template take<double>((size_t)m);
-        q8->yl1 = a.template take<double>((size_t)n);
         q8->xterm = a.template take<double>((size_t)m * 4);
-        q8->yterm = a.template take<double>((size_t)n * 4);
-        q8->qmax = a.template take<unsigned long long>(8);
+        q8->qmax_x = a.template take<unsigned long long>(4);
+        if (!y_resident) {
+            q8->yqs = a.template take<float>((size_t)n);
+            q8->yl1 = a.template take<double>((size_t)n);
+            q8->yterm = a.template take<double>((size_t)n * 4);
+            q8->qmax_y = a.template take<unsigned long long>(4);
+        }
+    }
+}
+
+// A resident Y side (hm_l2sq_resident_*): its norms, its sweep copy for the precision in `flags` and, for the int8
+// sweep, its scales, ||.||_1, error terms and their maxima, plus max ||y|| (an ordered key).
+struct ResidentY {
+    double* ynorm;
+    float* ysplit;
+    unsigned long long* ynorm_max;
+    I8Bufs q8;  // the Y half
+};
+
+template <class A>
+void resident_layout(A& a, int64_t n, int d, uint32_t flags, ResidentY* r) {
+    const bool i8 = (flags & HM_INT8X3) != 0;
+    const bool split = (flags & (HM_BF16X3 | HM_INT8X3)) != 0;
+    const size_t ldw = (size_t)(i8 ? i8_ld(d) : split_ld(d));
+    *r = ResidentY{};
+    r->ynorm = a.template take<double>((size_t)n);
+    r->ysplit = split ? a.template take<float>((size_t)panel_rows(n, BXW) * ldw) : nullptr;
+    r->ynorm_max = a.template take<unsigned long long>(2);  // [max ||y||, unused slot of the prep kernel]
+    if (i8) {
+        r->q8.yqs = a.template take<float>((size_t)n);
+        r->q8.yl1 = a.template take<double>((size_t)n);
+        r->q8.yterm = a.template take<double>((size_t)n * 4);
+        r->q8.qmax_y = a.template take<unsigned long long>(4);
     }
 }
 
@@ -2617,6 +2677,16 @@ inline int rescan_exact(hipStream_t st, const float* A, const float* B, int64_t 
     return HM_OK;
 }
 
+// int8 copy of one side (its maxima are cleared first, with a kernel)
+inline void launch_split_i8(hipStream_t st, const float* X, int64_t rows, int d, int sd, int ld, float* qs,
+                            const double* l1, const double* norm, float* out, double* qterm,
+                            unsigned long long* qmax) {
+    hipLaunchKernelGGL(zero_words, dim3(1), dim3(64), 0, st, qmax, 4);
+    hipLaunchKernelGGL(l2sq_split_i8, dim3((unsigned)std::min<int64_t>(panel_rows(rows, BXW) / 32, 8192)), dim3(256),
+                       0, st, X, rows, panel_rows(rows, BXW), d, sd, ld, qs, l1, norm,
+                       reinterpret_cast<unsigned int*>(out), qterm, qmax);
+}
+
 template <int K1, int KM>
 int run_bidir(hipStream_t st, const float* X, const float* Y, int64_t m, int64_t n, int d, int k, double scale,
               uint32_t flags, const double* qb, const double* db, const double* xnorm, const double* ynorm,
@@ -2647,24 +2717,20 @@ int run_bidir(hipStream_t st, const float* X, const float* Y, int64_t m, int64_t
     const DirPlan plan = cp.plan;
     const int bx = cp.bx;
     unsigned int* rowthr = wide.rowthr;
+    // sweep copies (the Y side's only when it is not a prepared resident side)
     if (i8) {
         // the row scales and ||.||_1 come from the prep pass; the copies add ||l||_2 and the error terms
-        hipLaunchKernelGGL(zero_words, dim3(1), dim3(64), 0, st, q8.qmax, 8);
-        hipLaunchKernelGGL(l2sq_split_i8, dim3((unsigned)std::min<int64_t>(panel_rows(m, BXW) / 32, 8192)), dim3(256),
-                           0, st, X, m, panel_rows(m, BXW), d, sd, ld, q8.xqs, q8.xl1, xnorm,
-                           reinterpret_cast<unsigned int*>(xsplit), q8.xterm, q8.qmax);
-        HM_LAUNCH_CHECK("l2sq_split_i8");
-        hipLaunchKernelGGL(l2sq_split_i8, dim3((unsigned)std::min<int64_t>(panel_rows(n, BXW) / 32, 8192)), dim3(256),
-                           0, st, Y, n, panel_rows(n, BXW), d, sd, ld, q8.yqs, q8.yl1, ynorm,
-                           reinterpret_cast<unsigned int*>(ysplit), q8.yterm, q8.qmax + 4);
-        HM_LAUNCH_CHECK("l2sq_split_i8");
+        launch_split_i8(st, X, m, d, sd, ld, q8.xqs, q8.xl1, xnorm, xsplit, q8.xterm, q8.qmax_x);
+        if (!q8.y_ready) launch_split_i8(st, Y, n, d, sd, ld, q8.yqs, q8.yl1, ynorm, ysplit, q8.yterm, q8.qmax_y);
     } else if (split) {
         hipLaunchKernelGGL(l2sq_split_bf16, dim3(4096), dim3(256), 0, st, X, m, panel_rows(m, BXW), d, sd, ld,
                            reinterpret_cast<unsigned short*>(xsplit));
         HM_LAUNCH_CHECK("l2sq_split_bf16");
-        hipLaunchKernelGGL(l2sq_split_bf16, dim3(4096), dim3(256), 0, st, Y, n, panel_rows(n, BXW), d, sd, ld,
-                           reinterpret_cast<unsigned short*>(ysplit));
-        HM_LAUNCH_CHECK("l2sq_split_bf16");
+        if (!q8.y_ready) {
+            hipLaunchKernelGGL(l2sq_split_bf16, dim3(4096), dim3(256), 0, st, Y, n, panel_rows(n, BXW), d, sd, ld,
+                               reinterpret_cast<unsigned short*>(ysplit));
+            HM_LAUNCH_CHECK("l2sq_split_bf16");
+        }
     }
     // Rigorous bound on |w - exact| in units of scale*||x||*||y||: accumulation of B-feature blocks in fp32
     // (gamma over the additions of a block, then over the blocks), plus for the split products the dropped
@@ -2687,7 +2753,7 @@ int run_bidir(hipStream_t st, const float* X, const float* Y, int64_t m, int64_t
         BoundArgs b = bnd;
         if (i8) {
             b.qterm = (y_rows ? q8.yterm : q8.xterm) + 4 * base;
-            b.qmax = y_rows ? q8.qmax : q8.qmax + 4;
+            b.qmax = y_rows ? q8.qmax_x : q8.qmax_y;
         }
         return b;
     };

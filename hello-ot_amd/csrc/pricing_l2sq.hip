@@ -134,8 +134,10 @@ uint32_t effective_flags(uint32_t flags) { return (flags & HM_STATS) ? (flags | 
 bool internal_rows(uint32_t flags) { return (flags & HM_STATS) && !(flags & HM_ROWS); }
 }  // namespace
 
-extern "C" size_t hm_pricing_l2sq_workspace_bytes(int64_t m, int64_t n, int32_t d, int32_t k, uint32_t flags) {
-    if (m < 1 || n < 1 || k < 1 || k > 32) return 0;
+namespace {
+
+size_t workspace_need(int64_t m, int64_t n, int32_t d, int32_t k, uint32_t flags, bool y_resident) {
+    if (m < 1 || n < 1 || d < 1 || k < 1 || k > 32) return 0;
     const bool own_rows = internal_rows(flags);
     flags = effective_flags(flags);
     Sizer s;
@@ -151,7 +153,7 @@ extern "C" size_t hm_pricing_l2sq_workspace_bytes(int64_t m, int64_t n, int32_t 
     WideBufs wide;
     I8Bufs q8;
     layout(s, m, n, d, k, flags, &a, &b, &c, &e, &f, &g, &mx, &part, &colpart, &thr, &cv, &ci, &bs, &redo, &rc, &xs,
-           &ys, &rpv, &rpi, &wide, &q8);
+           &ys, &rpv, &rpi, &wide, &q8, y_resident);
     if (own_rows) {
         s.template take<double>((size_t)m * k);
         s.template take<int>((size_t)m * k);
@@ -159,10 +161,28 @@ extern "C" size_t hm_pricing_l2sq_workspace_bytes(int64_t m, int64_t n, int32_t 
     return s.used;
 }
 
-extern "C" int hm_pricing_l2sq(void* stream, const float* X, const float* Y, const double* p, const double* q,
-                               const double* qb, const double* db, int64_t m, int64_t n, int32_t d, int32_t k,
-                               double scale, uint32_t flags, double* row_val, int32_t* row_idx, double* col_val,
-                               int32_t* col_idx, double* stats, void* workspace, size_t workspace_bytes) {
+// Header of a resident buffer (device memory, written by hm_l2sq_resident_prepare, read back by the calls)
+constexpr uint64_t RESIDENT_MAGIC = 0x4d4933353552455aull;
+struct ResidentHead {
+    uint64_t magic;
+    int64_t n;
+    int32_t d;
+    uint32_t precision;  // HM_BF16X3 / HM_INT8X3 bits of the preparation
+    const void* y;       // the Y the side was prepared from
+};
+constexpr uint32_t PRECISION_BITS = HM_BF16X3 | HM_INT8X3;
+
+size_t resident_bytes(int64_t n, int32_t d, uint32_t flags) {
+    Sizer s;
+    s.template take<ResidentHead>(1);
+    ResidentY r;
+    resident_layout(s, n, d, flags, &r);
+    return s.used;
+}
+
+int check_call(const float* X, const float* Y, const double* p, const double* q, const double* qb, const double* db,
+               int64_t m, int64_t n, int32_t d, int32_t k, double scale, uint32_t flags, const double* row_val,
+               const int32_t* row_idx, const double* col_val, const int32_t* col_idx, const double* stats) {
     HM_CHECK_ARG(X && Y && p && q && qb && db, "l2sq pricing: feature, cost and bias pointers are required");
     HM_CHECK_ARG(m >= 1 && n >= 1 && d >= 1 && m < INT32_MAX && n < INT32_MAX,
                  "l2sq pricing requires nonempty inputs with int32 dimensions (m=%lld n=%lld d=%d)",
@@ -174,8 +194,15 @@ extern "C" int hm_pricing_l2sq(void* stream, const float* X, const float* Y, con
     HM_CHECK_ARG(!(flags & HM_ROWS) || (row_val && row_idx), "HM_ROWS requires row outputs");
     HM_CHECK_ARG(!(flags & HM_COLS) || (col_val && col_idx), "HM_COLS requires column outputs");
     HM_CHECK_ARG(!(flags & HM_STATS) || stats, "HM_STATS requires a stats output");
-    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-    const size_t need = hm_pricing_l2sq_workspace_bytes(m, n, d, k, flags);
+    return HM_OK;
+}
+
+// One pricing call; `res` (or null) is a validated resident Y side
+int pricing_call(hipStream_t st, const float* X, const float* Y, const double* p, const double* q, const double* qb,
+                 const double* db, int64_t m, int64_t n, int32_t d, int32_t k, double scale, uint32_t flags,
+                 double* row_val, int32_t* row_idx, double* col_val, int32_t* col_idx, double* stats,
+                 const ResidentY* res, void* workspace, size_t workspace_bytes) {
+    const size_t need = workspace_need(m, n, d, k, flags, res != nullptr);
     HM_CHECK_ARG(workspace != nullptr, "workspace is required");
     if (workspace_bytes < need)
         return fail(HM_ENOSPC, "l2sq pricing workspace too small: %zu < %zu bytes", workspace_bytes, need);
@@ -194,22 +221,126 @@ extern "C" int hm_pricing_l2sq(void* stream, const float* X, const float* Y, con
     const bool own_rows = internal_rows(flags);
     flags = effective_flags(flags);
     layout(a, m, n, d, k, flags, &xnorm, &ynorm, &qb32, &p32, &db32, &ge32, &maxima, &part, &colpart, &colthr, &cval,
-           &cidx, &blockstats, &redo, &redo_count, &xsplit, &ysplit, &rpv, &rpi, &wide, &q8);
+           &cidx, &blockstats, &redo, &redo_count, &xsplit, &ysplit, &rpv, &rpi, &wide, &q8, res != nullptr);
     if (own_rows) {
         row_val = a.template take<double>((size_t)m * k);
         row_idx = a.template take<int>((size_t)m * k);
     }
+    if (res) {
+        ynorm = res->ynorm;
+        ysplit = res->ysplit;
+        q8.yqs = res->q8.yqs;
+        q8.yl1 = res->q8.yl1;
+        q8.yterm = res->q8.yterm;
+        q8.qmax_y = res->q8.qmax_y;
+        q8.y_ready = true;
+    }
     hipLaunchKernelGGL(zero_words, dim3(1), dim3(64), 0, st, maxima, 4);
     HM_LAUNCH_CHECK("zero_words");
     // X side: ||x||, qb32, p32 (maxima[0..1] = max||x||, max|qb|); Y side: ||y||, db32, ge32 = q + db
-    // with HM_INT8X3 also the int8 row scales and ||.||_1 of both sides
+    // (maxima[2..3]); with HM_INT8X3 also the int8 row maxima and ||.||_1 of both sides. A resident Y side has its
+    // norms and int8 data already: only its biases are converted.
     hipLaunchKernelGGL(l2sq_prep_rows, dim3(prep_grid(m)), dim3(256), 0, st, X, m, d, p, qb,
                        (const double*)nullptr, xnorm, qb32, p32, maxima, q8.xqs, q8.xl1);
     HM_LAUNCH_CHECK("l2sq_prep_rows");
-    hipLaunchKernelGGL(l2sq_prep_rows, dim3(prep_grid(n)), dim3(256), 0, st, Y, n, d, q, db, db, ynorm,
-                       db32, ge32, maxima + 2, q8.yqs, q8.yl1);
+    if (res)
+        hipLaunchKernelGGL(l2sq_prep_bias, dim3(prep_grid(n)), dim3(256), 0, st, n, q, db, res->ynorm_max, db32, ge32,
+                           maxima + 2);
+    else
+        hipLaunchKernelGGL(l2sq_prep_rows, dim3(prep_grid(n)), dim3(256), 0, st, Y, n, d, q, db, db, ynorm,
+                           db32, ge32, maxima + 2, q8.yqs, q8.yl1);
     HM_LAUNCH_CHECK("l2sq_prep_rows");
     return run_k(st, X, Y, m, n, d, k, scale, flags, qb, db, xnorm, ynorm, maxima, qb32, db32, p32, ge32, part,
                  colpart, colthr, cval, cidx, blockstats, redo, redo_count, row_val, row_idx, col_val, col_idx, stats,
                  xsplit, ysplit, rpv, rpi, wide, q8);
+}
+
+}  // namespace
+
+extern "C" size_t hm_pricing_l2sq_workspace_bytes(int64_t m, int64_t n, int32_t d, int32_t k, uint32_t flags) {
+    return workspace_need(m, n, d, k, flags, false);
+}
+
+extern "C" int hm_pricing_l2sq(void* stream, const float* X, const float* Y, const double* p, const double* q,
+                               const double* qb, const double* db, int64_t m, int64_t n, int32_t d, int32_t k,
+                               double scale, uint32_t flags, double* row_val, int32_t* row_idx, double* col_val,
+                               int32_t* col_idx, double* stats, void* workspace, size_t workspace_bytes) {
+    if (int rc = check_call(X, Y, p, q, qb, db, m, n, d, k, scale, flags, row_val, row_idx, col_val, col_idx, stats))
+        return rc;
+    return pricing_call(reinterpret_cast<hipStream_t>(stream), X, Y, p, q, qb, db, m, n, d, k, scale, flags, row_val,
+                        row_idx, col_val, col_idx, stats, nullptr, workspace, workspace_bytes);
+}
+
+extern "C" size_t hm_l2sq_resident_bytes(int64_t n, int32_t d, uint32_t flags) {
+    if (n < 1 || d < 1 || n >= INT32_MAX) return 0;
+    return resident_bytes(n, d, flags);
+}
+
+extern "C" int hm_l2sq_resident_prepare(void* stream, const float* Y, int64_t n, int32_t d, uint32_t flags,
+                                        void* resident, size_t bytes) {
+    HM_CHECK_ARG(Y && resident, "resident side: feature and buffer pointers are required");
+    HM_CHECK_ARG(n >= 1 && d >= 1 && n < INT32_MAX, "resident side requires n >= 1, d >= 1 (n=%lld d=%d)",
+                 (long long)n, d);
+    HM_CHECK_ARG(!((flags & HM_BF16X3) && (flags & HM_INT8X3)), "HM_BF16X3 and HM_INT8X3 exclude each other");
+    HM_CHECK_ARG(!(flags & HM_INT8X3) || d <= 65536, "the int8 sweep supports d <= 65536 (d=%d)", d);
+    const size_t need = resident_bytes(n, d, flags);
+    if (bytes < need) return fail(HM_ENOSPC, "resident buffer too small: %zu < %zu bytes", bytes, need);
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    Arena a(resident, bytes);
+    ResidentHead* head = a.template take<ResidentHead>(1);
+    ResidentY r;
+    resident_layout(a, n, d, flags, &r);
+    const bool i8 = (flags & HM_INT8X3) != 0, split = (flags & PRECISION_BITS) != 0;
+    const int sd = i8 ? i8_words(d) : split_features(d), ld = i8 ? i8_ld(d) : split_ld(d);
+    hipLaunchKernelGGL(zero_words, dim3(1), dim3(64), 0, st, r.ynorm_max, 2);
+    hipLaunchKernelGGL(l2sq_prep_rows, dim3(prep_grid(n)), dim3(256), 0, st, Y, n, d, (const double*)nullptr,
+                       (const double*)nullptr, (const double*)nullptr, r.ynorm, (float*)nullptr, (float*)nullptr,
+                       r.ynorm_max, r.q8.yqs, r.q8.yl1);
+    HM_LAUNCH_CHECK("l2sq_prep_rows");
+    if (i8) {
+        launch_split_i8(st, Y, n, d, sd, ld, r.q8.yqs, r.q8.yl1, r.ynorm, r.ysplit, r.q8.yterm, r.q8.qmax_y);
+        HM_LAUNCH_CHECK("l2sq_split_i8");
+    } else if (split) {
+        hipLaunchKernelGGL(l2sq_split_bf16, dim3(4096), dim3(256), 0, st, Y, n, panel_rows(n, BXW), d, sd, ld,
+                           reinterpret_cast<unsigned short*>(r.ysplit));
+        HM_LAUNCH_CHECK("l2sq_split_bf16");
+    }
+    const ResidentHead h{RESIDENT_MAGIC, n, d, flags & PRECISION_BITS, Y};
+    HM_HIP(hipMemcpyAsync(head, &h, sizeof(h), hipMemcpyHostToDevice, st));
+    HM_HIP(hipStreamSynchronize(st));  // `h` lives on this stack frame
+    return HM_OK;
+}
+
+extern "C" size_t hm_pricing_l2sq_resident_workspace_bytes(int64_t m, int64_t n, int32_t d, int32_t k,
+                                                           uint32_t flags) {
+    return workspace_need(m, n, d, k, flags, true);
+}
+
+extern "C" int hm_pricing_l2sq_resident(void* stream, const float* X, const float* Y, const double* p, const double* q,
+                                        const double* qb, const double* db, int64_t m, int64_t n, int32_t d, int32_t k,
+                                        double scale, uint32_t flags, double* row_val, int32_t* row_idx,
+                                        double* col_val, int32_t* col_idx, double* stats, const void* resident,
+                                        size_t resident_bytes_, void* workspace, size_t workspace_bytes) {
+    if (int rc = check_call(X, Y, p, q, qb, db, m, n, d, k, scale, flags, row_val, row_idx, col_val, col_idx, stats))
+        return rc;
+    HM_CHECK_ARG(resident != nullptr, "resident side buffer is required");
+    if (resident_bytes_ < sizeof(ResidentHead))
+        return fail(HM_EINVAL, "resident buffer smaller than a side of n=%lld d=%d needs", (long long)n, d);
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    ResidentHead h{};
+    HM_HIP(hipMemcpyAsync(&h, resident, sizeof(h), hipMemcpyDeviceToHost, st));
+    HM_HIP(hipStreamSynchronize(st));
+    if (h.magic != RESIDENT_MAGIC) return fail(HM_EINVAL, "resident buffer was not prepared");
+    if (h.n != n || h.d != d || h.y != (const void*)Y)
+        return fail(HM_EINVAL, "resident side was prepared for other features (n=%lld d=%d)", (long long)h.n, h.d);
+    if (h.precision != (flags & PRECISION_BITS))
+        return fail(HM_EINVAL, "resident side was prepared for another sweep precision");
+    if (resident_bytes_ < resident_bytes(n, d, flags))
+        return fail(HM_EINVAL, "resident buffer smaller than a side of n=%lld d=%d needs", (long long)n, d);
+    Arena a(const_cast<void*>(resident), resident_bytes_);
+    a.template take<ResidentHead>(1);
+    ResidentY r;
+    resident_layout(a, n, d, flags, &r);
+    return pricing_call(st, X, Y, p, q, qb, db, m, n, d, k, scale, flags, row_val, row_idx, col_val, col_idx, stats,
+                        &r, workspace, workspace_bytes);
 }

@@ -67,36 +67,75 @@ def sweep_precision(precision: str, d: int) -> str:
     return precision
 
 
+def _precision_flags(precision: str) -> int:
+    return (_lib.HM_BF16X3 if precision == "bf16x3" else 0) | (_lib.HM_INT8X3 if precision == "int8x3" else 0)
+
+
+class ResidentSide:
+    """The Y side of chunked l2^2 scans prepared once on the device (``hm_l2sq_resident_prepare``): its norms, its
+    sweep copy for ``precision`` and the int8 scales and error terms. The reference's chunked check places one side
+    on the device the same way and streams query chunks against it (kernels/bilinear_topk.py:255-293).
+    ``pricing_l2sq(..., resident=side)`` then skips the side's preparation; ``y`` must stay unchanged."""
+
+    def __init__(self, y, precision: str = "auto"):
+        lib = _lib.load()
+        self.y = _c(y)
+        self.n, self.d = int(self.y.shape[0]), int(self.y.shape[1])
+        self.precision = sweep_precision(precision, self.d)
+        flags = _precision_flags(self.precision)
+        dev = self.y.device
+        self.buffer = _workspace(lib.hm_l2sq_resident_bytes(self.n, self.d, flags), dev)
+        with torch.cuda.device(dev):
+            rc = lib.hm_l2sq_resident_prepare(_lib.stream_handle(dev), _lib.ptr(self.y), self.n, self.d, flags,
+                                              _lib.ptr(self.buffer), self.buffer.numel())
+        _lib.check(rc, "hm_l2sq_resident_prepare")
+
+
 def pricing_l2sq(x, y, nx, ny, qb, dbb, k, *, dot_scale=2.0, rows=True, cols=True, stats=True, linf=False,
-                 precision="auto"):
+                 precision="auto", resident: ResidentSide | None = None):
     """Raw l2^2 pricing: returns (row_vals, row_idx, col_vals, col_idx, stats5) with None for skipped parts.
 
     ``stats5`` = (num, den, count, max sigma+, max|cost|); max|cost| is 0 unless ``linf``. ``precision`` picks the
     candidate sweep: ``"fp32"`` MFMA, ``"bf16x3"`` split-bf16 MFMA (three products), ``"int8x3"`` int8 MFMA over a
     16-bit fixed-point split (three exact int32 products, d <= 65536) or ``"auto"`` (split-bf16 from d = SPLIT_MIN_D
     on); all feed the same exact fp64 re-evaluation, so the outputs are identical and only the speed (and the
-    rescan rate) differs.
+    rescan rate) differs. With ``resident`` (a ``ResidentSide`` of ``y``) the side's preparation is reused and the
+    precision is the side's.
     """
+    if resident is not None:
+        if precision not in ("auto", resident.precision):
+            raise ValueError(f"the resident side was prepared for precision {resident.precision!r}")
+        if y.data_ptr() != resident.y.data_ptr() or tuple(y.shape) != (resident.n, resident.d):
+            raise ValueError("pricing against a resident side needs the tensor it was prepared from")
+        precision, y = resident.precision, resident.y
     precision = sweep_precision(precision, int(x.shape[1]))
     lib = _lib.load()
     x, y, nx, ny, qb, dbb = map(_c, (x, y, nx, ny, qb, dbb))
     m, n, d = x.shape[0], y.shape[0], x.shape[1]
     flags = (_lib.HM_ROWS if rows else 0) | (_lib.HM_COLS if cols else 0) | (_lib.HM_STATS if stats else 0) \
-        | (_lib.HM_LINF if (stats and linf) else 0) | (_lib.HM_BF16X3 if precision == "bf16x3" else 0) \
-        | (_lib.HM_INT8X3 if precision == "int8x3" else 0)
+        | (_lib.HM_LINF if (stats and linf) else 0) | _precision_flags(precision)
     dev = x.device
     rv = torch.empty((m, k), dtype=torch.float64, device=dev) if rows else None
     ri = torch.empty((m, k), dtype=torch.int32, device=dev) if rows else None
     cv = torch.empty((n, k), dtype=torch.float64, device=dev) if cols else None
     ci = torch.empty((n, k), dtype=torch.int32, device=dev) if cols else None
     st = torch.zeros(5, dtype=torch.float64, device=dev) if stats else None
-    ws_bytes = lib.hm_pricing_l2sq_workspace_bytes(m, n, d, k, flags)
-    ws = _workspace(ws_bytes, dev)
+    if resident is None:
+        ws = _workspace(lib.hm_pricing_l2sq_workspace_bytes(m, n, d, k, flags), dev)
+        with torch.cuda.device(dev):
+            rc = lib.hm_pricing_l2sq(_lib.stream_handle(dev), _lib.ptr(x), _lib.ptr(y), _lib.ptr(nx), _lib.ptr(ny),
+                                     _lib.ptr(qb), _lib.ptr(dbb), m, n, d, k, float(dot_scale), flags, _lib.ptr(rv),
+                                     _lib.ptr(ri), _lib.ptr(cv), _lib.ptr(ci), _lib.ptr(st), _lib.ptr(ws), ws.numel())
+        _lib.check(rc, "hm_pricing_l2sq")
+        return rv, ri, cv, ci, st
+    ws = _workspace(lib.hm_pricing_l2sq_resident_workspace_bytes(m, n, d, k, flags), dev)
     with torch.cuda.device(dev):
-        rc = lib.hm_pricing_l2sq(_lib.stream_handle(dev), _lib.ptr(x), _lib.ptr(y), _lib.ptr(nx), _lib.ptr(ny),
-                                 _lib.ptr(qb), _lib.ptr(dbb), m, n, d, k, float(dot_scale), flags, _lib.ptr(rv),
-                                 _lib.ptr(ri), _lib.ptr(cv), _lib.ptr(ci), _lib.ptr(st), _lib.ptr(ws), ws.numel())
-    _lib.check(rc, "hm_pricing_l2sq")
+        rc = lib.hm_pricing_l2sq_resident(_lib.stream_handle(dev), _lib.ptr(x), _lib.ptr(y), _lib.ptr(nx),
+                                          _lib.ptr(ny), _lib.ptr(qb), _lib.ptr(dbb), m, n, d, k, float(dot_scale),
+                                          flags, _lib.ptr(rv), _lib.ptr(ri), _lib.ptr(cv), _lib.ptr(ci), _lib.ptr(st),
+                                          _lib.ptr(resident.buffer), resident.buffer.numel(), _lib.ptr(ws),
+                                          ws.numel())
+    _lib.check(rc, "hm_pricing_l2sq_resident")
     return rv, ri, cv, ci, st
 
 
@@ -207,4 +246,4 @@ class ScanExtension:
         return norm_pair_costs(query, db, rows, cols, cost_type)
 
 
-__all__ = ["ScanExtension", "pricing_l2sq", "pricing_norm", "scan_routes"]
+__all__ = ["ResidentSide", "ScanExtension", "pricing_l2sq", "pricing_norm", "scan_routes"]

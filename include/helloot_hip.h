@@ -76,8 +76,8 @@ int hm_profile_query(const char* name, double* total_ms, int64_t* launches);
  *   row_val[m*k] fp64, row_idx[m*k] int32  -- per X row, best k columns (HM_ROWS)
  *   col_val[n*k] fp64, col_idx[n*k] int32  -- per Y row, best k X rows    (HM_COLS)
  *   stats[5] fp64 = (num = sum sigma+^2, den = sum c^2, count #{sigma>0}, max sigma+, max|c| (HM_LINF))
- * Values are exact fp64 re-evaluations (fixed-order fp64 dot) of candidates found by an MFMA sweep (fp32, or
- * split-bf16 with HM_BF16X3) with a rigorous error bound b. A row whose kept candidates cannot be separated
+ * Values are exact fp64 re-evaluations (fixed-order fp64 dot) of candidates found by an MFMA sweep (fp32,
+ * split-bf16 with HM_BF16X3, or the int8 split with HM_INT8X3, d <= 65536) with a rigorous error bound b. A row whose kept candidates cannot be separated
  * from the dropped ones by 2b goes through a wide pass (its candidates with approximate score >= k-th - 2b are
  * collected by a second sweep and evaluated exactly) and, past 512 such candidates, an exact full rescan.
  * Certificate: the maximum violation is the exact fp64 maximum (from the row lists, computed internally when
@@ -91,6 +91,27 @@ int hm_pricing_l2sq(void* stream, const float* X, const float* Y, const double* 
                     const double* qb, const double* db, int64_t m, int64_t n, int32_t d, int32_t k,
                     double scale, uint32_t flags, double* row_val, int32_t* row_idx, double* col_val,
                     int32_t* col_idx, double* stats, void* workspace, size_t workspace_bytes);
+
+/*
+ * Resident side of an l2^2 scan. The reference's chunked check places one side on the device once and streams
+ * query chunks against it (kernels/bilinear_topk.py:255-293, the plan of kernels/scan_contract.py:113-211);
+ * hm_l2sq_resident_prepare does the same for Y: its fp64 norms, its sweep copy for the precision bits of
+ * `flags` (HM_BF16X3 / HM_INT8X3 / neither) and, for the int8 sweep, its scales and error terms, into a
+ * caller-allocated buffer of hm_l2sq_resident_bytes(n, d, flags) bytes. hm_pricing_l2sq_resident is then
+ * hm_pricing_l2sq for one query chunk X against that Y (same arguments and outputs; Y must be the tensor the
+ * side was prepared from, unchanged, and `flags` must carry the same precision bits: otherwise HM_EINVAL), and
+ * skips Y's preparation; only Y's biases (db, q + db) are converted per call. Its workspace is
+ * hm_pricing_l2sq_resident_workspace_bytes. The call reads the buffer's header back (one stream synchronisation).
+ */
+size_t hm_l2sq_resident_bytes(int64_t n, int32_t d, uint32_t flags);
+int hm_l2sq_resident_prepare(void* stream, const float* Y, int64_t n, int32_t d, uint32_t flags, void* resident,
+                             size_t resident_bytes);
+size_t hm_pricing_l2sq_resident_workspace_bytes(int64_t m, int64_t n, int32_t d, int32_t k, uint32_t flags);
+int hm_pricing_l2sq_resident(void* stream, const float* X, const float* Y, const double* p, const double* q,
+                             const double* qb, const double* db, int64_t m, int64_t n, int32_t d, int32_t k,
+                             double scale, uint32_t flags, double* row_val, int32_t* row_idx, double* col_val,
+                             int32_t* col_idx, double* stats, const void* resident, size_t resident_bytes,
+                             void* workspace, size_t workspace_bytes);
 
 /*
  * Norm-cost (l1 / linf / l2) bidirectional pricing scan on VALU with the full-edge certificate.

@@ -60,6 +60,34 @@ def test_workspace_queries_are_host_arithmetic():
     assert lib.hm_pricing_norm_workspace_bytes(524288, 524288, 8, 2, 7) > 0
 
 
+def test_resident_side_sizes_and_validation():
+    """A resident Y side holds its norms and sweep copy (two bytes per feature for the int8 split, four for
+    split-bf16, none for fp32); a call against it needs that much less workspace. Invalid calls fail before any
+    device work."""
+    lib = _lib.load()
+    n, d = 1_280_000, 8192
+    i8, bf = _lib.HM_INT8X3, _lib.HM_BF16X3
+    r_i8, r_bf, r_32 = (lib.hm_l2sq_resident_bytes(n, d, f) for f in (i8, bf, 0))
+    assert 2 * n * d < r_i8 < 2 * n * d * 1.02 + (64 << 20)
+    assert 4 * n * d < r_bf < 4 * n * d * 1.02 + (64 << 20)
+    assert 8 * n <= r_32 < 8 * n + (1 << 20)
+    full = lib.hm_pricing_l2sq_workspace_bytes(8192, n, d, 2, 7 | i8)
+    part = lib.hm_pricing_l2sq_resident_workspace_bytes(8192, n, d, 2, 7 | i8)
+    assert full - part >= 2 * n * d
+    assert lib.hm_l2sq_resident_bytes(0, d, i8) == 0
+    one = ctypes.c_void_p(16)  # never dereferenced
+    rc = lib.hm_l2sq_resident_prepare(None, one, 10, 4, i8 | bf, one, 1 << 20)
+    assert rc == _lib.HM_EINVAL and "exclude each other" in _lib.last_error()
+    rc = lib.hm_l2sq_resident_prepare(None, one, 10, 4, i8, one, 16)
+    assert rc == _lib.HM_ENOSPC
+    rc = lib.hm_pricing_l2sq_resident(None, one, one, one, one, one, one, 10, 10, 4, 2, 2.0, 1, one, one, one, one,
+                                      one, None, 1 << 20, one, 1 << 20)
+    assert rc == _lib.HM_EINVAL and "resident side buffer" in _lib.last_error()
+    rc = lib.hm_pricing_l2sq_resident(None, one, one, one, one, one, one, 10, 10, 4, 2, 2.0, 1, one, one, one, one,
+                                      one, one, 8, one, 1 << 20)
+    assert rc == _lib.HM_EINVAL and "resident buffer smaller" in _lib.last_error()
+
+
 def test_python_mirror_rejects_host_tensors_like_the_reference():
     from hello_ot_amd.kernels.generic_scan import ScanExtension
 

@@ -6,7 +6,8 @@ import pytest
 import torch
 
 import oracle
-from hello_ot_amd.kernels.generic_scan import ScanExtension, pricing_l2sq, pricing_norm
+from hello_ot_amd import _lib
+from hello_ot_amd.kernels.generic_scan import ResidentSide, ScanExtension, pricing_l2sq, pricing_norm
 
 pytestmark = pytest.mark.gpu
 
@@ -348,3 +349,41 @@ def test_norm_directional_top16_with_one_zero_side(cuda, kind):
     _, _, cv, ci, _ = pricing_norm(*_to(cuda, X, Y, f, np.zeros(300)), 16, kind, rows=False, cols=True, stats=False)
     np.testing.assert_array_equal(ci.cpu().numpy(), oci)
     np.testing.assert_array_equal(cv.cpu().numpy(), ocv)
+
+
+@pytest.mark.parametrize("precision", ["fp32", "bf16x3", "int8x3"])
+def test_l2sq_resident_side_gives_the_same_outputs(cuda, precision):
+    """Query chunks priced against a resident Y side (prepared once) give exactly the ordinary call's outputs,
+    chunk after chunk; the first chunk also equals the oracle. A side prepared for another precision, or another
+    tensor, is rejected."""
+    X, Y, p, q, qb, db = _l2sq_case(600, 3000, 300, seed=31)
+    tX, tY, tp, tq, tqb, tdb = _to(cuda, X, Y, p, q, qb, db)
+    side = ResidentSide(tY, precision)
+    for s, e in ((0, 256), (256, 600), (0, 256)):
+        args = (tX[s:e], tY, tp[s:e], tq, tqb[s:e], tdb, 4)
+        ref = pricing_l2sq(*args, linf=True, precision=precision)
+        got = pricing_l2sq(*args, linf=True, resident=side)
+        for a, b in zip(ref, got):
+            assert torch.equal(a, b)
+    orv, ori, ocv, oci, _ = oracle.l2sq_scan(X[:256], Y, p[:256], q, qb[:256], db, 4, 2.0)
+    rv, ri, cv, ci, _ = pricing_l2sq(tX[:256], tY, tp[:256], tq, tqb[:256], tdb, 4, resident=side)
+    np.testing.assert_array_equal(ri.cpu().numpy(), ori)
+    np.testing.assert_array_equal(rv.cpu().numpy(), orv)
+    np.testing.assert_array_equal(ci.cpu().numpy(), oci)
+    other = "fp32" if precision != "fp32" else "bf16x3"
+    with pytest.raises(ValueError, match="prepared for precision"):
+        pricing_l2sq(tX, tY, tp, tq, tqb, tdb, 4, precision=other, resident=side)
+    with pytest.raises(ValueError, match="tensor it was prepared from"):
+        pricing_l2sq(tX, tY.clone(), tp, tq, tqb, tdb, 4, resident=side)
+    # the library's own check of the precision bits (the Python mirror is bypassed here)
+    lib = _lib.load()
+    flags = 7 | (_lib.HM_BF16X3 if other == "bf16x3" else 0)
+    ws = torch.empty(lib.hm_pricing_l2sq_resident_workspace_bytes(600, 3000, 300, 4, flags), dtype=torch.uint8,
+                     device=cuda)
+    out = [torch.empty((600, 4), dtype=torch.float64, device=cuda), torch.empty((600, 4), dtype=torch.int32, device=cuda),
+           torch.empty((3000, 4), dtype=torch.float64, device=cuda), torch.empty((3000, 4), dtype=torch.int32, device=cuda),
+           torch.empty(5, dtype=torch.float64, device=cuda)]
+    rc = lib.hm_pricing_l2sq_resident(_lib.stream_handle(cuda), *(_lib.ptr(t) for t in (tX, tY, tp, tq, tqb, tdb)), 600,
+                                      3000, 300, 4, 2.0, flags, *(_lib.ptr(t) for t in out), _lib.ptr(side.buffer),
+                                      side.buffer.numel(), _lib.ptr(ws), ws.numel())
+    assert rc == _lib.HM_EINVAL and "another sweep precision" in _lib.last_error()
