@@ -1952,13 +1952,71 @@ __device__ __forceinline__ void multi_dot64(const float* __restrict__ a, const f
     for (int t = 0; t < N; ++t) dots[t] = wave_tree_sum(acc[t]);
 }
 
-template <int KL, int KM, int G, bool COLS>
+// Exact evaluation of a row's `need` first candidates c_list[0..need) (lane e owns candidate e; `need` is uniform over
+// the wave): fixed-order fp64 dots, up to four per pass over the row's features, then the row's exact top k under the
+// tie rule into out_val / out_idx (missing slots -inf / -1).
+template <int KM, bool COLS>
+__device__ __forceinline__ void exact_topk_write(const float* __restrict__ ar, const float* __restrict__ B, int d,
+                                                 int lane, int need, const int (&c_list)[KM], double ab,
+                                                 const double* __restrict__ bbias, double scale, int k,
+                                                 double* __restrict__ out_val, int* __restrict__ out_idx) {
+    double sv = -INFINITY;
+    int sj = -1;
+    for (int e0 = 0; e0 < need;) {
+        const int nb = need - e0 >= 4 ? 4 : (need - e0 >= 2 ? 2 : 1);
+        int c[4] = {-1, -1, -1, -1};
+#pragma unroll
+        for (int e = 0; e < KM; ++e) {
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+                if (e == e0 + t && t < nb) c[t] = c_list[e];
+        }
+        double dots[4];
+        if (nb == 4) multi_dot64<4>(ar, B, c, d, lane, dots);
+        else if (nb == 2) multi_dot64<2>(ar, B, c, d, lane, dots);
+        else multi_dot64<1>(ar, B, c, d, lane, dots);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            if (t < nb) {
+                const double sdot = scale * dots[t];
+                const double sig = COLS ? (sdot + bbias[c[t]]) + ab : (sdot + ab) + bbias[c[t]];
+                if (lane == e0 + t) { sv = sig; sj = c[t]; }
+            }
+        }
+        e0 += nb;
+    }
+    int er = 0;
+    for (int src = 0; src < need; ++src) {
+        const double v2 = __shfl(sv, src, 64);
+        const int j2 = __shfl(sj, src, 64);
+        if (lane < need && src != lane && better(v2, j2, sv, sj)) ++er;
+    }
+    if (lane < need && er < k) {
+        out_val[er] = sv;
+        out_idx[er] = sj;
+    }
+    if (lane >= need && lane < k) {
+        out_val[lane] = -INFINITY;
+        out_idx[lane] = -1;
+    }
+}
+
+// Deferred exact evaluation (the fused column finalize): the selection kernel stores each row's candidates and
+// `need`, and the rows are evaluated later in an order that groups rows by their first candidate, so that the
+// candidate side's rows are re-read from cache rather than memory.
+struct DeferBufs {
+    int* key = nullptr;   // [R] first candidate (a row of B), -1 when the row has nothing to evaluate
+    int* need = nullptr;  // [R]
+    int* cand = nullptr;  // [R * KM]
+};
+
+template <int KL, int KM, int G, bool COLS, bool DEFER = false>
 __global__ __launch_bounds__(256) void l2sq_finalize(
     const float* __restrict__ A, const float* __restrict__ B, int64_t R, int d, int nlists,
     const Entry* __restrict__ lists, const double* __restrict__ abias, const double* __restrict__ bbias,
     const double* __restrict__ anorm, const unsigned long long* __restrict__ bmaxima, double scale, int k,
     BoundArgs bnd, double* __restrict__ out_val, int* __restrict__ out_idx, int* __restrict__ redo,
-    float* __restrict__ redo_thr, int* __restrict__ redo_count) {
+    float* __restrict__ redo_thr, int* __restrict__ redo_count, DeferBufs defer = DeferBufs{}) {
     static_assert(KL <= KM, "merged lists hold at least one partial list");
     const int lane = threadIdx.x & 63;
     const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -2040,6 +2098,9 @@ __global__ __launch_bounds__(256) void l2sq_finalize(
     if ((full || merge_dropped) && (double)dropped >= (double)wk - 2.0 * b) {
         // queued for the wide pass: a candidate of the exact top-k has sigma >= sigma_k* >= wk - b, hence
         // w >= wk - 2b (the threshold is rounded down to fp32)
+        if constexpr (DEFER) {
+            if (lane == 0) defer.key[row] = -1;  // nothing to evaluate later
+        }
         if (lane == 0) {
             const int slot = atomicAdd(redo_count, 1);
             redo[slot] = (int)row;
@@ -2059,48 +2120,89 @@ __global__ __launch_bounds__(256) void l2sq_finalize(
     for (int e = 0; e < KM; ++e)
         if (e < kept && (double)tw[e] >= cut) need = e + 1;
     if (need < (kept < k ? kept : k)) need = kept < k ? kept : k;
-    double sv = -INFINITY;
-    int sj = -1;
-    const float* ar = A + row * (int64_t)d;
-    // up to four candidates per pass over the row's features (each load of the row serves every dot of the pass;
-    // every dot keeps the dot64 order); `need` is uniform over the wave
-    for (int e0 = 0; e0 < need;) {
-        const int nb = need - e0 >= 4 ? 4 : (need - e0 >= 2 ? 2 : 1);
-        int c[4] = {-1, -1, -1, -1};
+    if constexpr (DEFER) {
+        if (lane == 0) {
+            defer.need[row] = need;
+            defer.key[row] = need > 0 ? ti[0] : -1;
 #pragma unroll
-        for (int e = 0; e < KM; ++e) {
-#pragma unroll
-            for (int t = 0; t < 4; ++t)
-                if (e == e0 + t && t < nb) c[t] = ti[e];
+            for (int e = 0; e < KM; ++e)
+                if (e < need) defer.cand[row * KM + e] = ti[e];
         }
-        double dots[4];
-        if (nb == 4) multi_dot64<4>(ar, B, c, d, lane, dots);
-        else if (nb == 2) multi_dot64<2>(ar, B, c, d, lane, dots);
-        else multi_dot64<1>(ar, B, c, d, lane, dots);
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            if (t < nb) {
-                const double sdot = scale * dots[t];
-                const double sig = COLS ? (sdot + bbias[c[t]]) + abias[row] : (sdot + abias[row]) + bbias[c[t]];
-                if (lane == e0 + t) { sv = sig; sj = c[t]; }
-            }
+        if (need == 0 && lane < k) {
+            out_val[row * k + lane] = -INFINITY;
+            out_idx[row * k + lane] = -1;
         }
-        e0 += nb;
+        return;
     }
-    int er = 0;
-    for (int src = 0; src < need; ++src) {
-        const double v2 = __shfl(sv, src, 64);
-        const int j2 = __shfl(sj, src, 64);
-        if (lane < need && src != lane && better(v2, j2, sv, sj)) ++er;
+    exact_topk_write<KM, COLS>(A + row * (int64_t)d, B, d, lane, need, ti, abias[row], bbias, scale, k,
+                               out_val + row * k, out_idx + row * k);
+}
+
+// Deferred finalize, step 2: rows bucketed by their first candidate (a counting sort; the order within a bucket is
+// whatever the atomics give, which changes no result).
+// (keys outside [base, base + nb) cannot occur: every stored key is a candidate of this chunk; the test keeps the
+// counts in bounds regardless)
+__global__ void defer_count(const int* __restrict__ key, int64_t R, int base, int nb, int* __restrict__ count) {
+    for (int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; r < R; r += (int64_t)gridDim.x * blockDim.x) {
+        const int b = key[r] - base;
+        if (key[r] >= 0 && b >= 0 && b < nb) atomicAdd(&count[b], 1);
     }
-    if (lane < need && er < k) {
-        out_val[row * k + er] = sv;
-        out_idx[row * k + er] = sj;
+}
+
+// exclusive prefix sum of count[0..nb) into offset[0..nb] (one workgroup of 1024 threads)
+__global__ __launch_bounds__(1024) void defer_scan(const int* __restrict__ count, int nb, int* __restrict__ offset,
+                                                   int* __restrict__ total) {
+    __shared__ int part[1024];
+    const int t = threadIdx.x;
+    const int per = (nb + 1023) / 1024;
+    int s = 0;
+    for (int i = t * per; i < nb && i < (t + 1) * per; ++i) s += count[i];
+    part[t] = s;
+    __syncthreads();
+    for (int o = 1; o < 1024; o <<= 1) {
+        const int v = t >= o ? part[t - o] : 0;
+        __syncthreads();
+        part[t] += v;
+        __syncthreads();
     }
-    if (lane >= need && lane < k) {
-        out_val[row * k + lane] = -INFINITY;
-        out_idx[row * k + lane] = -1;
+    int run = t > 0 ? part[t - 1] : 0;
+    for (int i = t * per; i < nb && i < (t + 1) * per; ++i) {
+        offset[i] = run;
+        run += count[i];
     }
+    if (t == 1023) {
+        offset[nb] = part[1023];
+        *total = part[1023];
+    }
+}
+
+__global__ void defer_scatter(const int* __restrict__ key, int64_t R, int base, int nb, int* __restrict__ offset,
+                              int* __restrict__ order) {
+    for (int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; r < R; r += (int64_t)gridDim.x * blockDim.x) {
+        const int b = key[r] - base;
+        if (key[r] >= 0 && b >= 0 && b < nb) order[atomicAdd(&offset[b], 1)] = (int)r;
+    }
+}
+
+// Deferred finalize, step 3: one wave per bucketed row, the exact evaluation of its stored candidates. `total`
+// (the number of bucketed rows) is read from the device.
+template <int KM, bool COLS>
+__global__ __launch_bounds__(256) void l2sq_finalize_exact(const float* __restrict__ A, const float* __restrict__ B,
+                                                           int d, const int* __restrict__ order,
+                                                           const int* __restrict__ total, DeferBufs defer,
+                                                           const double* __restrict__ abias,
+                                                           const double* __restrict__ bbias, double scale, int k,
+                                                           double* __restrict__ out_val, int* __restrict__ out_idx) {
+    const int lane = threadIdx.x & 63;
+    const int64_t w = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (w >= *total) return;  // uniform per wave
+    const int64_t row = order[w];
+    const int need = defer.need[row];
+    int c_list[KM];
+#pragma unroll
+    for (int e = 0; e < KM; ++e) c_list[e] = e < need ? defer.cand[row * KM + e] : -1;
+    exact_topk_write<KM, COLS>(A + row * (int64_t)d, B, d, lane, need, c_list, abias[row], bbias, scale, k,
+                               out_val + row * k, out_idx + row * k);
 }
 
 // Sliced exact rescan: item (queued row, candidate slice) is one wave. Candidates are evaluated four at a time
@@ -2333,6 +2435,13 @@ __global__ void l2sq_wide_merge(const double* __restrict__ pv, const int* __rest
 struct WideBufs {
     float* redo_thr;   // [m + n] thresholds of the rows a finalize queued, by queue slot
     float* qs;         // [panel_rows(WIDE_ROWS)] int8 scales of the gathered rows (int8 sweep)
+    // deferred column finalize (fused columns): per column its first candidate, need and candidates, the
+    // bucket counts / offsets of a chunk's X rows, the bucketed order and its length
+    DeferBufs defer;
+    int* dcount;
+    int* doffset;
+    int* dorder;
+    int* dtotal;
     float* rows;       // [panel_rows(WIDE_ROWS) * ld] gathered sweep rows
     float* thr;        // [panel_rows(WIDE_ROWS)]
     int* cnt;          // [panel_rows(WIDE_ROWS)]
@@ -2598,6 +2707,13 @@ void layout(A& a, int64_t m, int64_t n, int d, int k, uint32_t flags, double** x
     wide->counts = a.template take<int>(4);
     wide->rowthr = a.template take<unsigned int>((size_t)std::max<int64_t>(std::max<int64_t>(c.ch, c.ch2), 1));
     wide->qs = a.template take<float>((size_t)wq);
+    wide->defer.key = a.template take<int>(fused ? (size_t)n : 1);
+    wide->defer.need = a.template take<int>(fused ? (size_t)n : 1);
+    wide->defer.cand = a.template take<int>(fused ? (size_t)n * c.km : 1);
+    wide->dcount = a.template take<int>(fused ? (size_t)c.ch + 1 : 1);
+    wide->doffset = a.template take<int>(fused ? (size_t)c.ch + 1 : 1);
+    wide->dorder = a.template take<int>(fused ? (size_t)n : 1);
+    wide->dtotal = a.template take<int>(1);
     *q8 = I8Bufs{};
     if (i8) {
         q8->xqs = a.template take<float>((size_t)m);
@@ -2831,11 +2947,25 @@ int run_bidir(hipStream_t st, const float* X, const float* Y, int64_t m, int64_t
             // column finalize: one list per X panel of this chunk; candidates are the chunk's X rows (global ids)
             hipLaunchKernelGGL(zero_words, dim3(1), dim3(64), 0, st, reinterpret_cast<unsigned long long*>(redo_count), 1);
             prof_begin(st, "l2sq_col_finalize");
-            hipLaunchKernelGGL((l2sq_finalize<K1, KM, 1, true>), dim3((unsigned)((n + 3) / 4)), dim3(256), 0, st, Y, X, n, d,
-                               (int)panels, colpart, db, qb, ynorm, maxima, scale, k, bound_for(true, 0), cval, cidx,
-                               redo, wide.redo_thr, redo_count);
-            prof_end(st);
+            // selection (queued columns go to the wide pass), then the exact evaluation with the columns grouped by
+            // their first candidate: the chunk's X rows are then read about once each rather than once per column
+            hipLaunchKernelGGL((l2sq_finalize<K1, KM, 1, true, true>), dim3((unsigned)((n + 3) / 4)), dim3(256), 0, st,
+                               Y, X, n, d, (int)panels, colpart, db, qb, ynorm, maxima, scale, k, bound_for(true, 0),
+                               cval, cidx, redo, wide.redo_thr, redo_count, wide.defer);
             HM_LAUNCH_CHECK("l2sq_col_finalize");
+            const unsigned egrid = (unsigned)((n + 255) / 256 < 8192 ? (n + 255) / 256 : 8192);
+            hipLaunchKernelGGL(fill_u32, dim3((unsigned)((rows + 256) / 256)), dim3(256), 0, st,
+                               reinterpret_cast<unsigned int*>(wide.dcount), rows, 0u);
+            hipLaunchKernelGGL(defer_count, dim3(egrid), dim3(256), 0, st, wide.defer.key, n, (int)xb, (int)rows,
+                               wide.dcount);
+            hipLaunchKernelGGL(defer_scan, dim3(1), dim3(1024), 0, st, wide.dcount, (int)rows, wide.doffset,
+                               wide.dtotal);
+            hipLaunchKernelGGL(defer_scatter, dim3(egrid), dim3(256), 0, st, wide.defer.key, n, (int)xb, (int)rows,
+                               wide.doffset, wide.dorder);
+            hipLaunchKernelGGL((l2sq_finalize_exact<KM, true>), dim3((unsigned)((n + 3) / 4)), dim3(256), 0, st, Y, X,
+                               d, wide.dorder, wide.dtotal, wide.defer, db, qb, scale, k, cval, cidx);
+            prof_end(st);
+            HM_LAUNCH_CHECK("l2sq_col_finalize (exact)");
             if (int rc = wide_resolve(st, split, two_level, Y, SY, X + xb * d, SX + xb * ld, rows, d, sd, ld,
                                       qb32 + xb, db, qb + xb, scale, k, redo, redo_count, cval, cidx, 1, (int)xb,
                                       wide, rpv, rpi, q8.yqs, i8 ? q8.xqs + xb : nullptr))
