@@ -1047,7 +1047,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(COLS ? 1 : 
 
     const int nchunks = d / KC;
     const int64_t bstride = (int64_t)ld * 32;          // words per 32-row block
-    const float* Xw = X + ((x0 >> 5) + wave) * bstride;  // this wave's X block
+    const float* Xw = X + (((x0 - xb) >> 5) + wave) * bstride;  // this wave's X block (X starts at row xb)
     const unsigned lane16 = (unsigned)lane * 16u;
     const unsigned tid16 = (unsigned)tid * 16u;
     const unsigned ystep = (unsigned)(bstride * 4);     // bytes between consecutive Y blocks
@@ -1525,7 +1525,7 @@ __global__ __launch_bounds__(THREADS_W) void l2sq_sweep_split_w(
 
     const int nchunks = d / KC;
     const int64_t bstride = (int64_t)ld * 32;          // words per 32-row block
-    const float* Xw = X + ((x0 >> 5) + wave) * bstride;  // this wave's X block
+    const float* Xw = X + (((x0 - xb) >> 5) + wave) * bstride;  // this wave's X block (X starts at row xb)
     const unsigned lane16 = (unsigned)lane * 16u;
     const unsigned t16 = (unsigned)(tid & 255) * 16u;
     const unsigned bstep = (unsigned)(bstride * 4);     // bytes between consecutive 32-row blocks
@@ -1734,7 +1734,7 @@ __global__ __launch_bounds__(THREADS_W) void l2sq_sweep_i8_w(
 
     const int nchunks = d / KC;
     const int64_t bstride = (int64_t)ld * 32;          // words per 32-row block
-    const float* Xw = X + ((x0 >> 5) + wave) * bstride;  // this wave's X block
+    const float* Xw = X + (((x0 - xb) >> 5) + wave) * bstride;  // this wave's X block (X starts at row xb)
     const unsigned lane16 = (unsigned)lane * 16u;
     const unsigned t16 = (unsigned)(tid & 255) * 16u;
     const unsigned bstep = (unsigned)(bstride * 4);     // bytes between consecutive 32-row blocks
@@ -2623,6 +2623,9 @@ struct CallPlan {
     int kl, km;
     int bx;  // X rows per sweep workgroup
     bool fused, swapped, row_pass;
+    // split copies made per internal chunk of the swept side (the other side's copy is whole): X's when only the
+    // row pass runs, Y's when only the swapped pass runs; both whole when both run
+    bool x_chunked, y_chunked;
     int64_t ch, ch2;  // chunk rows of the row pass and of the swapped pass
     DirPlan plan, plan2;
 };
@@ -2634,6 +2637,9 @@ inline CallPlan plan_call(int64_t m, int64_t n, int d, int k, uint32_t flags) {
     c.swapped = (flags & HM_COLS) && !c.fused;
     c.row_pass = (flags & HM_ROWS) || c.fused || (flags & HM_STATS);
     c.bx = sweep_panel(d, flags);
+    const bool split = (flags & (HM_BF16X3 | HM_INT8X3)) != 0;
+    c.x_chunked = split && c.row_pass && !c.swapped;
+    c.y_chunked = split && c.swapped && !c.row_pass;
     static const int sizes[3] = {8, 16, 40};
     // the int8 sweep's wider bound also wants deeper partial lists once k > 2 (their last entries bound what
     // they dropped)
@@ -2690,8 +2696,9 @@ void layout(A& a, int64_t m, int64_t n, int d, int k, uint32_t flags, double** x
     const bool split = (flags & (HM_BF16X3 | HM_INT8X3)) != 0;
     const size_t ldw = (size_t)(i8 ? i8_ld(d) : split_ld(d));
     // split copies cover whole 256-row panels: either side may be the swept one
-    *xsplit = a.template take<float>(split ? (size_t)panel_rows(m, BXW) * ldw : 1);
-    *ysplit = y_resident ? nullptr : a.template take<float>(split ? (size_t)panel_rows(n, BXW) * ldw : 1);
+    *xsplit = a.template take<float>(split ? (size_t)panel_rows(c.x_chunked ? c.ch : m, BXW) * ldw : 1);
+    *ysplit = y_resident ? nullptr
+                         : a.template take<float>(split ? (size_t)panel_rows(c.y_chunked ? c.ch2 : n, BXW) * ldw : 1);
     *rpv = a.template take<double>((size_t)RESCAN_ITEMS * k);
     *rpi = a.template take<int>((size_t)RESCAN_ITEMS * k);
     const int64_t wq = panel_rows(WIDE_ROWS, BXW);
@@ -2833,21 +2840,27 @@ int run_bidir(hipStream_t st, const float* X, const float* Y, int64_t m, int64_t
     const DirPlan plan = cp.plan;
     const int bx = cp.bx;
     unsigned int* rowthr = wide.rowthr;
-    // sweep copies (the Y side's only when it is not a prepared resident side)
-    if (i8) {
-        // the row scales and ||.||_1 come from the prep pass; the copies add ||l||_2 and the error terms
-        launch_split_i8(st, X, m, d, sd, ld, q8.xqs, q8.xl1, xnorm, xsplit, q8.xterm, q8.qmax_x);
-        if (!q8.y_ready) launch_split_i8(st, Y, n, d, sd, ld, q8.yqs, q8.yl1, ynorm, ysplit, q8.yterm, q8.qmax_y);
-    } else if (split) {
-        hipLaunchKernelGGL(l2sq_split_bf16, dim3(4096), dim3(256), 0, st, X, m, panel_rows(m, BXW), d, sd, ld,
-                           reinterpret_cast<unsigned short*>(xsplit));
-        HM_LAUNCH_CHECK("l2sq_split_bf16");
-        if (!q8.y_ready) {
-            hipLaunchKernelGGL(l2sq_split_bf16, dim3(4096), dim3(256), 0, st, Y, n, panel_rows(n, BXW), d, sd, ld,
-                               reinterpret_cast<unsigned short*>(ysplit));
-            HM_LAUNCH_CHECK("l2sq_split_bf16");
+    // Sweep copies: rows [r0, r0 + rows) of one side into `out` (its row r0 first). A side whose copy is made per
+    // internal chunk (CallPlan::x_chunked / y_chunked) is copied in the chunk loops below, the others here whole (the
+    // Y side not at all when it is a prepared resident side). The int8 row scales and ||.||_1 come from the prep
+    // pass; the int8 copy adds ||l||_2, the rows' error terms and the copied rows' maxima.
+    auto copy_rows = [&](bool y_side, int64_t r0, int64_t rows, float* out) {
+        const float* src = (y_side ? Y : X) + r0 * d;
+        if (i8) {
+            if (y_side)
+                launch_split_i8(st, src, rows, d, sd, ld, q8.yqs + r0, q8.yl1 + r0, ynorm + r0, out,
+                                q8.yterm + 4 * r0, q8.qmax_y);
+            else
+                launch_split_i8(st, src, rows, d, sd, ld, q8.xqs + r0, q8.xl1 + r0, xnorm + r0, out,
+                                q8.xterm + 4 * r0, q8.qmax_x);
+        } else {
+            hipLaunchKernelGGL(l2sq_split_bf16, dim3(4096), dim3(256), 0, st, src, rows, panel_rows(rows, BXW), d, sd,
+                               ld, reinterpret_cast<unsigned short*>(out));
         }
-    }
+        HM_LAUNCH_CHECK("split copy");
+    };
+    if (split && !cp.x_chunked) copy_rows(false, 0, m, xsplit);
+    if (split && !cp.y_chunked && !q8.y_ready) copy_rows(true, 0, n, ysplit);
     // Rigorous bound on |w - exact| in units of scale*||x||*||y||: accumulation of B-feature blocks in fp32
     // (gamma over the additions of a block, then over the blocks), plus for the split products the dropped
     // terms lo*lo + hi*e + e*hi + ... <= (3 * 2^-16 * (1 + 2^-7) + 3 * 2^-24) |x_k y_k|.
@@ -2882,6 +2895,9 @@ int run_bidir(hipStream_t st, const float* X, const float* Y, int64_t m, int64_t
         const int64_t panels = (rows + bx - 1) / bx;
         const dim3 grid(sweep_grid(panels, plan.S));
         const unsigned neg_inf_key = 0x007fffffu;  // float_key(-INFINITY)
+        // this chunk's split copy of X (the sweeps take the copy from the chunk's first row)
+        if (split && cp.x_chunked) copy_rows(false, xb, rows, xsplit);
+        const float* SXc = !split ? SX : (cp.x_chunked ? xsplit : SX + xb * ld);
         if (fused) {
             // column thresholds start at -inf for every chunk (its lists only rank its own X rows)
             hipLaunchKernelGGL(fill_u32, dim3((unsigned)((n + 255) / 256 < 4096 ? (n + 255) / 256 : 4096)), dim3(256), 0,
@@ -2896,15 +2912,15 @@ int run_bidir(hipStream_t st, const float* X, const float* Y, int64_t m, int64_t
 #define HM_SWEEP(TL, CL)                                                                                             \
     do {                                                                                                             \
         if (i8)                                                                                                      \
-            hipLaunchKernelGGL((l2sq_sweep_i8_w<K1, CL>), grid, dim3(THREADS_W), 0, st, SX, SY, xb, xe, n, sd, ld,   \
+            hipLaunchKernelGGL((l2sq_sweep_i8_w<K1, CL>), grid, dim3(THREADS_W), 0, st, SXc, SY, xb, xe, n, sd, ld,  \
                                qb32, db32, p32, ge32, (float)scale, plan.seg_len, (int)panels, plan.S, part,         \
                                colpart, colthr, blockstats, (int)want_stats, cert, q8.xqs, q8.yqs, NOWIDE, rowthr); \
         else if (split && TL)                                                                                        \
-            hipLaunchKernelGGL((l2sq_sweep_split_w<K1, CL>), grid, dim3(THREADS_W), 0, st, SX, SY, xb, xe, n, sd,    \
+            hipLaunchKernelGGL((l2sq_sweep_split_w<K1, CL>), grid, dim3(THREADS_W), 0, st, SXc, SY, xb, xe, n, sd,   \
                                ld, qb32, db32, p32, ge32, (float)scale, plan.seg_len, (int)panels, plan.S, part,     \
                                colpart, colthr, blockstats, (int)want_stats, cert, NOWIDE, rowthr);                 \
         else if (split)                                                                                              \
-            hipLaunchKernelGGL((l2sq_sweep_split<K1, CL>), grid, dim3(256), 0, st, SX, SY, xb, xe, n, sd, ld, \
+            hipLaunchKernelGGL((l2sq_sweep_split<K1, CL>), grid, dim3(256), 0, st, SXc, SY, xb, xe, n, sd, ld, \
                                qb32, db32, p32, ge32, (float)scale, plan.seg_len, (int)panels, plan.S, part,         \
                                colpart, colthr, blockstats, (int)want_stats, cert, NOWIDE, rowthr);                 \
         else                                                                                                         \
@@ -2938,7 +2954,7 @@ int run_bidir(hipStream_t st, const float* X, const float* Y, int64_t m, int64_t
                                redo_count);
             prof_end(st);
             HM_LAUNCH_CHECK("l2sq_finalize");
-            if (int rc = wide_resolve(st, split, two_level, X + xb * d, SX + xb * ld, Y, SY, n, d, sd, ld, db32,
+            if (int rc = wide_resolve(st, split, two_level, X + xb * d, SXc, Y, SY, n, d, sd, ld, db32,
                                       qb + xb, db, scale, k, redo, redo_count, row_val + xb * k, row_idx + xb * k, 0,
                                       0, wide, rpv, rpi, i8 ? q8.xqs + xb : nullptr, q8.yqs))
                 return rc;
@@ -2966,7 +2982,7 @@ int run_bidir(hipStream_t st, const float* X, const float* Y, int64_t m, int64_t
                                d, wide.dorder, wide.dtotal, wide.defer, db, qb, scale, k, cval, cidx);
             prof_end(st);
             HM_LAUNCH_CHECK("l2sq_col_finalize (exact)");
-            if (int rc = wide_resolve(st, split, two_level, Y, SY, X + xb * d, SX + xb * ld, rows, d, sd, ld,
+            if (int rc = wide_resolve(st, split, two_level, Y, SY, X + xb * d, SXc, rows, d, sd, ld,
                                       qb32 + xb, db, qb + xb, scale, k, redo, redo_count, cval, cidx, 1, (int)xb,
                                       wide, rpv, rpi, q8.yqs, i8 ? q8.xqs + xb : nullptr))
                 return rc;
@@ -2985,21 +3001,24 @@ int run_bidir(hipStream_t st, const float* X, const float* Y, int64_t m, int64_t
             const int64_t rows = ye - yb;
             const int64_t panels2 = (rows + bx - 1) / bx;
             const dim3 grid(sweep_grid(panels2, plan2.S));
+            // this chunk's split copy of Y (from its first row; a resident side's copy is whole)
+            if (split && cp.y_chunked && !q8.y_ready) copy_rows(true, yb, rows, ysplit);
+            const float* SYc = !split ? SY : ((cp.y_chunked && !q8.y_ready) ? ysplit : SY + yb * ld);
             hipLaunchKernelGGL(fill_u32, dim3((unsigned)((rows + 255) / 256 < 4096 ? (rows + 255) / 256 : 4096)),
                                dim3(256), 0, st, rowthr, rows, 0x007fffffu /* float_key(-INFINITY) */);
             HM_LAUNCH_CHECK("fill_u32");
 #define HM_SWEEP2(TL)                                                                                                \
     do {                                                                                                             \
         if (i8)                                                                                                      \
-            hipLaunchKernelGGL((l2sq_sweep_i8_w<K1, false>), grid, dim3(THREADS_W), 0, st, SY, SX, yb, ye, m, sd,    \
+            hipLaunchKernelGGL((l2sq_sweep_i8_w<K1, false>), grid, dim3(THREADS_W), 0, st, SYc, SX, yb, ye, m, sd,   \
                                ld, db32, qb32, ge32, p32, (float)scale, plan2.seg_len, (int)panels2, plan2.S, part,  \
                                colpart, colthr, blockstats, 0, CertArgs{}, q8.yqs, q8.xqs, NOWIDE, rowthr);         \
         else if (split && TL)                                                                                        \
-            hipLaunchKernelGGL((l2sq_sweep_split_w<K1, false>), grid, dim3(THREADS_W), 0, st, SY, SX, yb, ye, m, sd, \
+            hipLaunchKernelGGL((l2sq_sweep_split_w<K1, false>), grid, dim3(THREADS_W), 0, st, SYc, SX, yb, ye, m, sd,\
                                ld, db32, qb32, ge32, p32, (float)scale, plan2.seg_len, (int)panels2, plan2.S, part,  \
                                colpart, colthr, blockstats, 0, CertArgs{}, NOWIDE, rowthr);                         \
         else if (split)                                                                                              \
-            hipLaunchKernelGGL((l2sq_sweep_split<K1, false>), grid, dim3(256), 0, st, SY, SX, yb, ye, m, sd,  \
+            hipLaunchKernelGGL((l2sq_sweep_split<K1, false>), grid, dim3(256), 0, st, SYc, SX, yb, ye, m, sd, \
                                ld, db32, qb32, ge32, p32, (float)scale, plan2.seg_len, (int)panels2, plan2.S, part,  \
                                colpart, colthr, blockstats, 0, CertArgs{}, NOWIDE, rowthr);                         \
         else                                                                                                         \
@@ -3022,7 +3041,7 @@ int run_bidir(hipStream_t st, const float* X, const float* Y, int64_t m, int64_t
                                redo_count);
             prof_end(st);
             HM_LAUNCH_CHECK("l2sq_col_finalize");
-            if (int rc = wide_resolve(st, split, two_level, Y + yb * d, SY + yb * ld, X, SX, m, d, sd, ld, qb32,
+            if (int rc = wide_resolve(st, split, two_level, Y + yb * d, SYc, X, SX, m, d, sd, ld, qb32,
                                       db + yb, qb, scale, k, redo, redo_count, col_val + yb * k, col_idx + yb * k, 1,
                                       0, wide, rpv, rpi, i8 ? q8.yqs + yb : nullptr, q8.xqs))
                 return rc;
