@@ -56,6 +56,7 @@ constexpr int KC = 32;             // features per LDS chunk
 constexpr int STR = KC + 4;        // LDS row stride (floats)
 constexpr int STAGE = (BX + BY) * STR;  // floats per LDS stage of the sweep (X tile, then Y tile)
 constexpr int CST = BX + 1;        // LDS row stride of the column-score tile (floats)
+constexpr int QN = 12;             // queued row candidates per lane and tile (128-row sweeps; one spare slot more)
 constexpr int FLUSH_CHUNKS = 8;    // fp32 block length 256 features before folding into the outer sum
 constexpr int FLUSH_SPLIT = 4;     // split-bf16 block length 128 features (3 product terms per feature)
 constexpr int64_t CHUNK_MAX = 65536;          // X rows per internal chunk
@@ -539,7 +540,7 @@ __device__ __forceinline__ void sweep_epilogue(const v16f (&tot)[NB], SweepRow<K
                                                float* sC, Entry* __restrict__ colpart,
                                                unsigned int* __restrict__ colthr, int* __restrict__ wcnt,
                                                int* __restrict__ wbuf, int wcap, unsigned int* __restrict__ rowthr,
-                                               int64_t xb) {
+                                               int64_t xb, Entry* sQ) {
     float tnum = 0.0f, tden = 0.0f;
     unsigned int tcnt = 0;
     bool near = false;  // a pair of this tile within the certificate slack (cert_fast)
@@ -549,6 +550,12 @@ __device__ __forceinline__ void sweep_epilogue(const v16f (&tot)[NB], SweepRow<K
     // the row's shared threshold: scores at or below it cannot enter the row's merged lists (row_threshold_*)
     const float rthr = (!APPEND && s.ok) ? row_threshold_get(rowthr, s.row - xb) : -INFINITY;
     const float last0 = APPEND ? 0.0f : s.lv[K1 - 1];
+    // Row candidates of the tile: every score above the lane's threshold at the start of the tile is queued in the
+    // lane's LDS slots, without branches (a full queue writes its spare slot), and inserted after the tile in pair
+    // order. A lane with more than QN candidates (a segment's first tiles) inserts the tile directly instead.
+    const float qthr = fmaxf(s.lv[K1 - 1], rthr);
+    Entry* myq = sQ + tid * (QN + 1);
+    int qn = 0;
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
 #pragma unroll
@@ -571,22 +578,37 @@ __device__ __forceinline__ void sweep_epilogue(const v16f (&tot)[NB], SweepRow<K
                         const int pos = atomicAdd(&wcnt[s.row], 1);
                         if (pos < wcap) wbuf[s.row * (int64_t)wcap + pos] = (int)j;
                     }
-                } else if (ok && w > s.lv[K1 - 1] && w > rthr) {
-                    float cv = w;
-                    int ci = (int)j;
-#pragma unroll
-                    for (int i = 0; i < K1; ++i) {
-                        if (cv > s.lv[i]) {
-                            const float tv = s.lv[i];
-                            const int ti = s.li[i];
-                            s.lv[i] = cv;
-                            s.li[i] = ci;
-                            cv = tv;
-                            ci = ti;
-                        }
-                    }
+                } else {
+                    const bool cand = ok && w > qthr;
+                    myq[qn < QN ? qn : QN] = Entry{w, (int)j};
+                    qn += cand ? 1 : 0;
                 }
                 if (STATS) cert_fast(ok, w, ges[cc], s.pi, s.qbi, slack, tden, s.cmax, tnum, tcnt, near);
+            }
+        }
+    }
+    if (!APPEND) {
+        if (qn > QN) {
+            // direct insertion of the whole tile (the queue overflowed)
+            asm volatile("" ::: "memory");
+#pragma unroll
+            for (int b = 0; b < NB; ++b) {
+#pragma unroll
+                for (int q = 0; q < 16; ++q) {
+                    const int jl = b * 32 + 8 * (q / 4) + 4 * h + (q % 4);
+                    const float w = fmaf(scale, tot[b][q], sDB[jl]);
+                    const bool ok = s.ok && 4 * h < ylim - (jl - 4 * h);
+                    if (ok && w > s.lv[K1 - 1] && w > rthr) insert_e<K1>(s.lv, s.li, w, (int)(ytile + jl));
+                }
+            }
+        } else {
+            // the queue, in pair order; the loop runs as often as the wave's longest queue
+            for (int e = 0; e < QN; ++e) {
+                if (!__any(e < qn)) break;
+                if (e < qn) {
+                    const Entry c = myq[e];
+                    if (c.w > s.lv[K1 - 1]) insert_e<K1>(s.lv, s.li, c.w, c.j);
+                }
             }
         }
     }
@@ -613,6 +635,7 @@ __device__ __forceinline__ void sweep_epilogue(const v16f (&tot)[NB], SweepRow<K
         s.cnt += tcnt;
     }
     if (COLS) {
+        __syncthreads();  // every lane's queue (in sC's space) is read before the column scores overwrite it
         // each Y row of the tile: its best K1 over this workgroup's 128 X rows (TPR threads per row, merged by
         // shuffles). colthr[j] is the K1-th value of some full list of this chunk, a lower bound of the chunk's
         // K1-th value: scores at or below it cannot enter the merged top-K1 and are skipped.
@@ -727,7 +750,9 @@ __global__ __launch_bounds__(256) void l2sq_sweep(
     __shared__ double sQB64[STATS_LDS(BX)], sDB64[STATS_LDS(BY)];  // fp64 biases for the certificate's near pairs
     __shared__ float sDB[BY];
     __shared__ float sGE[BY];
-    __shared__ float sC[COLS ? BY * CST : 1];
+    __shared__ __align__(16) float sC[COLS ? BY * CST : 1];
+    // queued row candidates (sweep_epilogue); with column lists they use the column-score tile's space
+    __shared__ Entry sQ[(APPEND || COLS) ? 1 : 256 * (QN + 1)];
     __shared__ double sRed[4][5];
 
     const int tid = threadIdx.x;
@@ -905,7 +930,8 @@ __global__ __launch_bounds__(256) void l2sq_sweep(
         }
         sweep_epilogue<K1, COLS, APPEND>(acc, s, tid, wave, h, r, ytile, y_end, x0, panel, n, scale, STATS, slack,
                                          sQB64, sDB64, sDB, sGE,
-                                         sC, colpart, colthr, wcnt, wbuf, wcap, rowthr, xb);
+                                         sC, colpart, colthr, wcnt, wbuf, wcap, rowthr, xb,
+                                         COLS ? reinterpret_cast<Entry*>(sC) : sQ);
     }
     sweep_finish<K1, APPEND>(s, tid, lane, wave, h, seg, rows, xb, P, panel, STATS, part, blockstats, sRed);
 }
@@ -1028,7 +1054,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(COLS ? 1 : 
     __shared__ double sQB64[STATS_LDS(BX)], sDB64[STATS_LDS(BY)];  // fp64 biases for the certificate's near pairs
     __shared__ float sDB[BY];
     __shared__ float sGE[BY];
-    __shared__ float sC[COLS ? BY * CST : 1];
+    __shared__ __align__(16) float sC[COLS ? BY * CST : 1];
+    // queued row candidates (sweep_epilogue); with column lists they use the column-score tile's space
+    __shared__ Entry sQ[(APPEND || COLS) ? 1 : 256 * (QN + 1)];
     __shared__ double sRed[4][5];
 
     const int tid = threadIdx.x;
@@ -1171,7 +1199,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(COLS ? 1 : 
         }
         sweep_epilogue<K1, COLS, APPEND>(acc, s, tid, wave, h, r, ytile, y_end, x0, panel, n, scale, STATS, slack,
                                          sQB64, sDB64, sDB, sGE,
-                                         sC, colpart, colthr, wcnt, wbuf, wcap, rowthr, xb);
+                                         sC, colpart, colthr, wcnt, wbuf, wcap, rowthr, xb,
+                                         COLS ? reinterpret_cast<Entry*>(sC) : sQ);
     }
     wait_vmcnt<0>();  // the loads ahead into LDS land before the workgroup can end
     sweep_finish<K1, APPEND>(s, tid, lane, wave, h, seg, rows, xb, P, panel, STATS, part, blockstats, sRed);
