@@ -1972,7 +1972,23 @@ __device__ __forceinline__ void multi_dot64(const float* __restrict__ a, const f
     double acc[N];
 #pragma unroll
     for (int t = 0; t < N; ++t) acc[t] = 0.0;
-    for (int f = lane; f < d; f += 64) {
+    // eight strides of loads in flight per pass (the sums still take each lane's features in order)
+    constexpr int U = 8;
+    int f = lane;
+    for (; f + 64 * (U - 1) < d; f += 64 * U) {
+        float xa[U], xb[U][N];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            xa[u] = a[f + 64 * u];
+#pragma unroll
+            for (int t = 0; t < N; ++t) xb[u][t] = b[t][f + 64 * u];
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+#pragma unroll
+            for (int t = 0; t < N; ++t) acc[t] = acc[t] + (double)xa[u] * (double)xb[u][t];
+    }
+    for (; f < d; f += 64) {
         const double xa = (double)a[f];
 #pragma unroll
         for (int t = 0; t < N; ++t) acc[t] = acc[t] + xa * (double)b[t][f];
@@ -2057,19 +2073,41 @@ __global__ __launch_bounds__(256) void l2sq_finalize(
     int nreal = 0, full = 0;
     float tail = -INFINITY;  // largest last entry of a full list: everything its sweep dropped is <= it
     if (valid) {
+        static_assert(KL % 2 == 0, "lists are read two entries per 16-byte load");
         for (int L = lane; L < nlists; L += 64) {
-            const Entry* src = lists + ((((int64_t)(L / G)) * R + row) * G + (L % G)) * KL;
+            // a list is KL entries, filled from the front (missing entries j = -1), 16-byte aligned: it is read
+            // eight entries per group of four independent loads
+            const int4* src = reinterpret_cast<const int4*>(lists +
+                                                            ((((int64_t)(L / G)) * R + row) * G + (L % G)) * KL);
             int cnt = 0;
-            for (int s = 0; s < KL; ++s) {
-                const Entry e = src[s];
-                if (e.j < 0) break;
-                ++cnt;
-                if (better_e(e.w, e.j, lw[KM - 1], li[KM - 1])) insert_e<KM>(lw, li, e.w, e.j);
+            bool open = true;
+            float last = -INFINITY;
+            for (int g = 0; g < KL / 2 && open; g += 4) {
+                int4 q[4];
+#pragma unroll
+                for (int u = 0; u < 4; ++u)
+                    if (g + u < KL / 2) q[u] = src[g + u];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    if (g + u < KL / 2) {
+#pragma unroll
+                        for (int h = 0; h < 2; ++h) {
+                            const float w = __int_as_float(h ? q[u].z : q[u].x);
+                            const int j = h ? q[u].w : q[u].y;
+                            open = open && j >= 0;
+                            if (open) {
+                                ++cnt;
+                                last = w;
+                                if (better_e(w, j, lw[KM - 1], li[KM - 1])) insert_e<KM>(lw, li, w, j);
+                            }
+                        }
+                    }
+                }
             }
             nreal += cnt;
             if (cnt == KL) {
                 full = 1;
-                tail = fmaxf(tail, src[KL - 1].w);
+                tail = fmaxf(tail, last);
             }
         }
     }
@@ -2078,36 +2116,8 @@ __global__ __launch_bounds__(256) void l2sq_finalize(
         full |= __shfl_xor(full, o, 64);
         tail = fmaxf(tail, __shfl_xor(tail, o, 64));
     }
-    // wave top-KM: KM rounds of an arg-best over the lanes' list heads
-    float tw[KM];
-    int ti[KM];
-#pragma unroll
-    for (int t = 0; t < KM; ++t) {
-        float bw = lw[0];
-        int bi = li[0];
-        int bl = lane;
-        for (int o = 32; o >= 1; o >>= 1) {
-            const float ow = __shfl_xor(bw, o, 64);
-            const int oi = __shfl_xor(bi, o, 64);
-            const int ol = __shfl_xor(bl, o, 64);
-            if (better_e(ow, oi, bw, bi)) { bw = ow; bi = oi; bl = ol; }
-        }
-        tw[t] = bw;
-        ti[t] = bi;
-        if (lane == bl) {
-#pragma unroll
-            for (int s = 0; s + 1 < KM; ++s) { lw[s] = lw[s + 1]; li[s] = li[s + 1]; }
-            lw[KM - 1] = -INFINITY;
-            li[KM - 1] = -1;
-        }
-    }
-    if (!valid) return;
+    if (!valid) return;  // uniform per wave; nothing below synchronises across waves
     const int kept = nreal < KM ? nreal : KM;
-    float wk = -INFINITY;
-#pragma unroll
-    for (int t = 0; t < KM; ++t)
-        if (t == k - 1) wk = tw[t];
-    if (nreal < k) wk = -INFINITY;
     const double bmax = key_double(bmaxima[0]);
     const double dmax = key_double(bmaxima[1]);
     const double nxy = scale * anorm[row] * bmax;
@@ -2118,6 +2128,39 @@ __global__ __launch_bounds__(256) void l2sq_finalize(
         const double ma = key_double(bnd.qmax[0]), mb = key_double(bnd.qmax[1]);
         const double mg = key_double(bnd.qmax[2]), mr = key_double(bnd.qmax[3]);
         b += scale * (qt[0] * mb + qt[1] * ma + qt[2] * mg + 5.0 * 0x1p-24 * qt[3] * mr) * (1.0 + 1e-6);
+    }
+    // wave top-KM: rounds of an arg-best over the lanes' list heads (tw non-increasing). The rounds stop after the
+    // first entry t >= k - 1 below wk - 2b (or after the last real entry): no later entry is evaluated, and one
+    // that the merge drops then has w <= tw[t] < wk - 2b, so every decision below is what all KM rounds give.
+    float tw[KM];
+    int ti[KM];
+#pragma unroll
+    for (int t = 0; t < KM; ++t) { tw[t] = -INFINITY; ti[t] = -1; }
+    float wk = -INFINITY;
+    bool more = true;  // uniform per wave: every lane holds the same round results
+#pragma unroll
+    for (int t = 0; t < KM; ++t) {
+        if (more) {
+            float bw = lw[0];
+            int bi = li[0];
+            int bl = lane;
+            for (int o = 32; o >= 1; o >>= 1) {
+                const float ow = __shfl_xor(bw, o, 64);
+                const int oi = __shfl_xor(bi, o, 64);
+                const int ol = __shfl_xor(bl, o, 64);
+                if (better_e(ow, oi, bw, bi)) { bw = ow; bi = oi; bl = ol; }
+            }
+            tw[t] = bw;
+            ti[t] = bi;
+            if (lane == bl) {
+#pragma unroll
+                for (int s = 0; s + 1 < KM; ++s) { lw[s] = lw[s + 1]; li[s] = li[s + 1]; }
+                lw[KM - 1] = -INFINITY;
+                li[KM - 1] = -1;
+            }
+            if (t == k - 1) wk = nreal < k ? -INFINITY : bw;
+            if (t + 1 >= k && (t + 1 >= kept || (double)bw < (double)wk - 2.0 * b)) more = false;
+        }
     }
     // Candidates outside the kept list were dropped by a full partial list (w <= tail) or by the merge
     // (w <= tw[KM-1]); they cannot reach the exact top-k when that bound is below wk - 2b.
