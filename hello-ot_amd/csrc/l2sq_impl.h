@@ -2055,13 +2055,21 @@ struct DeferBufs {
     int* cand = nullptr;  // [R * KM]
 };
 
+// Rows of a finalize call that its partial lists resolve (queued with the count at redo_count[1]); without
+// `rows` every queued row goes to the sweep queue.
+struct ListQueue {
+    int* rows = nullptr;
+    float* thr = nullptr;
+};
+
 template <int KL, int KM, int G, bool COLS, bool DEFER = false>
 __global__ __launch_bounds__(256) void l2sq_finalize(
     const float* __restrict__ A, const float* __restrict__ B, int64_t R, int d, int nlists,
     const Entry* __restrict__ lists, const double* __restrict__ abias, const double* __restrict__ bbias,
     const double* __restrict__ anorm, const unsigned long long* __restrict__ bmaxima, double scale, int k,
     BoundArgs bnd, double* __restrict__ out_val, int* __restrict__ out_idx, int* __restrict__ redo,
-    float* __restrict__ redo_thr, int* __restrict__ redo_count, DeferBufs defer = DeferBufs{}) {
+    float* __restrict__ redo_thr, int* __restrict__ redo_count, DeferBufs defer = DeferBufs{},
+    ListQueue lq = ListQueue{}) {
     static_assert(KL <= KM, "merged lists hold at least one partial list");
     const int lane = threadIdx.x & 63;
     const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -2165,21 +2173,29 @@ __global__ __launch_bounds__(256) void l2sq_finalize(
     // Candidates outside the kept list were dropped by a full partial list (w <= tail) or by the merge
     // (w <= tw[KM-1]); they cannot reach the exact top-k when that bound is below wk - 2b.
     const bool merge_dropped = nreal > KM;
-    float dropped = full ? tail : -INFINITY;
-    if (merge_dropped) dropped = fmaxf(dropped, tw[KM - 1]);
-    if ((full || merge_dropped) && (double)dropped >= (double)wk - 2.0 * b) {
+    const bool list_hit = full && (double)tail >= (double)wk - 2.0 * b;
+    const bool merge_hit = merge_dropped && (double)tw[KM - 1] >= (double)wk - 2.0 * b;
+    if (list_hit || merge_hit) {
         // queued for the wide pass: a candidate of the exact top-k has sigma >= sigma_k* >= wk - b, hence
-        // w >= wk - 2b (the threshold is rounded down to fp32)
+        // w >= wk - 2b (the threshold is rounded down to fp32). Unless a full list's tail reaches that bound, the
+        // lists hold every such candidate (a full list dropped, and the shared thresholds skipped, only scores
+        // <= tail): the row is then resolved from its lists (queue 1) rather than by a new sweep (queue 0).
         if constexpr (DEFER) {
             if (lane == 0) defer.key[row] = -1;  // nothing to evaluate later
         }
         if (lane == 0) {
-            const int slot = atomicAdd(redo_count, 1);
-            redo[slot] = (int)row;
+            const bool from_lists = !list_hit && lq.rows != nullptr;
+            const int slot = atomicAdd(redo_count + (from_lists ? 1 : 0), 1);
             const double t = (double)wk - 2.0 * b;
             float t32 = (float)t;
             if ((double)t32 > t) t32 = nextafterf(t32, -INFINITY);
-            redo_thr[slot] = t32;
+            if (from_lists) {
+                lq.rows[slot] = (int)row;
+                lq.thr[slot] = t32;
+            } else {
+                redo[slot] = (int)row;
+                redo_thr[slot] = t32;
+            }
         }
         return;
     }
@@ -2404,6 +2420,45 @@ __global__ void l2sq_wide_gather_split(const float* __restrict__ src, int ld, in
     }
 }
 
+// Wide pass from the partial lists (steps 1 and 2 for the rows of queue 1): queued row q0 + q is one wave; it
+// collects the entries of its partial lists with w >= its threshold (a prefix of each sorted list) into
+// buf[q * cap ...] as candidate ids relative to cbase, the first row of the candidate side the exact step reads.
+// A count above cap sends the row to the next round (l2sq_wide_merge). The list layout is l2sq_finalize's.
+template <int KL>
+__global__ __launch_bounds__(256) void l2sq_list_collect(const Entry* __restrict__ lists, int64_t R, int nlists, int G,
+                                                         const int* __restrict__ queue, int q0, int Q,
+                                                         const float* __restrict__ queue_thr, int cbase, int cap,
+                                                         float* __restrict__ thr, int* __restrict__ cnt,
+                                                         int* __restrict__ buf) {
+    const int lane = threadIdx.x & 63;
+    for (int q = blockIdx.x * 4 + (threadIdx.x >> 6); q < Q; q += gridDim.x * 4) {  // uniform per wave
+        const int64_t row = queue[q0 + q];
+        const float t = queue_thr[q0 + q];
+        int* dst = buf + (int64_t)q * cap;
+        int pos = 0;  // entries collected so far (uniform)
+        for (int L0 = 0; L0 < nlists; L0 += 64) {
+            const int L = L0 + lane;
+            const Entry* src = lists + ((((int64_t)(L / G)) * R + row) * G + (L % G)) * KL;
+            int c = 0;
+            if (L < nlists)
+                while (c < KL && src[c].j >= 0 && src[c].w >= t) ++c;
+            int incl = c;  // inclusive prefix sum over the lanes
+            for (int o = 1; o < 64; o <<= 1) {
+                const int v = __shfl_up(incl, o, 64);
+                if (lane >= o) incl += v;
+            }
+            const int off = pos + incl - c;
+            for (int e = 0; e < c; ++e)
+                if (off + e < cap) dst[off + e] = src[e].j - cbase;
+            pos += __shfl(incl, 63, 64);
+        }
+        if (lane == 0) {
+            cnt[q] = pos;
+            thr[q] = t;
+        }
+    }
+}
+
 // Wide pass, step 3: item (row q, slice of its collected candidates) is one wave; it evaluates WIDE_SLICE
 // candidates with the fixed-order fp64 dot (four at a time, as the rescan) and keeps their exact top-k under the
 // tie rule in pv / pi. A row whose candidates overflowed the capacity yields empty lists (it goes to the next
@@ -2522,6 +2577,8 @@ struct WideBufs {
     float* redo2_thr;  // [m + n] their thresholds
     int* redo3;        // [m + n] rows that overflowed the second round (exact full rescan)
     float* redo3_thr;  // [m + n]
+    int* redo_l;       // [m + n] queued rows their partial lists resolve (ListQueue of the finalize), with
+    float* redo_l_thr;  // [m + n] their thresholds
     int* counts;       // [4]: redo2 and redo3 lengths
     unsigned int* rowthr;  // [rows of a sweep launch] the sweeps' shared row thresholds (row_threshold_*)
 };
@@ -2545,11 +2602,21 @@ struct I8Bufs {
 // rescan of rows that overflowed it. A / B are the fp32 row and candidate sides (row stride d), Asw / Bsw their
 // sweep copies (split-bf16 or int8 with row stride ld when `split`, else A / B), cand32 the candidates' fp32 biases,
 // aqs / bqs the int8 scales of both sides (null unless the sweep is the int8 one).
+// The partial lists a finalize call merged (its lists, R, nlists, G and KL), for the rows it queued to be
+// resolved from them (WideBufs::redo_l, count at redo_count[1]); lists == nullptr when there are none.
+struct ListSource {
+    const Entry* lists = nullptr;
+    int64_t R = 0;
+    int nlists = 0;
+    int G = 1;
+    int KL = 8;
+};
+
 int wide_resolve(hipStream_t st, bool split, bool two_level, const float* A, const float* Asw, const float* B,
                  const float* Bsw, int64_t nb, int d, int sd, int ld, const float* cand32, const double* abias,
                  const double* bbias, double scale, int k, const int* redo, const int* redo_count,
                  double* out_val, int* out_idx, int cols, int cbase, const WideBufs& w, double* rpv, int* rpi,
-                 const float* aqs, const float* bqs);
+                 const float* aqs, const float* bqs, const ListSource& ls = ListSource{});
 
 namespace {
 
@@ -2783,6 +2850,8 @@ void layout(A& a, int64_t m, int64_t n, int d, int k, uint32_t flags, double** x
     wide->redo2_thr = a.template take<float>((size_t)(m + n));
     wide->redo3 = a.template take<int>((size_t)(m + n));
     wide->redo3_thr = a.template take<float>((size_t)(m + n));
+    wide->redo_l = a.template take<int>((size_t)(m + n));
+    wide->redo_l_thr = a.template take<float>((size_t)(m + n));
     wide->counts = a.template take<int>(4);
     wide->rowthr = a.template take<unsigned int>((size_t)std::max<int64_t>(std::max<int64_t>(c.ch, c.ch2), 1));
     wide->qs = a.template take<float>((size_t)wq);
@@ -3023,12 +3092,13 @@ int run_bidir(hipStream_t st, const float* X, const float* Y, int64_t m, int64_t
             hipLaunchKernelGGL((l2sq_finalize<K1, KM, 2, false>), dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, st,
                                X + xb * d, Y, rows, d, 2 * plan.S, part, qb + xb, db, xnorm + xb, maxima + 2, scale, k,
                                bound_for(false, xb), row_val + xb * k, row_idx + xb * k, redo, wide.redo_thr,
-                               redo_count);
+                               redo_count, DeferBufs{}, ListQueue{wide.redo_l, wide.redo_l_thr});
             prof_end(st);
             HM_LAUNCH_CHECK("l2sq_finalize");
             if (int rc = wide_resolve(st, split, two_level, X + xb * d, SXc, Y, SY, n, d, sd, ld, db32,
                                       qb + xb, db, scale, k, redo, redo_count, row_val + xb * k, row_idx + xb * k, 0,
-                                      0, wide, rpv, rpi, i8 ? q8.xqs + xb : nullptr, q8.yqs))
+                                      0, wide, rpv, rpi, i8 ? q8.xqs + xb : nullptr, q8.yqs,
+                                      ListSource{part, rows, 2 * plan.S, 2, K1}))
                 return rc;
         }
         if (fused) {
@@ -3039,7 +3109,8 @@ int run_bidir(hipStream_t st, const float* X, const float* Y, int64_t m, int64_t
             // their first candidate: the chunk's X rows are then read about once each rather than once per column
             hipLaunchKernelGGL((l2sq_finalize<K1, KM, 1, true, true>), dim3((unsigned)((n + 3) / 4)), dim3(256), 0, st,
                                Y, X, n, d, (int)panels, colpart, db, qb, ynorm, maxima, scale, k, bound_for(true, 0),
-                               cval, cidx, redo, wide.redo_thr, redo_count, wide.defer);
+                               cval, cidx, redo, wide.redo_thr, redo_count, wide.defer,
+                               ListQueue{wide.redo_l, wide.redo_l_thr});
             HM_LAUNCH_CHECK("l2sq_col_finalize");
             const unsigned egrid = (unsigned)((n + 255) / 256 < 8192 ? (n + 255) / 256 : 8192);
             hipLaunchKernelGGL(fill_u32, dim3((unsigned)((rows + 256) / 256)), dim3(256), 0, st,
@@ -3056,7 +3127,8 @@ int run_bidir(hipStream_t st, const float* X, const float* Y, int64_t m, int64_t
             HM_LAUNCH_CHECK("l2sq_col_finalize (exact)");
             if (int rc = wide_resolve(st, split, two_level, Y, SY, X + xb * d, SXc, rows, d, sd, ld,
                                       qb32 + xb, db, qb + xb, scale, k, redo, redo_count, cval, cidx, 1, (int)xb,
-                                      wide, rpv, rpi, q8.yqs, i8 ? q8.xqs + xb : nullptr))
+                                      wide, rpv, rpi, q8.yqs, i8 ? q8.xqs + xb : nullptr,
+                                      ListSource{colpart, n, (int)panels, 1, K1}))
                 return rc;
             hipLaunchKernelGGL(l2sq_merge_columns, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, col_val, col_idx,
                                cval, cidx, n, k, chunk_index == 0 ? 1 : 0);
@@ -3110,12 +3182,13 @@ int run_bidir(hipStream_t st, const float* X, const float* Y, int64_t m, int64_t
             hipLaunchKernelGGL((l2sq_finalize<K1, KM, 2, true>), dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, st,
                                Y + yb * d, X, rows, d, 2 * plan2.S, part, db + yb, qb, ynorm + yb, maxima, scale, k,
                                bound_for(true, yb), col_val + yb * k, col_idx + yb * k, redo, wide.redo_thr,
-                               redo_count);
+                               redo_count, DeferBufs{}, ListQueue{wide.redo_l, wide.redo_l_thr});
             prof_end(st);
             HM_LAUNCH_CHECK("l2sq_col_finalize");
             if (int rc = wide_resolve(st, split, two_level, Y + yb * d, SYc, X, SX, m, d, sd, ld, qb32,
                                       db + yb, qb, scale, k, redo, redo_count, col_val + yb * k, col_idx + yb * k, 1,
-                                      0, wide, rpv, rpi, i8 ? q8.yqs + yb : nullptr, q8.xqs))
+                                      0, wide, rpv, rpi, i8 ? q8.yqs + yb : nullptr, q8.xqs,
+                                      ListSource{part, rows, 2 * plan2.S, 2, K1}))
                 return rc;
         }
     }

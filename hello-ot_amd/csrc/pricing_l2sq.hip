@@ -27,6 +27,30 @@ int read_count(hipStream_t st, const int* count_dev, int* out) {
     return HM_OK;
 }
 
+// Steps 3 and 4 of the wide pass for queued rows q0 .. q0+Q-1 whose candidates (w.cnt, w.buf) are collected: exact
+// evaluation in slices, then the merge into the outputs (rows past `cap` go to the next queue).
+int wide_exact(hipStream_t st, const float* A, const float* B, int d, const double* abias, const double* bbias,
+               double scale, int k, const int* queue, int q0, int Q, int cap, double* out_val, int* out_idx, int cols,
+               int cbase, const WideBufs& w, double* rpv, int* rpi, int* next, float* next_thr, int* next_count) {
+    const int spr = cap / WIDE_SLICE;
+    const int64_t items = (int64_t)Q * spr;
+    const unsigned eg = (unsigned)((items + 3) / 4 < 8192 ? (items + 3) / 4 : 8192);
+    const unsigned mg = (unsigned)((Q + 255) / 256);
+#define HM_WIDE_EXACT(KK)                                                                                           \
+    do {                                                                                                            \
+        hipLaunchKernelGGL((l2sq_wide_slices<KK>), dim3(eg), dim3(256), 0, st, A, B, d, abias, bbias, scale, k,       \
+                           queue, q0, Q, w.cnt, w.buf, cap, spr, cols, cbase, rpv, rpi);                            \
+        hipLaunchKernelGGL((l2sq_wide_merge<KK>), dim3(mg), dim3(256), 0, st, rpv, rpi, Q, spr, k, w.cnt, cap, queue, \
+                           w.thr, q0, out_val, out_idx, next, next_thr, next_count);                                \
+    } while (0)
+    if (k <= 2) HM_WIDE_EXACT(2);
+    else if (k <= 8) HM_WIDE_EXACT(8);
+    else HM_WIDE_EXACT(32);
+#undef HM_WIDE_EXACT
+    HM_LAUNCH_CHECK("l2sq_wide_exact");
+    return HM_OK;
+}
+
 // One round of the wide pass over `count` queued rows: per batch, gather the rows' sweep copies, re-sweep them
 // against all candidates collecting ids with w >= threshold (up to `cap` per row), evaluate the collected ids
 // exactly in slices, merge; rows past `cap` go to (next, next_thr, next_count).
@@ -38,7 +62,6 @@ int wide_round(hipStream_t st, bool split, bool two_level, const float* A, const
     const bool i8 = aqs != nullptr;  // the int8 sweep: the gathered rows carry their scales
     const int gld = split ? ld : d;  // row stride of the gathered sweep rows
     const int batch = (int)(WIDE_BUF / cap) < WIDE_ROWS ? (int)(WIDE_BUF / cap) : WIDE_ROWS;
-    const int spr = cap / WIDE_SLICE;
     const int vec4 = split || (d % 4) == 0;
     for (int q0 = 0; q0 < count; q0 += batch) {
         const int Q = count - q0 < batch ? count - q0 : batch;
@@ -69,21 +92,36 @@ int wide_round(hipStream_t st, bool split, bool two_level, const float* A, const
         }
 #undef HM_WIDE
         HM_LAUNCH_CHECK("l2sq_sweep (wide)");
-        const int64_t items = (int64_t)Q * spr;
-        const unsigned eg = (unsigned)((items + 3) / 4 < 8192 ? (items + 3) / 4 : 8192);
-        const unsigned mg = (unsigned)((Q + 255) / 256);
-#define HM_WIDE_EXACT(KK)                                                                                           \
-    do {                                                                                                            \
-        hipLaunchKernelGGL((l2sq_wide_slices<KK>), dim3(eg), dim3(256), 0, st, A, B, d, abias, bbias, scale, k,       \
-                           queue, q0, Q, w.cnt, w.buf, cap, spr, cols, cbase, rpv, rpi);                            \
-        hipLaunchKernelGGL((l2sq_wide_merge<KK>), dim3(mg), dim3(256), 0, st, rpv, rpi, Q, spr, k, w.cnt, cap, queue, \
-                           w.thr, q0, out_val, out_idx, next, next_thr, next_count);                                \
-    } while (0)
-        if (k <= 2) HM_WIDE_EXACT(2);
-        else if (k <= 8) HM_WIDE_EXACT(8);
-        else HM_WIDE_EXACT(32);
-#undef HM_WIDE_EXACT
-        HM_LAUNCH_CHECK("l2sq_wide_exact");
+        if (int rc = wide_exact(st, A, B, d, abias, bbias, scale, k, queue, q0, Q, cap, out_val, out_idx, cols, cbase,
+                                w, rpv, rpi, next, next_thr, next_count))
+            return rc;
+    }
+    return HM_OK;
+}
+
+// The rows of the list queue: per batch, each row's partial-list entries at or above its threshold are collected
+// (l2sq_list_collect) and evaluated exactly as in the wide pass; rows past `cap` go to (next, next_thr,
+// next_count), the second round's sweep.
+int list_round(hipStream_t st, const ListSource& ls, const float* A, const float* B, int d, const double* abias,
+               const double* bbias, double scale, int k, const int* queue, const float* queue_thr, int count, int cap,
+               double* out_val, int* out_idx, int cols, int cbase, const WideBufs& w, double* rpv, int* rpi,
+               int* next, float* next_thr, int* next_count) {
+    const int batch = (int)(WIDE_BUF / cap) < WIDE_ROWS ? (int)(WIDE_BUF / cap) : WIDE_ROWS;
+    for (int q0 = 0; q0 < count; q0 += batch) {
+        const int Q = count - q0 < batch ? count - q0 : batch;
+        const unsigned cg = (unsigned)((Q + 3) / 4 < 8192 ? (Q + 3) / 4 : 8192);
+#define HM_COLLECT(KK)                                                                                              \
+    hipLaunchKernelGGL((l2sq_list_collect<KK>), dim3(cg), dim3(256), 0, st, ls.lists, ls.R, ls.nlists, ls.G, queue, \
+                       q0, Q, queue_thr, cbase, cap, w.thr, w.cnt, w.buf)
+        if (ls.KL == 8) HM_COLLECT(8);
+        else if (ls.KL == 16) HM_COLLECT(16);
+        else if (ls.KL == 40) HM_COLLECT(40);
+        else return fail(HM_EINVAL, "internal: partial lists of %d entries", ls.KL);
+#undef HM_COLLECT
+        HM_LAUNCH_CHECK("l2sq_list_collect");
+        if (int rc = wide_exact(st, A, B, d, abias, bbias, scale, k, queue, q0, Q, cap, out_val, out_idx, cols, cbase,
+                                w, rpv, rpi, next, next_thr, next_count))
+            return rc;
     }
     return HM_OK;
 }
@@ -94,19 +132,29 @@ int wide_resolve(hipStream_t st, bool split, bool two_level, const float* A, con
                  const float* Bsw, int64_t nb, int d, int sd, int ld, const float* cand32, const double* abias,
                  const double* bbias, double scale, int k, const int* redo, const int* redo_count,
                  double* out_val, int* out_idx, int cols, int cbase, const WideBufs& w, double* rpv, int* rpi,
-                 const float* aqs, const float* bqs) {
+                 const float* aqs, const float* bqs, const ListSource& ls) {
     static_assert(WIDE_CAP1 % WIDE_SLICE == 0 && WIDE_CAP2 % WIDE_SLICE == 0, "whole slices per row");
     static_assert((WIDE_BUF / WIDE_CAP1) * (WIDE_CAP1 / WIDE_SLICE) <= RESCAN_ITEMS &&
                       (WIDE_BUF / WIDE_CAP2) * (WIDE_CAP2 / WIDE_SLICE) <= RESCAN_ITEMS,
                   "slice lists of a batch fit the rescan scratch");
-    int count = 0;
-    if (int rc = read_count(st, redo_count, &count)) return rc;
+    // queue 0 (a new sweep) and queue 1 (resolved from the partial lists): both counts in one read
+    int counts[2] = {0, 0};
+    HM_HIP(hipMemcpyAsync(counts, redo_count, 2 * sizeof(int), hipMemcpyDeviceToHost, st));
+    HM_HIP(hipStreamSynchronize(st));
+    const int count = counts[0];
+    const int lcount = ls.lists ? counts[1] : 0;
     prof_count(cols ? "l2sq_wide_columns" : "l2sq_wide_rows", count);
-    if (count <= 0) return HM_OK;
+    prof_count(cols ? "l2sq_list_columns" : "l2sq_list_rows", lcount);
+    if (count <= 0 && lcount <= 0) return HM_OK;
     hipLaunchKernelGGL(zero_words, dim3(1), dim3(64), 0, st, reinterpret_cast<unsigned long long*>(w.counts), 2);
     HM_LAUNCH_CHECK("zero_words");
     prof_begin(st, "l2sq_wide");
-    int rc = wide_round(st, split, two_level, A, Asw, B, Bsw, nb, d, sd, ld, cand32, abias, bbias, scale, k, redo,
+    int rc = HM_OK;
+    if (lcount > 0)
+        rc = list_round(st, ls, A, B, d, abias, bbias, scale, k, w.redo_l, w.redo_l_thr, lcount, WIDE_CAP1, out_val,
+                        out_idx, cols, cbase, w, rpv, rpi, w.redo2, w.redo2_thr, w.counts);
+    if (!rc && count > 0)
+        rc = wide_round(st, split, two_level, A, Asw, B, Bsw, nb, d, sd, ld, cand32, abias, bbias, scale, k, redo,
                         w.redo_thr, count, WIDE_CAP1, out_val, out_idx, cols, cbase, w, rpv, rpi, w.redo2, w.redo2_thr,
                         w.counts, aqs, bqs);
     int count2 = 0;

@@ -175,6 +175,41 @@ def test_l2sq_dense_near_ties_resolved_exactly(cuda, precision, copies):
     assert_l2sq_certificate(st, l2sq_certificate_bounds(X, Y, p, q, qb, db))
 
 
+@pytest.mark.parametrize("d,precision", [(300, "fp32"), (300, "bf16x3"), (300, "int8x3"), (64, "fp32"),
+                                         (64, "bf16x3")])
+def test_l2sq_scattered_near_ties_resolved_from_lists(cuda, d, precision):
+    # 40 query rows and 40 candidates sit within 1e-3 of one point, scattered over both sides: each such row (and
+    # column) has 40 candidates inside twice the sweep's error bound, more than its merged list keeps, but spread
+    # over its partial lists so that none holds KL of them. The finalize then resolves it from the lists it
+    # already has (queue 1, no new sweep); the lists must still be the oracle's exact ones.
+    rng = np.random.default_rng(d)
+    m, n, k = 2048, 2000, 8
+    base = rng.standard_normal(d).astype(np.float32)
+    X = (3.0 * rng.standard_normal((m, d))).astype(np.float32)
+    Y = (3.0 * rng.standard_normal((n, d))).astype(np.float32)
+    xs = rng.choice(m, 40, replace=False)
+    ys = rng.choice(n, 40, replace=False)
+    X[xs] = (base + 1e-3 * rng.standard_normal((40, d))).astype(np.float32)
+    Y[ys] = (base + 1e-3 * rng.standard_normal((40, d))).astype(np.float32)
+    p = (X.astype(np.float64) ** 2).sum(1)
+    q = (Y.astype(np.float64) ** 2).sum(1)
+    qb, db = -p, -q
+    orv, ori, ocv, oci, ost = oracle.l2sq_scan(X, Y, p, q, qb, db, k, 2.0)
+    _lib.profile_reset()
+    _lib.profile_enable(True)
+    try:
+        rv, ri, cv, ci, st = pricing_l2sq(*_to(cuda, X, Y, p, q, qb, db), k, linf=True, precision=precision)
+        torch.cuda.synchronize()
+        from_lists = _lib.profile_query("l2sq_list_rows")[1], _lib.profile_query("l2sq_list_columns")[1]
+    finally:
+        _lib.profile_enable(False)
+    np.testing.assert_array_equal(ri.cpu().numpy(), ori)
+    np.testing.assert_array_equal(rv.cpu().numpy(), orv)
+    np.testing.assert_array_equal(ci.cpu().numpy(), oci)
+    np.testing.assert_array_equal(cv.cpu().numpy(), ocv)
+    assert from_lists[0] > 0 and from_lists[1] > 0, from_lists
+
+
 @pytest.mark.parametrize("m,d,precision", [(70, 4, "fp32"), (300, 256, "bf16x3"), (300, 256, "int8x3")])
 def test_l2sq_all_equal_scores_take_lowest_indices(cuda, m, d, precision):
     # every pair ties exactly: integer-valued identical points -> every row's top-k is columns 0..k-1 and every
