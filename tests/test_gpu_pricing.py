@@ -386,6 +386,56 @@ def test_norm_directional_top16_with_one_zero_side(cuda, kind):
     np.testing.assert_array_equal(cv.cpu().numpy(), ocv)
 
 
+def _norm_call(dev, X, Y, f, g, k, kind, ws_bytes, flags):
+    lib = _lib.load()
+    m, n, d = X.shape[0], Y.shape[0], X.shape[1]
+    out = (torch.full((m, k), 7.0, dtype=torch.float64, device=dev), torch.full((m, k), 7, dtype=torch.int32, device=dev),
+           torch.full((n, k), 7.0, dtype=torch.float64, device=dev), torch.full((n, k), 7, dtype=torch.int32, device=dev),
+           torch.full((5,), 7.0, dtype=torch.float64, device=dev))
+    ws = torch.full((ws_bytes,), 0xAB, dtype=torch.uint8, device=dev)    # stale bytes: nothing may be read unwritten
+    rc = lib.hm_pricing_norm(_lib.stream_handle(dev), *map(_lib.ptr, (X, Y, f, g)), m, n, d, k, kind, flags,
+                             *map(_lib.ptr, out), _lib.ptr(ws), ws.numel())
+    return rc, out
+
+
+@pytest.mark.parametrize("kind", [0, 1, 2])
+@pytest.mark.parametrize("k,grid", [(2, False), (1, False), (2, True)])
+def test_norm_fused_columns_overflow_and_two_sweep_paths_agree(cuda, kind, k, grid):
+    """k <= 2 bidirectional calls evaluate each pair once and collect the column lists through the candidate buffer.
+    The workspace size picks the path: the full buffer, a buffer of about 100 candidates (it overflows, so the
+    role-swapped sweep supplies the columns) and the smallest accepted workspace (two sweeps). All three equal the
+    oracle. The grid case makes most scores tie exactly (integer features, zero duals)."""
+    rng = np.random.default_rng(70 + kind + 3 * k + 10 * grid)
+    m, n, d = 3000, 2100, 6
+    if grid:
+        X = rng.integers(0, 3, (m, d)).astype(np.float32)
+        Y = rng.integers(0, 3, (n, d)).astype(np.float32)
+        f, g = np.zeros(m), np.zeros(n)
+    else:
+        X = rng.random((m, d)).astype(np.float32)
+        Y = rng.random((n, d)).astype(np.float32)
+        f, g = rng.normal(0.3, 0.2, m), rng.normal(0.3, 0.2, n)
+    orv, ori, ocv, oci, ost = oracle.norm_scan(X, Y, f, g, k, kind)
+    tX, tY, tf, tg = _to(cuda, X, Y, f, g)
+    flags = _lib.HM_ROWS | _lib.HM_COLS | _lib.HM_STATS | _lib.HM_LINF
+    lib = _lib.load()
+    full = int(lib.hm_pricing_norm_workspace_bytes(m, n, d, k, flags))
+    # the library's full capacity is 16 n k + 65536 candidates of 20 bytes (16 in the buffer, 4 in the grouping)
+    small = full - 20 * (16 * n * k + 65536 - 100)
+    rc, _ = _norm_call(cuda, tX, tY, tf, tg, k, kind, 1024, flags)
+    assert rc == _lib.HM_ENOSPC and "too small" in _lib.last_error()
+    least = int(_lib.last_error().split("<")[1].split()[0])         # the two-sweep minimum the error names
+    assert least < small < full
+    for ws in (full, small, least):
+        rc, (rv, ri, cv, ci, st) = _norm_call(cuda, tX, tY, tf, tg, k, kind, ws, flags)
+        _lib.check(rc, "hm_pricing_norm")
+        np.testing.assert_array_equal(ri.cpu().numpy(), ori)
+        np.testing.assert_array_equal(rv.cpu().numpy(), orv)
+        np.testing.assert_array_equal(ci.cpu().numpy(), oci)
+        np.testing.assert_array_equal(cv.cpu().numpy(), ocv)
+        _assert_stats(st, ost)
+
+
 @pytest.mark.parametrize("precision", ["fp32", "bf16x3", "int8x3"])
 def test_l2sq_resident_side_gives_the_same_outputs(cuda, precision):
     """Query chunks priced against a resident Y side (prepared once) give exactly the ordinary call's outputs,
