@@ -342,6 +342,33 @@ def bench_library_gemm(dev, warmup=10, steps=40):
             "frac_of_bf16_peak": flops / sec / PEAK_BF16_MFMA}
 
 
+def bench_library_int8_gemm(dev, warmup=10, steps=40):
+    """Reference point for the int8 sweep's MFMA rate: the vendor library's plain int8 GEMM (`torch._int_mm`, int8
+    in, int32 out, hipBLASLt) on the same product shape, B given column-major (the faster of the two layouts
+    measured), timed like the bf16 GEMM. It computes one int8 product per pair; the int8 sweep computes three limb
+    products plus the selection and the certificate."""
+    m, n, d = 8192, 131072, C5_D
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(6)
+    A = torch.randint(-127, 128, (m, d), device=dev, dtype=torch.int8, generator=gen)
+    B = torch.randint(-127, 128, (n, d), device=dev, dtype=torch.int8, generator=gen).t()
+    for _ in range(warmup):
+        C = torch._int_mm(A, B)
+    sync()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        C = torch._int_mm(A, B)
+    end.record()
+    sync()
+    sec = start.elapsed_time(end) / 1e3 / steps
+    ops = 2.0 * m * n * d
+    del A, B, C
+    torch.cuda.empty_cache()
+    return {"shape_m_n_d": [m, n, d], "ms": sec * 1e3, "tops": ops / sec / 1e12,
+            "frac_of_int8_peak": ops / sec / PEAK_INT8_MFMA}
+
+
 def bench_c2(dev, steps=3):
     from hello_ot_amd import _lib
     from hello_ot_amd.kernels.generic_scan import pricing_l2sq, sweep_precision
@@ -643,6 +670,8 @@ def main():
     if not args.no_extras:
         log("[bench] hipBLASLt bf16 GEMM of the sweep's product shape ...")
         extras["library_bf16_gemm_same_shape"] = bench_library_gemm(dev)
+        log("[bench] hipBLASLt int8 GEMM of the sweep's product shape ...")
+        extras["library_int8_gemm_same_shape"] = bench_library_int8_gemm(dev)
         log("[bench] C2 ...")
         extras["c2_scan_131072x131072_d64_k8"] = bench_c2(dev)
         log("[bench] C3 ...")

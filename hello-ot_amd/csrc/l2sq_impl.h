@@ -2999,9 +2999,12 @@ int run_bidir(hipStream_t st, const float* X, const float* Y, int64_t m, int64_t
                                ld, reinterpret_cast<unsigned short*>(out));
         }
         HM_LAUNCH_CHECK("split copy");
+        return HM_OK;
     };
-    if (split && !cp.x_chunked) copy_rows(false, 0, m, xsplit);
-    if (split && !cp.y_chunked && !q8.y_ready) copy_rows(true, 0, n, ysplit);
+    if (split && !cp.x_chunked)
+        if (int rc = copy_rows(false, 0, m, xsplit)) return rc;
+    if (split && !cp.y_chunked && !q8.y_ready)
+        if (int rc = copy_rows(true, 0, n, ysplit)) return rc;
     // Rigorous bound on |w - exact| in units of scale*||x||*||y||: accumulation of B-feature blocks in fp32
     // (gamma over the additions of a block, then over the blocks), plus for the split products the dropped
     // terms lo*lo + hi*e + e*hi + ... <= (3 * 2^-16 * (1 + 2^-7) + 3 * 2^-24) |x_k y_k|.
@@ -3037,7 +3040,8 @@ int run_bidir(hipStream_t st, const float* X, const float* Y, int64_t m, int64_t
         const dim3 grid(sweep_grid(panels, plan.S));
         const unsigned neg_inf_key = 0x007fffffu;  // float_key(-INFINITY)
         // this chunk's split copy of X (the sweeps take the copy from the chunk's first row)
-        if (split && cp.x_chunked) copy_rows(false, xb, rows, xsplit);
+        if (split && cp.x_chunked)
+            if (int rc = copy_rows(false, xb, rows, xsplit)) return rc;
         const float* SXc = !split ? SX : (cp.x_chunked ? xsplit : SX + xb * ld);
         if (fused) {
             // column thresholds start at -inf for every chunk (its lists only rank its own X rows)
@@ -3146,7 +3150,8 @@ int run_bidir(hipStream_t st, const float* X, const float* Y, int64_t m, int64_t
             const int64_t panels2 = (rows + bx - 1) / bx;
             const dim3 grid(sweep_grid(panels2, plan2.S));
             // this chunk's split copy of Y (from its first row; a resident side's copy is whole)
-            if (split && cp.y_chunked && !q8.y_ready) copy_rows(true, yb, rows, ysplit);
+            if (split && cp.y_chunked && !q8.y_ready)
+                if (int rc = copy_rows(true, yb, rows, ysplit)) return rc;
             const float* SYc = !split ? SY : ((cp.y_chunked && !q8.y_ready) ? ysplit : SY + yb * ld);
             hipLaunchKernelGGL(fill_u32, dim3((unsigned)((rows + 255) / 256 < 4096 ? (rows + 255) / 256 : 4096)),
                                dim3(256), 0, st, rowthr, rows, 0x007fffffu /* float_key(-INFINITY) */);
