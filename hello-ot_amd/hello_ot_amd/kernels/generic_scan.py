@@ -214,7 +214,76 @@ class ScanExtension:
                                       stats=True, linf=True)
         return st
 
+    def initialization_directional_topk_raw(self, query_feat, db_feat, query_bias, db_bias, query_tile, db_tile, k,
+                                            dot_scale):
+        """generic_scan.py:560-575 -> [values f64(q,k), indices i32(q,k)]: per query row the k largest raw scores
+        (dot_scale * <x_i, y_j> + query_bias_i) + db_bias_j, descending, the lowest index first among equal scores
+        (the rows-only l2^2 sweep; the query tile sizes are planning hints there and here)."""
+        x, y, qb, dbb = query_feat, db_feat, query_bias, db_bias
+        if x.dtype != y.dtype:
+            raise RuntimeError("query/db feature dtypes must match")
+        _check(x, y, k, (qb, len(x)), (dbb, len(y)))
+        if query_tile <= 0 or db_tile <= 0 or dot_scale not in (1., 2.):
+            raise ValueError("invalid raw directional tile or scale")
+        self._record("raw_initial")
+        zx = torch.zeros(len(x), dtype=torch.float64, device=x.device)   # costs enter only the certificate
+        zy = torch.zeros(len(y), dtype=torch.float64, device=x.device)
+        rv, ri, _, _, _ = pricing_l2sq(x, y, zx, zy, qb, dbb, k, dot_scale=float(dot_scale), rows=True, cols=False,
+                                       stats=False, linf=False)
+        return [rv, ri]
+
+    def fused_directional_topk_raw(self, query_feat, db_feat, query_bias, db_bias, query_tile, db_tile, k, dot_scale):
+        """generic_scan.py:512-518: the directional compatibility name of initialization_directional_topk_raw."""
+        self._record("raw_directional")
+        return self.initialization_directional_topk_raw(query_feat, db_feat, query_bias, db_bias, query_tile, db_tile,
+                                                        k, dot_scale)
+
     # -- (a) norm pricing -----------------------------------------------------------------------------
+    def fused_gcost_topk(self, query, db, dual_db, k, cost_type, query_global_index=None, database_global_index=None,
+                         sigma=0., seed=0, perturb_mode=1, row_is_source=True, index_hash_coeffs=None,
+                         compute_precision=0, collect_statistics=False):
+        """generic_scan.py:520-531 -> [values f64(q,k), indices i64(q,k)]: per query row the k smallest
+        cost_ij - dual_db_j, ascending, the lowest index first among equal values (the rows-only norm sweep with zero
+        query duals: its scores are dual_db_j - cost_ij exactly, so their negations are cost - dual exactly)."""
+        _check(query, db, k, (dual_db, len(db)))
+        if cost_type not in (0, 1, 2):
+            raise ValueError("generic directional cost must be l1, linf, l2 or raw")
+        if compute_precision not in (0, 1):
+            raise ValueError("norm scans require FP32 coordinate storage and precision 0 or 1")
+        if compute_precision == 1:
+            raise ValueError("the MI355X norm scan evaluates costs in FP32 (compute_precision=0)")
+        if float(sigma) != 0.0:
+            raise NotImplementedError("cost perturbation is not part of the MI355X native pricing path")
+        if collect_statistics:
+            raise NotImplementedError("assignment statistics are not collected by the MI355X norm scan")
+        self._record("norm_initial")
+        zero = torch.zeros(len(query), dtype=torch.float64, device=query.device)
+        rv, ri, _, _, _ = pricing_norm(query, db, zero, dual_db, k, cost_type, rows=True, cols=False, stats=False,
+                                       linf=False)
+        return [rv.neg(), ri.long()]
+
+    def fused_gcost_certificate(self, query, db, query_dual, db_dual, cost_type, query_global_index=None,
+                                database_global_index=None, sigma=0., seed=0, perturb_mode=1, row_is_source=True,
+                                index_hash_coeffs=None, compute_denominator=1, compute_precision=0):
+        """generic_scan.py:545-558 -> [num, den, max, costmax, count i64] of the norm certificate over all pairs
+        (den is zero when compute_denominator is off); the six-argument form passes compute_denominator sixth."""
+        if isinstance(query_global_index, (int, bool)) and database_global_index is None:
+            compute_denominator, query_global_index = query_global_index, None
+        _check(query, db, 1, (query_dual, len(query)), (db_dual, len(db)))
+        if cost_type not in (0, 1, 2):
+            raise ValueError("certificate-only requires a norm or raw cost")
+        if compute_precision not in (0, 1):
+            raise ValueError("norm scans require FP32 coordinate storage and precision 0 or 1")
+        if compute_precision == 1:
+            raise ValueError("the MI355X norm scan evaluates costs in FP32 (compute_precision=0)")
+        if float(sigma) != 0.0:
+            raise NotImplementedError("cost perturbation is not part of the MI355X native pricing path")
+        self._record("norm_certificate")
+        _, _, _, _, st = pricing_norm(query, db, query_dual, db_dual, 1, cost_type, rows=True, cols=False, stats=True,
+                                      linf=True)
+        den = st[1] if compute_denominator else torch.zeros_like(st[1])
+        return [st[0], den, st[3], st[4], st[2].long()]
+
     def fused_gcost_bidir_certificate(self, query, db, query_dual, db_dual, k, cost_type,
                                       query_global_index=None, database_global_index=None, sigma=0., seed=0,
                                       perturb_mode=1, row_is_source=True, index_hash_coeffs=None,

@@ -436,6 +436,69 @@ def test_norm_fused_columns_overflow_and_two_sweep_paths_agree(cuda, kind, k, gr
         _assert_stats(st, ost)
 
 
+@pytest.mark.parametrize("k", [1, 2])
+def test_reference_module_names_raw_entry_points(cuda, k):
+    """hello_ot_native.hierot_generic_{pricing_small,cost}_ext under the reference's module names: raw_scan_tiled's
+    lists and stats, raw_initial's rows-only top-k and raw_certificate_tiled in both stat layouts, against the
+    oracle on raw scores (scale * <x, y> + qb) + dbb and costs (nx + ny) - scale * <x, y>."""
+    import importlib
+
+    small = importlib.import_module("hello_ot_native.hierot_generic_pricing_small_ext")
+    cost = importlib.import_module("hello_ot_native.hierot_generic_cost_ext")
+    X, Y, p, q, qb, db = _l2sq_case(170, 230, 40, seed=50 + k)
+    tX, tY, tp, tq, tqb, tdb = _to(cuda, X, Y, p, q, qb, db)
+    orv, ori, ocv, oci, ost = oracle.l2sq_scan(X, Y, p, q, qb, db, k, 2.0)
+    rv, ri, cv, ci, st, timing = small.raw_scan_tiled(tX, tY, tp, tq, tqb, tdb, k, 2.0, True, True, 64, 64)
+    np.testing.assert_array_equal(ri.cpu().numpy(), ori)
+    np.testing.assert_array_equal(rv.cpu().numpy(), orv)
+    np.testing.assert_array_equal(ci.cpu().numpy(), oci)
+    np.testing.assert_array_equal(cv.cpu().numpy(), ocv)
+    assert ri.dtype == torch.int32 and timing.device.type == "cpu" and st.shape == (4,)
+    b, got = l2sq_certificate_bounds(X, Y, p, q, qb, db), st.cpu().numpy()     # (num, den, count, max|cost|)
+    assert b["num"][0] * (1 - 1e-9) <= got[0] <= b["num"][1] * (1 + 1e-9)
+    assert abs(got[1] - b["den"]) <= b["den_slack"] + 1e-5 * b["den"]
+    assert b["count"][0] <= got[2] <= b["count"][1]
+    assert abs(got[3] - b["cmax"]) <= b["envelope"] + 1e-6 * b["cmax"]
+    vals, idx = cost.raw_initial(tX, tY, tqb, tdb, 8, 64, 64, 2.0)
+    zr, zc = np.zeros(len(X)), np.zeros(len(Y))
+    dv, di, _, _, _ = oracle.l2sq_scan(X, Y, zr, zc, qb, db, 8, 2.0)     # raw scores do not involve the costs
+    np.testing.assert_array_equal(idx.cpu().numpy(), di)
+    np.testing.assert_array_equal(vals.cpu().numpy(), dv)
+    f, g = qb + p, db + q                                   # duals; the entry point forms f - nx and g - ny
+    tf, tg = _to(cuda, f, g)
+    caller = cost.raw_certificate_tiled(tX, tY, tp, tq, tf, tg, 64, 64, 2.0, True, False, True)
+    kernel = cost.raw_certificate_tiled(tX, tY, tp, tq, tf, tg, 64, 64, 2.0, True, False, False)
+    np.testing.assert_array_equal(kernel.cpu().numpy(), caller.cpu().numpy()[[0, 1, 3, 4, 2]])
+    assert_l2sq_certificate(caller, l2sq_certificate_bounds(X, Y, p, q, f - p, g - q))
+    # squared norms: fp64 sums of exact squares, equal up to the summation order
+    np.testing.assert_allclose(cost.norms(tX).cpu().numpy(), (X.astype(np.float64) ** 2).sum(1), rtol=1e-14)
+
+
+@pytest.mark.parametrize("kind", [0, 1, 2])
+def test_scan_extension_norm_directional_and_certificate(cuda, kind):
+    """ScanExtension.fused_gcost_topk (ascending cost - dual, int64 ids) and fused_gcost_certificate (num, den, max,
+    costmax, count), against the oracle's fp32 costs and exact scores."""
+    rng = np.random.default_rng(60 + kind)
+    X = rng.random((210, 6)).astype(np.float32)
+    Y = rng.random((190, 6)).astype(np.float32)
+    f, g = rng.normal(0.3, 0.2, 210), rng.normal(0.3, 0.2, 190)
+    ext = ScanExtension()
+    tX, tY, tf, tg = _to(cuda, X, Y, f, g)
+    vals, ids = ext.fused_gcost_topk(tX, tY, tg, 4, kind)
+    orv, ori, _, _, _ = oracle.norm_scan(X, Y, np.zeros(210), g, 4, kind)
+    assert ids.dtype == torch.int64
+    np.testing.assert_array_equal(ids.cpu().numpy(), ori)
+    np.testing.assert_array_equal(vals.cpu().numpy(), -orv)
+    assert (np.diff(vals.cpu().numpy(), axis=1) >= 0).all()
+    num, den, mx, cmax, count = ext.fused_gcost_certificate(tX, tY, tf, tg, kind)
+    _, _, _, _, ost = oracle.norm_scan(X, Y, f, g, 1, kind)
+    _assert_stats(torch.stack((num, den, count.double(), mx, cmax)), ost)
+    np.testing.assert_allclose(cmax.item(), ost[4], rtol=1e-7)
+    assert count.dtype == torch.int64
+    _, den0, _, _, _ = ext.fused_gcost_certificate(tX, tY, tf, tg, kind, 0)    # six-argument form, no denominator
+    assert den0.item() == 0.0
+
+
 @pytest.mark.parametrize("precision", ["fp32", "bf16x3", "int8x3"])
 def test_l2sq_resident_side_gives_the_same_outputs(cuda, precision):
     """Query chunks priced against a resident Y side (prepared once) give exactly the ordinary call's outputs,
