@@ -277,7 +277,6 @@ def cpu_baseline_c5(dev, sample_rows=4096, sample_cols=196608, threads=16):
     X, Y = Xd.cpu(), Yd.cpu()
     p, q, f = pd_.cpu().numpy(), qd.cpu().numpy(), fd.cpu().numpy()
     g = np.zeros(sample_cols)
-    del Xd, Yd
     sc = oracle.ref_scan()
     k = 2
     rv = np.full((sample_rows, k), -np.inf)
@@ -295,19 +294,47 @@ def cpu_baseline_c5(dev, sample_rows=4096, sample_cols=196608, threads=16):
             sc.dot_tile(dots, p, q[s:s + tile], f, g[s:s + tile], rv, ri, cvv, cii, 2.0, 0, s, 0, threads)
             cv[s:s + tile], ci[s:s + tile] = cvv, cii
         sec = time.perf_counter() - t0
+        agreement = _agreement_with_reference(Xd, Yd, pd_, qd, fd, rv, ri, cv, ci, k)
     else:
         kind = "port"
+        agreement = None
         sample_cols = 4096
         Y = Y[:sample_cols]
         q = q[:sample_cols]
         t0 = time.perf_counter()
         oracle.l2sq_scan(X.numpy(), Y.numpy(), p, q, f - p, g[:sample_cols] - q, k, 2.0)
         sec = time.perf_counter() - t0
+    del Xd, Yd
     pairs = sample_rows * sample_cols
     return {"value": pairs / sec, "unit": "pairs/s", "cores": threads, "kind": kind,
+            "agreement_with_gpu": agreement,
             "sample": f"{sample_rows} query x {sample_cols} resident rows of the C5 mixture, d={C5_D}, k=2, "
                       f"bidirectional + certificate, sampled c-transform duals as the GPU step ({sec:.1f} s)",
             **host_info()}
+
+
+def _agreement_with_reference(Xd, Yd, pd_, qd, fd, rv, ri, cv, ci, k):
+    """The GPU step on the CPU baseline's sample against the reference CPU path's own lists: the share of rows and
+    columns whose top-k index lists are identical, and the largest score difference over the entries both name
+    (same pair). The reference ranks by scores from fp32 dot products (torch.mm) with a (f + g) - cost epilogue; the
+    GPU ranks by exact fp64 scores (scale * dot64 + (f - p)) + (g - q), so lists differ where near-equal scores trade
+    places under the fp32 dot error."""
+    from hello_ot_amd.kernels.generic_scan import pricing_l2sq
+
+    g = torch.zeros(len(Yd), dtype=torch.float64, device=Yd.device)
+    out = pricing_l2sq(Xd, Yd, pd_, qd, fd - pd_, g - qd, k, dot_scale=2.0, rows=True, cols=True, stats=False)
+    grv, gri, gcv, gci = (t.cpu().numpy() for t in out[:4])
+
+    def share(a, b):
+        return float((a == b).all(axis=1).mean())
+
+    def spread(a, ia, b, ib):
+        same = (ia == ib) & np.isfinite(a) & np.isfinite(b)
+        return float(np.max(np.abs(a - b)[same])) if same.any() else None
+
+    return {"rows_identical": share(gri, ri), "columns_identical": share(gci, ci),
+            "row_score_max_abs_diff": spread(grv, gri, rv, ri), "column_score_max_abs_diff": spread(gcv, gci, cv, ci),
+            "score_magnitude": float(np.max(np.abs(rv[np.isfinite(rv)]))) if np.isfinite(rv).any() else None}
 
 
 # ----------------------------------------------------------------------------------------------------------
