@@ -649,12 +649,14 @@ inline size_t norm_workspace(int64_t m, int64_t n, int k, uint32_t flags, int64_
     return s.used;
 }
 
-// the candidate capacity a workspace of `bytes` holds: the full capacity when it fits, else what fits (the fused
-// path stays exact with any capacity: an overflow hands the columns to the role-swapped sweep); 0: two sweeps
-inline int64_t fused_capacity(int64_t m, int64_t n, int k, uint32_t flags, size_t bytes) {
+// the candidate capacity a workspace of `bytes` holds: the full capacity when it fits, else (with partial) what fits
+// (the fused path stays exact with any capacity: an overflow hands the columns to the role-swapped sweep); 0: two
+// sweeps
+inline int64_t fused_capacity(int64_t m, int64_t n, int k, uint32_t flags, size_t bytes, bool partial) {
     if (!fusable(n, k, flags)) return 0;
     const int64_t full = fused_cap(n, k);
     if (norm_workspace(m, n, k, flags, full) <= bytes) return full;
+    if (!partial) return 0;
     const size_t fixed = norm_workspace(m, n, k, flags, 1);
     const size_t per = sizeof(ColCand) + sizeof(int);
     if (bytes < fixed + 512 + per) return 0;
@@ -682,7 +684,8 @@ namespace {
 // not memsets.
 int norm_scan_run(void* stream, const float* X, const float* Y, const double* f, const double* g, int64_t m,
                   int64_t n, int32_t d, int32_t k, int32_t kind, uint32_t flags, double* row_val, int32_t* row_idx,
-                  double* col_val, int32_t* col_idx, double* stats, void* workspace, size_t workspace_bytes) {
+                  double* col_val, int32_t* col_idx, double* stats, void* workspace, size_t workspace_bytes,
+                  bool partial_buffer) {
     HM_CHECK_ARG(X && Y && f && g, "norm pricing: feature and dual pointers are required");
     HM_CHECK_ARG(m >= 1 && n >= 1 && d >= 1 && m < INT32_MAX && n < INT32_MAX,
                  "norm pricing requires nonempty inputs with int32 dimensions");
@@ -696,7 +699,7 @@ int norm_scan_run(void* stream, const float* X, const float* Y, const double* f,
     const size_t need = norm_workspace(m, n, k, flags, 0);
     if (workspace_bytes < need)
         return fail(HM_ENOSPC, "norm pricing workspace too small: %zu < %zu bytes", workspace_bytes, need);
-    const int64_t cap = fused_capacity(m, n, k, flags, workspace_bytes);
+    const int64_t cap = fused_capacity(m, n, k, flags, workspace_bytes, partial_buffer);
     const bool fused = cap > 0;
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     Arena a(workspace, workspace_bytes);
@@ -797,7 +800,7 @@ extern "C" int hm_pricing_norm(void* stream, const float* X, const float* Y, con
                                double* row_val, int32_t* row_idx, double* col_val, int32_t* col_idx, double* stats,
                                void* workspace, size_t workspace_bytes) {
     return norm_scan_run(stream, X, Y, f, g, m, n, d, k, kind, flags, row_val, row_idx, col_val, col_idx, stats,
-                         workspace, workspace_bytes);
+                         workspace, workspace_bytes, true);
 }
 
 extern "C" size_t hm_pricing_norm_noalloc_max_bytes(void) { return NORM_SCRATCH_BYTES; }
@@ -816,6 +819,7 @@ extern "C" int hm_pricing_norm_noalloc(void* stream, const float* X, const float
     void* scratch_ptr = nullptr;
     if (int rc = scratch_for_current_device(&scratch_ptr)) return rc;
     const ProfileOff no_events;  // timing events would be created on demand
+    // the fused path only with its full candidate buffer: a partial one that overflows would cost both sweeps
     return norm_scan_run(stream, X, Y, f, g, m, n, d, k, kind, flags, row_val, row_idx, col_val, col_idx, stats,
-                         scratch_ptr, NORM_SCRATCH_BYTES);
+                         scratch_ptr, NORM_SCRATCH_BYTES, false);
 }

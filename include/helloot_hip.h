@@ -120,6 +120,10 @@ int hm_pricing_l2sq_resident(void* stream, const float* X, const float* Y, const
  * and the direct_norm tiles (cost.cu:10-157) for fp32 cost precision.
  *   c_ij = fp32 distance (l1 sum|x-y|, linf max|x-y|, l2 sqrt(sum (x-y)^2), 32-feature chunks),
  *   sigma_ij = (g_j - c_ij) + f_i in fp64. Exact (bit-reproducible) values; no perturbation.
+ * With k <= 2 and both HM_ROWS and HM_COLS, the column lists come from the row sweep through a candidate buffer in
+ * the workspace: hm_pricing_norm_workspace_bytes returns the size with the full buffer. A smaller workspace (at
+ * least the two-sweep size, which a too-small call names in its HM_ENOSPC message) gets a smaller buffer or none;
+ * the outputs are the same, as they are when the buffer overflows (the columns then come from a second sweep).
  */
 size_t hm_pricing_norm_workspace_bytes(int64_t m, int64_t n, int32_t d, int32_t k, uint32_t flags);
 int hm_pricing_norm(void* stream, const float* X, const float* Y, const double* f, const double* g,
@@ -131,8 +135,9 @@ int hm_pricing_norm(void* stream, const float* X, const float* Y, const double* 
  * hm_pricing_norm without a workspace and without any allocation. No counterpart in the reference: this entry
  * point is for callers that cannot allocate device memory (code under HIP graph capture, tight serving loops,
  * harnesses that forbid hipMalloc). Its scratch is a file-scope device array of hm_pricing_norm_noalloc_max_bytes()
- * bytes (64 MiB) per GPU, held until the process ends; calls whose hm_pricing_norm_workspace_bytes exceeds it fail
- * with HM_ENOSPC (524288 x 524288 at d = 8, k = 2 needs 12 MiB). The scratch of the CURRENT device is used, so the
+ * bytes (64 MiB) per GPU, held until the process ends; calls whose two-sweep workspace exceeds it fail with HM_ENOSPC
+ * (524288 x 524288 at d = 8, k = 2 needs 12 MiB), and k <= 2 calls use the row sweep's column buffer only when all
+ * of it fits (else two sweeps, same outputs). The scratch of the CURRENT device is used, so the
  * stream must belong to it. Every call on a GPU shares that GPU's array: calls that overlap on one GPU (other host
  * threads, other streams) race. Nothing in the array has to start at zero (the call clears what it accumulates,
  * with a kernel). Kernel timing (hm_profile_enable) records no events for these launches. Same outputs as
