@@ -326,7 +326,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(FUSED ? 8 :
                 float c;
                 if constexpr (EXACT) c = distance_exact<KIND, DR>(x, yj);
                 else if (DR > 0) c = distance_reg<KIND, (DR > 0 ? DR : 1)>(x, yj, d);
-                else c = distance_mem<KIND>(X + row * d, yj, d);
+                else c = distance_mem<KIND>(X + (row_ok ? row : 0) * d, yj, d);  // fused: lanes past m read row 0
                 const float s32 = (scb[jj] - c) + fi32;
                 if constexpr (FUSED) {
                     const float tcol = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ct[q]), jj - jb));

@@ -399,6 +399,24 @@ def _norm_call(dev, X, Y, f, g, k, kind, ws_bytes, flags):
 
 
 @pytest.mark.parametrize("kind", [0, 1, 2])
+@pytest.mark.parametrize("m,n,d,k", [(300, 257, 100, 2), (130, 400, 65, 1), (257, 129, 9, 2)])
+def test_norm_fused_sweep_ragged_rows_and_wide_features(cuda, kind, m, n, d, k):
+    """The fused sweep (k <= 2, rows and columns) with a partial last workgroup of rows, features past the register
+    width (d > 64: streamed from memory) and ragged column tiles, against the oracle."""
+    rng = np.random.default_rng(m + 3 * n + d + kind)
+    X = rng.random((m, d)).astype(np.float32)
+    Y = rng.random((n, d)).astype(np.float32)
+    f, g = rng.normal(0.3, 0.2, m), rng.normal(0.3, 0.2, n)
+    orv, ori, ocv, oci, ost = oracle.norm_scan(X, Y, f, g, k, kind)
+    rv, ri, cv, ci, st = pricing_norm(*_to(cuda, X, Y, f, g), k, kind)
+    np.testing.assert_array_equal(ri.cpu().numpy(), ori)
+    np.testing.assert_array_equal(rv.cpu().numpy(), orv)
+    np.testing.assert_array_equal(ci.cpu().numpy(), oci)
+    np.testing.assert_array_equal(cv.cpu().numpy(), ocv)
+    _assert_stats(st, ost)
+
+
+@pytest.mark.parametrize("kind", [0, 1, 2])
 @pytest.mark.parametrize("k,grid", [(2, False), (1, False), (2, True)])
 def test_norm_fused_columns_overflow_and_two_sweep_paths_agree(cuda, kind, k, grid):
     """k <= 2 bidirectional calls evaluate each pair once and collect the column lists through the candidate buffer.
