@@ -659,7 +659,7 @@ def main():
     if args.only:
         names = [x.strip() for x in args.only.split(",") if x.strip()]
         runs = {"c2": ("c2_scan_131072x131072_d64_k8", bench_c2), "c3": ("c3_sddmm_pdhg_262144_d256", bench_c3),
-                "c4": ("c4_norm_scan_524288_d8", bench_c4)}
+                "c4": ("c4_norm_scan_524288_d8", bench_c4), "solves": ("solve_seconds", bench_solves)}
         bad = [x for x in names if x not in runs]
         if bad:
             raise SystemExit(f"--only: unknown workload(s) {bad}; choose from {sorted(runs)}")

@@ -156,6 +156,30 @@ def test_pdhg_warm_start_matches_oracle(cuda):
     np.testing.assert_allclose(r.y.cpu().numpy(), ref["y"], rtol=1e-9, atol=1e-12)
 
 
+def test_pdhg_node_blocks_with_hub_nodes_match_oracle(cuda):
+    """Degrees far above the lane-group chunk on both sides, so both passes run as node blocks: source 0 reaches
+    all 2600 targets (two 2048-edge rounds in its workgroup, its running sum carried across them), target 0 all
+    40 sources, the other nodes a handful of edges."""
+    ns, nt = 40, 2600
+    rng = np.random.default_rng(21)
+    rows = np.concatenate([np.zeros(nt, np.int64), np.arange(1, ns), rng.integers(1, ns, 200)])
+    cols = np.concatenate([np.arange(nt), np.zeros(ns - 1, np.int64), rng.integers(1, nt, 200)])
+    perm = rng.permutation(rows.size)
+    rows, cols = rows[perm], cols[perm]
+    costs = rng.random(rows.size)
+    a = rng.random(ns)
+    a /= a.sum()
+    b = rng.random(nt)
+    b /= b.sum()
+    ref = oracle.pdhg_solve(rows, cols, costs, a, b, evaluation_frequency=50, iteration_limit=600, tolerance=0.0)
+    r = NativeRestrictedOTPDLP(device=cuda, evaluation_frequency=50, iteration_limit=600).solve_restricted(
+        rows=rows, cols=cols, costs=costs, source_mass=a, target_mass=b, tolerance=0.0)
+    assert r.iterations == ref["iterations"] == 600
+    assert r.solver_diag["restart_count"] == ref["restart_count"]
+    np.testing.assert_allclose(r.x.cpu().numpy(), ref["x"], rtol=1e-9, atol=1e-12)
+    np.testing.assert_allclose(r.y.cpu().numpy(), ref["y"], rtol=1e-9, atol=1e-12)
+
+
 def test_pdhg_c3_shape_1000_iterations_against_oracle(cuda):
     """C3 structure (16 sorted uniform columns per row, uniform marginals, SDDMM costs), 1000 iterations,
     at m = n = 8192 where the CPU oracle finishes in seconds."""
