@@ -541,9 +541,12 @@ def _level_summary(result):
     for level in result.solve_stage.levels:
         if level.kind == "refined":
             its = level.solve.iterations
+            pdhg = sum(int(i.solve_lp.backend_iterations or 0) for i in its)
+            lp = sum(i.solve_lp.wall_time for i in its)
             out.append({"n": level.n_source, "m": level.n_target, "iterations": len(its),
                         "seconds": round(level.wall_time, 3),
-                        "lp_seconds": round(sum(i.solve_lp.wall_time for i in its), 3),
+                        "lp_seconds": round(lp, 3), "pdhg_iterations": pdhg,
+                        "lp_us_per_pdhg_iteration": round(lp / pdhg * 1e6, 1) if pdhg else None,
                         "scan_seconds": round(sum(i.full_scan_time for i in its), 3),
                         "init_seconds": round(level.initialization.wall_time, 3)})
         else:
