@@ -71,6 +71,9 @@ def _shuffled_features(value, perm, device, consume: bool):
 def solve_problem(problem: Problem, options: SolverOptions, *, max_iterations: int = 100,
                   random_seed: int = 42) -> Result:
     options.check_supported()
+    if options.cost_precision != "fp32" and problem.cost_type != "l2^2":
+        raise NotImplementedError("the MI355X norm scans rank by fp32 costs (cost_precision='fp32'); fp64 cost "
+                                  "arithmetic is available for cost='l2^2'")
     if options.stopping_norm != "l2":
         raise NotImplementedError("the MI355X build stops on the relative l2 dual infeasibility (stopping_norm='l2')")
     require_native_runtime_compatibility()

@@ -6,8 +6,10 @@ so callers can switch without edits. Only the native GPU-resident path exists he
 * ``backend`` must be ``"native"`` (the reference's torch / cpp CPU backends are not part of this build);
 * ``cost_perturbation="on"`` raises ``NotImplementedError``, and ``"auto"`` records a re-entry trigger but keeps
   refining on the original cost (the perturbed cost stage is outside this build's scope);
-* ``cost_precision`` other than ``"fp32"`` raises ``NotImplementedError`` (the kernels evaluate costs from fp32
-  features with exact fp64 re-checks).
+* ``cost_precision``: the kernels read fp32 features and rank squared-Euclidean pairs by fp64 scores (fp64 dots
+  re-evaluated for every candidate near a list's cut; pair costs in fp64), which is what ``"fp64"`` and
+  ``"finest_fp64"`` ask for, so all three run the same ℓ2² path. The ℓ1 / ℓ2 / ℓ∞ scans rank by the fp32 cost of
+  the reference's fp32 path, so those costs accept ``"fp32"`` only (``NotImplementedError`` otherwise).
 """
 from __future__ import annotations
 
@@ -124,8 +126,6 @@ class SolverOptions:
             raise NotImplementedError("the MI355X build runs on the GPU only (torch_device='cpu' is unsupported)")
         if self.cost_perturbation == "on":
             raise NotImplementedError("cost_perturbation='on' is not part of the MI355X build; use 'auto' or 'off'")
-        if self.cost_precision != "fp32":
-            raise NotImplementedError("the MI355X build evaluates costs from fp32 features (cost_precision='fp32')")
         if self.assignment_topk > 32 or self.pricing_topk > 32:
             raise NotImplementedError("the MI355X scans keep at most 32 candidates per row")
 

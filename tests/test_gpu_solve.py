@@ -95,6 +95,25 @@ def test_tight_tolerance_solve_matches_the_exact_optimum_to_1e7(cuda, kind, n, m
     assert abs(r.objective - exact) <= 1e-7 * abs(exact)
 
 
+@pytest.mark.parametrize("precision", ["fp64", "finest_fp64"])
+def test_fp64_cost_precision_runs_the_exact_l2sq_path(cuda, precision):
+    """cost_precision='fp64' / 'finest_fp64' on l2^2: the path already ranks by fp64 scores and evaluates pair
+    costs in fp64, so the solve lands on the same optimum as the default (HiGHS to 5e-6, the fp32 run to 1e-9) and
+    records the option."""
+    rng = np.random.default_rng(77)
+    n, m, d = 200, 180, 6
+    X = rng.random((n, d)).astype(np.float32)
+    Y = (rng.random((m, d)) + 0.2).astype(np.float32)
+    base = SolverOptions(coarsest_size_threshold=40, verbose="off", cost_perturbation="off")
+    r32 = solve(X, Y, cost="l2^2", options=base)
+    r64 = solve(X, Y, cost="l2^2", options=SolverOptions(coarsest_size_threshold=40, verbose="off",
+                                                         cost_perturbation="off", cost_precision=precision))
+    exact = _exact(_cost_matrix(X, Y, "l2^2"), np.full(n, 1.0 / n), np.full(m, 1.0 / m))
+    assert r64.metadata["cost_precision"] == precision
+    assert abs(r64.objective - exact) <= 5e-6 * abs(exact)
+    assert r64.objective == pytest.approx(r32.objective, rel=1e-9)
+
+
 def test_coarsest_only_problem_is_solved_exactly(cuda):
     """A problem that fits the coarsest threshold is one network-simplex solve: HiGHS's optimum to 1e-12 and a
     vertex (at most n + m - 1 positive flows)."""

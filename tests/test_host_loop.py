@@ -27,6 +27,17 @@ def test_options_defaults_and_validation_match_the_reference():
         SolverOptions(backend="cpp").check_supported()
     with pytest.raises(NotImplementedError, match="cost_perturbation='on'"):
         SolverOptions(cost_perturbation="on").check_supported()
+    for precision in ("fp32", "fp64", "finest_fp64"):   # the l2^2 path ranks by fp64 scores for all three
+        SolverOptions(cost_precision=precision).check_supported()
+
+
+@pytest.mark.parametrize("cost", ["l1", "l2", "linf"])
+def test_fp64_cost_precision_is_refused_for_norm_costs(cost):
+    from hello_ot_amd.api import solve_problem
+
+    problem = Problem(np.zeros((3, 2), np.float32), np.ones((3, 2), np.float32), cost)
+    with pytest.raises(NotImplementedError, match="norm scans rank by fp32 costs"):
+        solve_problem(problem, SolverOptions(cost_precision="fp64"))
 
 
 def test_problem_validation():
