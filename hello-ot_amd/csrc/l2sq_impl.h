@@ -532,7 +532,7 @@ __device__ __forceinline__ void sweep_row_init(SweepRow<K1>& s, int64_t row, int
 // passes the tile's scores scale*dot + qb through LDS so that each Y row keeps its best K1 over the workgroup's
 // 128 X rows, CPASS Y rows at a time (sC holds CPASS * CST floats; 256 / CPASS threads scan each row and merge
 // their lists). Ends with a barrier: the next tile may rewrite sDB / sGE / sC.
-template <int K1, bool COLS, bool APPEND, int CPASS = BY>
+template <int K1, bool COLS, bool APPEND, int CPASS = BY, bool FULL = false>
 __device__ __forceinline__ void sweep_epilogue(const v16f (&tot)[NB], SweepRow<K1>& s, int tid, int wave, int h,
                                                int r, int64_t ytile, int64_t y_end, int64_t x0, int64_t panel,
                                                int64_t n, float scale, int STATS, float slack, const double* sQB64,
@@ -546,9 +546,11 @@ __device__ __forceinline__ void sweep_epilogue(const v16f (&tot)[NB], SweepRow<K
     bool near = false;  // a pair of this tile within the certificate slack (cert_fast)
     // Y rows of the tile inside the segment; pair (lane half h, offset c) is inside when 4h < ylim - c, a compare
     // against a wave-uniform bound
-    const int ylim = (int)(y_end - ytile < (int64_t)(NB * 32) ? y_end - ytile : (int64_t)(NB * 32));
+    // (FULL: the whole tile lies inside the segment and the whole panel inside the chunk, so every pair is inside)
+    const int ylim = FULL ? NB * 32 : (int)(y_end - ytile < (int64_t)(NB * 32) ? y_end - ytile : (int64_t)(NB * 32));
+    const bool rok = FULL || s.ok;
     // the row's shared threshold: scores at or below it cannot enter the row's merged lists (row_threshold_*)
-    const float rthr = (!APPEND && s.ok) ? row_threshold_get(rowthr, s.row - xb) : -INFINITY;
+    const float rthr = (!APPEND && rok) ? row_threshold_get(rowthr, s.row - xb) : -INFINITY;
     const float last0 = APPEND ? 0.0f : s.lv[K1 - 1];
     // Row candidates of the tile: every score above the lane's threshold at the start of the tile is queued in the
     // lane's LDS slots, without branches (a full queue writes its spare slot), and inserted after the tile in pair
@@ -572,7 +574,7 @@ __device__ __forceinline__ void sweep_epilogue(const v16f (&tot)[NB], SweepRow<K
                 const float t = tot[b][q];
                 const float w = fmaf(scale, t, dbs[cc]);
                 const int64_t j = ytile + jl0 + cc;
-                const bool ok = s.ok && 4 * h < ylim - (b * 32 + 8 * a + cc);
+                const bool ok = rok && (FULL || 4 * h < ylim - (b * 32 + 8 * a + cc));
                 if (APPEND) {
                     if (ok && w >= s.wt) {
                         const int pos = atomicAdd(&wcnt[s.row], 1);
@@ -597,7 +599,7 @@ __device__ __forceinline__ void sweep_epilogue(const v16f (&tot)[NB], SweepRow<K
                 for (int q = 0; q < 16; ++q) {
                     const int jl = b * 32 + 8 * (q / 4) + 4 * h + (q % 4);
                     const float w = fmaf(scale, tot[b][q], sDB[jl]);
-                    const bool ok = s.ok && 4 * h < ylim - (jl - 4 * h);
+                    const bool ok = rok && (FULL || 4 * h < ylim - (jl - 4 * h));
                     if (ok && w > s.lv[K1 - 1] && w > rthr) insert_e<K1>(s.lv, s.li, w, (int)(ytile + jl));
                 }
             }
@@ -622,7 +624,7 @@ __device__ __forceinline__ void sweep_epilogue(const v16f (&tot)[NB], SweepRow<K
             for (int q = 0; q < 16; ++q) {
                 const int jl = b * 32 + 8 * (q / 4) + 4 * h + (q % 4);
                 const float t = tot[b][q];
-                cert_near(s.ok && 4 * h < ylim - (jl - 4 * h), t, fmaf(scale, t, sDB[jl]), s.qbi, slack, scale, qb64,
+                cert_near(rok && (FULL || 4 * h < ylim - (jl - 4 * h)), t, fmaf(scale, t, sDB[jl]), s.qbi, slack, scale, qb64,
                           sDB64[jl], tcnt, s.num64);
             }
         }
@@ -928,10 +930,14 @@ __global__ __launch_bounds__(256) void l2sq_sweep(
                 for (int q = 0; q < 16; ++q) acc[b][q] = outer[b][q] + acc[b][q];
             }
         }
-        sweep_epilogue<K1, COLS, APPEND>(acc, s, tid, wave, h, r, ytile, y_end, x0, panel, n, scale, STATS, slack,
-                                         sQB64, sDB64, sDB, sGE,
-                                         sC, colpart, colthr, wcnt, wbuf, wcap, rowthr, xb,
-                                         COLS ? reinterpret_cast<Entry*>(sC) : sQ);
+#define HM_EPILOGUE(FULL_TILE)                                                                                  \
+    sweep_epilogue<K1, COLS, APPEND, BY, FULL_TILE>(acc, s, tid, wave, h, r, ytile, y_end, x0, panel, n, scale,  \
+                                                   STATS, slack, sQB64, sDB64, sDB, sGE, sC, colpart, colthr,    \
+                                                   wcnt, wbuf, wcap, rowthr, xb,                                 \
+                                                   COLS ? reinterpret_cast<Entry*>(sC) : sQ)
+        if (y_end - ytile >= (int64_t)(NB * 32) && x0 + BX <= xe) HM_EPILOGUE(true);
+        else HM_EPILOGUE(false);
+#undef HM_EPILOGUE
     }
     sweep_finish<K1, APPEND>(s, tid, lane, wave, h, seg, rows, xb, P, panel, STATS, part, blockstats, sRed);
 }
@@ -1197,10 +1203,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(COLS ? 1 : 
             step(I2{});
             step(I3{});
         }
-        sweep_epilogue<K1, COLS, APPEND>(acc, s, tid, wave, h, r, ytile, y_end, x0, panel, n, scale, STATS, slack,
-                                         sQB64, sDB64, sDB, sGE,
-                                         sC, colpart, colthr, wcnt, wbuf, wcap, rowthr, xb,
-                                         COLS ? reinterpret_cast<Entry*>(sC) : sQ);
+#define HM_EPILOGUE(FULL_TILE)                                                                                  \
+    sweep_epilogue<K1, COLS, APPEND, BY, FULL_TILE>(acc, s, tid, wave, h, r, ytile, y_end, x0, panel, n, scale,  \
+                                                   STATS, slack, sQB64, sDB64, sDB, sGE, sC, colpart, colthr,    \
+                                                   wcnt, wbuf, wcap, rowthr, xb,                                 \
+                                                   COLS ? reinterpret_cast<Entry*>(sC) : sQ)
+        if (y_end - ytile >= (int64_t)(NB * 32) && x0 + BX <= xe) HM_EPILOGUE(true);
+        else HM_EPILOGUE(false);
+#undef HM_EPILOGUE
     }
     wait_vmcnt<0>();  // the loads ahead into LDS land before the workgroup can end
     sweep_finish<K1, APPEND>(s, tid, lane, wave, h, seg, rows, xb, P, panel, STATS, part, blockstats, sRed);
