@@ -456,6 +456,21 @@ __global__ __launch_bounds__(256) void k_target_pass(const Pdhg P, double primal
 constexpr int EB = 2048;  // edges per round
 constexpr int PT = 256;   // threads per workgroup (also the largest npb)
 
+// sum + v[a] + v[a+1] + ... + v[b-1], added one by one in that order; the LDS reads go out eight at a time so that
+// a long node waits for one read latency per eight values rather than per value.
+__device__ __forceinline__ double fold_in_order(const double* v, int a, int b, double sum) {
+    int k = a;
+    for (; k + 8 <= b; k += 8) {
+        double t[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) t[u] = v[k + u];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) sum += t[u];
+    }
+    for (; k < b; ++k) sum += v[k];
+    return sum;
+}
+
 template <bool CHECKPOINT, bool STORE>
 __global__ __launch_bounds__(PT) void k_source_block(const Pdhg P, double primal_step, double dual_step,
                                                      double halpern, int npb) {
@@ -491,8 +506,7 @@ __global__ __launch_bounds__(PT) void k_source_block(const Pdhg P, double primal
             sr[q] = r;
         }
         __syncthreads();
-        const int32_t a = k0 > base ? k0 : base, b = k1 < base + len ? k1 : base + len;
-        for (int32_t k = a; k < b; ++k) sum += sr[k - base];
+        sum = fold_in_order(sr, (k0 > base ? k0 : base) - base, (k1 < base + len ? k1 : base + len) - base, sum);
         __syncthreads();
     }
     if (tid < nn) {
@@ -535,8 +549,7 @@ __global__ __launch_bounds__(PT) void k_target_block(const Pdhg P, double primal
             sr[q] = r;
         }
         __syncthreads();
-        const int32_t a = k0 > base ? k0 : base, b = k1 < base + len ? k1 : base + len;
-        for (int32_t k = a; k < b; ++k) sum += sr[k - base];
+        sum = fold_in_order(sr, (k0 > base ? k0 : base) - base, (k1 < base + len ? k1 : base + len) - base, sum);
         __syncthreads();
     }
     if (tid < nn) {
