@@ -350,6 +350,14 @@ __global__ void k_fixed_point(const Pdhg P, double* __restrict__ partial) {
 // a sequential loop over the group's edges).
 template <int G>
 __device__ inline double group_ordered_sum(double running, double value, int count) {
+    if (count == G) {  // a whole group: every shuffle issued before the first add
+        double t[G];
+#pragma unroll
+        for (int u = 0; u < G; ++u) t[u] = __shfl(value, u, G);
+#pragma unroll
+        for (int u = 0; u < G; ++u) running += t[u];
+        return running;
+    }
     for (int t = 0; t < count; ++t) running += __shfl(value, t, G);
     return running;
 }
