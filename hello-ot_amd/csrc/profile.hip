@@ -54,7 +54,9 @@ thread_local int g_quiet = 0;
 ProfileOff::ProfileOff() { ++g_quiet; }
 ProfileOff::~ProfileOff() { --g_quiet; }
 
-bool profiling() { return g_on; }
+// profiling() gates host-side readbacks for the timing report: never inside an allocation-free call, which must
+// not synchronise its stream (a caller may be capturing it into a graph)
+bool profiling() { return g_on && !g_quiet; }
 
 void prof_begin(hipStream_t st, const char* name) {
     if (!g_on || g_quiet) return;

@@ -11,6 +11,12 @@
 // the leaving arc is the last blocking arc of the cycle met from its apex in the direction of the push, which
 // rules out cycling on degenerate pivots.
 //
+// BIG is symbolic (the big-M method): a potential is k * BIG + r with an integer k (artificial arcs on the tree
+// path to the root, with their orientation) and a double r (the transport costs on that path), and reduced costs
+// compare lexicographically, first by their BIG multiple and then by their remainder. No value ever carries a
+// rounding error at the scale of BIG, so the entering threshold eps sits far above the rounding of the remainders
+// (sums of at most n + m costs) at every problem size.
+//
 // Pricing: block search over the n*m arcs (blocks of about sqrt(n*m)), the most negative reduced cost of the
 // first block that has one below -eps enters. Tree: parent, the arc to the parent, its orientation, depth, and
 // child lists; a pivot re-hangs the subtree cut off by the leaving arc and recomputes its depths and potentials
@@ -46,15 +52,14 @@ struct Simplex {
     const double* c;
     std::vector<int> parent, pred_arc, dir, depth;
     std::vector<double> flow_up;   // flow of the tree arc to the parent
-    std::vector<double> pot;
+    std::vector<int> kbig;         // potential = kbig * BIG + rem
+    std::vector<double> rem;
     std::vector<std::vector<int>> children;
     std::vector<int> child_slot;   // position of a node in its parent's child list
-    double big;
 
     // arc ids: transport i*m + j; artificial source i: n*m + i; artificial target j: n*m + n + j
     int64_t art_base() const { return (int64_t)n * m; }
     bool artificial(int64_t a) const { return a >= art_base(); }
-    double arc_cost(int64_t a) const { return artificial(a) ? big : c[a]; }
 
     void attach(int x, int p) {
         child_slot[x] = (int)children[p].size();
@@ -78,9 +83,15 @@ struct Simplex {
             stack.pop_back();
             const int p = parent[x];
             depth[x] = depth[p] + 1;
-            const double ca = arc_cost(pred_arc[x]);
-            // tree arc (tail -> head): c + pi_tail - pi_head = 0
-            pot[x] = dir[x] == UP ? pot[p] - ca : pot[p] + ca;
+            // tree arc (tail -> head): c + pi_tail - pi_head = 0, the artificial cost counted in kbig
+            const int sign = dir[x] == UP ? -1 : 1;
+            if (artificial(pred_arc[x])) {
+                kbig[x] = kbig[p] + sign;
+                rem[x] = rem[p];
+            } else {
+                kbig[x] = kbig[p];
+                rem[x] = sign < 0 ? rem[p] - c[pred_arc[x]] : rem[p] + c[pred_arc[x]];
+            }
             for (int ch : children[x]) stack.push_back(ch);
         }
     }
@@ -121,13 +132,13 @@ extern "C" int hm_transport_simplex(int64_t n_source, int64_t n_target, const do
     s.V = n + m + 1;
     s.root = n + m;
     s.c = costs;
-    s.big = (cmax + 1.0) * (double)(n + m);
     s.parent.assign(s.V, -1);
     s.pred_arc.assign(s.V, -1);
     s.dir.assign(s.V, 0);
     s.depth.assign(s.V, 0);
     s.flow_up.assign(s.V, 0.0);
-    s.pot.assign(s.V, 0.0);
+    s.kbig.assign(s.V, 0);
+    s.rem.assign(s.V, 0.0);
     s.children.assign(s.V, {});
     s.child_slot.assign(s.V, 0);
     for (int i = 0; i < n; ++i) {
@@ -136,7 +147,7 @@ extern "C" int hm_transport_simplex(int64_t n_source, int64_t n_target, const do
         s.dir[i] = UP;
         s.flow_up[i] = a[i];
         s.depth[i] = 1;
-        s.pot[i] = -s.big;
+        s.kbig[i] = -1;
         s.attach(i, s.root);
     }
     for (int j = 0; j < m; ++j) {
@@ -146,13 +157,13 @@ extern "C" int hm_transport_simplex(int64_t n_source, int64_t n_target, const do
         s.dir[x] = DOWN;
         s.flow_up[x] = b[j];
         s.depth[x] = 1;
-        s.pot[x] = s.big;
+        s.kbig[x] = 1;
         s.attach(x, s.root);
     }
 
     const int64_t arcs = (int64_t)n * m;
     const int64_t block = std::max<int64_t>(16, (int64_t)std::sqrt((double)arcs));
-    // entering threshold: above the rounding of reduced costs computed from potentials of magnitude up to about BIG
+    // entering threshold, against the rounding of the remainders (tree-path sums of costs)
     const double eps = 1e-12 * (cmax + 1.0);
     int64_t next = 0, pivots = 0;
     std::vector<int> stack;
@@ -160,7 +171,8 @@ extern "C" int hm_transport_simplex(int64_t n_source, int64_t n_target, const do
     for (;;) {
         // --- pricing: block search ---
         int64_t enter = -1;
-        double best = -eps;
+        int best_k = 0;         // best reduced cost so far: best_k * BIG + best_r, below (0, -eps)
+        double best_r = -eps;
         int64_t scanned = 0;
         while (scanned < arcs) {
             const int64_t stop = std::min<int64_t>(scanned + block, arcs);
@@ -168,9 +180,11 @@ extern "C" int hm_transport_simplex(int64_t n_source, int64_t n_target, const do
                 int64_t e = next + t;
                 if (e >= arcs) e -= arcs;
                 const int i = (int)(e / m), j = (int)(e - (int64_t)i * m);
-                const double rc = costs[e] + s.pot[i] - s.pot[n + j];
-                if (rc < best) {
-                    best = rc;
+                const int rk = s.kbig[i] - s.kbig[n + j];
+                const double rr = costs[e] + s.rem[i] - s.rem[n + j];
+                if (rk < best_k || (rk == best_k && rr < best_r)) {
+                    best_k = rk;
+                    best_r = rr;
                     enter = e;
                 }
             }

@@ -114,6 +114,31 @@ def fp64_certificate(X, Y, p, q, qb, db, scale=2.0, chunk=65536, envelope=2.0 **
             "cmax": cmax, "envelope": env_max}
 
 
+def certified_lower_bounds(a, b, f, g, row_max, col_max):
+    """Lower bounds on the optimal transport cost that weak duality certifies from duals (f, g) of any quality.
+
+    With sigma_ij = f_i + g_j - c_ij and masses summing to 1 on each side:
+
+    * ``row``: the c-transform f^c_i = min_j (c_ij - g_j) = f_i - max_j sigma_ij makes (f^c, g) dual feasible, so
+      sum a_i (f_i - row_max_i) + sum b_j g_j <= OPT;
+    * ``col``: the same with the roles swapped, sum a_i f_i + sum b_j (g_j - col_max_j);
+    * ``uniform``: shifting every f_i by the largest violation, sum a f + sum b g - max(max sigma, 0).
+
+    ``row_max`` / ``col_max`` are the exact maxima of sigma over each row / column (the scans' top-1 entries)."""
+    dual_value = float(a @ f + b @ g)
+    row = float(a @ (f - row_max) + b @ g)
+    col = float(a @ f + b @ (g - col_max))
+    uniform = dual_value - max(float(row_max.max()), 0.0)
+    return {"dual_value": dual_value, "row": row, "col": col, "uniform": uniform, "best": max(row, col, uniform)}
+
+
+def plan_residual(sol, a, b):
+    """Marginal residual of a sparse plan (host arrays): A x - (a, b)."""
+    n, m = a.size, b.size
+    return np.concatenate((np.bincount(sol.rows, weights=sol.values, minlength=n) - a,
+                           np.bincount(sol.cols, weights=sol.values, minlength=m) - b))
+
+
 def random_csr(rng, m, n, per_row):
     """CSR with `per_row` distinct uniformly random columns per row, sorted within each row (the C3 support)."""
     cols = np.empty((m, per_row), np.int64)

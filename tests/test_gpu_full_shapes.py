@@ -16,8 +16,8 @@ import pytest
 import torch
 
 import oracle
-from _shapes import (exact_col_topk, exact_row_topk, fp64_certificate, gmm, norm_costs_fp32, random_csr,
-                     sampled_c_transform, sqnorms)
+from _shapes import (certified_lower_bounds, exact_col_topk, exact_row_topk, fp64_certificate, gmm, norm_costs_fp32,
+                     random_csr, sampled_c_transform, sqnorms)
 from hello_ot_amd import SolverOptions, solve
 from hello_ot_amd.costs.pairs import lowrank_csr_costs
 from hello_ot_amd.kernels.generic_scan import pricing_l2sq, pricing_norm
@@ -25,6 +25,10 @@ from hello_ot_amd.lp import NativeRestrictedOTPDLP
 from test_gpu_pricing import assert_l2sq_certificate
 
 pytestmark = pytest.mark.gpu
+
+# Certified optimality gap of the full solves at the default tolerance 1e-6: objective minus the best weak-duality
+# lower bound of the returned duals, relative to the objective.
+CERTIFIED_GAP = 1e-5
 
 
 def _say(msg):
@@ -92,14 +96,20 @@ def _c4_inputs(dev, seed=4):
     return rng, X, Y
 
 
-def _norm_certificate(X, Y, f, g, kind, block=2048):
-    """(num, den, count, max sigma+, max|c|) of the fp32 norm costs over all pairs, on the device."""
+def _norm_certificate(X, Y, f, g, kind, block=2048, extrema=False):
+    """(num, den, count, max sigma+, max|c|) of the fp32 norm costs over all pairs, on the device; with ``extrema``
+    also the maximum of sigma over each row and over each column (fp64 tensors)."""
     num = den = 0.0
     count = 0
     mx = cmax = 0.0
+    row_max = torch.empty(X.shape[0], dtype=torch.float64, device=X.device)
+    col_max = torch.full((Y.shape[0],), -torch.inf, dtype=torch.float64, device=X.device)
     for s in range(0, X.shape[0], block):
         c = norm_costs_fp32(X[s:s + block], Y, kind).double()
         sigma = (g[None, :] - c) + f[s:s + block, None]
+        if extrema:
+            row_max[s:s + block] = sigma.max(1).values
+            torch.maximum(col_max, sigma.max(0).values, out=col_max)
         pos = sigma.clamp_min(0.0)
         num += float((pos * pos).sum())
         den += float((c * c).sum())
@@ -107,7 +117,8 @@ def _norm_certificate(X, Y, f, g, kind, block=2048):
         mx = max(mx, float(pos.max()))
         cmax = max(cmax, float(c.max()))
         del c, sigma, pos
-    return np.array([num, den, float(count), mx, cmax])
+    cert = np.array([num, den, float(count), mx, cmax])
+    return (cert, row_max, col_max) if extrema else cert
 
 
 @pytest.mark.parametrize("kind", [0, 1])
@@ -144,8 +155,13 @@ def test_c4_full_solve(cuda, kind):
     over all 2.7e11 pairs: the relative l2 dual infeasibility sqrt(sum sigma+^2) / (1 + sqrt(sum c^2)) of the
     returned duals at most the 1e-6 tolerance (gpu_resident/solver.py:_refine stops on exactly this quantity),
     the last LP's primal residual and duality gap within 1e-6, and the solver's own certificate equal to the
-    recomputed one. The weak-duality bound sum(a f) + sum(b g) - max sigma+ is reported: the l2 rule lets a few
-    pairs stay violated, so that bound sits below the objective by about the largest violation."""
+    recomputed one.
+
+    Objective: weak duality certifies OPT >= LB for the c-transform of the returned duals (each f_i lowered by its
+    row's largest violation; the best of the row, column and uniform bounds, ``certified_lower_bounds``), computed
+    from the exact maxima over all pairs. The objective of the returned plan must lie within CERTIFIED_GAP of that
+    bound, relative to the objective, so it is within CERTIFIED_GAP of the optimum whatever the reference returns
+    at the same tolerance."""
     rng, X, Y = _c4_inputs(cuda)
     m = X.shape[0]
     a, b = rng.uniform(0.5, 1.5, m), rng.uniform(0.5, 1.5, m)
@@ -164,17 +180,24 @@ def test_c4_full_solve(cuda, kind):
     f, g = r.solution.source_dual, r.solution.target_dual
     code = {"l1": 0, "linf": 1}[kind]
     _say(f"C4 solve {kind}: certificate of the returned duals over all pairs")
-    cert = _norm_certificate(X, Y, f, g, code)
+    cert, row_max, col_max = _norm_certificate(X, Y, f, g, code, extrema=True)
     infeasibility = np.sqrt(cert[0]) / (1.0 + np.sqrt(cert[1]))
-    dual_value = float(torch.as_tensor(a, device=cuda) @ f + torch.as_tensor(b, device=cuda) @ g)
+    at, bt = torch.as_tensor(a, device=cuda), torch.as_tensor(b, device=cuda)
+    lb = certified_lower_bounds(at, bt, f, g, row_max, col_max)
+    dual_value = lb["dual_value"]
     gap = abs(r.objective - dual_value) / (1.0 + abs(r.objective) + abs(dual_value))
+    certified = (r.objective - lb["best"]) / abs(r.objective)
     _say(f"C4 solve {kind}: objective {r.objective!r} dual value {dual_value!r} infeasibility {infeasibility:.3e} "
-         f"violated pairs {int(cert[2])} max violation {cert[3]:.3e} weak-duality bound {dual_value - cert[3]!r}")
+         f"violated pairs {int(cert[2])} max violation {cert[3]:.3e} lower bounds row {lb['row']!r} col "
+         f"{lb['col']!r} uniform {lb['uniform']!r} certified relative gap {certified:.3e}")
     assert infeasibility <= 1e-6
     np.testing.assert_allclose(infeasibility, last.convergence.dual_feasibility, rtol=1e-6)
     assert last.dual_violation.violations_found == int(cert[2])
     assert last.convergence.max_dual_violation == cert[3]
+    assert max(float(row_max.max()), 0.0) == cert[3] == max(float(col_max.max()), 0.0)
     assert gap <= 1e-6
+    # the plan is feasible only to the LP's 1e-6 residual, so its objective may sit that far below the optimum
+    assert -1e-6 <= certified <= CERTIFIED_GAP
 
 
 def test_c3_sddmm_and_pdhg_full_shape(cuda):

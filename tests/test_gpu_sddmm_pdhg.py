@@ -18,7 +18,8 @@ def _csr(rng, m, n, per_row):
     return rowptr, np.concatenate(cols).astype(np.int32)
 
 
-@pytest.mark.parametrize("m,n,d,per_row", [(300, 400, 256, 16), (100, 90, 7, 5), (64, 64, 600, 3), (33, 50, 64, 50)])
+@pytest.mark.parametrize("m,n,d,per_row", [(300, 400, 256, 16), (100, 90, 7, 5), (64, 64, 600, 3), (33, 50, 64, 50),
+                                            (200, 300, 8192, 16), (64, 80, 8194, 5)])   # C5's d, and d + 2
 def test_sddmm_csr_bit_exact(cuda, m, n, d, per_row):
     rng = np.random.default_rng(m + d)
     X = rng.standard_normal((m, d)).astype(np.float32)
@@ -48,7 +49,7 @@ def test_sddmm_csr_empty_rows_and_validation(cuda):
         lowrank_csr_costs(t[0], t[1], t[2], t[3], t[4], bad)
 
 
-@pytest.mark.parametrize("d", [1, 8, 20, 64, 130])
+@pytest.mark.parametrize("d", [1, 8, 20, 64, 130, 8192])
 def test_pair_costs_l2sq_and_norms_bit_exact(cuda, d):
     rng = np.random.default_rng(d)
     X = rng.random((40, d)).astype(np.float32)
@@ -175,6 +176,38 @@ def test_pdhg_node_blocks_with_hub_nodes_match_oracle(cuda):
     r = NativeRestrictedOTPDLP(device=cuda, evaluation_frequency=50, iteration_limit=600).solve_restricted(
         rows=rows, cols=cols, costs=costs, source_mass=a, target_mass=b, tolerance=0.0)
     assert r.iterations == ref["iterations"] == 600
+    assert r.solver_diag["restart_count"] == ref["restart_count"]
+    np.testing.assert_allclose(r.x.cpu().numpy(), ref["x"], rtol=1e-9, atol=1e-12)
+    np.testing.assert_allclose(r.y.cpu().numpy(), ref["y"], rtol=1e-9, atol=1e-12)
+
+
+def test_pdhg_node_blocks_of_several_nodes_across_rounds_match_oracle(cuda):
+    """Node blocks holding several nodes each (16384 sources: four per workgroup) whose edges exceed one 2048-edge
+    round, so a node's edges straddle a round boundary and its running sum is carried across rounds inside a
+    workgroup with other nodes: blocks of degrees (300, 900, 1400, 200) put the third node across the boundary,
+    blocks of (10, 4500, 30, 5) stretch the second over three rounds; the other sources have 4 edges. The C5
+    finest level runs this shape on its source side (256 nodes and about 3300 edges per workgroup)."""
+    ns, nt = 16384, 5000
+    rng = np.random.default_rng(33)
+    degree = np.full(ns, 4)
+    degree[: 32 * 4] = np.tile([300, 900, 1400, 200], 32)
+    degree[32 * 4: 48 * 4] = np.tile([10, 4500, 30, 5], 16)
+    rows = np.repeat(np.arange(ns), degree)
+    cols = np.concatenate([rng.choice(nt, k, replace=False) for k in degree])
+    missing = np.setdiff1d(np.arange(nt), cols)         # every target gets at least one edge
+    rows = np.concatenate((rows, rng.integers(0, ns, missing.size)))
+    cols = np.concatenate((cols, missing))
+    perm = rng.permutation(rows.size)
+    rows, cols = rows[perm].astype(np.int64), cols[perm].astype(np.int64)
+    costs = rng.random(rows.size)
+    a = rng.random(ns)
+    a /= a.sum()
+    b = rng.random(nt)
+    b /= b.sum()
+    ref = oracle.pdhg_solve(rows, cols, costs, a, b, evaluation_frequency=50, iteration_limit=400, tolerance=0.0)
+    r = NativeRestrictedOTPDLP(device=cuda, evaluation_frequency=50, iteration_limit=400).solve_restricted(
+        rows=rows, cols=cols, costs=costs, source_mass=a, target_mass=b, tolerance=0.0)
+    assert r.iterations == ref["iterations"] == 400
     assert r.solver_diag["restart_count"] == ref["restart_count"]
     np.testing.assert_allclose(r.x.cpu().numpy(), ref["x"], rtol=1e-9, atol=1e-12)
     np.testing.assert_allclose(r.y.cpu().numpy(), ref["y"], rtol=1e-9, atol=1e-12)

@@ -227,6 +227,55 @@ def test_transport_simplex_is_exact(n, m, uniform, kind):
     assert abs(primal - (a @ u + b @ v)) <= 1e-12 * scale
 
 
+def _assert_exact_vertex(C, a, b, r, c, x, u, v, optimum):
+    n, m = C.shape
+    scale = np.abs(C).max() + 1.0
+    assert len(x) <= n + m - 1 and (x >= 0).all()
+    np.testing.assert_allclose(np.bincount(r, weights=x, minlength=n), a, rtol=0, atol=1e-15)
+    np.testing.assert_allclose(np.bincount(c, weights=x, minlength=m), b, rtol=0, atol=1e-15)
+    primal = float(C[r, c] @ x)
+    assert abs(primal - optimum) <= 1e-12 * scale
+    assert np.abs(C[r, c] - u[r] - v[c]).max() <= 1e-12 * scale
+    assert (C - u[:, None] - v[None, :]).min() >= -1e-12 * scale
+    assert abs(primal - (a @ u + b @ v)) <= 1e-12 * scale
+
+
+@pytest.mark.parametrize("kind", ["l2", "grid"])
+def test_transport_simplex_at_the_default_coarsest_size(kind):
+    """1024 x 1024 with uniform masses, the largest level the default coarsest_size_threshold hands to the simplex:
+    an assignment problem, so its optimum is the Hungarian method's (scipy linear_sum_assignment) divided by n.
+    Integer grid costs make almost every pivot degenerate (ties everywhere)."""
+    from scipy.optimize import linear_sum_assignment
+
+    n = 1024
+    rng = np.random.default_rng(1024 if kind == "l2" else 2048)
+    if kind == "l2":
+        X, Y = rng.normal(size=(n, 8)), rng.normal(size=(n, 8))
+        C = ((X[:, None, :] - Y[None, :, :]) ** 2).sum(-1)
+    else:
+        P, Q = rng.integers(0, 12, (n, 2)), rng.integers(0, 12, (n, 2))
+        C = np.abs(P[:, None, :] - Q[None, :, :]).sum(-1).astype(np.float64)
+    a = b = np.full(n, 1.0 / n)
+    r, c, x, u, v, pivots = transport_simplex(C, a, b)
+    ri, ci = linear_sum_assignment(C)
+    _assert_exact_vertex(C, a, b, r, c, x, u, v, float(C[ri, ci].sum()) / n)
+    assert pivots > n
+
+
+def test_transport_simplex_with_zero_masses():
+    """Points with zero mass (their rows / columns carry no flow, and their duals must still be feasible)."""
+    rng = np.random.default_rng(17)
+    n, m = 50, 64
+    C = rng.random((n, m))
+    a, b = rng.uniform(0.5, 1.5, n), rng.uniform(0.5, 1.5, m)
+    a[rng.choice(n, 9, replace=False)] = 0.0
+    b[rng.choice(m, 13, replace=False)] = 0.0
+    a, b = a / a.sum(), b / b.sum()
+    r, c, x, u, v, _ = transport_simplex(C, a, b)
+    _assert_exact_vertex(C, a, b, r, c, x, u, v, _highs(C, a, b))
+    assert np.all(x[a[r] == 0.0] == 0.0) and np.all(x[b[c] == 0.0] == 0.0)
+
+
 def test_transport_simplex_rejects_bad_input():
     with pytest.raises(ValueError, match="unbalanced"):
         transport_simplex(np.ones((2, 2)), np.array([0.5, 0.5]), np.array([0.2, 0.2]))

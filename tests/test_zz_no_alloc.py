@@ -66,6 +66,37 @@ def test_no_alloc_matches_the_workspace_entry_point(cuda, kind):
             assert torch.equal(a, b)
 
 
+def test_no_alloc_with_profiling_on_is_captured_into_a_graph(cuda):
+    """With the library's timing report switched on, the allocation-free fused call (k <= 2, rows and columns)
+    still makes no host readback and no stream synchronisation: it is captured into a HIP graph, and every replay,
+    with eager work between replays, matches the workspace entry point."""
+    lib = _lib.load()
+    m, n, d, k, kind = 700, 900, 5, 2, 0
+    X, Y, f, g = _inputs(cuda, m, n, d, 3)
+    want = _with_workspace(cuda, X, Y, f, g, k, kind)
+    _no_alloc(cuda, X, Y, f, g, k, kind)                # first call on the device: scratch address lookup
+    out = _outputs(cuda, m, n, k)
+    graph = torch.cuda.CUDAGraph()
+    _lib.profile_enable(True)
+    try:
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph):
+            rc = lib.hm_pricing_norm_noalloc(_lib.stream_handle(cuda), *map(_lib.ptr, (X, Y, f, g)), m, n, d, k,
+                                             kind, FLAGS, *map(_lib.ptr, out))
+        _lib.check(rc, "hm_pricing_norm_noalloc (captured)")
+        for _ in range(3):
+            for t in out:
+                t.fill_(7)
+            torch.cuda.synchronize()
+            graph.replay()
+            torch.cuda.synchronize()
+            for a, b in zip(out, want):
+                assert torch.equal(a, b)
+    finally:
+        _lib.profile_enable(False)
+        _lib.profile_reset()
+
+
 def test_no_alloc_rejects_calls_beyond_its_scratch(cuda):
     lib = _lib.load()
     cap = int(lib.hm_pricing_norm_noalloc_max_bytes())
