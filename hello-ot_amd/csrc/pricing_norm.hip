@@ -399,6 +399,107 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(FUSED ? 8 :
     }
 }
 
+// fp64 costs (HM_FP64, the reference's direct_norm_fp64: cost.cu:10-104 with CHAINS = 1 and a double accumulator):
+// each feature difference is taken in fp64 from the fp32 inputs and the features combine one after another in
+// feature order; l2 accumulates fma(z, z, acc) (nvcc contracts the multiply-add) and takes one fp64 sqrt.
+template <int KIND>
+__device__ inline double feature_op64(double part, double z) {
+    if (KIND == HM_COST_L1) return part + fabs(z);
+    if (KIND == HM_COST_LINF) return fmax(part, fabs(z));
+    return fma(z, z, part);
+}
+
+// One thread per X row (its features in registers as fp64 when DR > 0, else read from memory), Y tiles in LDS as
+// fp32 with their duals as fp64. Scores sigma = (g_j - c) + f_i, the row lists and the certificate are fp64; there
+// is no fp32 filter. The lists are exact whatever the order of the pairs, the certificate sums fp64-grade.
+template <int KIND, int K, int DR>
+__global__ __launch_bounds__(256) void norm_sweep64(const float* __restrict__ X, const float* __restrict__ Y, int64_t m,
+                                                    int64_t n, int d, const double* __restrict__ rb,
+                                                    const double* __restrict__ cb, int k, int64_t seg_len,
+                                                    double* __restrict__ part_v, int* __restrict__ part_i,
+                                                    double* __restrict__ blockstats, int STATS, int TRANSPOSED,
+                                                    int ntile) {
+    extern __shared__ float4 smem4[];
+    double* scb = reinterpret_cast<double*>(smem4);   // ntile column duals
+    float* sy = reinterpret_cast<float*>(scb + ntile);  // ntile * d features
+    __shared__ double sRed[4][5];
+    const int tid = threadIdx.x;
+    const int64_t row = (int64_t)blockIdx.x * NB_ROWS + tid;
+    const bool row_ok = row < m;
+    const int64_t y_begin = (int64_t)blockIdx.y * seg_len;
+    const int64_t y_end = y_begin + seg_len < n ? y_begin + seg_len : n;
+
+    double x[DR > 0 ? DR : 1];
+    if (DR > 0) {
+#pragma unroll
+        for (int t = 0; t < (DR > 0 ? DR : 1); ++t) x[t] = (row_ok && t < d) ? (double)X[row * d + t] : 0.0;
+    }
+    const float* xr = X + (row_ok ? row : 0) * d;
+    const double fi = row_ok ? rb[row] : 0.0;
+    double v[K];
+    int id[K];
+#pragma unroll
+    for (int s = 0; s < K; ++s) { v[s] = -INFINITY; id[s] = -1; }
+    double num = 0.0, den = 0.0, cnt = 0.0, cmax = 0.0;
+    for (int64_t t0 = y_begin; t0 < y_end; t0 += ntile) {
+        const int tn = (int)((y_end - t0) < ntile ? (y_end - t0) : ntile);
+        __syncthreads();
+        for (int e = tid; e < tn * d; e += 256) sy[e] = Y[t0 * d + e];
+        for (int e = tid; e < tn; e += 256) scb[e] = cb[t0 + e];
+        __syncthreads();
+        if (!row_ok) continue;
+        for (int jj = 0; jj < tn; ++jj) {
+            const float* yj = sy + (size_t)jj * d;
+            double c = 0.0;
+            if (DR > 0) {
+#pragma unroll
+                for (int t = 0; t < (DR > 0 ? DR : 1); ++t)
+                    if (t < d) c = feature_op64<KIND>(c, x[t] - (double)yj[t]);
+            } else {
+                for (int t = 0; t < d; ++t) c = feature_op64<KIND>(c, (double)xr[t] - (double)yj[t]);
+            }
+            if (KIND == HM_COST_L2) c = sqrt(c);
+            const double sig = TRANSPOSED ? (fi - c) + scb[jj] : (scb[jj] - c) + fi;
+            const int j = (int)(t0 + jj);
+            if (sig == sig && better(sig, j, v[k - 1], id[k - 1])) put_sorted<K>(v, id, k, sig, j);
+            if (STATS) {
+                den = fma(c, c, den);
+                cmax = fmax(cmax, c);
+                if (sig > 0.0) {
+                    num = fma(sig, sig, num);
+                    cnt += 1.0;
+                }
+            }
+        }
+    }
+    if (row_ok) {
+        double* ov = part_v + ((int64_t)blockIdx.y * m + row) * k;
+        int* oi = part_i + ((int64_t)blockIdx.y * m + row) * k;
+        for (int s = 0; s < k; ++s) { ov[s] = v[s]; oi[s] = id[s]; }
+    }
+    if (STATS) {
+        const int lane = tid & 63, wave = tid >> 6;
+        double r[5] = {num, den, cnt, 0.0, cmax};  // slot 3: exact row maximum later
+#pragma unroll
+        for (int e = 0; e < 5; ++e)
+            for (int o = 32; o >= 1; o >>= 1) {
+                const double t = __shfl_xor(r[e], o, 64);
+                r[e] = e >= 3 ? fmax(r[e], t) : r[e] + t;
+            }
+        if (lane == 0)
+            for (int e = 0; e < 5; ++e) sRed[wave][e] = r[e];
+        __syncthreads();
+        if (tid == 0) {
+            double* dst = blockstats + ((int64_t)blockIdx.y * gridDim.x + blockIdx.x) * 5;
+            for (int e = 0; e < 5; ++e) {
+                double o = sRed[0][e];
+                for (int w = 1; w < 4; ++w) o = e >= 3 ? fmax(o, sRed[w][e]) : o + sRed[w][e];
+                dst[e] = o;
+            }
+        }
+    }
+}
+
 // merge S exact segment lists per row (tie rule), one thread per row; gated like norm_sweep
 template <int K>
 __global__ void norm_merge(const double* __restrict__ part_v, const int* __restrict__ part_i, int64_t m, int S, int k,
@@ -534,7 +635,7 @@ inline int kbucket(int k) { return k <= 2 ? 2 : (k <= 8 ? 8 : 32); }
 
 // columns ride on the row sweep (k <= 2 with rows and columns requested; buffer slots in int32)
 inline bool fusable(int64_t n, int k, uint32_t flags) {
-    return k <= 2 && (flags & HM_ROWS) && (flags & HM_COLS) && fused_cap(n, k) < INT32_MAX;
+    return k <= 2 && (flags & HM_ROWS) && (flags & HM_COLS) && !(flags & HM_FP64) && fused_cap(n, k) < INT32_MAX;
 }
 
 struct NormWork {
@@ -642,6 +743,48 @@ int norm_direction(hipStream_t st, const Direction& D, int d, int k, const NormW
     return fail(HM_EINVAL, "unsupported k");
 }
 
+template <int KIND, int K, int DR>
+int norm_direction64_t(hipStream_t st, const Direction& D, int d, int k, const NormWork& w, double* stats_out,
+                       int linf) {
+    dim3 grid((unsigned)((D.m + NB_ROWS - 1) / NB_ROWS), (unsigned)D.plan.S);
+    const size_t budget = (size_t)LDS_FLOATS * sizeof(float);
+    auto bytes = [d](int t) { return (size_t)t * sizeof(double) + (size_t)t * d * sizeof(float); };
+    int ntile = NT;
+    while (ntile > 1 && bytes(ntile) > budget) ntile >>= 1;
+    if (bytes(ntile) > budget) return fail(HM_EINVAL, "fp64 norm pricing supports d <= %d", LDS_FLOATS - 2);
+    prof_begin(st, D.transposed ? "norm_sweep64_swapped" : "norm_sweep64");
+    hipLaunchKernelGGL((norm_sweep64<KIND, K, DR>), grid, dim3(256), bytes(ntile), st, D.X, D.Y, D.m, D.n, d, D.rb, D.cb,
+                       k, D.plan.seg_len, w.pv, w.pi, w.bs, (int)D.stats, (int)D.transposed, ntile);
+    prof_end(st);
+    HM_LAUNCH_CHECK("norm_sweep64");
+    hipLaunchKernelGGL((norm_merge<K>), dim3((unsigned)((D.m + 255) / 256)), dim3(256), 0, st, w.pv, w.pi, D.m, D.plan.S,
+                       k, D.out_v, D.out_i, nullptr, (int64_t)0);
+    HM_LAUNCH_CHECK("norm_merge");
+    if (D.stats) {
+        hipLaunchKernelGGL(norm_reduce_stats, dim3(1), dim3(256), 0, st, w.bs, (int64_t)grid.x * grid.y, stats_out, linf);
+        HM_LAUNCH_CHECK("norm_reduce_stats");
+    }
+    return HM_OK;
+}
+
+template <int KIND, int K>
+int norm_direction64_d(hipStream_t st, const Direction& D, int d, int k, const NormWork& w, double* stats_out, int linf) {
+    if (d <= 8) return norm_direction64_t<KIND, K, 8>(st, D, d, k, w, stats_out, linf);
+    if (d <= 32) return norm_direction64_t<KIND, K, 32>(st, D, d, k, w, stats_out, linf);
+    if (d <= 64) return norm_direction64_t<KIND, K, 64>(st, D, d, k, w, stats_out, linf);
+    return norm_direction64_t<KIND, K, 0>(st, D, d, k, w, stats_out, linf);
+}
+
+template <int KIND>
+int norm_direction64(hipStream_t st, const Direction& D, int d, int k, const NormWork& w, double* stats_out, int linf) {
+    switch (kbucket(k)) {
+        case 2: return norm_direction64_d<KIND, 2>(st, D, d, k, w, stats_out, linf);
+        case 8: return norm_direction64_d<KIND, 8>(st, D, d, k, w, stats_out, linf);
+        case 32: return norm_direction64_d<KIND, 32>(st, D, d, k, w, stats_out, linf);
+    }
+    return fail(HM_EINVAL, "unsupported k");
+}
+
 inline size_t norm_workspace(int64_t m, int64_t n, int k, uint32_t flags, int64_t cap) {
     Sizer s;
     NormWork w;
@@ -712,7 +855,13 @@ int norm_scan_run(void* stream, const float* X, const float* Y, const double* f,
     hipLaunchKernelGGL(norm_prep, dim3((unsigned)((m + 255) / 256)), dim3(256), 0, st, X, m, d, f, w.maxima + 2);
     HM_LAUNCH_CHECK("norm_prep");
     const int linf = (flags & HM_LINF) ? 1 : 0;
+    const bool fp64 = (flags & HM_FP64) != 0;
     auto dispatch = [&](const Direction& D) {
+        if (fp64) {
+            if (kind == HM_COST_L1) return norm_direction64<HM_COST_L1>(st, D, d, k, w, stats, linf);
+            if (kind == HM_COST_LINF) return norm_direction64<HM_COST_LINF>(st, D, d, k, w, stats, linf);
+            return norm_direction64<HM_COST_L2>(st, D, d, k, w, stats, linf);
+        }
         if (kind == HM_COST_L1) return norm_direction<HM_COST_L1>(st, D, d, k, w, stats, linf);
         if (kind == HM_COST_LINF) return norm_direction<HM_COST_LINF>(st, D, d, k, w, stats, linf);
         return norm_direction<HM_COST_L2>(st, D, d, k, w, stats, linf);

@@ -15,7 +15,7 @@ LIB_PATH = Path(__file__).resolve().parent / LIB_NAME
 HEADER_PATH = Path(__file__).resolve().parents[2] / "include" / "helloot_hip.h"
 
 HM_OK, HM_EINVAL, HM_EHIP, HM_ENOSPC, HM_ESOLVE = 0, 1, 2, 3, 4
-HM_ROWS, HM_COLS, HM_STATS, HM_LINF, HM_BF16X3, HM_INT8X3 = 1, 2, 4, 8, 16, 32
+HM_ROWS, HM_COLS, HM_STATS, HM_LINF, HM_BF16X3, HM_INT8X3, HM_FP64 = 1, 2, 4, 8, 16, 32, 64
 COST_KINDS = {"l1": 0, "linf": 1, "l2": 2}
 
 _P = ctypes.c_void_p

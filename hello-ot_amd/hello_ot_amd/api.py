@@ -14,7 +14,7 @@ import numpy as np
 import torch
 
 from ._native_compat import require_native_runtime_compatibility
-from .config import SolverOptions
+from .config import SolverOptions, level_precision
 from .resident.cost import Cost
 from .resident.leaf import solve_coarsest
 from .resident.solver import level_sizes, refine_level, shuffle_once_permutation
@@ -71,9 +71,6 @@ def _shuffled_features(value, perm, device, consume: bool):
 def solve_problem(problem: Problem, options: SolverOptions, *, max_iterations: int = 100,
                   random_seed: int = 42) -> Result:
     options.check_supported()
-    if options.cost_precision != "fp32" and problem.cost_type != "l2^2":
-        raise NotImplementedError("the MI355X norm scans rank by fp32 costs (cost_precision='fp32'); fp64 cost "
-                                  "arithmetic is available for cost='l2^2'")
     if options.stopping_norm != "l2":
         raise NotImplementedError("the MI355X build stops on the relative l2 dual infeasibility (stopping_norm='l2')")
     require_native_runtime_compatibility()
@@ -100,7 +97,7 @@ def solve_problem(problem: Problem, options: SolverOptions, *, max_iterations: i
         sparsified = []
         for level_index in reversed(range(len(sizes))):
             nn, mm = sizes[level_index]
-            cost = full.sliced(nn, mm)
+            cost = full.sliced(nn, mm, level_precision(options.cost_precision, level_index))
             aa, bb = balanced_masses(a[:nn].clone(), b[:mm].clone())
             if previous is None:
                 support, dual, level = solve_coarsest(cost, aa, bb, level_index)

@@ -8,8 +8,9 @@ so callers can switch without edits. Only the native GPU-resident path exists he
   refining on the original cost (the perturbed cost stage is outside this build's scope);
 * ``cost_precision``: the kernels read fp32 features and rank squared-Euclidean pairs by fp64 scores (fp64 dots
   re-evaluated for every candidate near a list's cut; pair costs in fp64), which is what ``"fp64"`` and
-  ``"finest_fp64"`` ask for, so all three run the same ℓ2² path. The ℓ1 / ℓ2 / ℓ∞ scans rank by the fp32 cost of
-  the reference's fp32 path, so those costs accept ``"fp32"`` only (``NotImplementedError`` otherwise).
+  ``"finest_fp64"`` ask for, so all three run the same ℓ2² path. The ℓ1 / ℓ2 / ℓ∞ costs follow the level's
+  precision (``level_precision``, ``config.py:23-28`` of the reference): fp32 chunked costs, or fp64 costs in the
+  scans (the reference's ``compute_precision = 1``) and fp64 pair costs on the support.
 """
 from __future__ import annotations
 
@@ -18,6 +19,13 @@ from dataclasses import dataclass
 from typing import Literal, Optional
 
 POSITIVE_SUPPORT_TOLERANCE = 1e-15
+
+
+def level_precision(policy: str, level_index: int) -> str:
+    """Cost arithmetic of hierarchy level ``level_index`` (0 = finest) under ``cost_precision`` (config.py:23-28)."""
+    if policy not in {"fp32", "fp64", "finest_fp64"}:
+        raise ValueError("cost_precision must be one of: fp32, fp64, finest_fp64")
+    return "fp64" if policy == "fp64" or (policy == "finest_fp64" and int(level_index) == 0) else "fp32"
 
 
 def normalize_pricing_topk(value) -> int:
@@ -130,5 +138,5 @@ class SolverOptions:
             raise NotImplementedError("the MI355X scans keep at most 32 candidates per row")
 
 
-__all__ = ["POSITIVE_SUPPORT_TOLERANCE", "SolverOptions", "active_support_budget", "normalize_pricing_topk",
-           "primal_support_cap", "validate_support_budget_factor"]
+__all__ = ["POSITIVE_SUPPORT_TOLERANCE", "SolverOptions", "active_support_budget", "level_precision",
+           "normalize_pricing_topk", "primal_support_cap", "validate_support_budget_factor"]

@@ -139,13 +139,20 @@ def pricing_l2sq(x, y, nx, ny, qb, dbb, k, *, dot_scale=2.0, rows=True, cols=Tru
     return rv, ri, cv, ci, st
 
 
-def pricing_norm(x, y, f, g, k, cost_type, *, rows=True, cols=True, stats=True, linf=True):
-    """l1 / linf / l2 pricing (cost_type 0/1/2): (row_vals, row_idx, col_vals, col_idx, stats5)."""
+NORM_PRECISIONS = ("fp32", "fp64")
+
+
+def pricing_norm(x, y, f, g, k, cost_type, *, rows=True, cols=True, stats=True, linf=True, precision="fp32"):
+    """l1 / linf / l2 pricing (cost_type 0/1/2): (row_vals, row_idx, col_vals, col_idx, stats5). ``precision``
+    "fp32" ranks by the reference's fp32 chunked costs, "fp64" by its fp64 costs (compute_precision = 1)."""
+    if precision not in NORM_PRECISIONS:
+        raise ValueError(f"precision must be one of {NORM_PRECISIONS}")
     lib = _lib.load()
     x, y, f, g = map(_c, (x, y, f, g))
     m, n, d = x.shape[0], y.shape[0], x.shape[1]
     flags = (_lib.HM_ROWS if (rows or stats) else 0) | (_lib.HM_COLS if cols else 0) \
-        | (_lib.HM_STATS if stats else 0) | (_lib.HM_LINF if (stats and linf) else 0)
+        | (_lib.HM_STATS if stats else 0) | (_lib.HM_LINF if (stats and linf) else 0) \
+        | (_lib.HM_FP64 if precision == "fp64" else 0)
     dev = x.device
     need_rows = bool(flags & _lib.HM_ROWS)
     rv = torch.empty((m, k), dtype=torch.float64, device=dev) if need_rows else None
@@ -160,6 +167,9 @@ def pricing_norm(x, y, f, g, k, cost_type, *, rows=True, cols=True, stats=True, 
                                  _lib.ptr(st), _lib.ptr(ws), ws.numel())
     _lib.check(rc, "hm_pricing_norm")
     return (rv if rows else None), (ri if rows else None), cv, ci, st
+
+
+_NORM_PRECISION = {0: "fp32", 1: "fp64"}  # compute_precision of the reference's norm scans
 
 
 class ScanExtension:
@@ -250,8 +260,6 @@ class ScanExtension:
             raise ValueError("generic directional cost must be l1, linf, l2 or raw")
         if compute_precision not in (0, 1):
             raise ValueError("norm scans require FP32 coordinate storage and precision 0 or 1")
-        if compute_precision == 1:
-            raise ValueError("the MI355X norm scan evaluates costs in FP32 (compute_precision=0)")
         if float(sigma) != 0.0:
             raise NotImplementedError("cost perturbation is not part of the MI355X native pricing path")
         if collect_statistics:
@@ -259,7 +267,7 @@ class ScanExtension:
         self._record("norm_initial")
         zero = torch.zeros(len(query), dtype=torch.float64, device=query.device)
         rv, ri, _, _, _ = pricing_norm(query, db, zero, dual_db, k, cost_type, rows=True, cols=False, stats=False,
-                                       linf=False)
+                                       linf=False, precision=_NORM_PRECISION[compute_precision])
         return [rv.neg(), ri.long()]
 
     def fused_gcost_certificate(self, query, db, query_dual, db_dual, cost_type, query_global_index=None,
@@ -274,13 +282,11 @@ class ScanExtension:
             raise ValueError("certificate-only requires a norm or raw cost")
         if compute_precision not in (0, 1):
             raise ValueError("norm scans require FP32 coordinate storage and precision 0 or 1")
-        if compute_precision == 1:
-            raise ValueError("the MI355X norm scan evaluates costs in FP32 (compute_precision=0)")
         if float(sigma) != 0.0:
             raise NotImplementedError("cost perturbation is not part of the MI355X native pricing path")
         self._record("norm_certificate")
         _, _, _, _, st = pricing_norm(query, db, query_dual, db_dual, 1, cost_type, rows=True, cols=False, stats=True,
-                                      linf=True)
+                                      linf=True, precision=_NORM_PRECISION[compute_precision])
         den = st[1] if compute_denominator else torch.zeros_like(st[1])
         return [st[0], den, st[3], st[4], st[2].long()]
 
@@ -294,13 +300,11 @@ class ScanExtension:
             raise ValueError("generic bidirectional cost must be l1, linf, l2 or raw")
         if compute_precision not in (0, 1):
             raise ValueError("norm scans require FP32 coordinate storage and precision 0 or 1")
-        if compute_precision == 1:
-            raise ValueError("the MI355X norm scan evaluates costs in FP32 (compute_precision=0)")
         if float(sigma) != 0.0:
             raise NotImplementedError("cost perturbation is not part of the MI355X native pricing path")
         self._record("norm_pricing")
         rv, ri, cv, ci, st = pricing_norm(query, db, query_dual, db_dual, k, cost_type, rows=True, cols=True,
-                                          stats=True, linf=True)
+                                          stats=True, linf=True, precision=_NORM_PRECISION[compute_precision])
         return [rv, ri.long(), cv, ci.long(), st[0], st[1], st[3], st[4], st[2].long()]
 
     # -- (b) SDDMM / pair costs -------------------------------------------------------------------------

@@ -34,6 +34,7 @@ class Cost:
     kind: str
     source_offset: torch.Tensor | None = None
     target_offset: torch.Tensor | None = None
+    precision: str = "fp32"   # cost arithmetic of the norm costs: "fp32" or "fp64" (l2^2 is fp64-exact in both)
 
     @classmethod
     def create(cls, source: torch.Tensor, target: torch.Tensor, kind: str) -> "Cost":
@@ -43,22 +44,24 @@ class Cost:
             raise ValueError(f"unsupported cost type {kind!r}")
         return cls(source, target, kind)
 
-    def sliced(self, n: int, m: int) -> "Cost":
-        """The first n source and m target points: a hierarchy level after the global shuffle."""
+    def sliced(self, n: int, m: int, precision: str = "fp32") -> "Cost":
+        """The first n source and m target points: a hierarchy level after the global shuffle, with that level's
+        cost precision (gpu_resident/cost.py:31-37)."""
         return replace(self, source=self.source[:n], target=self.target[:m],
                        source_offset=None if self.source_offset is None else self.source_offset[:n],
-                       target_offset=None if self.target_offset is None else self.target_offset[:m])
+                       target_offset=None if self.target_offset is None else self.target_offset[:m],
+                       precision=precision)
 
     @property
     def shape(self):
         return len(self.source), len(self.target)
 
     def pairs(self, rows: torch.Tensor, cols: torch.Tensor) -> torch.Tensor:
-        """fp64 costs of (rows[e], cols[e]): exact p + q - 2<x, y> for l2^2, the pricing scan's fp32 cost for
-        the norms."""
+        """fp64 costs of (rows[e], cols[e]): exact p + q - 2<x, y> for l2^2; for the norms the pricing scan's fp32
+        cost, or at fp64 precision the fp64 norm of the reference's pair-cost kernel (costs/metric.py:94-118)."""
         if self.kind == "l2^2":
             return lowrank_pair_costs(self.source, self.target, self.source_offset, self.target_offset, rows, cols)
-        return norm_pair_costs(self.source, self.target, rows, cols, NORM_KINDS[self.kind], precision="fp32")
+        return norm_pair_costs(self.source, self.target, rows, cols, NORM_KINDS[self.kind], precision=self.precision)
 
     def scan(self, dual: torch.Tensor, k: int, *, certificate: bool = False, direction: str | None = None):
         """Pricing / directional scans in the reference's output convention (gpu_resident/cost.py:104-161):
@@ -86,7 +89,8 @@ class Cost:
                                               stats=certificate, linf=certificate)
         else:
             rv, ri, cv, ci, st = pricing_norm(self.source, self.target, f, g, k, NORM_KINDS[self.kind], rows=rows,
-                                              cols=cols, stats=certificate, linf=certificate)
+                                              cols=cols, stats=certificate, linf=certificate,
+                                              precision=self.precision)
         if direction == "source":
             return rv[:, :kr], ri[:, :kr], None, None, None
         if direction == "target":

@@ -36,6 +36,7 @@ extern "C" {
 #define HM_LINF 8u    /* also max|cost| (collect_linf_stats) */
 #define HM_BF16X3 16u /* l2^2 sweep on split-bf16 MFMA (hi*hi + hi*lo + lo*hi) instead of fp32 MFMA; same outputs */
 #define HM_INT8X3 32u /* l2^2 sweep on int8 MFMA over a 16-bit fixed-point split (h*h + h*l + l*h); same outputs */
+#define HM_FP64 64u   /* norm scans: fp64 costs (compute_precision = 1 of the reference, direct_norm_fp64) */
 
 /* Norm cost kinds (generic_scan.py cost_type: 0=l1, 1=linf, 2=l2) */
 #define HM_COST_L1 0
@@ -120,6 +121,10 @@ int hm_pricing_l2sq_resident(void* stream, const float* X, const float* Y, const
  * and the direct_norm tiles (cost.cu:10-157) for fp32 cost precision.
  *   c_ij = fp32 distance (l1 sum|x-y|, linf max|x-y|, l2 sqrt(sum (x-y)^2), 32-feature chunks),
  *   sigma_ij = (g_j - c_ij) + f_i in fp64. Exact (bit-reproducible) values; no perturbation.
+ * With HM_FP64 the costs are fp64 instead, as the reference's compute_precision = 1 (generic_scan.py:166-167 ->
+ * direct_norm_fp64, cost.cu:84-104): per pair every feature difference in fp64 from the fp32 inputs, combined in
+ * feature order (l1 sum|z|, linf max|z|, l2 sqrt of fma(z, z, acc)); scores and certificate are then fp64 throughout
+ * and the column lists come from a second, role-swapped sweep.
  * With k <= 2 and both HM_ROWS and HM_COLS, the column lists come from the row sweep through a candidate buffer in
  * the workspace: hm_pricing_norm_workspace_bytes returns the size with the full buffer. A smaller workspace (at
  * least the two-sweep size, which a too-small call names in its HM_ENOSPC message) gets a smaller buffer or none;

@@ -68,6 +68,7 @@ def lib() -> ctypes.CDLL:
         _LIB.orc_dot64.argtypes = [P, P, I64]
         _LIB.orc_l2sq_matrices.argtypes = [P, P, P, P, P, P, I64, I64, I64, D, P, P]
         _LIB.orc_norm_matrices.argtypes = [P, P, P, P, I64, I64, I64, ctypes.c_int, P, P]
+        _LIB.orc_norm_matrices64.argtypes = [P, P, P, P, I64, I64, I64, ctypes.c_int, P, P]
         _LIB.orc_topk.argtypes = [P, I64, I64, ctypes.c_int, ctypes.c_int, P, P]
         _LIB.orc_stats.argtypes = [P, P, I64, I64, P]
         _LIB.orc_sddmm_l2sq.argtypes = [P, P, P, P, P, P, I64, I64, D, P]
@@ -106,13 +107,16 @@ def l2sq_matrices(X, Y, p, q, qb, db, scale=2.0):
     return sigma, cost
 
 
-def norm_matrices(X, Y, f, g, kind: int):
+def norm_matrices(X, Y, f, g, kind: int, precision: int = 0):
+    """Norm score / cost matrices: fp32 costs (precision 0, the chunked sums) or fp64 costs (precision 1, the
+    reference's compute_precision = 1)."""
     X, Y, f, g = _f32(X), _f32(Y), _f64(f), _f64(g)
     m, d = X.shape
     n = Y.shape[0]
     sigma = np.empty((m, n), np.float64)
     cost = np.empty((m, n), np.float64)
-    lib().orc_norm_matrices(_ptr(X), _ptr(Y), _ptr(f), _ptr(g), m, n, d, int(kind), _ptr(sigma), _ptr(cost))
+    fn = lib().orc_norm_matrices64 if precision == 1 else lib().orc_norm_matrices
+    fn(_ptr(X), _ptr(Y), _ptr(f), _ptr(g), m, n, d, int(kind), _ptr(sigma), _ptr(cost))
     return sigma, cost
 
 
@@ -141,8 +145,8 @@ def l2sq_scan(X, Y, p, q, qb, db, k: int, scale=2.0):
     return rv, ri, cv, ci, stats(sigma, cost)
 
 
-def norm_scan(X, Y, f, g, k: int, kind: int):
-    sigma, cost = norm_matrices(X, Y, f, g, kind)
+def norm_scan(X, Y, f, g, k: int, kind: int, precision: int = 0):
+    sigma, cost = norm_matrices(X, Y, f, g, kind, precision)
     rv, ri = topk(sigma, k, False)
     cv, ci = topk(sigma, k, True)
     return rv, ri, cv, ci, stats(sigma, cost)

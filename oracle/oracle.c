@@ -21,6 +21,10 @@
  *                  order (pricing.cu:89-103 and cost.cu:20-77 with F=32): l1 sum|x-y|, linf max|x-y|,
  *                  l2 sqrtf(sum fmaf(z,z,.)) (nvcc contracts a+z*z, pricing.cu:65-70); the score is
  *                  (g_j - (double)c) + f_i (pricing.cu:113, matrix_selection.cuh:25).
+ *  norm cost64  -- compute_precision = 1 (generic_scan.py:166-167 -> direct_norm_fp64, cost.cu:84-104, which
+ *                  instantiates direct_norm_kernel with one chain and a double accumulator, cost.cu:10-80): each
+ *                  difference (double)x - (double)y, the features combined one after another in order (l1 sum|z|,
+ *                  linf max|z|, l2 sum z*z contracted to fma(z,z,acc) by nvcc, then sqrt); same score association.
  *  tie rule     -- better(a,b) = a.v > b.v || (a.v == b.v && a.i < b.i); -0 == +0; NaN never enters
  *                  (pricing.cu:38-51). Missing slots hold (-inf, -1).
  *  pair costs   -- fp64 norms of fp32 rows for the sparse support (norm_cost_scan_kernel.cu:233-245):
@@ -90,6 +94,30 @@ void orc_norm_matrices(const float* X, const float* Y, const double* f, const do
     for (int64_t i = 0; i < m; ++i) {
         for (int64_t j = 0; j < n; ++j) {
             const double c = (double)norm_distance(X + i * d, Y + j * d, d, kind);
+            if (sigma) sigma[i * n + j] = (g[j] - c) + f[i];
+            if (cost) cost[i * n + j] = c;
+        }
+    }
+}
+
+static double norm_distance64(const float* x, const float* y, int64_t d, int kind) {
+    double acc = 0.0;
+    for (int64_t k = 0; k < d; ++k) {
+        const double z = (double)x[k] - (double)y[k];
+        if (kind == 0) acc = acc + fabs(z);
+        else if (kind == 1) acc = fmax(acc, fabs(z));
+        else acc = fma(z, z, acc);
+    }
+    return kind == 2 ? sqrt(acc) : acc;
+}
+
+/* As orc_norm_matrices with fp64 costs (compute_precision = 1, cost.cu:84-104). */
+void orc_norm_matrices64(const float* X, const float* Y, const double* f, const double* g,
+                         int64_t m, int64_t n, int64_t d, int kind, double* sigma, double* cost) {
+    #pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < m; ++i) {
+        for (int64_t j = 0; j < n; ++j) {
+            const double c = norm_distance64(X + i * d, Y + j * d, d, kind);
             if (sigma) sigma[i * n + j] = (g[j] - c) + f[i];
             if (cost) cost[i * n + j] = c;
         }

@@ -150,7 +150,7 @@ def test_c4_norm_scan_full_shape(cuda, kind):
 
 
 @pytest.mark.parametrize("kind", ["l1", "linf"])
-def test_c4_full_solve(cuda, kind):
+def test_c4_full_solve(cuda, capsys, kind):
     """C4 solve (524288^2, d = 8, U(0.5, 1.5) masses) against an independent recomputation of HELLO's stopping rule
     over all 2.7e11 pairs: the relative l2 dual infeasibility sqrt(sum sigma+^2) / (1 + sqrt(sum c^2)) of the
     returned duals at most the 1e-6 tolerance (gpu_resident/solver.py:_refine stops on exactly this quantity),
@@ -187,9 +187,10 @@ def test_c4_full_solve(cuda, kind):
     dual_value = lb["dual_value"]
     gap = abs(r.objective - dual_value) / (1.0 + abs(r.objective) + abs(dual_value))
     certified = (r.objective - lb["best"]) / abs(r.objective)
-    _say(f"C4 solve {kind}: objective {r.objective!r} dual value {dual_value!r} infeasibility {infeasibility:.3e} "
-         f"violated pairs {int(cert[2])} max violation {cert[3]:.3e} lower bounds row {lb['row']!r} col "
-         f"{lb['col']!r} uniform {lb['uniform']!r} certified relative gap {certified:.3e}")
+    with capsys.disabled():
+        _say(f"C4 solve {kind}: objective {r.objective!r} dual value {dual_value!r} infeasibility {infeasibility:.3e} "
+             f"violated pairs {int(cert[2])} max violation {cert[3]:.3e} lower bounds row {lb['row']!r} col "
+             f"{lb['col']!r} uniform {lb['uniform']!r} certified relative gap {certified:.3e}")
     assert infeasibility <= 1e-6
     np.testing.assert_allclose(infeasibility, last.convergence.dual_feasibility, rtol=1e-6)
     assert last.dual_violation.violations_found == int(cert[2])

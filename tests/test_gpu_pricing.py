@@ -275,6 +275,63 @@ def test_norm_bidirectional_matches_oracle(cuda, kind, m, n, d, k):
     np.testing.assert_allclose(st[4].item(), ost[4], rtol=1e-7)
 
 
+@pytest.mark.parametrize("kind", [0, 1, 2])
+@pytest.mark.parametrize("m,n,d,k", [(300, 257, 8, 2), (129, 700, 3, 8), (64, 64, 40, 1), (20, 30, 100, 5),
+                                     (257, 300, 64, 32), (40, 600, 130, 2)])
+def test_norm_fp64_bidirectional_matches_oracle(cuda, kind, m, n, d, k):
+    """fp64 costs (HM_FP64, the reference's compute_precision = 1): lists bit-exact against the oracle's fp64 costs,
+    count and maximum exact, the fp64 sums to 1e-12 (their order is not fixed)."""
+    rng = np.random.default_rng(7 * m + n + d + kind)
+    X = rng.random((m, d)).astype(np.float32)
+    Y = rng.random((n, d)).astype(np.float32)
+    f = rng.normal(0.3, 0.2, m) * d ** 0.5
+    g = rng.normal(0.3, 0.2, n) * d ** 0.5
+    orv, ori, ocv, oci, ost = oracle.norm_scan(X, Y, f, g, k, kind, precision=1)
+    rv, ri, cv, ci, st = pricing_norm(*_to(cuda, X, Y, f, g), k, kind, precision="fp64")
+    np.testing.assert_array_equal(ri.cpu().numpy(), ori)
+    np.testing.assert_array_equal(ci.cpu().numpy(), oci)
+    np.testing.assert_array_equal(rv.cpu().numpy(), orv)
+    np.testing.assert_array_equal(cv.cpu().numpy(), ocv)
+    got = st.cpu().numpy()
+    np.testing.assert_allclose(got[[0, 1]], ost[[0, 1]], rtol=1e-12)
+    assert got[2] == ost[2] and got[3] == ost[3] and got[4] == ost[4]
+    # the fp64 and fp32 costs rank differently somewhere (the flag reaches the kernel)
+    _, _, _, _, ost32 = oracle.norm_scan(X, Y, f, g, k, kind)
+    assert ost32[0] != ost[0] or ost32[1] != ost[1]
+
+
+def test_norm_fp64_scan_extension_and_solve(cuda):
+    """ScanExtension's compute_precision = 1 reaches the fp64 sweep, and an l1 solve at cost_precision='fp64'
+    (fp64 scans and fp64 pair costs on every level) lands on the exact LP optimum of the fp64 costs."""
+    from scipy.optimize import linprog
+
+    from hello_ot_amd import SolverOptions, solve
+
+    rng = np.random.default_rng(64)
+    X = rng.random((90, 5)).astype(np.float32)
+    Y = rng.random((110, 5)).astype(np.float32)
+    f, g = rng.normal(0.5, 0.1, 90), rng.normal(0.5, 0.1, 110)
+    ext = ScanExtension()
+    out = ext.fused_gcost_bidir_certificate(*_to(cuda, X, Y, f, g), 2, 0, compute_precision=1)
+    orv, ori, ocv, oci, ost = oracle.norm_scan(X, Y, f, g, 2, 0, precision=1)
+    np.testing.assert_array_equal(out[0].cpu().numpy(), orv)
+    np.testing.assert_array_equal(out[3].cpu().numpy(), oci)
+    assert int(out[8]) == ost[2]
+    a, b = np.full(90, 1 / 90), np.full(110, 1 / 110)
+    r = solve(X, Y, source_mass=a, target_mass=b, cost="l1",
+              options=SolverOptions(cost_precision="fp64", coarsest_size_threshold=30, verbose="off"))
+    assert all(l.solve.summary.converged for l in r.solve_stage.levels if l.kind == "refined")
+    _, C = oracle.norm_matrices(X, Y, np.zeros(90), np.zeros(110), 0, precision=1)
+    A = np.zeros((200, 90 * 110))
+    for i in range(90):
+        A[i, i * 110:(i + 1) * 110] = 1.0
+    for j in range(110):
+        A[90 + j, j::110] = 1.0
+    exact = linprog(C.reshape(-1), A_eq=A, b_eq=np.concatenate((a, b)), bounds=(0, None), method="highs").fun
+    assert abs(r.objective - exact) <= 5e-6 * exact
+    assert r.metadata["cost_precision"] == "fp64"
+
+
 def test_norm_ties_on_a_grid(cuda):
     # integer grid points: many exactly equal l1 distances
     rng = np.random.default_rng(2)

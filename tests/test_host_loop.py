@@ -31,13 +31,15 @@ def test_options_defaults_and_validation_match_the_reference():
         SolverOptions(cost_precision=precision).check_supported()
 
 
-@pytest.mark.parametrize("cost", ["l1", "l2", "linf"])
-def test_fp64_cost_precision_is_refused_for_norm_costs(cost):
-    from hello_ot_amd.api import solve_problem
+def test_cost_precision_per_level_follows_the_reference():
+    """config.py:23-28: fp64 everywhere, or only at the finest level (index 0) for finest_fp64."""
+    from hello_ot_amd.config import level_precision
 
-    problem = Problem(np.zeros((3, 2), np.float32), np.ones((3, 2), np.float32), cost)
-    with pytest.raises(NotImplementedError, match="norm scans rank by fp32 costs"):
-        solve_problem(problem, SolverOptions(cost_precision="fp64"))
+    assert [level_precision("fp32", i) for i in range(3)] == ["fp32"] * 3
+    assert [level_precision("fp64", i) for i in range(3)] == ["fp64"] * 3
+    assert [level_precision("finest_fp64", i) for i in range(3)] == ["fp64", "fp32", "fp32"]
+    with pytest.raises(ValueError, match="cost_precision must be one of"):
+        level_precision("fp16", 0)
 
 
 def test_problem_validation():

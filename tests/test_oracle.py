@@ -201,6 +201,65 @@ def test_norm_chunked_fp32_accumulation_is_pinned():
     assert c[0, 0] == 2.0**24 + 32
 
 
+@pytest.mark.parametrize("kind,name", [(0, "l1"), (1, "linf"), (2, "l2")])
+def test_norm_fp64_costs_kat_and_closed_forms(kind, name):
+    """fp64 costs (compute_precision = 1): the reference KAT (tests/torch_scan_test.py:61-96), exact for l1 / linf
+    (every difference and partial sum is exact there); and on random data linf exactly the numpy maximum (no rounding
+    at all), l1 / l2 within 2 fp64 units per feature of the exactly rounded value (math.fsum)."""
+    source = np.array([[0.0, 0.0], [1.0, 0.5], [2.0, -1.0]])
+    target = np.array([[0.25, 0.0], [1.5, 0.25]])
+    diff = source[:, None, :] - target[None, :, :]
+    dense = {"l1": np.abs(diff).sum(2), "linf": np.abs(diff).max(2), "l2": np.linalg.norm(diff, axis=2)}[name]
+    _, cost = oracle.norm_matrices(source, target, np.zeros(3), np.zeros(2), kind, precision=1)
+    np.testing.assert_allclose(cost, dense, rtol=0 if kind < 2 else 1e-15, atol=0)
+    rng = np.random.default_rng(70 + kind)
+    X = rng.standard_normal((9, 37)).astype(np.float32)
+    Y = rng.standard_normal((11, 37)).astype(np.float32)
+    f, g = rng.standard_normal(9), rng.standard_normal(11)
+    sigma, cost = oracle.norm_matrices(X, Y, f, g, kind, precision=1)
+    z = X.astype(np.float64)[:, None, :] - Y.astype(np.float64)[None, :, :]
+    if kind == 1:
+        np.testing.assert_array_equal(cost, np.abs(z).max(2))
+    else:
+        terms = np.abs(z) if kind == 0 else z * z
+        exact = np.array([[math.fsum(t) for t in row] for row in terms])
+        exact = exact if kind == 0 else np.sqrt(exact)
+        np.testing.assert_allclose(cost, exact, rtol=2 * 37 * 2.0**-53, atol=0)
+    np.testing.assert_array_equal(sigma, (g[None, :] - cost) + f[:, None])
+
+
+def test_norm_fp64_order_and_contraction_are_pinned():
+    """The fp64 l1 cost is the left-to-right sum (a sequential prefix sum gives the same bits; fp32 or chunked sums
+    do not), and the l2 cost accumulates fma(z, z, acc) with one rounding per feature (emulated exactly with
+    rationals), which differs from a separate multiply and add on these inputs."""
+    from fractions import Fraction
+
+    rng = np.random.default_rng(11)
+    X = rng.standard_normal((6, 45)).astype(np.float32)
+    Y = rng.standard_normal((7, 45)).astype(np.float32)
+    _, c1 = oracle.norm_matrices(X, Y, np.zeros(6), np.zeros(7), 0, precision=1)
+    z = X.astype(np.float64)[:, None, :] - Y.astype(np.float64)[None, :, :]
+    np.testing.assert_array_equal(c1, np.cumsum(np.abs(z), axis=2)[:, :, -1])
+    # fp64 sums of fp32 differences are mostly exact; a huge first feature makes the order visible: left to right
+    # every later 16 is absorbed by 2^60 (half its ulp is 128), while summing the 44 sixteens first keeps 704
+    x = np.zeros((1, 45), np.float32)
+    x[0, 0], x[0, 1:] = 2.0**60, 16.0
+    _, c = oracle.norm_matrices(x, np.zeros((1, 45), np.float32), np.zeros(1), np.zeros(1), 0, precision=1)
+    assert c[0, 0] == 2.0**60 != 2.0**60 + 768.0 == float(np.float64(2.0**60) + np.float64(704.0))
+    _, c2 = oracle.norm_matrices(X, Y, np.zeros(6), np.zeros(7), 2, precision=1)
+    fused = np.empty((6, 7))
+    plain = np.empty((6, 7))
+    for i in range(6):
+        for j in range(7):
+            acc = sep = 0.0
+            for t in z[i, j]:
+                acc = float(Fraction(acc) + Fraction(float(t)) * Fraction(float(t)))
+                sep = sep + float(t) * float(t)
+            fused[i, j], plain[i, j] = math.sqrt(acc), math.sqrt(sep)
+    np.testing.assert_array_equal(c2, fused)
+    assert (fused != plain).any()
+
+
 # ----------------------------------------------------------------------------------------------------
 # SDDMM and pair costs
 # ----------------------------------------------------------------------------------------------------
