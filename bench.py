@@ -163,6 +163,21 @@ def gmm(rows, d, seed, dev, means_seed, chunk=32768):
     return out
 
 
+def gmm_host(rows, d, seed, dev, means_seed, chunk=32768):
+    """The same rows as gmm(...) (same generator stream), generated chunk by chunk on the device and kept in host
+    memory: the device never holds the whole side."""
+    g = torch.Generator(device=dev)
+    g.manual_seed(means_seed)
+    means = 2.0 * torch.randn(64, d, generator=g, device=dev)
+    g.manual_seed(seed)
+    out = torch.empty(rows, d, dtype=torch.float32)
+    for s in range(0, rows, chunk):
+        e = min(rows, s + chunk)
+        lab = torch.randint(0, 64, (e - s,), generator=g, device=dev)
+        out[s:e].copy_(torch.randn(e - s, d, generator=g, device=dev) + means[lab])
+    return out
+
+
 def sqnorms(x, chunk=65536):
     out = torch.empty(x.shape[0], dtype=torch.float64, device=x.device)
     for s in range(0, x.shape[0], chunk):
@@ -589,22 +604,36 @@ def bench_solves(dev):
     return out
 
 
-def bench_c5_solve(dev, rows):
+def bench_c5_solve(dev, rows, stream="auto"):
     """C5 full solve: rows x 8192 fp32 on each side from independent 64-component Gaussian mixtures (means
     ~ N(0, 4I), identity covariance, equal weights), uniform masses, squared-Euclidean cost, default options,
-    tolerance 1e-6. The solver reorders the generated features in place (consume_input_features) so only one
-    shuffled copy of each side is resident."""
-    from hello_ot_amd import SolverOptions, solve
+    tolerance 1e-6; the sides are reordered in place (consume_input_features).
 
-    log(f"[bench] C5 solve: generating {rows} x {C5_D} per side ({2 * rows * C5_D * 4 / 2**30:.1f} GiB) ...")
-    X = gmm(rows, C5_D, seed=1, dev=dev, means_seed=11)
+    ``stream``: "auto" hands both sides over on the device and lets the solver's memory planner choose (at C5 on
+    one MI355X both sides stay resident); "always" hands the source side over in host memory and streams it, which
+    bounds the device memory (the reference's non-resident path and its 41.6 GiB figure)."""
+    from hello_ot_amd import SolverOptions, solve
+    from hello_ot_amd.resident import host as host_module
+
+    log(f"[bench] C5 solve ({stream}): generating {rows} x {C5_D} per side "
+        f"({2 * rows * C5_D * 4 / 2**30:.1f} GiB) ...")
+    X = gmm_host(rows, C5_D, seed=1, dev=dev, means_seed=11) if stream == "always" else \
+        gmm(rows, C5_D, seed=1, dev=dev, means_seed=11)
     Y = gmm(rows, C5_D, seed=2, dev=dev, means_seed=12)
     sync()
-    log("[bench] C5 solve: solving ...")
-    r = solve(X, Y, options=SolverOptions(verbose="detailed", consume_input_features=True))
+    torch.cuda.empty_cache()
+    log(f"[bench] C5 solve ({stream}): solving ...")
+    policy = host_module.STREAM_POLICY
+    host_module.STREAM_POLICY = stream
+    try:
+        r = solve(X, Y, options=SolverOptions(verbose="detailed", consume_input_features=True))
+    finally:
+        host_module.STREAM_POLICY = policy
     del X, Y
+    torch.cuda.empty_cache()
     finest = r.solve_stage.levels[-1].solve.summary
     return {"rows": rows, "d": C5_D, "seconds": r.total_wall_time, "objective": r.objective,
+            "streamed_source": bool(r.metadata["streamed_source"]),
             "converged": bool(finest.converged),
             "final_dual_infeasibility": r.solve_stage.levels[-1].solve.iterations[-1].convergence.dual_feasibility,
             "peak_gpu_memory_gib": r.peak_gpu_memory_mib / 1024.0,
@@ -640,6 +669,9 @@ def main():
     ap.add_argument("--c5-solve", type=int, default=0, metavar="ROWS",
                     help="instead of the default run, solve the C5 instance with ROWS points per side "
                          "(1280000 = the full instance) and print its JSON line")
+    ap.add_argument("--stream", default="auto", choices=("auto", "always", "never"),
+                    help="with --c5-solve: where the source side lives (auto: the solver's memory planner; always: "
+                         "host memory, streamed; never: on the device)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -674,7 +706,7 @@ def main():
         return
     if args.c5_solve:
         print(json.dumps({"metric": "C5 solve seconds to relative dual infeasibility 1e-6 (l2^2, d=8192)",
-                          **bench_c5_solve(dev, args.c5_solve)}), flush=True)
+                          **bench_c5_solve(dev, args.c5_solve, stream=args.stream)}), flush=True)
         return
     from hello_ot_amd.kernels.generic_scan import sweep_precision
 
@@ -714,10 +746,11 @@ def main():
     if not args.no_cpu_baseline:
         log("[bench] CPU baseline ...")
         cpu = cpu_baseline_c5(dev)
-    solve_c5 = None
+    solve_c5 = solve_c5_streamed = None
     if not args.no_c5_solve:
         torch.cuda.empty_cache()
         solve_c5 = bench_c5_solve(dev, C5_N)
+        solve_c5_streamed = bench_c5_solve(dev, C5_N, stream="always")
     line = {
         "metric": "pricing pairs/s (l2^2 bidirectional scan + certificate, m=n=1.28M d=8192)",
         "value": pairs / sec,
@@ -736,7 +769,7 @@ def main():
                    "d": C5_D, "k": 2},
         "roofline": roofline(precision, achieved),
         "cpu_baseline": cpu,
-        "solve_seconds": {"c5": solve_c5},
+        "solve_seconds": {"c5": solve_c5, "c5_streamed_source": solve_c5_streamed},
         "detail": info,
         "extras": extras,
     }

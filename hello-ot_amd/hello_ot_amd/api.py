@@ -6,6 +6,7 @@ solve runs on ``cuda:0`` (or the device of CUDA input tensors) and returns a dev
 """
 from __future__ import annotations
 
+import os
 import sys
 import time
 from typing import Any, Optional
@@ -16,6 +17,8 @@ import torch
 from ._native_compat import require_native_runtime_compatibility
 from .config import SolverOptions, level_precision
 from .resident.cost import Cost
+from .resident import host as _host
+from .resident.host import HostRows, permute_rows_inplace, shuffled_rows
 from .resident.leaf import solve_coarsest
 from .resident.solver import level_sizes, refine_level, shuffle_once_permutation
 from .resident.support import balanced_masses
@@ -56,15 +59,45 @@ def _to_device(value, device, dtype):
     return torch.as_tensor(np.asarray(value), dtype=dtype, device=device)
 
 
-def _shuffled_features(value, perm, device, consume: bool):
+def _shuffled_features(value, perm, device, consume: bool, bounded: bool = False):
     """Rows of ``value`` in shuffle order as contiguous fp32 on ``device``. With ``consume`` a contiguous fp32
     tensor already on the device is reordered in place (the caller's tensor then holds the shuffled rows), like the
-    reference's in-place feature reorder (prewarm.py:177-214): only one temporary copy is alive at a time."""
+    reference's in-place feature reorder (prewarm.py:177-214): through one full temporary, or, with ``bounded`` (a
+    memory-bounded solve) or when the device has no room for the temporary, with one chunk of extra device memory
+    (``permute_rows_inplace``, a host round trip: about 4 s for 39 GiB)."""
     if consume and torch.is_tensor(value) and value.device == device and value.dtype == torch.float32 \
             and value.is_contiguous():
+        nbytes = 4 * value.numel()
+        if nbytes > _host.STREAM_MIN_BYTES and (bounded or torch.cuda.mem_get_info(device)[0] < nbytes + (4 << 30)):
+            return permute_rows_inplace(value, perm)
         value.copy_(value[perm])
         return value
     return _to_device(value, device, torch.float32)[perm].contiguous()
+
+
+def _stream_source(value, target, cost_type: str, device, options: SolverOptions) -> bool:
+    """Whether the source side stays in host memory and is streamed in chunks (the reference's non-resident path:
+    kernels/bilinear_topk.py:255-368). ``gpu_resident=True`` keeps both sides on the device. Otherwise a source side
+    of more than STREAM_MIN_BYTES of fp32 features is streamed when the resident plan would take more than
+    RESIDENT_BUDGET of the device's memory (``STREAM_POLICY`` / HELLOOT_STREAM_SOURCE can force either way), which
+    leaves the device one side's features plus bounded chunk staging. A streamed side is copied once into host
+    memory in the shuffled order (``consume_input_features`` then applies to the target side only)."""
+    if options.gpu_resident:
+        return False
+    rows, d = (int(s) for s in value.shape)
+    if 4 * rows * d <= _host.STREAM_MIN_BYTES:
+        return False
+    policy = os.environ.get("HELLOOT_STREAM_SOURCE", _host.STREAM_POLICY)
+    if policy not in ("auto", "always", "never"):
+        raise ValueError("HELLOOT_STREAM_SOURCE must be one of: auto, always, never")
+    if policy != "auto":
+        return policy == "always"
+    # the resident plan: both fp32 sides, the l2^2 sweep's int8 copy of the larger side, the scan's list budget
+    # (12 GiB) and the LP / support state
+    other = int(target.shape[0])
+    need = 4 * (rows + other) * d + (2 * max(rows, other) * d if cost_type == "l2^2" else 0) + (16 << 30)
+    total = torch.cuda.get_device_properties(device).total_memory
+    return need > _host.RESIDENT_BUDGET * total
 
 
 @torch.no_grad()
@@ -88,8 +121,11 @@ def solve_problem(problem: Problem, options: SolverOptions, *, max_iterations: i
         b = (torch.full((m,), 1.0 / m, dtype=torch.float64, device=device) if problem.target_mass is None
              else _to_device(problem.target_mass, device, torch.float64))[ti]
         consume = bool(options.consume_input_features)
-        x = _shuffled_features(problem.source_points, si, device, consume)
-        y = _shuffled_features(problem.target_points, ti, device, consume)
+        if _stream_source(problem.source_points, problem.target_points, problem.cost_type, device, options):
+            x = HostRows(shuffled_rows(problem.source_points, si), device)
+        else:
+            x = _shuffled_features(problem.source_points, si, device, consume)
+        y = _shuffled_features(problem.target_points, ti, device, consume, bounded=isinstance(x, HostRows))
         full = Cost.create(x, y, problem.cost_type)
         sizes = level_sizes(n, m, options.coarsest_size_threshold, options.split_count)
         levels, previous, triggers = [], None, []
@@ -123,7 +159,8 @@ def solve_problem(problem: Problem, options: SolverOptions, *, max_iterations: i
         peak = torch.cuda.max_memory_allocated(device) / 2**20
     stage = SolveStageResult(tuple(levels), wall)
     metadata = {
-        "gpu_resident": True, "backend": "native", "device": str(device), "cost_type": problem.cost_type,
+        "gpu_resident": not isinstance(x, HostRows), "streamed_source": isinstance(x, HostRows),
+        "backend": "native", "device": str(device), "cost_type": problem.cost_type,
         "cost_precision": options.cost_precision, "stopping_norm": options.stopping_norm,
         "coarsest_solver": "mi355x_network_simplex", "lp_solver": "mi355x_halpern_pdhg",
         "hierarchy_sizes": [list(s) for s in sizes],

@@ -4,6 +4,13 @@ The role of ``gpu_resident/cost.py:9-161`` in the reference: one object holding 
 source / target features, the l2^2 offsets p = ||x||^2, q = ||y||^2, prefix slicing per hierarchy level,
 pair costs on the active support and the pricing / directional scans. Every evaluation runs in the HIP
 library (``hm_pricing_l2sq``, ``hm_pricing_norm``, ``hm_pair_costs_*``); nothing falls back to PyTorch math.
+
+The source side may be streamed (``HostRows``: pinned host memory, read in row chunks), as in the reference's
+resident / streamed scan (``kernels/bilinear_topk.py:255-368``): the target side stays on the device, each source
+chunk is priced against it (l2^2: against its sweep copy, prepared once per scan), row lists are written per chunk,
+column lists are merged across chunks in exact fp64 with the lowest row index first among equal values, and the
+certificate sums add up (its maxima take the maximum). Pair costs are evaluated chunk by chunk over the pairs sorted
+by source row. The results are the same as with both sides on the device.
 """
 from __future__ import annotations
 
@@ -12,24 +19,62 @@ from dataclasses import dataclass, replace
 import torch
 
 from ..costs.pairs import lowrank_pair_costs, norm_pair_costs
-from ..kernels.generic_scan import pricing_l2sq, pricing_norm
+from ..kernels.generic_scan import ResidentSide, pricing_l2sq, pricing_norm
+from . import host as _host
+from .host import HostRows
 
 NORM_KINDS = {"l1": 0, "linf": 1, "l2": 2}
 
 
-def offsets(features: torch.Tensor) -> torch.Tensor:
-    """fp64 squared row norms, in bounded chunks (gpu_resident/cost.py:91-101)."""
+def _sq_rows(part: torch.Tensor) -> torch.Tensor:
+    part = part.double()
+    return (part * part).sum(-1)
+
+
+def offsets(features) -> torch.Tensor:
+    """fp64 squared row norms, in bounded chunks (gpu_resident/cost.py:91-101); a streamed side is read once."""
+    if isinstance(features, HostRows):
+        out = torch.empty(len(features), device=features.device, dtype=torch.float64)
+        block = max(1, (64 << 20) // (8 * features.d))
+        for s, e, x in features.chunks():
+            for b in range(0, e - s, block):
+                part = x[b:b + block]
+                out[s + b:s + b + len(part)] = _sq_rows(part)
+        return out
     out = torch.empty(len(features), device=features.device, dtype=torch.float64)
     block = max(1, (64 << 20) // (8 * features.shape[1]))
     for start in range(0, len(features), block):
-        part = features[start:start + block].double()
-        out[start:start + len(part)] = (part * part).sum(-1)
+        out[start:start + block] = _sq_rows(features[start:start + block])
     return out
+
+
+def merge_columns(best, new, k: int):
+    """Best k per column of two exact lists, each sorted (values descending, equal values by row index) and ``best``
+    holding only lower row indices than ``new``: the merged order puts ``best``'s entry first among equal values,
+    which is the lowest row index. Each entry's merged rank is its own position plus the entries of the other list
+    ahead of it (strictly greater values from ``new``, greater or equal ones from ``best``), found by binary search
+    in the other row; the entries of rank below k are scattered to their ranks."""
+    if best is None:
+        return new
+    av, ai = best
+    bv, bi = new
+    pos = torch.arange(av.shape[1], device=av.device).expand_as(av)
+    na, nb = (-av).contiguous(), (-bv).contiguous()          # ascending rows for the binary searches
+    rank_a = pos + torch.searchsorted(nb, na, right=False)   # entries of `new` strictly greater
+    rank_b = pos[:, : bv.shape[1]] + torch.searchsorted(na, nb, right=True)   # entries of `best` greater or equal
+    out_v = torch.empty((av.shape[0], k), dtype=av.dtype, device=av.device)
+    out_i = torch.empty((av.shape[0], k), dtype=ai.dtype, device=av.device)
+    for rank, v, i in ((rank_a, av, ai), (rank_b, bv, bi)):
+        keep = rank < k
+        rows = torch.nonzero(keep, as_tuple=True)[0]
+        out_v[rows, rank[keep]] = v[keep]
+        out_i[rows, rank[keep]] = i[keep]
+    return out_v, out_i
 
 
 @dataclass
 class Cost:
-    source: torch.Tensor
+    source: object                 # device fp32 tensor, or HostRows (streamed)
     target: torch.Tensor
     kind: str
     source_offset: torch.Tensor | None = None
@@ -37,7 +82,7 @@ class Cost:
     precision: str = "fp32"   # cost arithmetic of the norm costs: "fp32" or "fp64" (l2^2 is fp64-exact in both)
 
     @classmethod
-    def create(cls, source: torch.Tensor, target: torch.Tensor, kind: str) -> "Cost":
+    def create(cls, source, target: torch.Tensor, kind: str) -> "Cost":
         if kind == "l2^2":
             return cls(source, target, kind, offsets(source), offsets(target))
         if kind not in NORM_KINDS:
@@ -46,8 +91,11 @@ class Cost:
 
     def sliced(self, n: int, m: int, precision: str = "fp32") -> "Cost":
         """The first n source and m target points: a hierarchy level after the global shuffle, with that level's
-        cost precision (gpu_resident/cost.py:31-37)."""
-        return replace(self, source=self.source[:n], target=self.target[:m],
+        cost precision (gpu_resident/cost.py:31-37). A streamed source prefix small enough is copied to the device."""
+        source = self.source[:n] if torch.is_tensor(self.source) else self.source.prefix(n)
+        if isinstance(source, HostRows) and source.nbytes() <= _host.STREAM_MIN_BYTES:
+            source = source.to_device()
+        return replace(self, source=source, target=self.target[:m],
                        source_offset=None if self.source_offset is None else self.source_offset[:n],
                        target_offset=None if self.target_offset is None else self.target_offset[:m],
                        precision=precision)
@@ -56,12 +104,35 @@ class Cost:
     def shape(self):
         return len(self.source), len(self.target)
 
+    @property
+    def streamed(self) -> bool:
+        return isinstance(self.source, HostRows)
+
+    def _pairs_with(self, x, p, rows, cols):
+        if self.kind == "l2^2":
+            return lowrank_pair_costs(x, self.target, p, self.target_offset, rows, cols)
+        return norm_pair_costs(x, self.target, rows, cols, NORM_KINDS[self.kind], precision=self.precision)
+
     def pairs(self, rows: torch.Tensor, cols: torch.Tensor) -> torch.Tensor:
         """fp64 costs of (rows[e], cols[e]): exact p + q - 2<x, y> for l2^2; for the norms the pricing scan's fp32
         cost, or at fp64 precision the fp64 norm of the reference's pair-cost kernel (costs/metric.py:94-118)."""
-        if self.kind == "l2^2":
-            return lowrank_pair_costs(self.source, self.target, self.source_offset, self.target_offset, rows, cols)
-        return norm_pair_costs(self.source, self.target, rows, cols, NORM_KINDS[self.kind], precision=self.precision)
+        if not self.streamed:
+            return self._pairs_with(self.source, self.source_offset, rows, cols)
+        rows, cols = rows.reshape(-1).long(), cols.reshape(-1).long()
+        out = torch.empty(rows.numel(), dtype=torch.float64, device=self.target.device)
+        if rows.numel() == 0:
+            return out
+        order = torch.argsort(rows, stable=True)
+        rs, cs = rows[order], cols[order]
+        starts = torch.arange(0, len(self.source), self.source.chunk, device=rows.device)
+        edges = torch.searchsorted(rs, torch.cat((starts, starts.new_tensor([len(self.source)])))).tolist()
+        for index, (s, e, x) in enumerate(self.source.chunks()):
+            a, b = edges[index], edges[index + 1]
+            if a == b:
+                continue
+            p = None if self.source_offset is None else self.source_offset[s:e]
+            out[order[a:b]] = self._pairs_with(x, p, rs[a:b] - s, cs[a:b])
+        return out
 
     def scan(self, dual: torch.Tensor, k: int, *, certificate: bool = False, direction: str | None = None):
         """Pricing / directional scans in the reference's output convention (gpu_resident/cost.py:104-161):
@@ -83,7 +154,9 @@ class Cost:
             g = torch.zeros_like(g)
         rows = direction in (None, "source")
         cols = direction in (None, "target")
-        if self.kind == "l2^2":
+        if self.streamed:
+            rv, ri, cv, ci, st = self._scan_streamed(f, g, k, rows, cols, certificate)
+        elif self.kind == "l2^2":
             p, q = self.source_offset, self.target_offset
             rv, ri, cv, ci, st = pricing_l2sq(self.source, self.target, p, q, f - p, g - q, k, rows=rows, cols=cols,
                                               stats=certificate, linf=certificate)
@@ -102,5 +175,38 @@ class Cost:
                        "count": int(round(count))}
         return rv[:, :kr] - f[:, None], ri[:, :kr], cv[:, :kc] - g[:, None], ci[:, :kc], metrics
 
+    def _scan_streamed(self, f, g, k, rows, cols, certificate):
+        """The scan with the source side streamed in chunks against the device-resident target side."""
+        n, m = self.shape
+        dev = self.target.device
+        rv = torch.empty((n, k), dtype=torch.float64, device=dev) if rows else None
+        ri = torch.empty((n, k), dtype=torch.int32, device=dev) if rows else None
+        st = torch.zeros(5, dtype=torch.float64, device=dev) if certificate else None
+        best = None
+        l2sq = self.kind == "l2^2"
+        side = ResidentSide(self.target) if l2sq else None   # the target's sweep copy, for this scan only
+        if l2sq:
+            p, q = self.source_offset, self.target_offset
+            db = g - q
+        for s, e, x in self.source.chunks():
+            if l2sq:
+                # a chunk is short against the target side: its column lists come cheapest from the row sweep
+                # (columns fused into it), so a columns-only scan asks for the chunk's rows as well
+                out = pricing_l2sq(x, self.target, p[s:e], q, f[s:e] - p[s:e], db, k, rows=rows or cols, cols=cols,
+                                   stats=certificate, linf=certificate, resident=side)
+            else:
+                out = pricing_norm(x, self.target, f[s:e], g, k, NORM_KINDS[self.kind], rows=rows, cols=cols,
+                                   stats=certificate, linf=certificate, precision=self.precision)
+            if rows:
+                rv[s:e], ri[s:e] = out[0], out[1]
+            if cols:
+                shifted = torch.where(out[3] >= 0, out[3] + s, out[3])
+                best = merge_columns(best, (out[2], shifted), k)
+            if certificate:
+                st[:3] += out[4][:3]
+                st[3:] = torch.maximum(st[3:], out[4][3:])
+        cv, ci = best if cols else (None, None)
+        return rv, ri, cv, ci, st
 
-__all__ = ["Cost", "NORM_KINDS", "offsets"]
+
+__all__ = ["Cost", "NORM_KINDS", "merge_columns", "offsets"]

@@ -1,0 +1,141 @@
+"""One side of the problem kept in host memory and streamed to the device in row chunks.
+
+This is the reference's resident / streamed split (``kernels/bilinear_topk.py:99-118, 255-368``,
+``kernels/scan_contract.py:113-253``): one side stays on the device, the other is read in bounded chunks, so the
+device holds one side's features plus O(chunk * d) of staging instead of both sides. Here the streamed side's rows
+live in one host tensor (already in the solver's shuffled order) and pass through two pinned staging buffers of one
+chunk each (bounded pinned memory, as in the reference): the host copies chunk c into a staging buffer once that
+buffer's previous upload has finished, a side stream of default priority uploads it into one of two device buffers
+once the work queued on that buffer's previous chunk has finished, and the caller's stream waits for the upload.
+Uploads and host copies run one chunk ahead of the caller's work.
+"""
+from __future__ import annotations
+
+import torch
+
+# fp32 features per streamed chunk: 19968 rows at d = 8192, the internal chunk the l2^2 scan itself takes for
+# 1.28M columns (78 panels of 256 rows, whose column lists of k = 16 fill its 12 GiB list budget), so a streamed scan
+# finalizes its columns as often as a one-call scan
+STREAM_CHUNK_BYTES = 78 * 256 * 8192 * 4
+STREAM_MIN_BYTES = 4 << 30       # a side (or a level's prefix of it) smaller than this is copied to the device whole
+# Where the source side lives when the caller does not ask for both sides on the device: "auto" streams it when the
+# resident plan would need more than RESIDENT_BUDGET of the device's memory, "always" streams every source side
+# above STREAM_MIN_BYTES, "never" keeps it resident. The environment variable HELLOOT_STREAM_SOURCE overrides it.
+STREAM_POLICY = "auto"
+RESIDENT_BUDGET = 0.75
+
+
+class HostRows:
+    """Rows [0, rows) of a host fp32 matrix, read by the device in chunks of at most ``chunk`` rows."""
+
+    def __init__(self, host: torch.Tensor, device, chunk_rows: int | None = None):
+        if host.device.type != "cpu" or host.dtype != torch.float32 or host.ndim != 2 or not host.is_contiguous():
+            raise ValueError("streamed rows must be a contiguous fp32 host matrix")
+        self.host = host
+        self.device = torch.device(device)
+        self.rows, self.d = int(host.shape[0]), int(host.shape[1])
+        self.chunk = int(chunk_rows) if chunk_rows else max(1, STREAM_CHUNK_BYTES // (4 * max(1, self.d)))
+        self._copy = None
+
+    @property
+    def shape(self):
+        return (self.rows, self.d)
+
+    def __len__(self) -> int:
+        return self.rows
+
+    def nbytes(self) -> int:
+        return 4 * self.rows * self.d
+
+    def prefix(self, rows: int) -> "HostRows":
+        return HostRows(self.host[: int(rows)], self.device, self.chunk)
+
+    def to_device(self) -> torch.Tensor:
+        return self.host.to(self.device)
+
+    def chunks(self, start: int = 0, stop: int | None = None):
+        """Yields (s, e, x): x holds rows [s, e) on the device, valid on the current stream until the next step."""
+        stop = self.rows if stop is None else int(stop)
+        if stop <= start:
+            return
+        compute = torch.cuda.current_stream(self.device)
+        if self._copy is None:
+            self._copy = torch.cuda.Stream(self.device)
+        copy = self._copy
+        rows = min(self.chunk, stop - start)
+        staging = [torch.empty((rows, self.d), dtype=torch.float32, pin_memory=True) for _ in range(2)]
+        buffers = [torch.empty((rows, self.d), dtype=torch.float32, device=self.device) for _ in range(2)]
+        uploaded = [torch.cuda.Event(), torch.cuda.Event()]   # staging slot free again / device slot filled
+        released = [torch.cuda.Event(), torch.cuda.Event()]   # the caller's work on the device slot is queued before
+        used = [False, False]
+        bounds = [(s, min(stop, s + rows)) for s in range(start, stop, rows)]
+        copy.wait_stream(compute)   # the device buffers were allocated on the caller's stream
+
+        def issue(index):
+            slot = index % 2
+            s, e = bounds[index]
+            if used[slot]:
+                uploaded[slot].synchronize()     # the staging buffer's previous upload has finished
+            staging[slot][: e - s].copy_(self.host[s:e])
+            with torch.cuda.stream(copy):
+                if used[slot]:
+                    copy.wait_event(released[slot])
+                buffers[slot][: e - s].copy_(staging[slot][: e - s], non_blocking=True)
+                uploaded[slot].record(copy)
+
+        try:
+            issue(0)
+            for index, (s, e) in enumerate(bounds):
+                if index + 1 < len(bounds):
+                    issue(index + 1)
+                slot = index % 2
+                compute.wait_event(uploaded[slot])
+                yield s, e, buffers[slot][: e - s]
+                released[slot].record(compute)
+                used[slot] = True
+        finally:
+            # later work on the caller's stream (including reuse of the buffers' memory) follows every upload, and
+            # the staging buffers are not released while an upload still reads them
+            compute.wait_stream(copy)
+            copy.synchronize()
+
+
+def permute_rows_inplace(value: torch.Tensor, perm: torch.Tensor) -> torch.Tensor:
+    """value[i] = (old value)[perm[i]] for a contiguous device matrix, with one chunk of extra device memory instead
+    of a full copy: the rows are gathered chunk by chunk in the new order on the device and parked in host memory
+    (through a pinned staging buffer), then written back in order. The role of the reference's in-place reorder of
+    consumed inputs (hierarchy/plan.py:13-38), whose temporary is one row."""
+    rows, d = int(value.shape[0]), int(value.shape[1])
+    block = max(1, STREAM_CHUNK_BYTES // (value.element_size() * max(1, d)))
+    park = torch.empty((rows, d), dtype=value.dtype)
+    staging = torch.empty((min(block, rows), d), dtype=value.dtype, pin_memory=True)
+    perm_dev = perm.to(value.device)
+    for s in range(0, rows, block):
+        e = min(rows, s + block)
+        staging[: e - s].copy_(value[perm_dev[s:e]])          # device gather, then a synchronous download
+        park[s:e].copy_(staging[: e - s])
+    for s in range(0, rows, block):
+        e = min(rows, s + block)
+        staging[: e - s].copy_(park[s:e])
+        value[s:e].copy_(staging[: e - s])                    # synchronous upload (the staging buffer is reused)
+    return value
+
+
+def shuffled_rows(value, perm: torch.Tensor) -> torch.Tensor:
+    """The rows of ``value`` (host or device, any float dtype) in the order ``perm``, as a new fp32 host matrix,
+    gathered in bounded row blocks."""
+    rows, d = int(value.shape[0]), int(value.shape[1])
+    out = torch.empty((rows, d), dtype=torch.float32)
+    if torch.is_tensor(value) and value.is_cuda:
+        block = max(1, STREAM_CHUNK_BYTES // (4 * max(1, d)))
+        perm_dev = perm.to(value.device)
+        for s in range(0, rows, block):
+            e = min(rows, s + block)
+            out[s:e].copy_(value[perm_dev[s:e]].to(torch.float32))
+        return out
+    host = value if torch.is_tensor(value) else torch.as_tensor(value)
+    torch.index_select(host.to(torch.float32), 0, perm.detach().to("cpu", torch.int64), out=out)
+    return out
+
+
+__all__ = ["HostRows", "STREAM_CHUNK_BYTES", "STREAM_MIN_BYTES", "shuffled_rows"]

@@ -83,8 +83,10 @@ def candidate_keys(row_values, row_index, col_values, col_index, dual, n, m, pos
 
 
 def _progress(options, message: str) -> None:
+    """A progress line (verbose="detailed"), with the peak device memory of the solve so far."""
     if options.verbose == "detailed":
-        print(f"[hello-mi355x] {message}", file=sys.stderr, flush=True)
+        peak = torch.cuda.max_memory_allocated() / 2**30
+        print(f"[hello-mi355x] {message} peak={peak:.1f}GiB", file=sys.stderr, flush=True)
 
 
 class _Stopwatch:
