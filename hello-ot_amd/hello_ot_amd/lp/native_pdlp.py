@@ -24,6 +24,30 @@ def _as_1d(value: Any, *, dtype: torch.dtype, device: torch.device) -> torch.Ten
     return torch.as_tensor(np.asarray(value), device=device, dtype=dtype).contiguous().view(-1)
 
 
+def run_pdhg(rows_t, cols_t, costs_t, source_t, target_t, x0, y0, *, evaluation_frequency: int, rescale: bool,
+             iteration_limit: int, objective_tolerance: float, primal_tolerance: float, dual_tolerance: float,
+             time_limit_seconds: float, device: torch.device):
+    """One ``hm_pdhg_solve`` call on validated device tensors (int64 endpoints, fp64 costs / masses / warm starts
+    or None): returns (x, y, PdhgResult)."""
+    n_source, n_target, e = int(source_t.numel()), int(target_t.numel()), int(costs_t.numel())
+    masses_t = torch.cat((source_t, target_t))
+    x_out = torch.empty(e, dtype=torch.float64, device=device)
+    y_out = torch.empty(n_source + n_target, dtype=torch.float64, device=device)
+    lib = _lib.load()
+    ws = torch.empty(max(int(lib.hm_pdhg_workspace_bytes(n_source, n_target, e)), 256), dtype=torch.uint8,
+                     device=device)
+    params = _lib.PdhgParams(int(evaluation_frequency), int(bool(rescale)), int(iteration_limit),
+                             float(objective_tolerance), float(primal_tolerance), float(dual_tolerance),
+                             float(time_limit_seconds))
+    res = _lib.PdhgResult()
+    with torch.cuda.device(device):
+        rc = lib.hm_pdhg_solve(_lib.stream_handle(device), _lib.ptr(rows_t), _lib.ptr(cols_t), _lib.ptr(costs_t),
+                               _lib.ptr(masses_t), _lib.ptr(x0), _lib.ptr(y0), n_source, n_target, e, params,
+                               _lib.ptr(x_out), _lib.ptr(y_out), res, _lib.ptr(ws), ws.numel())
+    _lib.check(rc, "hm_pdhg_solve")
+    return x_out, y_out, res
+
+
 class NativeRestrictedOTPDLP:
     """FP64 Halpern-PDHG restricted OT solver for HELLO active supports, on MI355X."""
 
@@ -93,19 +117,11 @@ class NativeRestrictedOTPDLP:
         y0 = None if warm_start_dual is None else _as_1d(warm_start_dual, dtype=torch.float64, device=dev)
         if (x0 is not None and x0.numel() != e) or (y0 is not None and y0.numel() != n_source + n_target):
             raise ValueError("warm-start dimensions do not match the restricted OT problem")
-        x_out = torch.empty(e, dtype=torch.float64, device=dev)
-        y_out = torch.empty(n_source + n_target, dtype=torch.float64, device=dev)
-        lib = _lib.load()
-        ws = torch.empty(max(int(lib.hm_pdhg_workspace_bytes(n_source, n_target, e)), 256), dtype=torch.uint8,
-                         device=dev)
-        params = _lib.PdhgParams(self.evaluation_frequency, int(bool(scalar_rescaling)), self.iteration_limit,
-                                 objective_tolerance, primal_tolerance, dual_tolerance, self.time_limit_seconds)
-        res = _lib.PdhgResult()
-        with torch.cuda.device(dev):
-            rc = lib.hm_pdhg_solve(_lib.stream_handle(dev), _lib.ptr(rows_t), _lib.ptr(cols_t), _lib.ptr(costs_t),
-                                   _lib.ptr(masses_t), _lib.ptr(x0), _lib.ptr(y0), n_source, n_target, e, params,
-                                   _lib.ptr(x_out), _lib.ptr(y_out), res, _lib.ptr(ws), ws.numel())
-        _lib.check(rc, "hm_pdhg_solve")
+        x_out, y_out, res = run_pdhg(rows_t, cols_t, costs_t, source_t, target_t, x0, y0,
+                                     evaluation_frequency=self.evaluation_frequency, rescale=scalar_rescaling,
+                                     iteration_limit=self.iteration_limit, objective_tolerance=objective_tolerance,
+                                     primal_tolerance=primal_tolerance, dual_tolerance=dual_tolerance,
+                                     time_limit_seconds=self.time_limit_seconds, device=dev)
         reason = _lib.REASONS[int(res.reason)]
         duration = float(time.perf_counter() - started)
         diag = {
@@ -127,4 +143,4 @@ class NativeRestrictedOTPDLP:
                             dual_feas=res.rel_dual, gap=res.rel_gap, solver_diag=diag)
 
 
-__all__ = ["NativeRestrictedOTPDLP"]
+__all__ = ["NativeRestrictedOTPDLP", "run_pdhg"]

@@ -9,13 +9,14 @@ place of the reference's binary wheel, the entry points below run on the HIP ker
 * ``hierot_generic_cost_ext.raw_initial`` / ``raw_certificate_tiled`` / ``norms``: the directional raw scan, the
   certificate without candidates, fp64 squared row norms;
 * ``hierot_norm_cost_scan_ext.fused_gcost_pairs``: fp64 norm costs of selected pairs;
-* ``_support_sparsifier_ext.sparsify``: cycle-cancelling support sparsification.
+* ``_support_sparsifier_ext.sparsify``: cycle-cancelling support sparsification;
+* ``pycupdlpx.cupdlpx`` (``loadData_device_csr`` / ``setInitSol`` / ``solve`` / ``getSolution``,
+  ``GPU_ARRAY_IO_VERSION`` 1): the restricted transport LPs of the GPU-resident loop, on the Halpern-PDHG
+  (``hm_pdhg_solve``); general LPs and the host loaders raise ``NotImplementedError``.
 
 The reference's tile-level functions (``scan``, ``merge``, ``topk``, ``dots``, ``direct_norm``, ...) have no
 counterpart: the MI355X kernels fuse the tile loop, so those names raise ``NotImplementedError`` naming the fused
-entry point that replaces them. The CuPDLPx module (``pycupdlpx``) is replaced by the restricted-OT PDHG
-(``hello_ot_amd.lp.NativeRestrictedOTPDLP``), whose interface is the reference's restricted-OT contract rather than
-CuPDLPx's general LP loader.
+entry point that replaces them.
 """
 
 API_VERSION = 1

@@ -22,6 +22,9 @@ import oracle  # noqa: E402
 
 SCAN_CASES = [(40, 57, 16, 1), (33, 70, 9, 3), (64, 48, 130, 8)]
 PDHG_CASES = [(5, 40, 0.0), (20, 3000, 1e-7)]
+# scalar-rescaling mode (solve_once's rescale flag): costs in the hundreds and skewed masses; masses of 1e100 (only
+# the rescaled solve converges); one huge cost that makes the first residual non-finite (NUMERICAL_DIVERGENCE)
+PDHG_RESCALE_CASES = [("skewed", 10, 4000, 1e-8), ("heavy", 20, 2000, 1e-7), ("diverge", 20, 100, 1e-7)]
 SPARSIFY_CASES = [(0, 12, 15, 120, 0), (1, 20, 9, 150, 4)]
 
 
@@ -54,6 +57,23 @@ def pdhg_cases(lp):
                  target_mass=tm, frequency=freq, limit=limit, tolerance=tol, x=r["x"], y=r["y"],
                  iterations=r["iterations"], termination_reason=r["termination_reason"],
                  restart_count=r["solver_diag"]["restart_count"])
+    for name, freq, limit, tol in PDHG_RESCALE_CASES:
+        rng = np.random.default_rng(77)
+        costs = 250.0 * rng.random(35)
+        sm = rng.random(7) + 0.2
+        tm = rng.random(5) + 0.2
+        sm, tm = sm / sm.sum(), tm / tm.sum()
+        if name == "heavy":
+            sm, tm = sm * 1e100, tm * 1e100
+        if name == "diverge":
+            costs[3] = 1e200
+        for rescale in (False, True):
+            r = lp.solve_once(rows, cols, costs, np.concatenate([sm, tm]), np.zeros(35), np.zeros(12), 7, 1, freq,
+                              3600.0, limit, tol, tol, tol, rescale, False)
+            np.savez(HERE / f"pdhg_7x5_{name}_rescale{int(rescale)}.npz", rows=rows, cols=cols, costs=costs,
+                     source_mass=sm, target_mass=tm, frequency=freq, limit=limit, tolerance=tol, rescale=rescale,
+                     x=r["x"], y=r["y"], iterations=r["iterations"], termination_reason=r["termination_reason"],
+                     restart_count=r["solver_diag"]["restart_count"])
 
 
 def sparsify_cases(sp):

@@ -41,7 +41,8 @@ def test_pdhg_oracle_reproduces_reference_solver_vectors(path):
     z = np.load(path)
     tol = float(z["tolerance"])
     r = oracle.pdhg_solve(z["rows"], z["cols"], z["costs"], z["source_mass"], z["target_mass"],
-                          evaluation_frequency=int(z["frequency"]), iteration_limit=int(z["limit"]), tolerance=tol)
+                          evaluation_frequency=int(z["frequency"]), iteration_limit=int(z["limit"]), tolerance=tol,
+                          rescale=bool(z["rescale"]) if "rescale" in z else False)
     assert r["iterations"] == int(z["iterations"])
     assert r["termination_reason"] == str(z["termination_reason"])
     assert r["restart_count"] == int(z["restart_count"])

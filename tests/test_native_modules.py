@@ -58,3 +58,27 @@ def test_sparsifier_module_matches_the_reference_module():
     np.testing.assert_allclose(got["values"], want["values"], rtol=1e-12, atol=1e-14)
     for key_ in ("output_nnz", "cycle_updates", "tree_operations"):
         assert got[key_] == want[key_]
+
+
+def test_pycupdlpx_contract_on_the_host():
+    """The CuPDLPx module name the reference loads for its GPU-resident LPs (gpu_resident/solver.py:239-241): the
+    device-CSR loader is the served path; host loaders, CPU tensors and solving before loading are refused."""
+    import torch
+
+    m = importlib.import_module("hello_ot_native.pycupdlpx")
+    assert m.GPU_ARRAY_IO_VERSION == 1
+    params = m.make_default_params()
+    assert params["termination_norm"] == "l2" and params["step_size_method"] == 3
+    solver = m.cupdlpx()
+    for loader in (solver.loadData, solver.loadData_csr, solver.loadData_csc):
+        with pytest.raises(NotImplementedError, match="loadData_device_csr"):
+            loader()
+    with pytest.raises(RuntimeError, match="No problem loaded"):
+        solver.solve({})
+    with pytest.raises(RuntimeError, match="No solution"):
+        solver.getSolution()
+    one = torch.zeros(3, dtype=torch.int32)
+    with pytest.raises(TypeError, match="CUDA tensors"):
+        solver.loadData_device_csr(one, one, None, 2, 1, one.double(), one.double(), 0.0, float("inf"), 2)
+    with pytest.raises(ValueError):
+        m.set_free_mode(3)
