@@ -612,7 +612,7 @@ def bench_c5_solve(dev, rows, stream="auto"):
     ``stream``: "auto" hands both sides over on the device and lets the solver's memory planner choose (at C5 on
     one MI355X both sides stay resident); "always" hands the source side over in host memory and streams it, which
     bounds the device memory (the reference's non-resident path and its 41.6 GiB figure)."""
-    from hello_ot_amd import SolverOptions, solve
+    from hello_ot_amd import SolverOptions, _lib, solve
     from hello_ot_amd.resident import host as host_module
 
     log(f"[bench] C5 solve ({stream}): generating {rows} x {C5_D} per side "
@@ -625,10 +625,14 @@ def bench_c5_solve(dev, rows, stream="auto"):
     log(f"[bench] C5 solve ({stream}): solving ...")
     policy = host_module.STREAM_POLICY
     host_module.STREAM_POLICY = stream
+    # the library's kernel timing on for the PDHG iterations' own device time (HIP events around each iteration)
+    _lib.profile_reset()
+    _lib.profile_enable(True)
     try:
         r = solve(X, Y, options=SolverOptions(verbose="detailed", consume_input_features=True))
     finally:
         host_module.STREAM_POLICY = policy
+        _lib.profile_enable(False)
     del X, Y
     torch.cuda.empty_cache()
     finest = r.solve_stage.levels[-1].solve.summary
@@ -641,7 +645,25 @@ def bench_c5_solve(dev, rows, stream="auto"):
             "scan_seconds": r.metadata["total_scan_time"], "lp_seconds": r.metadata["total_lp_solve_time"],
             "init_seconds": sum(l.initialization.wall_time for l in r.solve_stage.levels
                                 if l.kind == "refined" and l.initialization is not None),
+            "finest_pdhg": _finest_pdhg(r),
             "levels": _level_summary(r)}
+
+
+def _finest_pdhg(result):
+    """The finest level's PDHG: iterations, seconds inside hm_pdhg_solve, the iterations' own average device time
+    (HIP events) and that time against the 120 E + 76 V byte model of one iteration (E: the level's final support,
+    V: its nodes)."""
+    device = next((d for d in result.metadata.get("lp_device_by_level", []) if d["level"] == 0), None)
+    finest = result.solve_stage.levels[-1]
+    if device is None or not device.get("passes"):
+        return None
+    E = int(finest.solve.summary.final_active_support_size)
+    V = finest.n_source + finest.n_target
+    us = device["pass_ms"] / device["passes"] * 1e3
+    return {"iterations": device["iterations"], "hm_pdhg_solve_seconds": round(device["seconds"], 3),
+            "pass_us": round(us, 1), "edges": E, "nodes": V,
+            "model_bytes_per_iteration": 120 * E + 76 * V,
+            "hbm_frac_model": (120 * E + 76 * V) / (us * 1e-6) / PEAK_HBM}
 
 
 # ----------------------------------------------------------------------------------------------------------

@@ -131,8 +131,18 @@ def ptr(t) -> ctypes.c_void_p:
     return ctypes.c_void_p(int(t.data_ptr()))
 
 
+_PROFILING = False
+
+
 def profile_enable(on: bool = True) -> None:
+    global _PROFILING
     load().hm_profile_enable(int(bool(on)))
+    _PROFILING = bool(on)
+
+
+def profiling() -> bool:
+    """Whether the library's kernel timing is on (profile_enable)."""
+    return _PROFILING
 
 
 def profile_reset() -> None:

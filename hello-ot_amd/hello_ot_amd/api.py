@@ -130,7 +130,7 @@ def solve_problem(problem: Problem, options: SolverOptions, *, max_iterations: i
         sizes = level_sizes(n, m, options.coarsest_size_threshold, options.split_count)
         levels, previous, triggers = [], None, []
         support = dual = None
-        sparsified = []
+        sparsified, lp_device = [], []
         for level_index in reversed(range(len(sizes))):
             nn, mm = sizes[level_index]
             cost = full.sliced(nn, mm, level_precision(options.cost_precision, level_index))
@@ -139,8 +139,10 @@ def solve_problem(problem: Problem, options: SolverOptions, *, max_iterations: i
                 support, dual, level = solve_coarsest(cost, aa, bb, level_index)
             else:
                 inherited = "target" if nn >= mm else "source"
-                support, dual, level, triggered = refine_level(cost, aa, bb, previous, inherited, options, level_index,
-                                                               max_iterations, options.cost_perturbation == "auto")
+                support, dual, level, triggered, lp_time = refine_level(cost, aa, bb, previous, inherited, options,
+                                                                        level_index, max_iterations,
+                                                                        options.cost_perturbation == "auto")
+                lp_device.append({"level": level_index, **lp_time})
                 if triggered:
                     triggers.append(level_index)
             levels.append(level)
@@ -170,6 +172,7 @@ def solve_problem(problem: Problem, options: SolverOptions, *, max_iterations: i
         "total_scan_time": sum(i.full_scan_time for l in levels if l.kind == "refined" for i in l.solve.iterations),
         "cost_perturbation": {"policy": options.cost_perturbation, "activated": False,
                               "reentry_trigger_levels": triggers},
+        "lp_device_by_level": lp_device,
         "support_sparsification": {"events": len(sparsified),
                                    "cycle_updates": sum(r.cycle_updates for r in sparsified),
                                    "removed_edges": sum(r.input_nnz - r.output_nnz for r in sparsified),

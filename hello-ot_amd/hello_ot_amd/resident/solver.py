@@ -121,6 +121,7 @@ class LevelRefinement:
         self.perturbation_triggered = False
         self.records = []
         self.lp = None
+        self.lp_device = {"seconds": 0.0, "iterations": 0}  # hm_pdhg_solve time of the level's LP solves
 
     # -- seeding ----------------------------------------------------------------------------------------
     def seed(self, previous: torch.Tensor, inherited: str | None) -> InitializationStats:
@@ -174,6 +175,12 @@ class LevelRefinement:
         self.dual, lp = support.solve_lp(self.cost, self.a, self.b, self.dual, tol, primal_cap=self.cap)
         self.lp = lp
         lp_seconds = watch.lap()
+        diag = lp.solver_diag or {}
+        self.lp_device["seconds"] += float(diag.get("device_loop_sec", 0.0))
+        self.lp_device["iterations"] += int(lp.iterations)
+        if "pdhg_pass_ms" in diag:
+            self.lp_device["pass_ms"] = self.lp_device.get("pass_ms", 0.0) + diag["pdhg_pass_ms"]
+            self.lp_device["passes"] = self.lp_device.get("passes", 0) + diag["pdhg_passes"]
         thinned = support.last_sparsification
         _progress(options, f"level={self.index} iteration={iteration} lp {lp_seconds:.3f}s support={size_before} "
                            f"pdhg_iters={lp.iterations}"
@@ -231,12 +238,14 @@ def _contains_any(sorted_keys: torch.Tensor, queries: torch.Tensor) -> bool:
 
 
 def refine_level(cost: Cost, a, b, previous, inherited, options, level_index, max_iterations, detect_reentry):
-    """Seed and refine one level; returns (support, duals, LevelResult, perturbation trigger)."""
+    """Seed and refine one level; returns (support, duals, LevelResult, perturbation trigger, LP device time:
+    seconds inside hm_pdhg_solve, PDHG iterations, and with the library's kernel timing on the iterations' own
+    milliseconds and count)."""
     started = time.perf_counter()
     level = LevelRefinement(cost, a, b, options, level_index, detect_reentry)
     initialization = level.seed(previous, inherited)
     result = level.run(max_iterations, initialization, started)
-    return level.support, level.dual, result, level.perturbation_triggered
+    return level.support, level.dual, result, level.perturbation_triggered, dict(level.lp_device)
 
 
 __all__ = ["LevelRefinement", "candidate_keys", "derive_hierarchy_seeds", "level_sizes", "refine_level",

@@ -16,6 +16,7 @@ from __future__ import annotations
 import torch
 
 from ..config import POSITIVE_SUPPORT_TOLERANCE
+from .. import _lib
 from ..lp import NativeRestrictedOTPDLP
 from .sparsify import sparsify_transport_support
 
@@ -162,8 +163,14 @@ class ActiveSet:
         rows, cols = self.endpoints()
         costs = cost.pairs(rows, cols)
         solver = NativeRestrictedOTPDLP(device=a.device, evaluation_frequency=200)
+        passes = _lib.profile_query("pdhg_iteration") if _lib.profiling() else None
         result = solver.solve_restricted(rows=rows, cols=cols, costs=costs, source_mass=a, target_mass=b,
                                          warm_start_primal=self.flow, warm_start_dual=dual, tolerance=tolerance)
+        if passes is not None:
+            # with the library's kernel timing on: the iterations' own device time (no pair costs, no set-up)
+            ms, count = _lib.profile_query("pdhg_iteration")
+            result.solver_diag["pdhg_pass_ms"] = ms - passes[0]
+            result.solver_diag["pdhg_passes"] = count - passes[1]
         if not result.success:
             raise RuntimeError(f"GPU restricted LP failed: {result.termination_reason}")
         self.flow = result.x

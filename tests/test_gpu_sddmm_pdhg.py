@@ -236,3 +236,88 @@ def test_pdhg_c3_shape_1000_iterations_against_oracle(cuda):
     np.testing.assert_allclose(r.x.cpu().numpy(), ref["x"], rtol=1e-8, atol=1e-14)
     np.testing.assert_allclose(r.y.cpu().numpy(), ref["y"], rtol=1e-8, atol=1e-10)
     assert r.obj_val == pytest.approx(ref["obj_val"], rel=1e-9)
+
+
+def _renumber_case(name):
+    """LPs of the tests above, for the solve with internal node numbers."""
+    rng = np.random.default_rng(0)
+    if name == "sparse":
+        rows, cols, costs, a, b = _sparse_lp(4, 60, 45, 400)
+        return rows, cols, costs, a, b, 50, 3000, 1e-9, None, None
+    if name == "warm":
+        rows, cols, costs, a, b = _sparse_lp(9, 30, 25, 120)
+        return rows, cols, costs, a, b, 50, 3000, 1e-9, rng.random(rows.size) * 0.01, rng.normal(0, 0.1, 55)
+    if name == "hubs":
+        ns, nt = 40, 2600
+        rng = np.random.default_rng(21)
+        rows = np.concatenate([np.zeros(nt, np.int64), np.arange(1, ns), rng.integers(1, ns, 200)])
+        cols = np.concatenate([np.arange(nt), np.zeros(ns - 1, np.int64), rng.integers(1, nt, 200)])
+        perm = rng.permutation(rows.size)
+        a, b = rng.random(ns), rng.random(nt)
+        return rows[perm], cols[perm], rng.random(rows.size), a / a.sum(), b / b.sum(), 50, 600, 0.0, None, None
+    # clustered: 8 clusters of about 500 sources and 400 targets under shuffled numbers, each cluster's mass 1/8
+    # and its support 6 random targets per source plus a north-west-corner staircase (so the LP is feasible), and
+    # 200 edges across clusters
+    ns, nt, k = 4000, 3200, 8
+    cs, ct = rng.integers(0, k, ns), rng.integers(0, k, nt)
+    a, b = rng.random(ns) + 0.1, rng.random(nt) + 0.1
+    rows, cols = [], []
+    for c in range(k):
+        si, ti = np.flatnonzero(cs == c), np.flatnonzero(ct == c)
+        a[si] /= a[si].sum() * k
+        b[ti] /= b[ti].sum() * k
+        rows.append(np.repeat(si, 6))
+        cols.append(rng.choice(ti, 6 * si.size))
+        u = v = 0
+        left_a, left_b = a[si[0]], b[ti[0]]
+        while u < si.size and v < ti.size:              # north-west corner rule on the cluster's masses
+            rows.append(si[u:u + 1])
+            cols.append(ti[v:v + 1])
+            if left_a <= left_b:
+                left_b -= left_a
+                u += 1
+                left_a = a[si[u]] if u < si.size else 0.0
+            else:
+                left_a -= left_b
+                v += 1
+                left_b = b[ti[v]] if v < ti.size else 0.0
+    rows.append(rng.integers(0, ns, 200))
+    cols.append(rng.integers(0, nt, 200))
+    key = np.unique(np.concatenate(rows) * nt + np.concatenate(cols))
+    return (key // nt).astype(np.int64), (key % nt).astype(np.int64), rng.random(key.size), a, b, 100, 3000, \
+        1e-8, None, None
+
+
+@pytest.mark.parametrize("name", ["sparse", "warm", "hubs", "clustered"])
+def test_pdhg_with_internal_node_numbers_matches_oracle(cuda, monkeypatch, name):
+    """The solve renumbers nodes by neighbour averaging when the problem has at least HELLOOT_PDHG_REORDER nodes
+    (2^20 by default; 1 here forces it): per-node and per-edge operations are unchanged, so the iterates, counts,
+    restarts and the caller-ordered outputs match the oracle as without the numbering."""
+    rows, cols, costs, a, b, freq, limit, tol, x0, y0 = _renumber_case(name)
+    ref = oracle.pdhg_solve(rows, cols, costs, a, b, warm_start_primal=x0, warm_start_dual=y0,
+                            evaluation_frequency=freq, iteration_limit=limit, tolerance=tol)
+    out = {}
+    for setting in ("off", "1"):
+        monkeypatch.setenv("HELLOOT_PDHG_REORDER", setting)
+        r = NativeRestrictedOTPDLP(device=cuda, evaluation_frequency=freq, iteration_limit=limit).solve_restricted(
+            rows=rows, cols=cols, costs=costs, source_mass=a, target_mass=b, warm_start_primal=x0,
+            warm_start_dual=y0, tolerance=tol)
+        assert r.iterations == ref["iterations"] and r.termination_reason == ref["termination_reason"], setting
+        assert r.solver_diag["restart_count"] == ref["restart_count"], setting
+        np.testing.assert_allclose(r.x.cpu().numpy(), ref["x"], rtol=1e-9, atol=1e-12)
+        np.testing.assert_allclose(r.y.cpu().numpy(), ref["y"], rtol=1e-9, atol=1e-12)
+        out[setting] = r
+    assert out["1"].obj_val == pytest.approx(out["off"].obj_val, rel=1e-12)
+
+
+def test_pdhg_internal_numbering_validates_endpoints(cuda, monkeypatch):
+    """The library's own check (the Python wrapper validates first), on the numbering path."""
+    from hello_ot_amd.lp.native_pdlp import run_pdhg
+
+    monkeypatch.setenv("HELLOOT_PDHG_REORDER", "1")
+    t = lambda v, dt: torch.as_tensor(np.asarray(v), dtype=dt, device=cuda)  # noqa: E731
+    with pytest.raises(ValueError, match="out of bounds"):
+        run_pdhg(t([0, 0, 1, 1], torch.int64), t([0, 1, 0, 2], torch.int64), t([0.0, 2.0, 1.0, 0.0], torch.float64),
+                 t([0.4, 0.6], torch.float64), t([0.5, 0.5], torch.float64), None, None, evaluation_frequency=20,
+                 rescale=False, iteration_limit=100, objective_tolerance=1e-6, primal_tolerance=1e-6,
+                 dual_tolerance=1e-6, time_limit_seconds=60.0, device=cuda)
