@@ -190,9 +190,10 @@ class Cost:
             db = g - q
         for s, e, x in self.source.chunks():
             if l2sq:
-                # a chunk is short against the target side: its column lists come cheapest from the row sweep
-                # (columns fused into it), so a columns-only scan asks for the chunk's rows as well
-                out = pricing_l2sq(x, self.target, p[s:e], q, f[s:e] - p[s:e], db, k, rows=rows or cols, cols=cols,
+                # a columns-only scan runs the library's role-swapped pass per chunk (the target rows against the
+                # chunk, reading the resident side's copy): as fast here as column lists fused into a row sweep,
+                # and without the fused lists' partial-list buffer (up to 12 GiB)
+                out = pricing_l2sq(x, self.target, p[s:e], q, f[s:e] - p[s:e], db, k, rows=rows, cols=cols,
                                    stats=certificate, linf=certificate, resident=side)
             else:
                 out = pricing_norm(x, self.target, f[s:e], g, k, NORM_KINDS[self.kind], rows=rows, cols=cols,
