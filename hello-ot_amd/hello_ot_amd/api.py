@@ -59,18 +59,28 @@ def _to_device(value, device, dtype):
     return torch.as_tensor(np.asarray(value), dtype=dtype, device=device)
 
 
-def _shuffled_features(value, perm, device, consume: bool, bounded: bool = False):
-    """Rows of ``value`` in shuffle order as contiguous fp32 on ``device``. With ``consume`` a contiguous fp32
-    tensor already on the device is reordered in place (the caller's tensor then holds the shuffled rows), like the
-    reference's in-place feature reorder (prewarm.py:177-214): through one full temporary, or, with ``bounded`` (a
+def _permute_in_place(value, perm, device, bounded: bool):
+    """value[i] = (old value)[perm[i]] in place: through one full temporary, or, with ``bounded`` (a
     memory-bounded solve) or when the device has no room for the temporary, with one chunk of extra device memory
     (``permute_rows_inplace``, a host round trip: about 4 s for 39 GiB)."""
+    nbytes = 4 * value.numel()
+    if nbytes > _host.STREAM_MIN_BYTES and (bounded or torch.cuda.mem_get_info(device)[0] < nbytes + (4 << 30)):
+        permute_rows_inplace(value, perm)
+    else:
+        value.copy_(value[perm])
+
+
+def _shuffled_features(value, perm, device, consume: bool, restore: list, bounded: bool = False):
+    """Rows of ``value`` in shuffle order as contiguous fp32 on ``device``. With ``consume`` a contiguous fp32
+    tensor already on the device is reordered in place, and (tensor, inverse permutation, bounded) is appended to
+    ``restore`` so that the caller's order comes back when the solve ends, as the reference's in-place reorder
+    does (``gpu_resident/storage.py:74-120``, ``prewarm.py:177-214``)."""
     if consume and torch.is_tensor(value) and value.device == device and value.dtype == torch.float32 \
             and value.is_contiguous():
-        nbytes = 4 * value.numel()
-        if nbytes > _host.STREAM_MIN_BYTES and (bounded or torch.cuda.mem_get_info(device)[0] < nbytes + (4 << 30)):
-            return permute_rows_inplace(value, perm)
-        value.copy_(value[perm])
+        _permute_in_place(value, perm, device, bounded)
+        inverse = torch.empty_like(perm)
+        inverse[perm] = torch.arange(perm.numel(), device=perm.device, dtype=perm.dtype)
+        restore.append((value, inverse, bounded))
         return value
     return _to_device(value, device, torch.float32)[perm].contiguous()
 
@@ -109,6 +119,10 @@ def solve_problem(problem: Problem, options: SolverOptions, *, max_iterations: i
     require_native_runtime_compatibility()
     device = _device_of(problem)
     n, m = problem.shape
+    consume = bool(options.consume_input_features)
+    if consume and all(torch.is_tensor(v) for v in (problem.source_points, problem.target_points)) and \
+            problem.source_points.untyped_storage().data_ptr() == problem.target_points.untyped_storage().data_ptr():
+        raise ValueError("consume_input_features requires source and target with disjoint storage")
     with torch.cuda.device(device):
         torch.cuda.synchronize(device)
         torch.cuda.reset_peak_memory_stats(device)
@@ -120,71 +134,86 @@ def solve_problem(problem: Problem, options: SolverOptions, *, max_iterations: i
              else _to_device(problem.source_mass, device, torch.float64))[si]
         b = (torch.full((m,), 1.0 / m, dtype=torch.float64, device=device) if problem.target_mass is None
              else _to_device(problem.target_mass, device, torch.float64))[ti]
-        consume = bool(options.consume_input_features)
-        if _stream_source(problem.source_points, problem.target_points, problem.cost_type, device, options):
-            x = HostRows(shuffled_rows(problem.source_points, si), device)
-        else:
-            x = _shuffled_features(problem.source_points, si, device, consume)
-        y = _shuffled_features(problem.target_points, ti, device, consume, bounded=isinstance(x, HostRows))
-        full = Cost.create(x, y, problem.cost_type)
-        sizes = level_sizes(n, m, options.coarsest_size_threshold, options.split_count)
-        levels, previous, triggers = [], None, []
-        support = dual = None
-        sparsified, lp_device = [], []
-        for level_index in reversed(range(len(sizes))):
-            nn, mm = sizes[level_index]
-            cost = full.sliced(nn, mm, level_precision(options.cost_precision, level_index))
-            aa, bb = balanced_masses(a[:nn].clone(), b[:mm].clone())
-            if previous is None:
-                support, dual, level = solve_coarsest(cost, aa, bb, level_index)
-            else:
-                inherited = "target" if nn >= mm else "source"
-                support, dual, level, triggered, lp_time = refine_level(cost, aa, bb, previous, inherited, options,
-                                                                        level_index, max_iterations,
-                                                                        options.cost_perturbation == "auto")
-                lp_device.append({"level": level_index, **lp_time})
-                if triggered:
-                    triggers.append(level_index)
-            levels.append(level)
-            sparsified.extend(support.sparsification_log)
-            previous = dual
-        rows, cols = support.endpoints()
-        objective = float(full.pairs(rows, cols) @ support.flow)
-        keys = si[rows] * m + ti[cols]
-        order = torch.argsort(keys, stable=True)
-        f = torch.empty(n, dtype=torch.float64, device=device)
-        g = torch.empty(m, dtype=torch.float64, device=device)
-        f[si], g[ti] = dual[:n], dual[n:]
-        solution = SparseOTSolution((n, m), si[rows][order], ti[cols][order], support.flow[order], f, g)
+        restore = []  # tensors reordered in place: the caller's order comes back when the solve ends, or fails
+        try:
+            run = _solve_levels(problem, options, device, si, ti, a, b, consume, restore, max_iterations)
+        finally:
+            for value, inverse, bounded in reversed(restore):
+                _permute_in_place(value, inverse, device, bounded)
         torch.cuda.synchronize(device)
         wall = time.perf_counter() - started
         peak = torch.cuda.max_memory_allocated(device) / 2**20
+    levels = run["levels"]
     stage = SolveStageResult(tuple(levels), wall)
+    sparsified = run["sparsified"]
     metadata = {
-        "gpu_resident": not isinstance(x, HostRows), "streamed_source": isinstance(x, HostRows),
+        "gpu_resident": not run["streamed"], "streamed_source": run["streamed"],
         "backend": "native", "device": str(device), "cost_type": problem.cost_type,
         "cost_precision": options.cost_precision, "stopping_norm": options.stopping_norm,
         "coarsest_solver": "mi355x_network_simplex", "lp_solver": "mi355x_halpern_pdhg",
-        "hierarchy_sizes": [list(s) for s in sizes],
+        "hierarchy_sizes": [list(s) for s in run["sizes"]],
         "total_refinement_iterations": sum(len(l.solve.iterations) for l in levels if l.kind == "refined"),
         "total_lp_solve_time": sum(i.solve_lp.wall_time for l in levels if l.kind == "refined"
                                    for i in l.solve.iterations),
         "total_scan_time": sum(i.full_scan_time for l in levels if l.kind == "refined" for i in l.solve.iterations),
         "cost_perturbation": {"policy": options.cost_perturbation, "activated": False,
-                              "reentry_trigger_levels": triggers},
-        "lp_device_by_level": lp_device,
+                              "reentry_trigger_levels": run["triggers"]},
+        "lp_device_by_level": run["lp_device"],
         "support_sparsification": {"events": len(sparsified),
                                    "cycle_updates": sum(r.cycle_updates for r in sparsified),
                                    "removed_edges": sum(r.input_nnz - r.output_nnz for r in sparsified),
                                    "wall_time": sum(r.wall_time for r in sparsified)},
     }
-    result = Result(objective, solution, stage, wall, peak, None, metadata, ())
+    result = Result(run["objective"], run["solution"], stage, wall, peak, None, metadata, ())
     if options.verbose != "off":
         finest = levels[-1]
         state = finest.solve.summary.stop_reason if finest.kind == "refined" else "coarsest"
-        print(f"[hello-mi355x] n={n} m={m} cost={problem.cost_type} objective={objective:.12g} "
+        print(f"[hello-mi355x] n={n} m={m} cost={problem.cost_type} objective={run['objective']:.12g} "
               f"time={wall:.3f}s levels={len(levels)} finest={state}", file=sys.stderr)
     return result
+
+
+def _solve_levels(problem, options, device, si, ti, a, b, consume, restore, max_iterations) -> dict:
+    """The hierarchy on the shuffled features, coarsest level first; the plan and duals come back in the caller's
+    numbering."""
+    n, m = problem.shape
+    if _stream_source(problem.source_points, problem.target_points, problem.cost_type, device, options):
+        x = HostRows(shuffled_rows(problem.source_points, si), device)
+    else:
+        x = _shuffled_features(problem.source_points, si, device, consume, restore)
+    y = _shuffled_features(problem.target_points, ti, device, consume, restore, bounded=isinstance(x, HostRows))
+    full = Cost.create(x, y, problem.cost_type)
+    sizes = level_sizes(n, m, options.coarsest_size_threshold, options.split_count)
+    levels, previous, triggers = [], None, []
+    support = dual = None
+    sparsified, lp_device = [], []
+    for level_index in reversed(range(len(sizes))):
+        nn, mm = sizes[level_index]
+        cost = full.sliced(nn, mm, level_precision(options.cost_precision, level_index))
+        aa, bb = balanced_masses(a[:nn].clone(), b[:mm].clone())
+        if previous is None:
+            support, dual, level = solve_coarsest(cost, aa, bb, level_index)
+        else:
+            inherited = "target" if nn >= mm else "source"
+            support, dual, level, triggered, lp_time = refine_level(cost, aa, bb, previous, inherited, options,
+                                                                    level_index, max_iterations,
+                                                                    options.cost_perturbation == "auto")
+            lp_device.append({"level": level_index, **lp_time})
+            if triggered:
+                triggers.append(level_index)
+        levels.append(level)
+        sparsified.extend(support.sparsification_log)
+        previous = dual
+    rows, cols = support.endpoints()
+    objective = float(full.pairs(rows, cols) @ support.flow)
+    keys = si[rows] * m + ti[cols]
+    order = torch.argsort(keys, stable=True)
+    f = torch.empty(n, dtype=torch.float64, device=device)
+    g = torch.empty(m, dtype=torch.float64, device=device)
+    f[si], g[ti] = dual[:n], dual[n:]
+    solution = SparseOTSolution((n, m), si[rows][order], ti[cols][order], support.flow[order], f, g)
+    return {"levels": levels, "sizes": sizes, "streamed": isinstance(x, HostRows), "objective": objective,
+            "solution": solution, "triggers": triggers, "sparsified": sparsified, "lp_device": lp_device}
 
 
 __all__ = ["solve", "solve_problem"]

@@ -170,3 +170,31 @@ def test_solve_with_the_smallest_support_budget_sparsifies(cuda):
     sol = r.solution.to_cpu()
     np.testing.assert_allclose(np.bincount(sol.rows, weights=sol.values, minlength=n), a, atol=5e-6)
     np.testing.assert_allclose(np.bincount(sol.cols, weights=sol.values, minlength=m), b, atol=5e-6)
+
+
+def test_consumed_inputs_come_back_in_the_callers_order(cuda, monkeypatch):
+    """consume_input_features reorders device inputs in place for the solve and puts them back when it ends, also
+    when it fails (the reference's in-place reorder, gpu_resident/storage.py:74-120, and its tests
+    hello_gpu_resident_test.py:234-249); inputs sharing storage are refused."""
+    import hello_ot_amd.api as api
+
+    rng = np.random.default_rng(19)
+    X = torch.as_tensor(rng.random((230, 5)).astype(np.float32)).to(cuda)
+    Y = torch.as_tensor((rng.random((190, 5)) + 0.2).astype(np.float32)).to(cuda)
+    Xc, Yc = X.clone(), Y.clone()
+    opts = dict(coarsest_size_threshold=40, verbose="off", cost_perturbation="off")
+    r = solve(X, Y, options=SolverOptions(consume_input_features=True, **opts))
+    assert torch.equal(X, Xc) and torch.equal(Y, Yc)
+    ref = solve(Xc, Yc, options=SolverOptions(**opts))
+    assert r.objective == pytest.approx(ref.objective, rel=1e-12)
+    assert torch.equal(r.solution.rows, ref.solution.rows) and torch.equal(r.solution.cols, ref.solution.cols)
+
+    def fail(*args, **kwargs):
+        raise RuntimeError("injected coarsest failure")
+
+    monkeypatch.setattr(api, "solve_coarsest", fail)
+    with pytest.raises(RuntimeError, match="injected coarsest failure"):
+        solve(X, Y, options=SolverOptions(consume_input_features=True, **opts))
+    assert torch.equal(X, Xc) and torch.equal(Y, Yc)
+    with pytest.raises(ValueError, match="disjoint storage"):
+        solve(X, X[:100], options=SolverOptions(consume_input_features=True, **opts))

@@ -103,7 +103,11 @@ def test_streamed_solve_matches_the_resident_solve(cuda, monkeypatch):
     monkeypatch.setattr(host_module, "STREAM_CHUNK_BYTES", 500 * d * 4)
     monkeypatch.setattr(host_module, "STREAM_POLICY", "always")
     monkeypatch.delenv("HELLOOT_STREAM_SOURCE", raising=False)
-    r = solve(X, Y, options=SolverOptions(**base))
+    # device inputs, consumed: the source side is copied to host memory in shuffle order, the target side is
+    # reordered in place through the bounded permutation and put back afterwards
+    Xd, Yd = torch.as_tensor(X).to(cuda), torch.as_tensor(Y).to(cuda)
+    r = solve(Xd, Yd, options=SolverOptions(consume_input_features=True, **base))
+    assert torch.equal(Xd.cpu(), torch.as_tensor(X)) and torch.equal(Yd.cpu(), torch.as_tensor(Y))
     assert r.metadata["streamed_source"] and not ref.metadata["streamed_source"]
     assert r.objective == pytest.approx(ref.objective, rel=1e-12)
     assert r.solution.values.numel() == ref.solution.values.numel()
