@@ -22,7 +22,7 @@ from .resident.host import HostRows, permute_rows_inplace, shuffled_rows
 from .resident.leaf import solve_coarsest
 from .resident.solver import level_sizes, refine_level, shuffle_once_permutation
 from .resident.support import balanced_masses
-from .types import Problem, Result, SolveStageResult, SparseOTSolution
+from .types import CostStageResult, Problem, Result, SolveStageResult, SparseOTSolution
 
 
 def solve(source_points: Problem | Any, target_points: Any | None = None, *, source_mass: Any | None = None,
@@ -119,6 +119,13 @@ def solve_problem(problem: Problem, options: SolverOptions, *, max_iterations: i
     require_native_runtime_compatibility()
     device = _device_of(problem)
     n, m = problem.shape
+    if options.gpu_resident:
+        # the reference's GPU-resident entry takes both sides as device tensors (gpu_resident/solver.py:230-234)
+        x, y = problem.source_points, problem.target_points
+        if not all(torch.is_tensor(v) and v.is_cuda for v in (x, y)) or x.device != y.device:
+            raise ValueError("gpu_resident requires source and target CUDA tensors on the same device")
+        if any(v.dtype != torch.float32 or not v.is_contiguous() for v in (x, y)):
+            raise ValueError("gpu_resident requires contiguous FP32 input features")
     consume = bool(options.consume_input_features)
     if consume and all(torch.is_tensor(v) for v in (problem.source_points, problem.target_points)) and \
             problem.source_points.untyped_storage().data_ptr() == problem.target_points.untyped_storage().data_ptr():
@@ -164,7 +171,8 @@ def solve_problem(problem: Problem, options: SolverOptions, *, max_iterations: i
                                    "removed_edges": sum(r.input_nnz - r.output_nnz for r in sparsified),
                                    "wall_time": sum(r.wall_time for r in sparsified)},
     }
-    result = Result(run["objective"], run["solution"], stage, wall, peak, None, metadata, ())
+    result = Result(run["objective"], run["solution"], stage, wall, peak, None, metadata,
+                    (CostStageResult("original", stage),))
     if options.verbose != "off":
         finest = levels[-1]
         state = finest.solve.summary.stop_reason if finest.kind == "refined" else "coarsest"

@@ -20,13 +20,21 @@ class HelloSolveError(RuntimeError):
 
 
 def _points(value, name):
+    """Point matrices as the reference's ``_float32_matrix`` (types.py:26-39) keeps them: a device tensor as it is
+    (its dtype and layout are checked where they matter), anything else as contiguous fp32 on the host."""
     if torch.is_tensor(value):
-        if value.ndim != 2 or value.shape[0] < 1 or value.shape[1] < 1:
-            raise ValueError(f"{name} must be a nonempty 2-D array.")
-        return value.detach().to(torch.float32).contiguous()
-    array = np.ascontiguousarray(np.asarray(value, dtype=np.float32))
-    if array.ndim != 2 or array.shape[0] < 1 or array.shape[1] < 1:
-        raise ValueError(f"{name} must be a nonempty 2-D array.")
+        value = value.detach()
+        if value.is_cuda:
+            if value.ndim != 2 or min(value.shape) < 1:
+                raise ValueError(f"{name} must be a non-empty 2D matrix")
+            return value
+        value = value.float().numpy()
+    array = np.asarray(value, dtype=np.float32)
+    if array.ndim != 2:
+        raise ValueError(f"{name} must be a 2D array; got shape={array.shape}.")
+    if array.shape[0] < 1 or array.shape[1] < 1:
+        raise ValueError(f"{name} must be non-empty; got shape={array.shape}.")
+    array = np.ascontiguousarray(array)
     if not np.all(np.isfinite(array)):
         raise ValueError(f"{name} must contain only finite values.")
     return array
@@ -244,6 +252,47 @@ class SparseOTSolution:
 
         return sparse.coo_matrix((self.values, (self.rows, self.cols)), shape=self.shape)
 
+    def to_warm_start_state(self) -> "WarmStartState | GPUWarmStartState":
+        """The plan and duals as a warm-start state (state.py:11-40): device tensors stay on their device."""
+        if torch.is_tensor(self.values):
+            return GPUWarmStartState(self.rows.int().clone(), self.cols.int().clone(), self.values.clone(),
+                                     torch.cat((self.source_dual, self.target_dual)), int(self.shape[0]),
+                                     int(self.shape[1]), str(self.values.device))
+        return WarmStartState(self.rows.astype(np.int32), self.cols.astype(np.int32), self.values.astype(np.float64),
+                              np.concatenate((self.source_dual, self.target_dual)).astype(np.float64),
+                              int(self.shape[0]), int(self.shape[1]), None)
+
+
+@dataclass(frozen=True)
+class WarmStartState:
+    """A host-side sparse plan with its duals (the reference's ``state.WarmStartState``)."""
+    rows: np.ndarray
+    cols: np.ndarray
+    x_prev: np.ndarray
+    dual_uv: Optional[np.ndarray]
+    n_source: int
+    n_target: int
+    northwest_positions: Optional[np.ndarray] = None
+
+
+@dataclass(frozen=True)
+class GPUWarmStartState:
+    """A device-side sparse plan with its duals (the reference's ``state.GPUWarmStartState``)."""
+    rows: torch.Tensor
+    cols: torch.Tensor
+    x_prev: torch.Tensor
+    dual_uv: Optional[torch.Tensor]
+    n_source: int
+    n_target: int
+    device: str = "cuda"
+
+
+@dataclass(frozen=True)
+class CostStageResult:
+    """One cost stage in execution order and its per-level statistics (types.py:352-359)."""
+    name: str
+    solve: SolveStageResult
+
 
 @dataclass(frozen=True)
 class Result:
@@ -260,9 +309,14 @@ class Result:
     def original_cost_stage(self) -> SolveStageResult:
         return self.solve_stage
 
+    @property
+    def perturbed_cost_stage(self) -> Optional[SolveStageResult]:
+        return next((stage.solve for stage in self.cost_stages if stage.name == "perturbed"), None)
+
 
 __all__ = [
     "ActiveSupportStats", "BudgetedPruningStats", "COST_TYPES", "CoarsestSolveStats", "ConvergenceStats",
-    "DualViolationStats", "HelloSolveError", "InitializationStats", "IterationStats", "LevelResult", "Problem",
-    "RefinementResult", "RefinementSummary", "Result", "SolveLPStats", "SolveStageResult", "SparseOTSolution",
+    "CostStageResult", "DualViolationStats", "GPUWarmStartState", "HelloSolveError", "InitializationStats",
+    "IterationStats", "LevelResult", "Problem", "RefinementResult", "RefinementSummary", "Result", "SolveLPStats",
+    "SolveStageResult", "SparseOTSolution", "WarmStartState",
 ]

@@ -198,3 +198,55 @@ def test_consumed_inputs_come_back_in_the_callers_order(cuda, monkeypatch):
     assert torch.equal(X, Xc) and torch.equal(Y, Yc)
     with pytest.raises(ValueError, match="disjoint storage"):
         solve(X, X[:100], options=SolverOptions(consume_input_features=True, **opts))
+
+
+def test_gpu_resident_input_validation(cuda):
+    """hello_gpu_resident_test.py:267-276: the GPU-resident entry wants both sides as contiguous fp32 tensors on one
+    device, with disjoint storage when consumed."""
+    x = torch.randn(5, 3, device=cuda)
+    options = SolverOptions(gpu_resident=True, consume_input_features=True, verbose="off")
+    with pytest.raises(ValueError, match="disjoint storage"):
+        solve(x, x, options=options)
+    with pytest.raises(ValueError, match="contiguous FP32"):
+        solve(x.double(), x.clone(), options=options)
+    with pytest.raises(ValueError, match="same device"):
+        solve(x, x.cpu(), options=options)
+    with pytest.raises(ValueError, match="same device"):
+        solve(x.cpu().numpy(), x.clone(), options=options)
+
+
+@pytest.mark.parametrize("cost", ["l2^2", "l1", "l2", "linf"])
+@pytest.mark.parametrize("precision", ["fp32", "fp64", "finest_fp64"])
+def test_solution_contract_against_the_dense_lp(cuda, cost, precision):
+    """The reference's end-to-end check of the GPU-resident solve (hello_gpu_resident_test.py:73-104, without the
+    perturbed stage): consumed inputs unchanged afterwards, the plan on the device, marginals to 4e-6, the
+    objective against the exact dense LP (abs 4e-5, rel 1e-5; HiGHS here, POT's emd2 there), one "original" cost
+    stage, the returned duals' relative l2 violation over all pairs at most 1.1e-6, host export and warm start."""
+    rng = np.random.default_rng(910)
+    x = torch.tensor(rng.normal(size=(37, 7)), device=cuda, dtype=torch.float32)
+    y = torch.tensor(rng.normal(size=(43, 7)), device=cuda, dtype=torch.float32)
+    before_x, before_y = x.clone(), y.clone()
+    a, b = rng.uniform(0.1, 2, 37), rng.uniform(0.1, 2, 43)
+    a, b = a / a.sum(), b / b.sum()
+    result = solve(x, y, source_mass=torch.tensor(a, device=cuda), target_mass=b, cost=cost,
+                   options=SolverOptions(gpu_resident=True, consume_input_features=True, coarsest_size_threshold=8,
+                                         assignment_topk=2, pricing_topk=2, support_budget_factor=4,
+                                         cost_perturbation="off", cost_precision=precision, verbose="off"))
+    assert torch.equal(x, before_x) and torch.equal(y, before_y)
+    solution = result.solution
+    assert all(getattr(solution, k).is_cuda for k in ("rows", "cols", "values", "source_dual", "target_dual"))
+    dense = solution.to_sparse_matrix().to_dense()
+    torch.testing.assert_close(dense.sum(1), torch.tensor(a, device=cuda), atol=4e-6, rtol=0)
+    torch.testing.assert_close(dense.sum(0), torch.tensor(b, device=cuda), atol=4e-6, rtol=0)
+    delta = x.double()[:, None] - y.double()[None]
+    costs = {"l2^2": lambda: delta.square().sum(-1), "l1": lambda: delta.abs().sum(-1),
+             "l2": lambda: delta.square().sum(-1).sqrt(), "linf": lambda: delta.abs().amax(-1)}[cost]()
+    expected = _exact(costs.cpu().numpy(), a, b)
+    assert result.objective == pytest.approx(expected, abs=4e-5, rel=1e-5)
+    assert [stage.name for stage in result.cost_stages] == ["original"]
+    assert result.perturbed_cost_stage is None and result.original_cost_stage is result.solve_stage
+    violation = (solution.source_dual[:, None] + solution.target_dual[None] - costs).clamp_min(0)
+    assert float(violation.norm() / (1 + costs.norm())) <= 1.1e-6
+    assert isinstance(solution.to_cpu().values, np.ndarray)
+    state = solution.to_warm_start_state()
+    assert state.x_prev.is_cuda and state.dual_uv.numel() == 80 and (state.n_source, state.n_target) == (37, 43)

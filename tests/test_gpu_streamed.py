@@ -98,7 +98,8 @@ def test_streamed_solve_matches_the_resident_solve(cuda, monkeypatch):
     X = rng.standard_normal((n, d)).astype(np.float32)
     Y = (rng.standard_normal((m, d)) + 0.3).astype(np.float32)
     base = dict(coarsest_size_threshold=200, verbose="off", cost_perturbation="off")
-    ref = solve(X, Y, options=SolverOptions(gpu_resident=True, **base))
+    ref = solve(torch.as_tensor(X).to(cuda), torch.as_tensor(Y).to(cuda), options=SolverOptions(gpu_resident=True,
+                                                                                                   **base))
     monkeypatch.setattr(host_module, "STREAM_MIN_BYTES", 200 * d * 4)
     monkeypatch.setattr(host_module, "STREAM_CHUNK_BYTES", 500 * d * 4)
     monkeypatch.setattr(host_module, "STREAM_POLICY", "always")
