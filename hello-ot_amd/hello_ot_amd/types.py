@@ -41,12 +41,21 @@ def _points(value, name):
 
 
 def _mass(value, size, name):
+    """Masses as the reference's ``_mass_vector`` (types.py:49-63): uniform when absent, a device tensor kept on its
+    device in fp64, anything else a host fp64 vector; finite and strictly positive."""
+    if torch.is_tensor(value):
+        value = value.detach()
+        if value.is_cuda:
+            value = value.to(dtype=torch.float64).reshape(-1).contiguous()
+            if value.numel() != size or not bool(torch.all(torch.isfinite(value) & (value > 0))):
+                raise ValueError(f"{name} must have length {size} and finite, strictly positive values")
+            return value
+        value = value.double().numpy()
     if value is None:
-        return None
-    array = value.detach().double().cpu().numpy() if torch.is_tensor(value) else np.asarray(value, dtype=np.float64)
-    array = np.ascontiguousarray(array.reshape(-1))
+        return np.full(int(size), 1.0 / float(size), dtype=np.float64)
+    array = np.ascontiguousarray(np.asarray(value, dtype=np.float64).reshape(-1))
     if array.size != size:
-        raise ValueError(f"{name} must have {size} entries.")
+        raise ValueError(f"{name} must have length {size}; got {array.size}.")
     if not np.all(np.isfinite(array)) or np.any(array <= 0.0):
         raise ValueError(f"{name} must contain only finite, strictly positive values.")
     return array

@@ -51,6 +51,18 @@ def test_problem_validation():
         Problem(np.zeros((3, 2)), np.zeros((3, 2)), "l1", source_mass=[1.0, 0.0, 1.0])
     p = Problem(np.ones((4, 2)), np.ones((5, 2)), " L2^2 ")
     assert p.shape == (4, 5) and p.cost_type == "l2^2" and p.source_points.dtype == np.float32
+    # test_hello_ot_public_api.py:35-62, 80-85: uniform masses by default; zero, negative, NaN and inf refused
+    np.testing.assert_array_equal(p.source_mass, np.full(4, 0.25))
+    np.testing.assert_array_equal(p.target_mass, np.full(5, 0.2))
+    for mass in ([0.0, 1.0], [-0.1, 1.1], [np.nan, 1.0], [np.inf, 1.0]):
+        with pytest.raises(ValueError, match="strictly positive"):
+            Problem(np.zeros((2, 1)), np.zeros((2, 1)), "l2^2", source_mass=np.asarray(mass))
+        with pytest.raises(ValueError, match="strictly positive"):
+            Problem(np.zeros((2, 1)), np.zeros((2, 1)), "l2^2", target_mass=np.asarray(mass))
+    with pytest.raises(ValueError, match="2D array"):
+        Problem(np.zeros(3), np.zeros((3, 1)), "l2^2")
+    with pytest.raises(ValueError, match="non-empty"):
+        Problem(np.zeros((0, 2)), np.zeros((3, 2)), "l2^2")
 
 
 def test_hierarchy_chain_and_global_shuffle():
