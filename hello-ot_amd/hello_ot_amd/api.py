@@ -114,8 +114,8 @@ def _stream_source(value, target, cost_type: str, device, options: SolverOptions
 def solve_problem(problem: Problem, options: SolverOptions, *, max_iterations: int = 100,
                   random_seed: int = 42) -> Result:
     options.check_supported()
-    if options.stopping_norm != "l2":
-        raise NotImplementedError("the MI355X build stops on the relative l2 dual infeasibility (stopping_norm='l2')")
+    if options.stopping_norm == "finest_linf" and problem.cost_type != "l2^2":
+        raise ValueError("finest_linf currently requires l2^2")   # gpu_resident/solver.py:235-236
     require_native_runtime_compatibility()
     device = _device_of(problem)
     n, m = problem.shape

@@ -21,6 +21,18 @@ from typing import Literal, Optional
 POSITIVE_SUPPORT_TOLERANCE = 1e-15
 
 
+def finest_stopping_norm(policy: str) -> str:
+    """The norm the finest level stops on under ``stopping_norm`` (config.py:31-36)."""
+    if policy not in {"l2", "finest_linf"}:
+        raise ValueError("stopping_norm must be one of: l2, finest_linf")
+    return "linf" if policy == "finest_linf" else "l2"
+
+
+def level_stopping_norm(policy: str, level_index: int) -> str:
+    """The norm hierarchy level ``level_index`` (0 = finest) stops on (config.py:39-46): coarser levels always l2."""
+    return finest_stopping_norm(policy) if int(level_index) == 0 else "l2"
+
+
 def level_precision(policy: str, level_index: int) -> str:
     """Cost arithmetic of hierarchy level ``level_index`` (0 = finest) under ``cost_precision`` (config.py:23-28)."""
     if policy not in {"fp32", "fp64", "finest_fp64"}:
@@ -138,5 +150,6 @@ class SolverOptions:
             raise NotImplementedError("the MI355X scans keep at most 32 candidates per row")
 
 
-__all__ = ["POSITIVE_SUPPORT_TOLERANCE", "SolverOptions", "active_support_budget", "level_precision",
-           "normalize_pricing_topk", "primal_support_cap", "validate_support_budget_factor"]
+__all__ = ["POSITIVE_SUPPORT_TOLERANCE", "SolverOptions", "active_support_budget", "finest_stopping_norm",
+           "level_precision", "level_stopping_norm", "normalize_pricing_topk", "primal_support_cap",
+           "validate_support_budget_factor"]

@@ -26,7 +26,7 @@ import time
 import numpy as np
 import torch
 
-from ..config import active_support_budget, primal_support_cap
+from ..config import active_support_budget, level_stopping_norm, primal_support_cap
 from ..types import (ActiveSupportStats, BudgetedPruningStats, ConvergenceStats, DualViolationStats,
                      HelloSolveError, InitializationStats, IterationStats, LevelResult, RefinementResult,
                      RefinementSummary, SolveLPStats)
@@ -187,7 +187,8 @@ class LevelRefinement:
                            + (f" sparsified {thinned.input_nnz}->{thinned.output_nnz}" if thinned else ""))
         xv, xi, yv, yi, metrics = self.cost.scan(self.dual, options.pricing_topk, certificate=True)
         scan_seconds = watch.lap()
-        converged = metrics["l2"] <= tol
+        norm = level_stopping_norm(options.stopping_norm, self.index)   # gpu_resident/solver.py:86, 100
+        converged = metrics[norm] <= tol
         if not converged and self.detect_reentry and self.reentry_seen:
             self.perturbation_triggered = True
         grown = size_before
@@ -212,9 +213,9 @@ class LevelRefinement:
             DualViolationStats(scan_seconds, metrics["count"], added),
             BudgetedPruningStats(prune_seconds, grown, len(support), self.budget, grown > self.budget),
             ActiveSupportStats(size_before, grown, len(support), self.peak),
-            ConvergenceStats(metrics["l2"], tol, converged, metrics["l2"], metrics["linf"], metrics["max"], "l2")))
+            ConvergenceStats(metrics[norm], tol, converged, metrics["l2"], metrics["linf"], metrics["max"], norm)))
         _progress(options, f"level={self.index} iteration={iteration} scan {scan_seconds:.3f}s "
-                           f"dual_l2={metrics['l2']:.3e} added={added} support={len(support)}")
+                           f"dual_{norm}={metrics[norm]:.3e} added={added} support={len(support)}")
         return converged
 
     def run(self, max_iterations: int, initialization: InitializationStats, started: float) -> LevelResult:

@@ -250,3 +250,27 @@ def test_solution_contract_against_the_dense_lp(cuda, cost, precision):
     assert isinstance(solution.to_cpu().values, np.ndarray)
     state = solution.to_warm_start_state()
     assert state.x_prev.is_cuda and state.dual_uv.numel() == 80 and (state.n_source, state.n_target) == (37, 43)
+
+
+def test_finest_linf_stops_the_finest_level_on_the_linf_violation(cuda):
+    """stopping_norm="finest_linf" (gpu_resident/solver.py:86-100): the finest level stops when the certificate's
+    linf metric max sigma+ / (1 + max|c|) is at most the tolerance, the other levels on l2; l2^2 only."""
+    rng = np.random.default_rng(31)
+    n, m, d = 220, 190, 5
+    X = rng.random((n, d)).astype(np.float32)
+    Y = (rng.random((m, d)) + 0.2).astype(np.float32)
+    opts = dict(coarsest_size_threshold=40, verbose="off", cost_perturbation="off")
+    r = solve(X, Y, options=SolverOptions(stopping_norm="finest_linf", **opts))
+    finest = r.solve_stage.levels[-1].solve
+    last = finest.iterations[-1].convergence
+    assert finest.summary.converged and last.norm == "linf"
+    assert last.dual_feasibility == last.relative_linf_dual_feasibility <= 1e-6
+    assert all(it.convergence.norm == "l2" for level in r.solve_stage.levels[1:-1] for it in level.solve.iterations)
+    # the dense check of the returned duals in linf
+    C = _cost_matrix(X, Y, "l2^2")
+    f, g = r.solution.source_dual.cpu().numpy(), r.solution.target_dual.cpu().numpy()
+    assert np.clip(f[:, None] + g[None, :] - C, 0, None).max() / (1.0 + np.abs(C).max()) <= 1.1e-6
+    exact = _exact(C, np.full(n, 1.0 / n), np.full(m, 1.0 / m))
+    assert abs(r.objective - exact) <= 5e-6 * abs(exact)
+    with pytest.raises(ValueError, match="finest_linf currently requires l2"):
+        solve(X, Y, cost="l1", options=SolverOptions(stopping_norm="finest_linf", **opts))

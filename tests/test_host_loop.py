@@ -31,6 +31,21 @@ def test_options_defaults_and_validation_match_the_reference():
         SolverOptions(cost_precision=precision).check_supported()
 
 
+def test_stopping_norm_per_level_follows_the_reference():
+    """test_hello_ot_public_api.py:114-130: finest_linf stops the finest level on linf, every other level on l2."""
+    from hello_ot_amd.config import finest_stopping_norm, level_stopping_norm
+
+    assert SolverOptions().stopping_norm == "l2"
+    assert SolverOptions(stopping_norm="finest_linf").stopping_norm == "finest_linf"
+    for bad in ("linf", "other"):
+        with pytest.raises(ValueError, match="stopping_norm"):
+            SolverOptions(stopping_norm=bad)
+    assert level_stopping_norm("l2", level_index=0) == "l2" and level_stopping_norm("l2", level_index=3) == "l2"
+    assert level_stopping_norm("finest_linf", level_index=0) == "linf"
+    assert level_stopping_norm("finest_linf", level_index=1) == "l2"
+    assert finest_stopping_norm("finest_linf") == "linf"
+
+
 def test_cost_precision_per_level_follows_the_reference():
     """config.py:23-28: fp64 everywhere, or only at the finest level (index 0) for finest_fp64."""
     from hello_ot_amd.config import level_precision
