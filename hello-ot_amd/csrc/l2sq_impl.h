@@ -2072,6 +2072,10 @@ struct ListQueue {
     float* thr = nullptr;
 };
 
+// floor (optional, per row of A): the caller already holds k entries of the row scoring at least floor[row], so
+// entries whose exact score is below it may be left out of the row's output (they cannot enter the caller's merged
+// top k). With a floor the output holds the row's exact top k among the entries that can reach it, and fewer
+// (padded with -inf / -1) when fewer can.
 template <int KL, int KM, int G, bool COLS, bool DEFER = false>
 __global__ __launch_bounds__(256) void l2sq_finalize(
     const float* __restrict__ A, const float* __restrict__ B, int64_t R, int d, int nlists,
@@ -2079,7 +2083,7 @@ __global__ __launch_bounds__(256) void l2sq_finalize(
     const double* __restrict__ anorm, const unsigned long long* __restrict__ bmaxima, double scale, int k,
     BoundArgs bnd, double* __restrict__ out_val, int* __restrict__ out_idx, int* __restrict__ redo,
     float* __restrict__ redo_thr, int* __restrict__ redo_count, DeferBufs defer = DeferBufs{},
-    ListQueue lq = ListQueue{}) {
+    ListQueue lq = ListQueue{}, const double* __restrict__ floor = nullptr) {
     static_assert(KL <= KM, "merged lists hold at least one partial list");
     const int lane = threadIdx.x & 63;
     const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -2147,9 +2151,12 @@ __global__ __launch_bounds__(256) void l2sq_finalize(
         const double mg = key_double(bnd.qmax[2]), mr = key_double(bnd.qmax[3]);
         b += scale * (qt[0] * mb + qt[1] * ma + qt[2] * mg + 5.0 * 0x1p-24 * qt[3] * mr) * (1.0 + 1e-6);
     }
+    // an entry with w < fcut has an exact score below the floor (|sigma - w| <= b); -inf without a floor
+    const double fcut = floor ? floor[row] - b : -INFINITY;
     // wave top-KM: rounds of an arg-best over the lanes' list heads (tw non-increasing). The rounds stop after the
-    // first entry t >= k - 1 below wk - 2b (or after the last real entry): no later entry is evaluated, and one
-    // that the merge drops then has w <= tw[t] < wk - 2b, so every decision below is what all KM rounds give.
+    // first entry t >= k - 1 below wk - 2b, at the first entry below fcut (or after the last real entry): no later
+    // entry is evaluated, and one that the merge drops then has w <= tw[t] < max(wk - 2b, fcut), so every decision
+    // below is what all KM rounds give.
     float tw[KM];
     int ti[KM];
 #pragma unroll
@@ -2177,14 +2184,17 @@ __global__ __launch_bounds__(256) void l2sq_finalize(
                 li[KM - 1] = -1;
             }
             if (t == k - 1) wk = nreal < k ? -INFINITY : bw;
-            if (t + 1 >= k && (t + 1 >= kept || (double)bw < (double)wk - 2.0 * b)) more = false;
+            if ((t + 1 >= k && (t + 1 >= kept || (double)bw < (double)wk - 2.0 * b)) || (double)bw < fcut)
+                more = false;
         }
     }
     // Candidates outside the kept list were dropped by a full partial list (w <= tail) or by the merge
-    // (w <= tw[KM-1]); they cannot reach the exact top-k when that bound is below wk - 2b.
+    // (w <= tw[KM-1]); they cannot reach the exact top-k when that bound is below wk - 2b, nor the output when it
+    // is below fcut.
+    const double cut = fmax((double)wk - 2.0 * b, fcut);
     const bool merge_dropped = nreal > KM;
-    const bool list_hit = full && (double)tail >= (double)wk - 2.0 * b;
-    const bool merge_hit = merge_dropped && (double)tw[KM - 1] >= (double)wk - 2.0 * b;
+    const bool list_hit = full && (double)tail >= cut;
+    const bool merge_hit = merge_dropped && (double)tw[KM - 1] >= cut;
     if (list_hit || merge_hit) {
         // queued for the wide pass: a candidate of the exact top-k has sigma >= sigma_k* >= wk - b, hence
         // w >= wk - 2b (the threshold is rounded down to fp32). Unless a full list's tail reaches that bound, the
@@ -2196,7 +2206,7 @@ __global__ __launch_bounds__(256) void l2sq_finalize(
         if (lane == 0) {
             const bool from_lists = !list_hit && lq.rows != nullptr;
             const int slot = atomicAdd(redo_count + (from_lists ? 1 : 0), 1);
-            const double t = (double)wk - 2.0 * b;
+            const double t = cut;
             float t32 = (float)t;
             if ((double)t32 > t) t32 = nextafterf(t32, -INFINITY);
             if (from_lists) {
@@ -2211,13 +2221,13 @@ __global__ __launch_bounds__(256) void l2sq_finalize(
     }
     // Exact re-evaluation of the kept entries that can reach the exact top-k: an entry with w < wk - 2b has an
     // exact score below wk - b, under each of the k entries with w >= wk, so only the sorted prefix with
-    // w >= wk - 2b is evaluated (always at least the first min(k, kept)). Lane e owns entry e.
-    const double cut = (double)wk - 2.0 * b;
+    // w >= cut is evaluated (without a floor for the row always at least the first min(k, kept)). Lane e owns
+    // entry e.
     int need = 0;
 #pragma unroll
     for (int e = 0; e < KM; ++e)
         if (e < kept && (double)tw[e] >= cut) need = e + 1;
-    if (need < (kept < k ? kept : k)) need = kept < k ? kept : k;
+    if (fcut == -INFINITY && need < (kept < k ? kept : k)) need = kept < k ? kept : k;
     if constexpr (DEFER) {
         if (lane == 0) {
             defer.need[row] = need;
@@ -2591,6 +2601,7 @@ struct WideBufs {
     float* redo_l_thr;  // [m + n] their thresholds
     int* counts;       // [4]: redo2 and redo3 lengths
     unsigned int* rowthr;  // [rows of a sweep launch] the sweeps' shared row thresholds (row_threshold_*)
+    const double* col_floor = nullptr;  // [n] the caller's column floors (l2sq_finalize's floor), or none
 };
 
 // Per-side data of the int8 sweep (HM_INT8X3; null otherwise): row scales, ||.||_1, the rows' error terms
@@ -3124,7 +3135,7 @@ int run_bidir(hipStream_t st, const float* X, const float* Y, int64_t m, int64_t
             hipLaunchKernelGGL((l2sq_finalize<K1, KM, 1, true, true>), dim3((unsigned)((n + 3) / 4)), dim3(256), 0, st,
                                Y, X, n, d, (int)panels, colpart, db, qb, ynorm, maxima, scale, k, bound_for(true, 0),
                                cval, cidx, redo, wide.redo_thr, redo_count, wide.defer,
-                               ListQueue{wide.redo_l, wide.redo_l_thr});
+                               ListQueue{wide.redo_l, wide.redo_l_thr}, wide.col_floor);
             HM_LAUNCH_CHECK("l2sq_col_finalize");
             const unsigned egrid = (unsigned)((n + 255) / 256 < 8192 ? (n + 255) / 256 : 8192);
             hipLaunchKernelGGL(fill_u32, dim3((unsigned)((rows + 256) / 256)), dim3(256), 0, st,
@@ -3197,7 +3208,8 @@ int run_bidir(hipStream_t st, const float* X, const float* Y, int64_t m, int64_t
             hipLaunchKernelGGL((l2sq_finalize<K1, KM, 2, true>), dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, st,
                                Y + yb * d, X, rows, d, 2 * plan2.S, part, db + yb, qb, ynorm + yb, maxima, scale, k,
                                bound_for(true, yb), col_val + yb * k, col_idx + yb * k, redo, wide.redo_thr,
-                               redo_count, DeferBufs{}, ListQueue{wide.redo_l, wide.redo_l_thr});
+                               redo_count, DeferBufs{}, ListQueue{wide.redo_l, wide.redo_l_thr},
+                               wide.col_floor ? wide.col_floor + yb : nullptr);
             prof_end(st);
             HM_LAUNCH_CHECK("l2sq_col_finalize");
             if (int rc = wide_resolve(st, split, two_level, Y + yb * d, SYc, X, SX, m, d, sd, ld, qb32,

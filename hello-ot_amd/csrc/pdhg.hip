@@ -135,10 +135,10 @@ inline int end_bit_for(int64_t nodes) {
 }
 
 inline size_t sort_tmp_bytes(int64_t nodes, int64_t e) {
-    size_t bytes = 0;
-    hipcub::DeviceRadixSort::SortPairs(nullptr, bytes, (const uint32_t*)nullptr, (uint32_t*)nullptr,
-                                       (const int32_t*)nullptr, (int32_t*)nullptr, (int)(2 * e), 0,
-                                       end_bit_for(nodes));
+    size_t bytes = 0;  // a size query: it only writes `bytes`
+    (void)hipcub::DeviceRadixSort::SortPairs(nullptr, bytes, (const uint32_t*)nullptr, (uint32_t*)nullptr,
+                                             (const int32_t*)nullptr, (int32_t*)nullptr, (int)(2 * e), 0,
+                                             end_bit_for(nodes));
     return bytes;
 }
 
@@ -146,9 +146,10 @@ inline size_t sort_tmp_bytes(int64_t nodes, int64_t e) {
 constexpr int ORDER_KEY_BITS = 63;
 
 inline size_t order_sort_tmp_bytes(int64_t n, int64_t nt) {
-    size_t bytes = 0;
-    hipcub::DeviceRadixSort::SortKeys(nullptr, bytes, (const unsigned long long*)nullptr,
-                                      (unsigned long long*)nullptr, (int)(n > nt ? n : nt), 0, ORDER_KEY_BITS);
+    size_t bytes = 0;  // a size query: it only writes `bytes`
+    (void)hipcub::DeviceRadixSort::SortKeys(nullptr, bytes, (const unsigned long long*)nullptr,
+                                            (unsigned long long*)nullptr, (int)(n > nt ? n : nt), 0,
+                                            ORDER_KEY_BITS);
     return bytes;
 }
 

@@ -249,7 +249,7 @@ int check_call(const float* X, const float* Y, const double* p, const double* q,
 int pricing_call(hipStream_t st, const float* X, const float* Y, const double* p, const double* q, const double* qb,
                  const double* db, int64_t m, int64_t n, int32_t d, int32_t k, double scale, uint32_t flags,
                  double* row_val, int32_t* row_idx, double* col_val, int32_t* col_idx, double* stats,
-                 const ResidentY* res, void* workspace, size_t workspace_bytes) {
+                 const ResidentY* res, void* workspace, size_t workspace_bytes, const double* col_floor = nullptr) {
     const size_t need = workspace_need(m, n, d, k, flags, res != nullptr);
     HM_CHECK_ARG(workspace != nullptr, "workspace is required");
     if (workspace_bytes < need)
@@ -270,6 +270,7 @@ int pricing_call(hipStream_t st, const float* X, const float* Y, const double* p
     flags = effective_flags(flags);
     layout(a, m, n, d, k, flags, &xnorm, &ynorm, &qb32, &p32, &db32, &ge32, &maxima, &part, &colpart, &colthr, &cval,
            &cidx, &blockstats, &redo, &redo_count, &xsplit, &ysplit, &rpv, &rpi, &wide, &q8, res != nullptr);
+    wide.col_floor = col_floor;
     if (own_rows) {
         row_val = a.template take<double>((size_t)m * k);
         row_idx = a.template take<int>((size_t)m * k);
@@ -364,13 +365,15 @@ extern "C" size_t hm_pricing_l2sq_resident_workspace_bytes(int64_t m, int64_t n,
     return workspace_need(m, n, d, k, flags, true);
 }
 
-extern "C" int hm_pricing_l2sq_resident(void* stream, const float* X, const float* Y, const double* p, const double* q,
-                                        const double* qb, const double* db, int64_t m, int64_t n, int32_t d, int32_t k,
-                                        double scale, uint32_t flags, double* row_val, int32_t* row_idx,
-                                        double* col_val, int32_t* col_idx, double* stats, const void* resident,
-                                        size_t resident_bytes_, void* workspace, size_t workspace_bytes) {
+extern "C" int hm_pricing_l2sq_resident_floor(void* stream, const float* X, const float* Y, const double* p,
+                                              const double* q, const double* qb, const double* db, int64_t m,
+                                              int64_t n, int32_t d, int32_t k, double scale, uint32_t flags,
+                                              const double* col_floor, double* row_val, int32_t* row_idx,
+                                              double* col_val, int32_t* col_idx, double* stats, const void* resident,
+                                              size_t resident_bytes_, void* workspace, size_t workspace_bytes) {
     if (int rc = check_call(X, Y, p, q, qb, db, m, n, d, k, scale, flags, row_val, row_idx, col_val, col_idx, stats))
         return rc;
+    HM_CHECK_ARG(!col_floor || (flags & HM_COLS), "a column floor needs HM_COLS");
     HM_CHECK_ARG(resident != nullptr, "resident side buffer is required");
     if (resident_bytes_ < sizeof(ResidentHead))
         return fail(HM_EINVAL, "resident buffer smaller than a side of n=%lld d=%d needs", (long long)n, d);
@@ -390,5 +393,15 @@ extern "C" int hm_pricing_l2sq_resident(void* stream, const float* X, const floa
     ResidentY r;
     resident_layout(a, n, d, flags, &r);
     return pricing_call(st, X, Y, p, q, qb, db, m, n, d, k, scale, flags, row_val, row_idx, col_val, col_idx, stats,
-                        &r, workspace, workspace_bytes);
+                        &r, workspace, workspace_bytes, col_floor);
+}
+
+extern "C" int hm_pricing_l2sq_resident(void* stream, const float* X, const float* Y, const double* p, const double* q,
+                                        const double* qb, const double* db, int64_t m, int64_t n, int32_t d, int32_t k,
+                                        double scale, uint32_t flags, double* row_val, int32_t* row_idx,
+                                        double* col_val, int32_t* col_idx, double* stats, const void* resident,
+                                        size_t resident_bytes_, void* workspace, size_t workspace_bytes) {
+    return hm_pricing_l2sq_resident_floor(stream, X, Y, p, q, qb, db, m, n, d, k, scale, flags, nullptr, row_val,
+                                          row_idx, col_val, col_idx, stats, resident, resident_bytes_, workspace,
+                                          workspace_bytes);
 }

@@ -62,6 +62,8 @@ SIGNATURES = {
     "hm_pricing_l2sq_resident_workspace_bytes": (_SZ, [_I64, _I64, _I32, _I32, _U32]),
     "hm_pricing_l2sq_resident": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I32, _I32, _D, _U32,
                                                 _P, _P, _P, _P, _P, _P, _SZ, _P, _SZ]),
+    "hm_pricing_l2sq_resident_floor": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I32, _I32, _D,
+                                                      _U32, _P, _P, _P, _P, _P, _P, _P, _SZ, _P, _SZ]),
     "hm_pricing_norm_workspace_bytes": (_SZ, [_I64, _I64, _I32, _I32, _U32]),
     "hm_pricing_norm": (ctypes.c_int, [_P, _P, _P, _P, _P, _I64, _I64, _I32, _I32, _I32, _U32,
                                        _P, _P, _P, _P, _P, _P, _SZ]),

@@ -92,7 +92,7 @@ class ResidentSide:
 
 
 def pricing_l2sq(x, y, nx, ny, qb, dbb, k, *, dot_scale=2.0, rows=True, cols=True, stats=True, linf=False,
-                 precision="auto", resident: ResidentSide | None = None):
+                 precision="auto", resident: ResidentSide | None = None, col_floor=None):
     """Raw l2^2 pricing: returns (row_vals, row_idx, col_vals, col_idx, stats5) with None for skipped parts.
 
     ``stats5`` = (num, den, count, max sigma+, max|cost|); max|cost| is 0 unless ``linf``. ``precision`` picks the
@@ -101,7 +101,13 @@ def pricing_l2sq(x, y, nx, ny, qb, dbb, k, *, dot_scale=2.0, rows=True, cols=Tru
     on); all feed the same exact fp64 re-evaluation, so the outputs are identical and only the speed (and the
     rescan rate) differs. With ``resident`` (a ``ResidentSide`` of ``y``) the side's preparation is reused and the
     precision is the side's.
+
+    ``col_floor`` (with ``resident`` and ``cols``): fp64 per column of ``y``, a score the caller's own list of that
+    column already reaches k times. Column entries scoring below it may then be left out (padded with -inf / -1);
+    merging the outputs into the caller's lists gives what the full lists give.
     """
+    if col_floor is not None and (resident is None or not cols):
+        raise ValueError("col_floor needs a resident side and the column lists")
     if resident is not None:
         if precision not in ("auto", resident.precision):
             raise ValueError(f"the resident side was prepared for precision {resident.precision!r}")
@@ -128,14 +134,19 @@ def pricing_l2sq(x, y, nx, ny, qb, dbb, k, *, dot_scale=2.0, rows=True, cols=Tru
                                      _lib.ptr(ri), _lib.ptr(cv), _lib.ptr(ci), _lib.ptr(st), _lib.ptr(ws), ws.numel())
         _lib.check(rc, "hm_pricing_l2sq")
         return rv, ri, cv, ci, st
+    if col_floor is not None:
+        col_floor = _c(col_floor)
+        if col_floor.dtype != torch.float64 or tuple(col_floor.shape) != (n,) or col_floor.device != dev:
+            raise ValueError(f"col_floor must be a float64 vector of {n} values on {dev}")
     ws = _workspace(lib.hm_pricing_l2sq_resident_workspace_bytes(m, n, d, k, flags), dev)
     with torch.cuda.device(dev):
-        rc = lib.hm_pricing_l2sq_resident(_lib.stream_handle(dev), _lib.ptr(x), _lib.ptr(y), _lib.ptr(nx),
-                                          _lib.ptr(ny), _lib.ptr(qb), _lib.ptr(dbb), m, n, d, k, float(dot_scale),
-                                          flags, _lib.ptr(rv), _lib.ptr(ri), _lib.ptr(cv), _lib.ptr(ci), _lib.ptr(st),
-                                          _lib.ptr(resident.buffer), resident.buffer.numel(), _lib.ptr(ws),
-                                          ws.numel())
-    _lib.check(rc, "hm_pricing_l2sq_resident")
+        rc = lib.hm_pricing_l2sq_resident_floor(_lib.stream_handle(dev), _lib.ptr(x), _lib.ptr(y), _lib.ptr(nx),
+                                                _lib.ptr(ny), _lib.ptr(qb), _lib.ptr(dbb), m, n, d, k,
+                                                float(dot_scale), flags, _lib.ptr(col_floor), _lib.ptr(rv),
+                                                _lib.ptr(ri), _lib.ptr(cv), _lib.ptr(ci), _lib.ptr(st),
+                                                _lib.ptr(resident.buffer), resident.buffer.numel(), _lib.ptr(ws),
+                                                ws.numel())
+    _lib.check(rc, "hm_pricing_l2sq_resident_floor")
     return rv, ri, cv, ci, st
 
 

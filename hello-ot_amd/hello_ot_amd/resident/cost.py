@@ -192,9 +192,11 @@ class Cost:
             if l2sq:
                 # a columns-only scan runs the library's role-swapped pass per chunk (the target rows against the
                 # chunk, reading the resident side's copy): as fast here as column lists fused into a row sweep,
-                # and without the fused lists' partial-list buffer (up to 12 GiB)
+                # and without the fused lists' partial-list buffer (up to 12 GiB). The k-th score of each running
+                # column list is the chunk's floor: columns the chunk cannot change skip their exact re-evaluation.
+                floor = best[0][:, k - 1].contiguous() if (cols and best is not None) else None
                 out = pricing_l2sq(x, self.target, p[s:e], q, f[s:e] - p[s:e], db, k, rows=rows, cols=cols,
-                                   stats=certificate, linf=certificate, resident=side)
+                                   stats=certificate, linf=certificate, resident=side, col_floor=floor)
             else:
                 out = pricing_norm(x, self.target, f[s:e], g, k, NORM_KINDS[self.kind], rows=rows, cols=cols,
                                    stats=certificate, linf=certificate, precision=self.precision)

@@ -115,6 +115,23 @@ int hm_pricing_l2sq_resident(void* stream, const float* X, const float* Y, const
                              void* workspace, size_t workspace_bytes);
 
 /*
+ * hm_pricing_l2sq_resident with a floor per column: col_floor[n] (fp64, HM_COLS only; NULL = none) holds for each
+ * Y row a score that the caller's own running list of that column already reaches k times, and entries whose
+ * exact score is below it may then be left out of the column's output (padded with -inf / -1). The outputs keep
+ * every entry of the column's exact top k that scores at least the floor, so merging them into the caller's lists
+ * gives the same lists as without a floor. No counterpart in the reference, whose streamed chunks merge full
+ * per-chunk lists (kernels/bilinear_topk.py:255-368, torch.topk): it is for a caller that streams the X side in
+ * chunks and keeps the column lists across them, where the floor lets each chunk skip the exact re-evaluation of
+ * columns that the chunk cannot change. col_floor = NULL is hm_pricing_l2sq_resident.
+ */
+int hm_pricing_l2sq_resident_floor(void* stream, const float* X, const float* Y, const double* p, const double* q,
+                                   const double* qb, const double* db, int64_t m, int64_t n, int32_t d, int32_t k,
+                                   double scale, uint32_t flags, const double* col_floor, double* row_val,
+                                   int32_t* row_idx, double* col_val, int32_t* col_idx, double* stats,
+                                   const void* resident, size_t resident_bytes, void* workspace,
+                                   size_t workspace_bytes);
+
+/*
  * Norm-cost (l1 / linf / l2) bidirectional pricing scan on VALU with the full-edge certificate.
  * Replaces ScanExtension.fused_gcost_bidir_certificate (kernels/generic_scan.py:533-543) ->
  * bidirectional(kind 0/1/2) (generic_scan.py:328-405), i.e. pricing.cu scan_kernel (pricing.cu:71-161)

@@ -86,6 +86,9 @@ def test_resident_side_sizes_and_validation():
     rc = lib.hm_pricing_l2sq_resident(None, one, one, one, one, one, one, 10, 10, 4, 2, 2.0, 1, one, one, one, one,
                                       one, one, 8, one, 1 << 20)
     assert rc == _lib.HM_EINVAL and "resident buffer smaller" in _lib.last_error()
+    rc = lib.hm_pricing_l2sq_resident_floor(None, one, one, one, one, one, one, 10, 10, 4, 2, 2.0, 1, one, one, one,
+                                            one, one, one, one, 1 << 20, one, 1 << 20)
+    assert rc == _lib.HM_EINVAL and "column floor needs HM_COLS" in _lib.last_error()
 
 
 def test_python_mirror_rejects_host_tensors_like_the_reference():

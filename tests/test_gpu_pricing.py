@@ -575,6 +575,54 @@ def test_scan_extension_norm_directional_and_certificate(cuda, kind):
 
 
 @pytest.mark.parametrize("precision", ["fp32", "bf16x3", "int8x3"])
+@pytest.mark.parametrize("k,rows", [(4, False), (2, True)])
+def test_l2sq_column_floor_keeps_every_entry_above_it(cuda, precision, k, rows):
+    """hm_pricing_l2sq_resident_floor: with a floor per column the column lists keep, in place, every entry of the
+    full lists that scores at least the floor (ties at the floor included), and whatever follows scores below it or
+    is padding; merged into the lists the floors came from they give exactly the full lists' merge. Columns-only
+    calls take the role-swapped pass, rows + columns with k <= 2 the fused column lists."""
+    from hello_ot_amd.resident.cost import merge_columns
+
+    X, Y, p, q, qb, db = _l2sq_case(600, 3000, 300, seed=37)
+    tX, tY, tp, tq, tqb, tdb = _to(cuda, X, Y, p, q, qb, db)
+    side = ResidentSide(tY, precision)
+    first = pricing_l2sq(tX[:256], tY, tp[:256], tq, tqb[:256], tdb, k, rows=rows, stats=False, resident=side)
+    full = pricing_l2sq(tX[256:], tY, tp[256:], tq, tqb[256:], tdb, k, rows=rows, stats=False, resident=side)
+    fv, fi = full[2].cpu().numpy(), full[3].cpu().numpy()
+    # floors: the first chunk's k-th scores, then some columns without one, some set to an entry of the full list
+    # (a tie at the floor) and some above every score
+    floor = first[2][:, k - 1].clone()
+    floor[::7] = -float("inf")
+    floor[3::11] = full[2][3::11, 0]
+    floor[5::13] = full[2][5::13, k - 1]
+    floor[9::17] = 1e300
+    got = pricing_l2sq(tX[256:], tY, tp[256:], tq, tqb[256:], tdb, k, rows=rows, stats=False, resident=side,
+                       col_floor=floor)
+    if rows:
+        assert torch.equal(got[0], full[0]) and torch.equal(got[1], full[1])
+    gv, gi = got[2].cpu().numpy(), got[3].cpu().numpy()
+    fl = floor.cpu().numpy()[:, None]
+    above = fv >= fl                                     # lists are sorted: a prefix of each row
+    np.testing.assert_array_equal(np.where(above, gv, 0.0), np.where(above, fv, 0.0))
+    np.testing.assert_array_equal(np.where(above, gi, 0), np.where(above, fi, 0))
+    rest = ~above
+    assert (gv[rest] < fl.repeat(k, axis=1)[rest]).all()
+    assert ((gi[rest] == -1) == np.isneginf(gv[rest])).all()
+    skipped = int(np.isneginf(gv).sum() - np.isneginf(fv).sum())
+    assert skipped > 0                                   # columns the chunk cannot change were left out
+    # the streamed scan's use: the floors of the first chunk's lists, then the merge
+    base = first[2][:, k - 1].contiguous()
+    got = pricing_l2sq(tX[256:], tY, tp[256:], tq, tqb[256:], tdb, k, rows=rows, stats=False, resident=side,
+                       col_floor=base)
+    shift = lambda out: (out[2], torch.where(out[3] >= 0, out[3] + 256, out[3]))
+    ref_v, ref_i = merge_columns((first[2], first[3]), shift(full), k)
+    mv, mi = merge_columns((first[2], first[3]), shift(got), k)
+    assert torch.equal(mv, ref_v) and torch.equal(mi, ref_i)
+    with pytest.raises(ValueError, match="col_floor"):
+        pricing_l2sq(tX, tY, tp, tq, tqb, tdb, k, col_floor=base)
+
+
+@pytest.mark.parametrize("precision", ["fp32", "bf16x3", "int8x3"])
 def test_l2sq_resident_side_gives_the_same_outputs(cuda, precision):
     """Query chunks priced against a resident Y side (prepared once) give exactly the ordinary call's outputs,
     chunk after chunk; the first chunk also equals the oracle. A side prepared for another precision, or another
