@@ -1966,6 +1966,52 @@ struct BoundArgs {
     const unsigned long long* qmax = nullptr;
 };
 
+// Rigorous bound b on |w - (sigma - abias[row])| for every candidate of row `row`: w is the sweep's fp32 score of the
+// pair (ranking without the row's own bias), sigma its exact fp64 score.
+__device__ __forceinline__ double row_bound(int64_t row, const double* __restrict__ anorm,
+                                            const double* __restrict__ abias,
+                                            const unsigned long long* __restrict__ bmaxima, double scale,
+                                            const BoundArgs& bnd) {
+    const double bmax = key_double(bmaxima[0]);
+    const double dmax = key_double(bmaxima[1]);
+    const double nxy = scale * anorm[row] * bmax;
+    double b = (nxy * bnd.acc_rel + dmax * bnd.db_rel + fabs(abias[row]) * 1e-15 + bnd.abs_slack) * (1.0 + 1e-6);
+    if (bnd.qterm) {
+        // quantization, dropped limb product and conversion terms of the int8 sweep (l2sq_split_i8)
+        const double* qt = bnd.qterm + row * 4;
+        const double ma = key_double(bnd.qmax[0]), mb = key_double(bnd.qmax[1]);
+        const double mg = key_double(bnd.qmax[2]), mr = key_double(bnd.qmax[3]);
+        b += scale * (qt[0] * mb + qt[1] * ma + qt[2] * mg + 5.0 * 0x1p-24 * qt[3] * mr) * (1.0 + 1e-6);
+    }
+    return b;
+}
+
+// A row's floor in the scale of its list values: an entry's exact score is sigma = w + abias to within b, so an
+// entry with w < floor_cut scores below the floor (the last term covers the rounding of the cut itself). -inf for
+// a floor of -inf.
+__device__ __forceinline__ double floor_cut(double floor, double abias, double b) {
+    const double fa = floor - abias;
+    return (fa - b) - 1e-15 * fabs(fa);
+}
+
+// Shared row thresholds of a sweep (row_threshold_*, or the fused sweep's column thresholds) seeded from the
+// caller's floors: the largest fp32 value strictly below the row's floor_cut, so that the sweep drops only scores
+// whose pairs score below the floor (float_key(-inf) without a floor).
+__global__ void seed_floor_thresholds(unsigned int* __restrict__ thr, int64_t rows, const double* __restrict__ floor,
+                                      const double* __restrict__ anorm, const double* __restrict__ abias,
+                                      const unsigned long long* __restrict__ bmaxima, double scale, BoundArgs bnd) {
+    for (int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; r < rows; r += (int64_t)gridDim.x * blockDim.x) {
+        const double c = floor_cut(floor[r], abias[r], row_bound(r, anorm, abias, bmaxima, scale, bnd));
+        float c32 = -INFINITY;
+        if (c > -INFINITY) {
+            c32 = (float)c;
+            if (!((double)c32 < c)) c32 = nextafterf(c32, -INFINITY);
+        }
+        if (c32 != c32) c32 = -INFINITY;  // a NaN floor seeds nothing
+        thr[r] = float_key(c32);
+    }
+}
+
 // Lists of row r: L in [0, nlists), each of KL entries at base + (((L / G) * R + r) * G + L % G) * KL (sorted,
 // missing = -1). One wave per row merges them into the best KM (KM >= KL).
 // The row side A (rows A[r], row bias abias[r], norm anorm[r]) pairs with candidates from side B (B[c],
@@ -2140,19 +2186,8 @@ __global__ __launch_bounds__(256) void l2sq_finalize(
     }
     if (!valid) return;  // uniform per wave; nothing below synchronises across waves
     const int kept = nreal < KM ? nreal : KM;
-    const double bmax = key_double(bmaxima[0]);
-    const double dmax = key_double(bmaxima[1]);
-    const double nxy = scale * anorm[row] * bmax;
-    double b = (nxy * bnd.acc_rel + dmax * bnd.db_rel + fabs(abias[row]) * 1e-15 + bnd.abs_slack) * (1.0 + 1e-6);
-    if (bnd.qterm) {
-        // quantization, dropped limb product and conversion terms of the int8 sweep (l2sq_split_i8)
-        const double* qt = bnd.qterm + row * 4;
-        const double ma = key_double(bnd.qmax[0]), mb = key_double(bnd.qmax[1]);
-        const double mg = key_double(bnd.qmax[2]), mr = key_double(bnd.qmax[3]);
-        b += scale * (qt[0] * mb + qt[1] * ma + qt[2] * mg + 5.0 * 0x1p-24 * qt[3] * mr) * (1.0 + 1e-6);
-    }
-    // an entry with w < fcut has an exact score below the floor (|sigma - w| <= b); -inf without a floor
-    const double fcut = floor ? floor[row] - b : -INFINITY;
+    const double b = row_bound(row, anorm, abias, bmaxima, scale, bnd);
+    const double fcut = floor ? floor_cut(floor[row], abias[row], b) : -INFINITY;
     // wave top-KM: rounds of an arg-best over the lanes' list heads (tw non-increasing). The rounds stop after the
     // first entry t >= k - 1 below wk - 2b, at the first entry below fcut (or after the last real entry): no later
     // entry is evaluated, and one that the merge drops then has w <= tw[t] < max(wk - 2b, fcut), so every decision
@@ -3065,10 +3100,15 @@ int run_bidir(hipStream_t st, const float* X, const float* Y, int64_t m, int64_t
             if (int rc = copy_rows(false, xb, rows, xsplit)) return rc;
         const float* SXc = !split ? SX : (cp.x_chunked ? xsplit : SX + xb * ld);
         if (fused) {
-            // column thresholds start at -inf for every chunk (its lists only rank its own X rows)
-            hipLaunchKernelGGL(fill_u32, dim3((unsigned)((n + 255) / 256 < 4096 ? (n + 255) / 256 : 4096)), dim3(256), 0,
-                               st, colthr, n, neg_inf_key);
-            HM_LAUNCH_CHECK("fill_u32");
+            // column thresholds start at -inf for every chunk (its lists only rank its own X rows), or at the
+            // caller's floors
+            const dim3 tgrid((unsigned)((n + 255) / 256 < 4096 ? (n + 255) / 256 : 4096));
+            if (wide.col_floor)
+                hipLaunchKernelGGL(seed_floor_thresholds, tgrid, dim3(256), 0, st, colthr, n, wide.col_floor, ynorm, db,
+                                   maxima, scale, bound_for(true, 0));
+            else
+                hipLaunchKernelGGL(fill_u32, tgrid, dim3(256), 0, st, colthr, n, neg_inf_key);
+            HM_LAUNCH_CHECK("column thresholds");
         }
         // row thresholds start at -inf for every chunk (they index the chunk's rows)
         hipLaunchKernelGGL(fill_u32, dim3((unsigned)((rows + 255) / 256 < 4096 ? (rows + 255) / 256 : 4096)), dim3(256), 0,
@@ -3174,9 +3214,15 @@ int run_bidir(hipStream_t st, const float* X, const float* Y, int64_t m, int64_t
             if (split && cp.y_chunked && !q8.y_ready)
                 if (int rc = copy_rows(true, yb, rows, ysplit)) return rc;
             const float* SYc = !split ? SY : ((cp.y_chunked && !q8.y_ready) ? ysplit : SY + yb * ld);
-            hipLaunchKernelGGL(fill_u32, dim3((unsigned)((rows + 255) / 256 < 4096 ? (rows + 255) / 256 : 4096)),
-                               dim3(256), 0, st, rowthr, rows, 0x007fffffu /* float_key(-INFINITY) */);
-            HM_LAUNCH_CHECK("fill_u32");
+            // the rows' shared thresholds start at -inf, or at the caller's column floors
+            const dim3 tgrid((unsigned)((rows + 255) / 256 < 4096 ? (rows + 255) / 256 : 4096));
+            if (wide.col_floor)
+                hipLaunchKernelGGL(seed_floor_thresholds, tgrid, dim3(256), 0, st, rowthr, rows, wide.col_floor + yb,
+                                   ynorm + yb, db + yb, maxima, scale, bound_for(true, yb));
+            else
+                hipLaunchKernelGGL(fill_u32, tgrid, dim3(256), 0, st, rowthr, rows,
+                                   0x007fffffu /* float_key(-INFINITY) */);
+            HM_LAUNCH_CHECK("row thresholds");
 #define HM_SWEEP2(TL)                                                                                                \
     do {                                                                                                             \
         if (i8)                                                                                                      \
