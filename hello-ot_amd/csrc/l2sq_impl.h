@@ -2776,14 +2776,16 @@ inline int64_t chunk_rows(int64_t m, int64_t n, int kl, bool fused, int bx) {
 }
 
 // Y segments per sweep launch: enough workgroups to fill the chip (SWEEP_WGS), and for k > 2 at least 8 so each
-// row has 16 partial lists; at most a quarter of the tiles and `cap`. Among up to twice that many segments the
-// first whose workgroups fill whole rounds of the CUs (within 3%) is taken: a partial last round idles CUs.
-inline int choose_segments(int64_t m, int64_t n, int k, int cap, int bx) {
+// row has 16 partial lists; at most `cap`, and segments of at least `min_tiles` tiles (4 amortise a workgroup's
+// start; the wide pass, whose few gathered rows make it latency-bound, takes 1). Among up to twice that many
+// segments the first whose workgroups fill whole rounds of the CUs (within 3%) is taken: a partial last round
+// idles CUs.
+inline int choose_segments(int64_t m, int64_t n, int k, int cap, int bx, int min_tiles = 4) {
     const int64_t panels = (m + bx - 1) / bx;
     const int64_t tiles = (n + BY - 1) / BY;
     int64_t s = (SWEEP_WGS + panels - 1) / panels;
     if (k > 2 && s < 8) s = 8;
-    int64_t max_s = tiles / 4 > 0 ? tiles / 4 : 1;
+    int64_t max_s = tiles / min_tiles > 0 ? tiles / min_tiles : 1;
     if (max_s > cap) max_s = cap;
     if (s > max_s) s = max_s;
     if (s < 1) s = 1;
@@ -2801,11 +2803,11 @@ inline int choose_segments(int64_t m, int64_t n, int k, int cap, int bx) {
     return (int)best;
 }
 
-inline DirPlan plan_dir(int64_t rows, int64_t cols, int k, int cap, int bx) {
+inline DirPlan plan_dir(int64_t rows, int64_t cols, int k, int cap, int bx, int min_tiles = 4) {
     DirPlan p;
     p.rows = rows;
     p.cols = cols;
-    p.S = choose_segments(rows, cols, k, cap, bx);
+    p.S = choose_segments(rows, cols, k, cap, bx, min_tiles);
     const int64_t tiles = (cols + BY - 1) / BY;
     const int64_t tiles_per = (tiles + p.S - 1) / p.S;
     p.seg_len = tiles_per * BY;

@@ -74,7 +74,7 @@ int wide_round(hipStream_t st, bool split, bool two_level, const float* A, const
             hipLaunchKernelGGL(l2sq_wide_gather, dim3(2048), dim3(256), 0, st, Asw, gld, queue, q0, Q, Qpad, queue_thr,
                                w.rows, w.thr, w.cnt);
         HM_LAUNCH_CHECK("l2sq_wide_gather");
-        const DirPlan plan = plan_dir(Qpad, nb, 0, 256, bx);
+        const DirPlan plan = plan_dir(Qpad, nb, 0, 256, bx, 1);
         const dim3 grid(sweep_grid(Qpad / bx, plan.S));
 #define HM_WIDE(KERNEL, THREADS, ...)                                                                               \
     hipLaunchKernelGGL(KERNEL, grid, dim3(THREADS), 0, st, w.rows, Bsw, (int64_t)0, (int64_t)Q, nb, sd, gld,        \

@@ -61,8 +61,8 @@ def _to_device(value, device, dtype):
 
 def _permute_in_place(value, perm, device, bounded: bool):
     """value[i] = (old value)[perm[i]] in place: through one full temporary, or, with ``bounded`` (a
-    memory-bounded solve) or when the device has no room for the temporary, with one chunk of extra device memory
-    (``permute_rows_inplace``, a host round trip: about 4 s for 39 GiB)."""
+    memory-bounded solve) or when the device has no room for the temporary, with one block of extra device memory
+    (``permute_rows_inplace``, which walks the permutation's cycles on the device)."""
     nbytes = 4 * value.numel()
     if nbytes > _host.STREAM_MIN_BYTES and (bounded or torch.cuda.mem_get_info(device)[0] < nbytes + (4 << 30)):
         permute_rows_inplace(value, perm)
@@ -90,8 +90,9 @@ def _stream_source(value, target, cost_type: str, device, options: SolverOptions
     kernels/bilinear_topk.py:255-368). ``gpu_resident=True`` keeps both sides on the device. Otherwise a source side
     of more than STREAM_MIN_BYTES of fp32 features is streamed when the resident plan would take more than
     RESIDENT_BUDGET of the device's memory (``STREAM_POLICY`` / HELLOOT_STREAM_SOURCE can force either way), which
-    leaves the device one side's features plus bounded chunk staging. A streamed side is copied once into host
-    memory in the shuffled order (``consume_input_features`` then applies to the target side only)."""
+    leaves the device one side's features plus bounded chunk staging. A streamed side is read from the caller's
+    host matrix, chunk by chunk in the shuffled order (``consume_input_features`` then applies to the target side
+    only)."""
     if options.gpu_resident:
         return False
     rows, d = (int(s) for s in value.shape)
@@ -108,6 +109,19 @@ def _stream_source(value, target, cost_type: str, device, options: SolverOptions
     need = 4 * (rows + other) * d + (2 * max(rows, other) * d if cost_type == "l2^2" else 0) + (16 << 30)
     total = torch.cuda.get_device_properties(device).total_memory
     return need > _host.RESIDENT_BUDGET * total
+
+
+def _streamed_side(value, perm, device) -> HostRows:
+    """The streamed source side: a contiguous fp32 host matrix (torch, or numpy without a conversion) is read in
+    place, its chunks gathered in shuffle order as they are streamed; anything else (device tensors, other dtypes or
+    layouts) is first copied into a host matrix in shuffle order."""
+    host = value
+    if isinstance(host, np.ndarray) and host.dtype == np.float32 and host.ndim == 2 and host.flags.c_contiguous:
+        host = torch.from_numpy(host)
+    if torch.is_tensor(host) and host.device.type == "cpu" and host.dtype == torch.float32 and host.ndim == 2 \
+            and host.is_contiguous():
+        return HostRows(host, device, order=perm)
+    return HostRows(shuffled_rows(value, perm), device)
 
 
 @torch.no_grad()
@@ -186,7 +200,7 @@ def _solve_levels(problem, options, device, si, ti, a, b, consume, restore, max_
     numbering."""
     n, m = problem.shape
     if _stream_source(problem.source_points, problem.target_points, problem.cost_type, device, options):
-        x = HostRows(shuffled_rows(problem.source_points, si), device)
+        x = _streamed_side(problem.source_points, si, device)
     else:
         x = _shuffled_features(problem.source_points, si, device, consume, restore)
     y = _shuffled_features(problem.target_points, ti, device, consume, restore, bounded=isinstance(x, HostRows))

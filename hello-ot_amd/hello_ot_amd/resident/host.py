@@ -3,8 +3,8 @@
 This is the reference's resident / streamed split (``kernels/bilinear_topk.py:99-118, 255-368``,
 ``kernels/scan_contract.py:113-253``): one side stays on the device, the other is read in bounded chunks, so the
 device holds one side's features plus O(chunk * d) of staging instead of both sides. Here the streamed side's rows
-live in one host tensor (already in the solver's shuffled order) and pass through two pinned staging buffers of one
-chunk each (bounded pinned memory, as in the reference): the host copies chunk c into a staging buffer once that
+stay in the caller's host tensor and pass, in the solver's shuffled order, through two pinned staging buffers of one
+chunk each (bounded pinned memory, as in the reference): the host gathers chunk c into a staging buffer once that
 buffer's previous upload has finished, a side stream of default priority uploads it into one of two device buffers
 once the work queued on that buffer's previous chunk has finished, and the caller's stream waits for the upload.
 Uploads and host copies run one chunk ahead of the caller's work.
@@ -26,14 +26,22 @@ RESIDENT_BUDGET = 0.75
 
 
 class HostRows:
-    """Rows [0, rows) of a host fp32 matrix, read by the device in chunks of at most ``chunk`` rows."""
+    """Rows of a host fp32 matrix, read by the device in chunks of at most ``chunk`` rows: rows [0, rows) of
+    ``host``, or with ``order`` (int64 host indices) the rows host[order[0]], host[order[1]], ..., gathered into the
+    staging buffers as each chunk is read (the solver's shuffled order without a shuffled host copy)."""
 
-    def __init__(self, host: torch.Tensor, device, chunk_rows: int | None = None):
+    def __init__(self, host: torch.Tensor, device, chunk_rows: int | None = None, order: torch.Tensor | None = None):
         if host.device.type != "cpu" or host.dtype != torch.float32 or host.ndim != 2 or not host.is_contiguous():
             raise ValueError("streamed rows must be a contiguous fp32 host matrix")
+        if order is not None:
+            order = order.detach().to("cpu", torch.int64).contiguous()
+            if order.ndim != 1:
+                raise ValueError("order must be a vector of row indices")
         self.host = host
+        self.order = order
         self.device = torch.device(device)
-        self.rows, self.d = int(host.shape[0]), int(host.shape[1])
+        self.rows = int(host.shape[0]) if order is None else int(order.numel())
+        self.d = int(host.shape[1])
         self.chunk = int(chunk_rows) if chunk_rows else max(1, STREAM_CHUNK_BYTES // (4 * max(1, self.d)))
         self._copy = None
 
@@ -48,10 +56,23 @@ class HostRows:
         return 4 * self.rows * self.d
 
     def prefix(self, rows: int) -> "HostRows":
-        return HostRows(self.host[: int(rows)], self.device, self.chunk)
+        if self.order is None:
+            return HostRows(self.host[: int(rows)], self.device, self.chunk)
+        return HostRows(self.host, self.device, self.chunk, self.order[: int(rows)])
+
+    def _read(self, s: int, e: int, out: torch.Tensor) -> None:
+        """Rows [s, e) into ``out`` (host)."""
+        if self.order is None:
+            out.copy_(self.host[s:e])
+        else:
+            torch.index_select(self.host, 0, self.order[s:e], out=out)
 
     def to_device(self) -> torch.Tensor:
-        return self.host.to(self.device)
+        if self.order is None:
+            return self.host.to(self.device)
+        out = torch.empty((self.rows, self.d), dtype=torch.float32)
+        self._read(0, self.rows, out)
+        return out.to(self.device)
 
     def chunks(self, start: int = 0, stop: int | None = None):
         """Yields (s, e, x): x holds rows [s, e) on the device, valid on the current stream until the next step."""
@@ -76,7 +97,7 @@ class HostRows:
             s, e = bounds[index]
             if used[slot]:
                 uploaded[slot].synchronize()     # the staging buffer's previous upload has finished
-            staging[slot][: e - s].copy_(self.host[s:e])
+            self._read(s, e, staging[slot][: e - s])
             with torch.cuda.stream(copy):
                 if used[slot]:
                     copy.wait_event(released[slot])
@@ -100,24 +121,68 @@ class HostRows:
             copy.synchronize()
 
 
-def permute_rows_inplace(value: torch.Tensor, perm: torch.Tensor) -> torch.Tensor:
-    """value[i] = (old value)[perm[i]] for a contiguous device matrix, with one chunk of extra device memory instead
-    of a full copy: the rows are gathered chunk by chunk in the new order on the device and parked in host memory
-    (through a pinned staging buffer), then written back in order. The role of the reference's in-place reorder of
-    consumed inputs (hierarchy/plan.py:13-38), whose temporary is one row."""
+def _cycles(perm: torch.Tensor):
+    """The cycles of length >= 2 of a permutation, each listed from its smallest element c0 as c0, perm[c0],
+    perm[perm[c0]], ... and concatenated: (seq, first) with first[t] the position in seq where t's cycle starts.
+    Pointer jumping on the permutation's device (log2 n rounds): the smallest element of each cycle, then each
+    element's distance to it."""
+    n = perm.numel()
+    dev = perm.device
+    idx = torch.arange(n, device=dev)
+    rounds = max(1, (n - 1).bit_length())
+    lead, p = idx.clone(), perm.clone()
+    for _ in range(rounds):
+        lead = torch.minimum(lead, lead[p])
+        p = p[p]
+    # steps forward from each element to its cycle's smallest element (0 there)
+    is_lead = lead == idx
+    dist = (~is_lead).to(torch.int64)
+    succ = torch.where(is_lead, idx, perm)
+    for _ in range(rounds):
+        dist = dist + dist[succ]
+        succ = succ[succ]
+    length = 1 + dist[perm[lead]]
+    moving = length > 1
+    rank = torch.remainder(length - dist, length)
+    seq = idx[moving][torch.argsort((lead * n + rank)[moving])]
+    pos = torch.arange(seq.numel(), device=dev)
+    first = torch.cummax(torch.where(rank[seq] == 0, pos, torch.zeros_like(pos)), 0).values
+    return seq, first
+
+
+def permute_rows_inplace(value: torch.Tensor, perm: torch.Tensor, block: int | None = None) -> torch.Tensor:
+    """value[i] = (old value)[perm[i]] for a contiguous matrix, on its own device, with one block of extra rows
+    instead of a full copy. The permutation's cycles are laid end to end (``_cycles``) and walked in blocks of
+    positions: a block gathers the old rows its positions take (the next element of each position's cycle, or for a
+    cycle's last element its first), then writes them. A block only reads positions at or after its own, except a
+    wrap to a cycle's first element, which an earlier block may have written when the cycle crosses a block
+    boundary: those first rows (at most one cycle per boundary) are saved before any write. The role of the
+    reference's in-place reorder of consumed inputs (hierarchy/plan.py:13-38), whose temporary is one row."""
     rows, d = int(value.shape[0]), int(value.shape[1])
-    block = max(1, STREAM_CHUNK_BYTES // (value.element_size() * max(1, d)))
-    park = torch.empty((rows, d), dtype=value.dtype)
-    staging = torch.empty((min(block, rows), d), dtype=value.dtype, pin_memory=True)
-    perm_dev = perm.to(value.device)
-    for s in range(0, rows, block):
-        e = min(rows, s + block)
-        staging[: e - s].copy_(value[perm_dev[s:e]])          # device gather, then a synchronous download
-        park[s:e].copy_(staging[: e - s])
-    for s in range(0, rows, block):
-        e = min(rows, s + block)
-        staging[: e - s].copy_(park[s:e])
-        value[s:e].copy_(staging[: e - s])                    # synchronous upload (the staging buffer is reused)
+    if block is None:
+        block = max(1, STREAM_CHUNK_BYTES // (value.element_size() * max(1, d)))
+    seq, first = _cycles(perm.to(value.device, torch.int64))
+    total = seq.numel()
+    if total == 0:
+        return value
+    pos = torch.arange(total, device=value.device)
+    nxt = pos + 1
+    wrap = nxt >= total
+    wrap[:-1] |= first[1:] == nxt[:-1]                  # the next position starts another cycle
+    src = torch.where(wrap, first, nxt)
+    # wraps whose cycle starts in an earlier block read a saved copy of that cycle's first row
+    saved = wrap & (first // block < pos // block)
+    starts = torch.unique(first[saved])
+    heads = value.index_select(0, seq[starts]) if starts.numel() else None
+    temp = torch.empty((min(block, total), d), dtype=value.dtype, device=value.device)
+    for t0 in range(0, total, block):
+        t1 = min(total, t0 + block)
+        out = temp[: t1 - t0]
+        torch.index_select(value, 0, seq[src[t0:t1]], out=out)
+        m = saved[t0:t1]
+        if heads is not None and bool(m.any()):
+            out[m] = heads[torch.searchsorted(starts, first[t0:t1][m])]
+        value.index_copy_(0, seq[t0:t1], out)
     return value
 
 

@@ -69,14 +69,18 @@ def test_streamed_scans_equal_the_resident_scans(cuda, kind, d, integer):
     assert torch.equal(resident.pairs(rows, cols), streamed.pairs(rows, cols))
 
 
-def test_bounded_inplace_row_permutation(cuda, monkeypatch):
-    """permute_rows_inplace gives value[perm] in place, through chunks of 300 rows (ragged last chunk)."""
+@pytest.mark.parametrize("kind", ["random", "reversal", "rotation", "swaps"])
+def test_bounded_inplace_row_permutation(cuda, monkeypatch, kind):
+    """permute_rows_inplace gives value[perm] in place on the device, walking the cycles in blocks of 300 positions
+    (ragged last block; cycles crossing block boundaries, one cycle of all rows, 500 two-cycles)."""
     from hello_ot_amd.resident.host import permute_rows_inplace
 
     monkeypatch.setattr(host_module, "STREAM_CHUNK_BYTES", 300 * 17 * 4)
     rng = np.random.default_rng(3)
     value = torch.as_tensor(rng.standard_normal((1000, 17)).astype(np.float32)).to(cuda)
-    perm = torch.as_tensor(rng.permutation(1000)).to(cuda)
+    perm = {"random": rng.permutation(1000), "reversal": np.arange(1000)[::-1].copy(),
+            "rotation": np.roll(np.arange(1000), 1), "swaps": np.arange(1000).reshape(500, 2)[:, ::-1].ravel()}[kind]
+    perm = torch.as_tensor(perm).to(cuda)
     want = value[perm].clone()
     assert permute_rows_inplace(value, perm) is value
     assert torch.equal(value, want)

@@ -333,3 +333,49 @@ def test_primal_support_cap_reserves_basis_and_violations():
     # refinement/support_budget.py:56-67: budget - (V - 1) - gamma * V
     assert primal_support_cap(10.0, 2, 300, 500) == active_support_budget(10.0, 300, 500) - 799 - 1600
     assert primal_support_cap(4.0, 2, 200, 200) == 401
+
+
+@pytest.mark.parametrize("n", [1, 2, 17, 1000])
+@pytest.mark.parametrize("block", [1, 3, 64, 5000])
+def test_inplace_row_permutation_walks_cycles(n, block):
+    """The bounded in-place row permutation on the host: value[perm] for random permutations and their inverses,
+    the identity, a reversal, a single n-cycle and adjacent swaps, with blocks shorter than, equal to and longer
+    than the cycles (cycles crossing block boundaries read their saved first rows)."""
+    from hello_ot_amd.resident.host import permute_rows_inplace
+
+    g = torch.Generator().manual_seed(n * 131 + block)
+    ar = torch.arange(n)
+    rand = torch.randperm(n, generator=g)
+    inverse = torch.empty_like(rand)
+    inverse[rand] = ar
+    swaps = ar.clone()
+    swaps[: n - n % 2] = ar[: n - n % 2].view(-1, 2).flip(1).reshape(-1)
+    for perm in (rand, inverse, ar, ar.flip(0), torch.roll(ar, 1), swaps):
+        value = torch.randn((n, 3), generator=g)
+        want = value[perm].clone()
+        assert permute_rows_inplace(value, perm, block) is value
+        assert torch.equal(value, want)
+
+
+def test_streamed_rows_in_shuffle_order_without_a_copy():
+    """HostRows with an order reads the caller's host rows in that order (prefixes too) and keeps no copy; the solve
+    streams a contiguous fp32 host source this way and copies anything else once in shuffle order."""
+    from hello_ot_amd.api import _streamed_side
+    from hello_ot_amd.resident.host import HostRows
+
+    g = torch.Generator().manual_seed(5)
+    host = torch.randn((50, 4), generator=g)
+    perm = torch.randperm(50, generator=g)
+    rows = _streamed_side(host, perm, "cpu")
+    assert rows.host is host and len(rows) == 50 and rows.shape == (50, 4)
+    assert torch.equal(rows.to_device(), host[perm])
+    assert torch.equal(rows.prefix(20).to_device(), host[perm[:20]])
+    out = torch.empty((7, 4))
+    rows._read(3, 10, out)
+    assert torch.equal(out, host[perm[3:10]])
+    as_numpy = _streamed_side(host.numpy(), perm, "cpu")
+    assert as_numpy.host.data_ptr() == host.data_ptr()
+    copied = _streamed_side(host.double(), perm, "cpu")
+    assert copied.order is None and torch.equal(copied.host, host[perm])
+    with pytest.raises(ValueError, match="vector"):
+        HostRows(host, "cpu", order=perm.view(5, 10))
