@@ -2637,6 +2637,7 @@ struct WideBufs {
     int* counts;       // [4]: redo2 and redo3 lengths
     unsigned int* rowthr;  // [rows of a sweep launch] the sweeps' shared row thresholds (row_threshold_*)
     const double* col_floor = nullptr;  // [n] the caller's column floors (l2sq_finalize's floor), or none
+    double* floor_run;  // [n] (fused columns) the floors of a chunk: its k-th running column value, or the caller's
 };
 
 // Per-side data of the int8 sweep (HM_INT8X3; null otherwise): row scales, ||.||_1, the rows' error terms
@@ -2697,6 +2698,16 @@ __global__ void l2sq_merge_columns(double* __restrict__ val, int* __restrict__ i
         else { ov[s] = v[a]; oi[s] = id[a]; ++a; }
     }
     for (int s = 0; s < k; ++s) { v[s] = ov[s]; id[s] = oi[s]; }
+}
+
+// Floors of a chunk's fused column lists: the k-th value of each column's running list (every entry of which is
+// an exact score of a pair already listed), or the caller's floor when that is higher.
+__global__ void running_floor(double* __restrict__ out, int64_t n, const double* __restrict__ val, int k,
+                              const double* __restrict__ user) {
+    for (int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; j < n; j += (int64_t)gridDim.x * blockDim.x) {
+        const double v = val[j * k + k - 1];
+        out[j] = user ? fmax(v, user[j]) : v;
+    }
 }
 
 __global__ void exact_row_max(const double* __restrict__ row_val, int64_t m, int k, double* __restrict__ stats) {
@@ -2912,6 +2923,7 @@ void layout(A& a, int64_t m, int64_t n, int d, int k, uint32_t flags, double** x
     wide->redo_l_thr = a.template take<float>((size_t)(m + n));
     wide->counts = a.template take<int>(4);
     wide->rowthr = a.template take<unsigned int>((size_t)std::max<int64_t>(std::max<int64_t>(c.ch, c.ch2), 1));
+    wide->floor_run = a.template take<double>(fused ? (size_t)n : 1);
     wide->qs = a.template take<float>((size_t)wq);
     wide->defer.key = a.template take<int>(fused ? (size_t)n : 1);
     wide->defer.need = a.template take<int>(fused ? (size_t)n : 1);
@@ -3101,12 +3113,20 @@ int run_bidir(hipStream_t st, const float* X, const float* Y, int64_t m, int64_t
         if (split && cp.x_chunked)
             if (int rc = copy_rows(false, xb, rows, xsplit)) return rc;
         const float* SXc = !split ? SX : (cp.x_chunked ? xsplit : SX + xb * ld);
+        // floors of this chunk's column lists: the caller's, and after the first chunk the running lists' k-th
+        // values (a chunk's lists then only keep what can enter the merged lists)
+        const double* cfloor = wide.col_floor;
+        if (fused && chunk_index > 0) {
+            hipLaunchKernelGGL(running_floor, dim3((unsigned)((n + 255) / 256 < 4096 ? (n + 255) / 256 : 4096)),
+                               dim3(256), 0, st, wide.floor_run, n, col_val, k, wide.col_floor);
+            HM_LAUNCH_CHECK("running_floor");
+            cfloor = wide.floor_run;
+        }
         if (fused) {
-            // column thresholds start at -inf for every chunk (its lists only rank its own X rows), or at the
-            // caller's floors
+            // column thresholds start at -inf for every chunk (its lists only rank its own X rows), or at the floors
             const dim3 tgrid((unsigned)((n + 255) / 256 < 4096 ? (n + 255) / 256 : 4096));
-            if (wide.col_floor)
-                hipLaunchKernelGGL(seed_floor_thresholds, tgrid, dim3(256), 0, st, colthr, n, wide.col_floor, ynorm, db,
+            if (cfloor)
+                hipLaunchKernelGGL(seed_floor_thresholds, tgrid, dim3(256), 0, st, colthr, n, cfloor, ynorm, db,
                                    maxima, scale, bound_for(true, 0));
             else
                 hipLaunchKernelGGL(fill_u32, tgrid, dim3(256), 0, st, colthr, n, neg_inf_key);
@@ -3177,7 +3197,7 @@ int run_bidir(hipStream_t st, const float* X, const float* Y, int64_t m, int64_t
             hipLaunchKernelGGL((l2sq_finalize<K1, KM, 1, true, true>), dim3((unsigned)((n + 3) / 4)), dim3(256), 0, st,
                                Y, X, n, d, (int)panels, colpart, db, qb, ynorm, maxima, scale, k, bound_for(true, 0),
                                cval, cidx, redo, wide.redo_thr, redo_count, wide.defer,
-                               ListQueue{wide.redo_l, wide.redo_l_thr}, wide.col_floor);
+                               ListQueue{wide.redo_l, wide.redo_l_thr}, cfloor);
             HM_LAUNCH_CHECK("l2sq_col_finalize");
             const unsigned egrid = (unsigned)((n + 255) / 256 < 8192 ? (n + 255) / 256 : 8192);
             hipLaunchKernelGGL(fill_u32, dim3((unsigned)((rows + 256) / 256)), dim3(256), 0, st,

@@ -19,7 +19,8 @@ from dataclasses import dataclass, replace
 import torch
 
 from ..costs.pairs import lowrank_pair_costs, norm_pair_costs
-from ..kernels.generic_scan import ResidentSide, pricing_l2sq, pricing_norm
+from .. import _lib
+from ..kernels.generic_scan import ResidentSide, _precision_flags, pricing_l2sq, pricing_norm
 from . import host as _host
 from .host import HostRows
 
@@ -46,6 +47,35 @@ def offsets(features) -> torch.Tensor:
     for start in range(0, len(features), block):
         out[start:start + block] = _sq_rows(features[start:start + block])
     return out
+
+
+# device bytes a streamed l2^2 scan's library call may take for its workspace: a call with both directions keeps
+# column lists per 256-row panel of its chunk for every column (6.6 GiB for 19968 x 1.28M), so such scans read the
+# streamed side in smaller chunks
+STREAMED_WORKSPACE_BYTES = 4 * _host.STREAM_CHUNK_BYTES
+
+
+def fused_chunk_rows(chunk: int, n: int, d: int, k: int, certificate: bool, precision: str) -> int:
+    """Source rows per call of a streamed scan with both directions: ``chunk``, or when its workspace against n
+    resident columns exceeds STREAMED_WORKSPACE_BYTES the largest multiple of 256 rows whose workspace fits (at
+    least 256)."""
+    lib = _lib.load()
+    flags = _lib.HM_ROWS | _lib.HM_COLS | (_lib.HM_STATS | _lib.HM_LINF if certificate else 0) \
+        | _precision_flags(precision)
+
+    def fits(rows):
+        return lib.hm_pricing_l2sq_resident_workspace_bytes(rows, n, d, k, flags) <= STREAMED_WORKSPACE_BYTES
+
+    if chunk <= 256 or fits(chunk):
+        return chunk
+    lo, hi = 1, chunk // 256              # 256 * lo rows are taken when nothing larger fits
+    while lo < hi:
+        mid = (lo + hi + 1) // 2
+        if fits(256 * mid):
+            lo = mid
+        else:
+            hi = mid - 1
+    return 256 * lo
 
 
 def merge_columns(best, new, k: int):
@@ -185,10 +215,13 @@ class Cost:
         best = None
         l2sq = self.kind == "l2^2"
         side = ResidentSide(self.target) if l2sq else None   # the target's sweep copy, for this scan only
+        chunk = None
         if l2sq:
             p, q = self.source_offset, self.target_offset
             db = g - q
-        for s, e, x in self.source.chunks():
+            if cols and (rows or certificate):
+                chunk = fused_chunk_rows(self.source.chunk, m, self.source.d, k, certificate, side.precision)
+        for s, e, x in self.source.chunks(rows=chunk):
             if l2sq:
                 # a columns-only scan runs the library's role-swapped pass per chunk (the target rows against the
                 # chunk, reading the resident side's copy): as fast here as column lists fused into a row sweep,

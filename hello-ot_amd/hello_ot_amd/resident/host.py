@@ -74,8 +74,9 @@ class HostRows:
         self._read(0, self.rows, out)
         return out.to(self.device)
 
-    def chunks(self, start: int = 0, stop: int | None = None):
-        """Yields (s, e, x): x holds rows [s, e) on the device, valid on the current stream until the next step."""
+    def chunks(self, start: int = 0, stop: int | None = None, rows: int | None = None):
+        """Yields (s, e, x): x holds rows [s, e) on the device, valid on the current stream until the next step.
+        ``rows`` (at most ``chunk``) reads smaller chunks, with smaller buffers."""
         stop = self.rows if stop is None else int(stop)
         if stop <= start:
             return
@@ -83,7 +84,7 @@ class HostRows:
         if self._copy is None:
             self._copy = torch.cuda.Stream(self.device)
         copy = self._copy
-        rows = min(self.chunk, stop - start)
+        rows = min(self.chunk if rows is None else max(1, min(int(rows), self.chunk)), stop - start)
         staging = [torch.empty((rows, self.d), dtype=torch.float32, pin_memory=True) for _ in range(2)]
         buffers = [torch.empty((rows, self.d), dtype=torch.float32, device=self.device) for _ in range(2)]
         uploaded = [torch.cuda.Event(), torch.cuda.Event()]   # staging slot free again / device slot filled

@@ -125,6 +125,7 @@ def test_l2sq_ties_and_duplicates_lowest_index_wins(cuda, precision):
 @pytest.mark.parametrize("m,n,d,k,integer", [
     (65536 + 300, 97, 256, 2, True),    # columns fused into the row sweep, merged across two query chunks
     (65536 + 300, 97, 256, 8, False),
+    (2 * 65536 + 300, 97, 256, 4, False),  # three query chunks: later chunks' lists start at the running floors
     (65536 + 300, 97, 12, 8, True),     # columns by a second, role-swapped sweep; query side in two chunks
     (97, 65536 + 300, 12, 3, True),     # role-swapped sweep over two resident-side chunks
 ])
