@@ -60,6 +60,9 @@ constexpr int QN = 12;             // queued row candidates per lane and tile (1
 constexpr int FLUSH_CHUNKS = 8;    // fp32 block length 256 features before folding into the outer sum
 constexpr int FLUSH_SPLIT = 4;     // split-bf16 block length 128 features (3 product terms per feature)
 constexpr int64_t CHUNK_MAX = 65536;          // X rows per internal chunk
+// Y rows per chunk of the role-swapped pass against a resident Y side (whose sweep copy is whole, so a chunk costs
+// only its partial lists): fewer, longer launches with one finalize each
+constexpr int64_t CHUNK_MAX_RESIDENT = 4 * CHUNK_MAX;
 constexpr int FUSE_MIN_D = 256;               // columns ride on the row sweep from this d on (below it the
                                               // per-tile column epilogue outweighs the MFMA work: two sweeps)
 constexpr int64_t SWEEP_WGS = 1024;           // target workgroups per sweep launch (sets the Y segments)
@@ -2772,8 +2775,8 @@ inline int sweep_panel(int d, uint32_t flags) {
 
 // Rows per internal chunk of the swept side (m rows against n): balanced chunks of whole bx-row panels, and with
 // fused columns the chunk's column partial lists (kl entries per panel and column) within COLPART_CAP.
-inline int64_t chunk_rows(int64_t m, int64_t n, int kl, bool fused, int bx) {
-    int64_t ch = CHUNK_MAX;
+inline int64_t chunk_rows(int64_t m, int64_t n, int kl, bool fused, int bx, int64_t cap = CHUNK_MAX) {
+    int64_t ch = cap;
     if (fused) {
         const int64_t per_panel = n * (int64_t)kl * (int64_t)sizeof(Entry);
         int64_t panels = (int64_t)(COLPART_CAP / (size_t)per_panel);
@@ -2838,7 +2841,7 @@ struct CallPlan {
     DirPlan plan, plan2;
 };
 
-inline CallPlan plan_call(int64_t m, int64_t n, int d, int k, uint32_t flags) {
+inline CallPlan plan_call(int64_t m, int64_t n, int d, int k, uint32_t flags, bool y_resident = false) {
     CallPlan c;
     c.km = merge_k(k, flags);
     c.fused = fused_columns(d, flags);
@@ -2856,7 +2859,7 @@ inline CallPlan plan_call(int64_t m, int64_t n, int d, int k, uint32_t flags) {
         c.kl = sizes[t];
         c.ch = chunk_rows(m, n, c.kl, c.fused, c.bx);
         c.plan = plan_dir(c.ch, n, k, 64, c.bx);
-        c.ch2 = c.swapped ? chunk_rows(n, m, c.kl, false, c.bx) : 0;
+        c.ch2 = c.swapped ? chunk_rows(n, m, c.kl, false, c.bx, y_resident ? CHUNK_MAX_RESIDENT : CHUNK_MAX) : 0;
         c.plan2 = plan_dir(c.swapped ? c.ch2 : 1, m, k, 64, c.bx);
         if (c.kl >= c.km) break;
         // fewest partial lists any finalized row or column of this call merges
@@ -2878,7 +2881,7 @@ void layout(A& a, int64_t m, int64_t n, int d, int k, uint32_t flags, double** x
             unsigned int** colthr, double** cval, int** cidx, double** blockstats, int** redo, int** redo_count,
             float** xsplit, float** ysplit, double** rpv, int** rpi, WideBufs* wide, I8Bufs* q8,
             bool y_resident = false) {
-    const CallPlan c = plan_call(m, n, d, k, flags);
+    const CallPlan c = plan_call(m, n, d, k, flags, y_resident);
     const int64_t panels = c.ch / c.bx;
     size_t part_entries = (size_t)c.plan.S * c.ch * 2 * c.kl;
     if (c.swapped && (size_t)c.plan2.S * c.ch2 * 2 * c.kl > part_entries)
@@ -3030,7 +3033,7 @@ int run_bidir(hipStream_t st, const float* X, const float* Y, int64_t m, int64_t
               int* col_idx, double* stats, float* xsplit, float* ysplit, double* rpv, int* rpi,
               const WideBufs& wide, const I8Bufs& q8) {
     // K1: entries per partial list of the sweep; KM: candidates the finalize merges and keeps
-    const CallPlan cp = plan_call(m, n, d, k, flags);
+    const CallPlan cp = plan_call(m, n, d, k, flags, q8.y_ready);
     if (cp.kl != K1 || cp.km != KM) return fail(HM_EINVAL, "l2sq pricing: list sizes %d/%d do not match the plan %d/%d", K1, KM, cp.kl, cp.km);
     const bool want_rows = (flags & HM_ROWS) != 0;
     const bool fused = cp.fused;

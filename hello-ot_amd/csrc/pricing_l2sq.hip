@@ -10,7 +10,7 @@ int l2sq_run_l16_m40(L2SQ_RUN_ARGS);
 int l2sq_run_l40_m40(L2SQ_RUN_ARGS);
 namespace {
 int run_k(L2SQ_RUN_ARGS) {
-    const CallPlan c = plan_call(m, n, d, k, flags);
+    const CallPlan c = plan_call(m, n, d, k, flags, q8.y_ready);
     if (c.km == 8) return l2sq_run_l8_m8(L2SQ_RUN_PASS);
     if (c.km == 16) return c.kl == 8 ? l2sq_run_l8_m16(L2SQ_RUN_PASS) : l2sq_run_l16_m16(L2SQ_RUN_PASS);
     if (c.kl == 8) return l2sq_run_l8_m40(L2SQ_RUN_PASS);
