@@ -534,12 +534,11 @@ __device__ __forceinline__ void sweep_row_init(SweepRow<K1>& s, int64_t row, int
 // w = scale*dot + db into the row list (or appends for the wide pass), adds the certificate terms and, with COLS,
 // passes the tile's scores scale*dot + qb through LDS so that each Y row keeps its best K1 over the workgroup's
 // 128 X rows, CPASS Y rows at a time (sC holds CPASS * CST floats; 256 / CPASS threads scan each row and merge
-// their lists). Ends with a barrier: the next tile may rewrite sDB / sGE / sC. STATS (the certificate) is a template
-// argument: a per-pair test of a runtime flag costs a scalar branch per score and splits the tile into blocks.
-template <int K1, bool COLS, bool APPEND, int CPASS, bool FULL, bool STATS>
+// their lists). Ends with a barrier: the next tile may rewrite sDB / sGE / sC.
+template <int K1, bool COLS, bool APPEND, int CPASS = BY, bool FULL = false>
 __device__ __forceinline__ void sweep_epilogue(const v16f (&tot)[NB], SweepRow<K1>& s, int tid, int wave, int h,
                                                int r, int64_t ytile, int64_t y_end, int64_t x0, int64_t panel,
-                                               int64_t n, float scale, float slack, const double* sQB64,
+                                               int64_t n, float scale, int STATS, float slack, const double* sQB64,
                                                const double* sDB64, const float* sDB, const float* sGE,
                                                float* sC, Entry* __restrict__ colpart,
                                                unsigned int* __restrict__ colthr, int* __restrict__ wcnt,
@@ -934,21 +933,13 @@ __global__ __launch_bounds__(256) void l2sq_sweep(
                 for (int q = 0; q < 16; ++q) acc[b][q] = outer[b][q] + acc[b][q];
             }
         }
-#define HM_EPILOGUE(FULL_TILE, ST)                                                                              \
-    sweep_epilogue<K1, COLS, APPEND, BY, FULL_TILE, ST>(acc, s, tid, wave, h, r, ytile, y_end, x0, panel, n,     \
-                                                       scale, slack, sQB64, sDB64, sDB, sGE, sC, colpart, colthr, \
-                                                       wcnt, wbuf, wcap, rowthr, xb,                             \
-                                                       COLS ? reinterpret_cast<Entry*>(sC) : sQ)
-        {
-            const bool full_tile = y_end - ytile >= (int64_t)(NB * 32) && x0 + BX <= xe;
-            if (!APPEND && STATS) {
-                if (full_tile) HM_EPILOGUE(true, !APPEND);
-                else HM_EPILOGUE(false, !APPEND);
-            } else {
-                if (full_tile) HM_EPILOGUE(true, false);
-                else HM_EPILOGUE(false, false);
-            }
-        }
+#define HM_EPILOGUE(FULL_TILE)                                                                                  \
+    sweep_epilogue<K1, COLS, APPEND, BY, FULL_TILE>(acc, s, tid, wave, h, r, ytile, y_end, x0, panel, n, scale,  \
+                                                   STATS, slack, sQB64, sDB64, sDB, sGE, sC, colpart, colthr,    \
+                                                   wcnt, wbuf, wcap, rowthr, xb,                                 \
+                                                   COLS ? reinterpret_cast<Entry*>(sC) : sQ)
+        if (y_end - ytile >= (int64_t)(NB * 32) && x0 + BX <= xe) HM_EPILOGUE(true);
+        else HM_EPILOGUE(false);
 #undef HM_EPILOGUE
     }
     sweep_finish<K1, APPEND>(s, tid, lane, wave, h, seg, rows, xb, P, panel, STATS, part, blockstats, sRed);
@@ -1215,21 +1206,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(COLS ? 1 : 
             step(I2{});
             step(I3{});
         }
-#define HM_EPILOGUE(FULL_TILE, ST)                                                                              \
-    sweep_epilogue<K1, COLS, APPEND, BY, FULL_TILE, ST>(acc, s, tid, wave, h, r, ytile, y_end, x0, panel, n,     \
-                                                       scale, slack, sQB64, sDB64, sDB, sGE, sC, colpart, colthr, \
-                                                       wcnt, wbuf, wcap, rowthr, xb,                             \
-                                                       COLS ? reinterpret_cast<Entry*>(sC) : sQ)
-        {
-            const bool full_tile = y_end - ytile >= (int64_t)(NB * 32) && x0 + BX <= xe;
-            if (!APPEND && STATS) {
-                if (full_tile) HM_EPILOGUE(true, !APPEND);
-                else HM_EPILOGUE(false, !APPEND);
-            } else {
-                if (full_tile) HM_EPILOGUE(true, false);
-                else HM_EPILOGUE(false, false);
-            }
-        }
+#define HM_EPILOGUE(FULL_TILE)                                                                                  \
+    sweep_epilogue<K1, COLS, APPEND, BY, FULL_TILE>(acc, s, tid, wave, h, r, ytile, y_end, x0, panel, n, scale,  \
+                                                   STATS, slack, sQB64, sDB64, sDB, sGE, sC, colpart, colthr,    \
+                                                   wcnt, wbuf, wcap, rowthr, xb,                                 \
+                                                   COLS ? reinterpret_cast<Entry*>(sC) : sQ)
+        if (y_end - ytile >= (int64_t)(NB * 32) && x0 + BX <= xe) HM_EPILOGUE(true);
+        else HM_EPILOGUE(false);
 #undef HM_EPILOGUE
     }
     wait_vmcnt<0>();  // the loads ahead into LDS land before the workgroup can end
@@ -1360,11 +1343,12 @@ __device__ __forceinline__ void cand_merge(unsigned long long (&k)[K], int m) {
 // ytile + 32y + 8(q/4) + 4h + q%4. Rows: the lane's list (half h of segment seg) is read from `part` (or starts
 // empty at the segment's first tile), takes w = scale*dot + db in increasing j and is written back; APPEND
 // queues candidates instead. Columns as in sweep_epilogue, over the panel's 256 X rows.
-template <int K1, bool COLS, bool APPEND, bool STATS>
+template <int K1, bool COLS, bool APPEND>
 __device__ __forceinline__ void sweep_epilogue_w(const float (&tot)[NB][16], int64_t row, bool ok, float qbi,
                                                  float pi, float wt, bool first, int tid, int wave, int h, int r,
                                                  int64_t ytile, int64_t y_end, int64_t x0, int64_t xb, int64_t rows,
-                                                 int64_t seg, int64_t panel, int64_t n, float scale, float slack, const double* sQB64, const double* sDB64,
+                                                 int64_t seg, int64_t panel, int64_t n, float scale, int STATS,
+                                                 float slack, const double* sQB64, const double* sDB64,
                                                  const float* sDB, const float* sGE, float* sC,
                                                  Entry* __restrict__ part, Entry* __restrict__ colpart,
                                                  unsigned int* __restrict__ colthr, int* __restrict__ wcnt,
@@ -1696,17 +1680,11 @@ __global__ __launch_bounds__(THREADS_W) void l2sq_sweep_split_w(
                 acc[y][q] = 0.0f;
             }
         }
-        {
-            // the certificate flag as a template argument (STATS of sweep_epilogue)
-            auto epilogue = [&](auto st) {
-                sweep_epilogue_w<K1, COLS, APPEND, decltype(st)::value>(
-                    outer, row, ok, qbi, pi, wt, ytile == y_begin, tid, wave, h, r, ytile, y_end, x0, xb, rows, seg,
-                    panel, n, scale, slack, sQB64, sDB64, sDB, sGE, sC, part, colpart, colthr, wcnt, wbuf, wcap,
-                    num64, den64, cnt, cmax, rowthr);
-            };
-            if (!APPEND && STATS) epilogue(std::integral_constant<bool, !APPEND>{});
-            else epilogue(std::false_type{});
-        }
+        sweep_epilogue_w<K1, COLS, APPEND>(outer, row, ok, qbi, pi, wt, ytile == y_begin, tid, wave, h, r, ytile,
+                                           y_end, x0, xb, rows, seg, panel, n, scale, STATS, slack, sQB64, sDB64, sDB,
+                                           sGE, sC,
+                                           part,
+                                           colpart, colthr, wcnt, wbuf, wcap, num64, den64, cnt, cmax, rowthr);
 #pragma unroll
         for (int y = 0; y < NB; ++y) {
 #pragma unroll
@@ -1914,17 +1892,11 @@ __global__ __launch_bounds__(THREADS_W) void l2sq_sweep_i8_w(
                 outer[y][q] = (u * sy) * sx;
             }
         }
-        {
-            // the certificate flag as a template argument (STATS of sweep_epilogue)
-            auto epilogue = [&](auto st) {
-                sweep_epilogue_w<K1, COLS, APPEND, decltype(st)::value>(
-                    outer, row, ok, qbi, pi, wt, ytile == y_begin, tid, wave, h, r, ytile, y_end, x0, xb, rows, seg,
-                    panel, n, scale, slack, sQB64, sDB64, sDB, sGE, sC, part, colpart, colthr, wcnt, wbuf, wcap,
-                    num64, den64, cnt, cmax, rowthr);
-            };
-            if (!APPEND && STATS) epilogue(std::integral_constant<bool, !APPEND>{});
-            else epilogue(std::false_type{});
-        }
+        sweep_epilogue_w<K1, COLS, APPEND>(outer, row, ok, qbi, pi, wt, ytile == y_begin, tid, wave, h, r, ytile,
+                                           y_end, x0, xb, rows, seg, panel, n, scale, STATS, slack, sQB64, sDB64, sDB,
+                                           sGE, sC,
+                                           part,
+                                           colpart, colthr, wcnt, wbuf, wcap, num64, den64, cnt, cmax, rowthr);
     }
     wait_vmcnt<0>();  // the loads ahead into LDS land before the workgroup can end
     if (STATS) {
