@@ -535,15 +535,19 @@ __device__ __forceinline__ void sweep_row_init(SweepRow<K1>& s, int64_t row, int
 // passes the tile's scores scale*dot + qb through LDS so that each Y row keeps its best K1 over the workgroup's
 // 128 X rows, CPASS Y rows at a time (sC holds CPASS * CST floats; 256 / CPASS threads scan each row and merge
 // their lists). Ends with a barrier: the next tile may rewrite sDB / sGE / sC.
-template <int K1, bool COLS, bool APPEND, int CPASS = BY, bool FULL = false>
+template <int K1, bool COLS, bool APPEND, int CPASS, bool FULL, bool ST>
 __device__ __forceinline__ void sweep_epilogue(const v16f (&tot)[NB], SweepRow<K1>& s, int tid, int wave, int h,
                                                int r, int64_t ytile, int64_t y_end, int64_t x0, int64_t panel,
-                                               int64_t n, float scale, int STATS, float slack, const double* sQB64,
+                                               int64_t n, float scale, int STATS_, float slack, const double* sQB64,
                                                const double* sDB64, const float* sDB, const float* sGE,
                                                float* sC, Entry* __restrict__ colpart,
                                                unsigned int* __restrict__ colthr, int* __restrict__ wcnt,
                                                int* __restrict__ wbuf, int wcap, unsigned int* __restrict__ rowthr,
                                                int64_t xb, Entry* sQ) {
+    // ST = false (sweeps without the certificate) drops the certificate code, and with it a per-score test of the
+    // runtime flag (a scalar branch per score). With ST = true the flag stays a runtime test: as a compile-time
+    // constant the certificate terms get scheduled across scores and the sweeps spill.
+    const int STATS = ST ? STATS_ : 0;
     float tnum = 0.0f, tden = 0.0f;
     unsigned int tcnt = 0;
     bool near = false;  // a pair of this tile within the certificate slack (cert_fast)
@@ -739,7 +743,7 @@ __device__ __forceinline__ void sweep_finish(SweepRow<K1>& s, int tid, int lane,
 // fp32 sweep: X / Y are the fp32 features (row stride ld = d), products on v_mfma_f32_32x32x2f32.
 // APPEND (the wide pass of queued rows): no lists, columns or certificate; every candidate j of row r with
 // w >= wthr[r] is appended to wbuf[r * wcap + ...] (wcnt[r] counts all of them, also past the capacity).
-template <int K1, bool TWO_LEVEL, bool COLS, bool APPEND = false>
+template <int K1, bool TWO_LEVEL, bool COLS, bool APPEND = false, bool ST = false>
 __global__ __launch_bounds__(256) void l2sq_sweep(
     const float* __restrict__ X, const float* __restrict__ Y, int64_t xb, int64_t xe, int64_t n, int d, int ld,
     const float* __restrict__ qb32, const float* __restrict__ db32, const float* __restrict__ p32,
@@ -934,7 +938,7 @@ __global__ __launch_bounds__(256) void l2sq_sweep(
             }
         }
 #define HM_EPILOGUE(FULL_TILE)                                                                                  \
-    sweep_epilogue<K1, COLS, APPEND, BY, FULL_TILE>(acc, s, tid, wave, h, r, ytile, y_end, x0, panel, n, scale,  \
+    sweep_epilogue<K1, COLS, APPEND, BY, FULL_TILE, ST>(acc, s, tid, wave, h, r, ytile, y_end, x0, panel, n, scale,  \
                                                    STATS, slack, sQB64, sDB64, sDB, sGE, sC, colpart, colthr,    \
                                                    wcnt, wbuf, wcap, rowthr, xb,                                 \
                                                    COLS ? reinterpret_cast<Entry*>(sC) : sQ)
@@ -1041,7 +1045,7 @@ __device__ __forceinline__ void ring_barrier() {
 // scheduling groups (masks of __builtin_amdgcn_sched_group_barrier)
 constexpr int SG_VALU = 0x002, SG_MFMA = 0x008, SG_VMEM_READ = 0x020, SG_DS_READ = 0x100;
 
-template <int K1, bool COLS, bool APPEND = false>
+template <int K1, bool COLS, bool APPEND = false, bool ST = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(COLS ? 1 : 2))) void l2sq_sweep_split(
     const float* __restrict__ X, const float* __restrict__ Y, int64_t xb, int64_t xe, int64_t n, int d, int ld,
     const float* __restrict__ qb32, const float* __restrict__ db32, const float* __restrict__ p32,
@@ -1207,7 +1211,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(COLS ? 1 : 
             step(I3{});
         }
 #define HM_EPILOGUE(FULL_TILE)                                                                                  \
-    sweep_epilogue<K1, COLS, APPEND, BY, FULL_TILE>(acc, s, tid, wave, h, r, ytile, y_end, x0, panel, n, scale,  \
+    sweep_epilogue<K1, COLS, APPEND, BY, FULL_TILE, ST>(acc, s, tid, wave, h, r, ytile, y_end, x0, panel, n, scale,  \
                                                    STATS, slack, sQB64, sDB64, sDB, sGE, sC, colpart, colthr,    \
                                                    wcnt, wbuf, wcap, rowthr, xb,                                 \
                                                    COLS ? reinterpret_cast<Entry*>(sC) : sQ)
@@ -1343,11 +1347,11 @@ __device__ __forceinline__ void cand_merge(unsigned long long (&k)[K], int m) {
 // ytile + 32y + 8(q/4) + 4h + q%4. Rows: the lane's list (half h of segment seg) is read from `part` (or starts
 // empty at the segment's first tile), takes w = scale*dot + db in increasing j and is written back; APPEND
 // queues candidates instead. Columns as in sweep_epilogue, over the panel's 256 X rows.
-template <int K1, bool COLS, bool APPEND>
+template <int K1, bool COLS, bool APPEND, bool ST>
 __device__ __forceinline__ void sweep_epilogue_w(const float (&tot)[NB][16], int64_t row, bool ok, float qbi,
                                                  float pi, float wt, bool first, int tid, int wave, int h, int r,
                                                  int64_t ytile, int64_t y_end, int64_t x0, int64_t xb, int64_t rows,
-                                                 int64_t seg, int64_t panel, int64_t n, float scale, int STATS,
+                                                 int64_t seg, int64_t panel, int64_t n, float scale, int STATS_,
                                                  float slack, const double* sQB64, const double* sDB64,
                                                  const float* sDB, const float* sGE, float* sC,
                                                  Entry* __restrict__ part, Entry* __restrict__ colpart,
@@ -1355,6 +1359,7 @@ __device__ __forceinline__ void sweep_epilogue_w(const float (&tot)[NB][16], int
                                                  int* __restrict__ wbuf, int wcap, double& num64, double& den64,
                                                  unsigned int& cnt, float& cmax,
                                                  unsigned int* __restrict__ rowthr) {
+    const int STATS = ST ? STATS_ : 0;  // as in sweep_epilogue
     float tnum = 0.0f, tden = 0.0f;
     unsigned int tcnt = 0;
     bool near = false;  // a pair of this tile within the certificate slack (cert_fast)
@@ -1523,7 +1528,7 @@ __device__ __forceinline__ void sweep_epilogue_w(const float (&tot)[NB][16], int
     __syncthreads();  // all epilogue reads of sDB/sGE/sC finish before the next tile rewrites them
 }
 
-template <int K1, bool COLS, bool APPEND = false>
+template <int K1, bool COLS, bool APPEND = false, bool ST = false>
 __global__ __launch_bounds__(THREADS_W) void l2sq_sweep_split_w(
     const float* __restrict__ X, const float* __restrict__ Y, int64_t xb, int64_t xe, int64_t n, int d, int ld,
     const float* __restrict__ qb32, const float* __restrict__ db32, const float* __restrict__ p32,
@@ -1680,7 +1685,7 @@ __global__ __launch_bounds__(THREADS_W) void l2sq_sweep_split_w(
                 acc[y][q] = 0.0f;
             }
         }
-        sweep_epilogue_w<K1, COLS, APPEND>(outer, row, ok, qbi, pi, wt, ytile == y_begin, tid, wave, h, r, ytile,
+        sweep_epilogue_w<K1, COLS, APPEND, ST>(outer, row, ok, qbi, pi, wt, ytile == y_begin, tid, wave, h, r, ytile,
                                            y_end, x0, xb, rows, seg, panel, n, scale, STATS, slack, sQB64, sDB64, sDB,
                                            sGE, sC,
                                            part,
@@ -1731,7 +1736,7 @@ __device__ __forceinline__ void i8_pass(v16i (&acc)[NB], const YHalf& yp, const 
     acc[3] = __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(v4i, yp.b3), xv, acc[3], 0, 0, 0);
 }
 
-template <int K1, bool COLS, bool APPEND = false>
+template <int K1, bool COLS, bool APPEND = false, bool ST = false>
 __global__ __launch_bounds__(THREADS_W) void l2sq_sweep_i8_w(
     const float* __restrict__ X, const float* __restrict__ Y, int64_t xb, int64_t xe, int64_t n, int d, int ld,
     const float* __restrict__ qb32, const float* __restrict__ db32, const float* __restrict__ p32,
@@ -1892,7 +1897,7 @@ __global__ __launch_bounds__(THREADS_W) void l2sq_sweep_i8_w(
                 outer[y][q] = (u * sy) * sx;
             }
         }
-        sweep_epilogue_w<K1, COLS, APPEND>(outer, row, ok, qbi, pi, wt, ytile == y_begin, tid, wave, h, r, ytile,
+        sweep_epilogue_w<K1, COLS, APPEND, ST>(outer, row, ok, qbi, pi, wt, ytile == y_begin, tid, wave, h, r, ytile,
                                            y_end, x0, xb, rows, seg, panel, n, scale, STATS, slack, sQB64, sDB64, sDB,
                                            sGE, sC,
                                            part,
@@ -3140,32 +3145,46 @@ int run_bidir(hipStream_t st, const float* X, const float* Y, int64_t m, int64_t
                            st, rowthr, rows, neg_inf_key);
         HM_LAUNCH_CHECK("fill_u32");
 #define NOWIDE (const float*)nullptr, (int*)nullptr, (int*)nullptr, 0
-#define HM_SWEEP(TL, CL)                                                                                             \
+#define HM_SWEEP(TL, CL, ST)                                                                                         \
     do {                                                                                                             \
         if (i8)                                                                                                      \
-            hipLaunchKernelGGL((l2sq_sweep_i8_w<K1, CL>), grid, dim3(THREADS_W), 0, st, SXc, SY, xb, xe, n, sd, ld,  \
+            hipLaunchKernelGGL((l2sq_sweep_i8_w<K1, CL, false, ST>), grid, dim3(THREADS_W), 0, st, SXc, SY, xb, xe, n, sd, ld,  \
                                qb32, db32, p32, ge32, (float)scale, plan.seg_len, (int)panels, plan.S, part,         \
                                colpart, colthr, blockstats, (int)want_stats, cert, q8.xqs, q8.yqs, NOWIDE, rowthr); \
         else if (split && TL)                                                                                        \
-            hipLaunchKernelGGL((l2sq_sweep_split_w<K1, CL>), grid, dim3(THREADS_W), 0, st, SXc, SY, xb, xe, n, sd,   \
+            hipLaunchKernelGGL((l2sq_sweep_split_w<K1, CL, false, ST>), grid, dim3(THREADS_W), 0, st, SXc, SY, xb,   \
+                               xe, n, sd,                                                                            \
                                ld, qb32, db32, p32, ge32, (float)scale, plan.seg_len, (int)panels, plan.S, part,     \
                                colpart, colthr, blockstats, (int)want_stats, cert, NOWIDE, rowthr);                 \
         else if (split)                                                                                              \
-            hipLaunchKernelGGL((l2sq_sweep_split<K1, CL>), grid, dim3(256), 0, st, SXc, SY, xb, xe, n, sd, ld, \
+            hipLaunchKernelGGL((l2sq_sweep_split<K1, CL, false, ST>), grid, dim3(256), 0, st, SXc, SY, xb, xe, n,    \
+                               sd, ld,                                                                               \
                                qb32, db32, p32, ge32, (float)scale, plan.seg_len, (int)panels, plan.S, part,         \
                                colpart, colthr, blockstats, (int)want_stats, cert, NOWIDE, rowthr);                 \
         else                                                                                                         \
-            hipLaunchKernelGGL((l2sq_sweep<K1, TL, CL>), grid, dim3(256), 0, st, X, Y, xb, xe, n, d, d, qb32,        \
+            hipLaunchKernelGGL((l2sq_sweep<K1, TL, CL, false, ST>), grid, dim3(256), 0, st, X, Y, xb, xe, n, d, d,   \
+                               qb32,                                                                                 \
                                db32, p32, ge32, (float)scale, plan.seg_len, (int)panels, plan.S, part, colpart,      \
                                colthr, blockstats, (int)vec4, (int)want_stats, cert, NOWIDE, rowthr);               \
     } while (0)
         prof_begin(st, "l2sq_sweep");
-        if (two_level) {
-            if (fused) HM_SWEEP(true, true);
-            else HM_SWEEP(true, false);
+        // sweeps without the certificate take the instantiation without its code (ST of sweep_epilogue)
+        if (want_stats) {
+            if (two_level) {
+                if (fused) HM_SWEEP(true, true, true);
+                else HM_SWEEP(true, false, true);
+            } else {
+                if (fused) HM_SWEEP(false, true, true);
+                else HM_SWEEP(false, false, true);
+            }
         } else {
-            if (fused) HM_SWEEP(false, true);
-            else HM_SWEEP(false, false);
+            if (two_level) {
+                if (fused) HM_SWEEP(true, true, false);
+                else HM_SWEEP(true, false, false);
+            } else {
+                if (fused) HM_SWEEP(false, true, false);
+                else HM_SWEEP(false, false, false);
+            }
         }
         prof_end(st);
 #undef HM_SWEEP
