@@ -229,16 +229,18 @@ __device__ void column_enter(const ColArgs& ca, SlotRun& run, unsigned long long
 // gate: the role-swapped column sweep of a fused call runs only when the fused buffer overflowed (*gate > cap).
 // The fused sweep is held to 64 VGPRs (eight waves per SIMD): the slow path's temporaries then spill to scratch,
 // which costs far less than the three waves per SIMD its registers would take from the pair loop.
-template <int KIND, int K, int DR, bool EXACT, bool FUSED>
+template <int KIND, int K, int DR, bool EXACT, bool FUSED, bool ST>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(FUSED ? 8 : 1))) void norm_sweep(const float* __restrict__ X, const float* __restrict__ Y, int64_t m,
                                                   int64_t n, int d, const double* __restrict__ rb,
                                                   const double* __restrict__ cb,
                                                   const unsigned long long* __restrict__ ymaxima, int k,
                                                   int64_t seg_len, double* __restrict__ part_v, int* __restrict__ part_i,
-                                                  double* __restrict__ blockstats, int STATS, int TRANSPOSED, int ntile,
+                                                  double* __restrict__ blockstats, int STATS_, int TRANSPOSED, int ntile,
                                                   ColArgs ca, const unsigned long long* __restrict__ gate,
                                                   int64_t gate_cap) {
     static_assert(!FUSED || K == 2, "fused column lists hold two slots");
+    // sweeps without the certificate (ST = false) drop its code, and with it a per-pair test of the runtime flag
+    const int STATS = ST ? STATS_ : 0;
     if (gate != nullptr && *gate <= (unsigned long long)gate_cap) return;  // uniform: the fused lists are complete
     extern __shared__ float4 smem4[];
     float* smem = reinterpret_cast<float*>(smem4);
@@ -709,9 +711,14 @@ int norm_direction_t(hipStream_t st, const Direction& D, int d, int k, const Nor
     if ((size_t)ntile * (d + 1) > LDS_FLOATS) return fail(HM_EINVAL, "norm pricing supports d <= %d", LDS_FLOATS - 1);
     const size_t shmem = ((size_t)ntile * d + ntile) * sizeof(float);
     prof_begin(st, D.gate != nullptr ? "norm_sweep_swapped" : "norm_sweep");
-    hipLaunchKernelGGL((norm_sweep<KIND, K, DR, EXACT, FUSED>), grid, dim3(256), shmem, st, D.X, D.Y, D.m, D.n, d, D.rb,
-                       D.cb, D.ymaxima, k, D.plan.seg_len, w.pv, w.pi, w.bs, (int)D.stats, (int)D.transposed, ntile,
-                       D.cols, D.gate, D.gate_cap);
+    if (D.stats)
+        hipLaunchKernelGGL((norm_sweep<KIND, K, DR, EXACT, FUSED, true>), grid, dim3(256), shmem, st, D.X, D.Y, D.m, D.n,
+                           d, D.rb, D.cb, D.ymaxima, k, D.plan.seg_len, w.pv, w.pi, w.bs, 1, (int)D.transposed, ntile,
+                           D.cols, D.gate, D.gate_cap);
+    else
+        hipLaunchKernelGGL((norm_sweep<KIND, K, DR, EXACT, FUSED, false>), grid, dim3(256), shmem, st, D.X, D.Y, D.m,
+                           D.n, d, D.rb, D.cb, D.ymaxima, k, D.plan.seg_len, w.pv, w.pi, w.bs, 0, (int)D.transposed,
+                           ntile, D.cols, D.gate, D.gate_cap);
     prof_end(st);
     HM_LAUNCH_CHECK("norm_sweep");
     hipLaunchKernelGGL((norm_merge<K>), dim3((unsigned)((D.m + 255) / 256)), dim3(256), 0, st, w.pv, w.pi, D.m, D.plan.S,
