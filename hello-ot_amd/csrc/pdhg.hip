@@ -58,6 +58,9 @@ struct Pdhg {
     // edges, target order
     int32_t *row_t, *col_t;
     double *cs_t, *x_t, *ax_t, *px_t;
+    // node-block passes: each edge's own node within its block (the low bits of row / col_t; blocks hold a power
+    // of two of consecutive nodes), one byte per edge instead of the four-byte node number
+    uint8_t *loc_s, *loc_t;
     // nodes
     double *scale, *bs, *ns, *y, *ay, *py, *dy, *td, *sd;
     int32_t *deg, *off, *eid;
@@ -96,6 +99,8 @@ void pdhg_layout(A& a, int64_t n, int64_t nt, int64_t e, size_t sort_tmp, size_t
     P.x_t = a.template take<double>(e);
     P.ax_t = a.template take<double>(e);
     P.px_t = a.template take<double>(e);
+    P.loc_s = a.template take<uint8_t>(e);
+    P.loc_t = a.template take<uint8_t>(e);
     P.scale = a.template take<double>(nodes);
     P.bs = a.template take<double>(nodes);
     P.ns = a.template take<double>(nodes);
@@ -168,6 +173,12 @@ constexpr int ORDER_ROUNDS = 6;  // neighbour-averaging rounds (each: sources fr
 // ---------------------------------------------------------------------------------------------------------
 // setup kernels
 // ---------------------------------------------------------------------------------------------------------
+// low bits of each edge's node number (its index within a node block of mask + 1 nodes)
+__global__ void k_low_bits(const int32_t* __restrict__ node, int64_t e, int32_t mask, uint8_t* __restrict__ out) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < e; i += (int64_t)gridDim.x * blockDim.x)
+        out[i] = (uint8_t)(node[i] & mask);
+}
+
 __global__ void k_fill_i32(int32_t* p, int64_t count, int32_t v) {
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < count; i += (int64_t)gridDim.x * blockDim.x)
         p[i] = v;
@@ -627,7 +638,7 @@ __global__ __launch_bounds__(PT) void k_source_block(const Pdhg P, double primal
         const int len = e1 - base < EB ? e1 - base : EB;
         for (int q = tid; q < len; q += PT) {
             const int32_t p = base + q;
-            const double at = sdl[P.row[p] - n0] + P.td[P.col[p]];
+            const double at = sdl[P.loc_s[p]] + P.td[P.col[p]];
             const double xj = P.x[p];
             const double pxj = fmax(xj - primal_step * (P.cs[p] - at), 0.0);
             const double r = 2.0 * pxj - xj;
@@ -671,7 +682,7 @@ __global__ __launch_bounds__(PT) void k_target_block(const Pdhg P, double primal
         const int len = e1 - base < EB ? e1 - base : EB;
         for (int q = tid; q < len; q += PT) {
             const int32_t k = base + q;
-            const double at = P.sd[P.row_t[k]] + tdl[P.col_t[k] - t0];
+            const double at = P.sd[P.row_t[k]] + tdl[P.loc_t[k]];
             const double xj = P.x_t[k];
             const double pxj = fmax(xj - primal_step * (P.cs_t[k] - at), 0.0);
             const double r = 2.0 * pxj - xj;
@@ -961,6 +972,10 @@ extern "C" int hm_pdhg_solve(void* stream, const int64_t* rows, const int64_t* c
     int64_t local_count = 0, local_inner = 0;
     const unsigned gr = grid_of(e > nodes ? e : nodes);
     const SidePlan src = side_plan(e, n, flag[1]), tgt = side_plan(e, nt, flag[2]);
+    static_assert(PT <= 256, "a node's index within its block fits one byte");
+    if (src.u == 0) hipLaunchKernelGGL(k_low_bits, dim3(grid_of(e)), dim3(256), 0, st, P.row, e, src.npb - 1, P.loc_s);
+    if (tgt.u == 0) hipLaunchKernelGGL(k_low_bits, dim3(grid_of(e)), dim3(256), 0, st, P.col_t, e, tgt.npb - 1, P.loc_t);
+    HM_LAUNCH_CHECK("k_low_bits");
     for (;;) {
         if (local_count % freq == 0) {
             hipLaunchKernelGGL(k_evaluate, dim3(RB), dim3(RT), 0, st, P, masses, costs, variable, bound, objective,
