@@ -61,6 +61,11 @@ struct Pdhg {
     // node-block passes: each edge's own node within its block (the low bits of row / col_t; blocks hold a power
     // of two of consecutive nodes), one byte per edge instead of the four-byte node number
     uint8_t *loc_s, *loc_t;
+    // node-block passes: the other side's node each edge gathers from (col / row_t) as a 16-bit offset from its
+    // block's smallest one, when the block's edges span fewer than 65536 nodes of that side (gbase = that
+    // smallest node), else gbase = -1 and the pass reads the 4-byte number
+    uint16_t *g16_s, *g16_t;
+    int32_t *gbase_s, *gbase_t;
     // nodes
     double *scale, *bs, *ns, *y, *ay, *py, *dy, *td, *sd;
     int32_t *deg, *off, *eid;
@@ -101,6 +106,10 @@ void pdhg_layout(A& a, int64_t n, int64_t nt, int64_t e, size_t sort_tmp, size_t
     P.px_t = a.template take<double>(e);
     P.loc_s = a.template take<uint8_t>(e);
     P.loc_t = a.template take<uint8_t>(e);
+    P.g16_s = a.template take<uint16_t>(e);
+    P.g16_t = a.template take<uint16_t>(e);
+    P.gbase_s = a.template take<int32_t>(n + 1);
+    P.gbase_t = a.template take<int32_t>(nt + 1);
     P.scale = a.template take<double>(nodes);
     P.bs = a.template take<double>(nodes);
     P.ns = a.template take<double>(nodes);
@@ -173,6 +182,40 @@ constexpr int ORDER_ROUNDS = 6;  // neighbour-averaging rounds (each: sources fr
 // ---------------------------------------------------------------------------------------------------------
 // setup kernels
 // ---------------------------------------------------------------------------------------------------------
+// Per node block (one workgroup each): the range of the other side's nodes its edges gather from, and when it spans
+// fewer than 65536 nodes, each edge's gathered node as an offset from the smallest (Pdhg::g16_*, gbase_*). The
+// block's edges are [off[b * npb] - ebase, off[min((b + 1) * npb, nodes)] - ebase).
+__global__ __launch_bounds__(256) void k_gather_base(const int32_t* __restrict__ off, int64_t nodes, int npb,
+                                                     int32_t ebase, const int32_t* __restrict__ gidx,
+                                                     int32_t* __restrict__ gbase, uint16_t* __restrict__ g16) {
+    __shared__ int32_t smin[256], smax[256];
+    const int64_t b = blockIdx.x;
+    const int64_t n0 = b * npb, n1 = n0 + npb < nodes ? n0 + npb : nodes;
+    const int32_t e0 = off[n0] - ebase, e1 = off[n1] - ebase;
+    int32_t lo = INT32_MAX, hi = INT32_MIN;
+    for (int32_t p = e0 + (int32_t)threadIdx.x; p < e1; p += 256) {
+        const int32_t g = gidx[p];
+        lo = g < lo ? g : lo;
+        hi = g > hi ? g : hi;
+    }
+    smin[threadIdx.x] = lo;
+    smax[threadIdx.x] = hi;
+    __syncthreads();
+    for (int w = 128; w >= 1; w >>= 1) {
+        if ((int)threadIdx.x < w) {
+            smin[threadIdx.x] = smin[threadIdx.x + w] < smin[threadIdx.x] ? smin[threadIdx.x + w] : smin[threadIdx.x];
+            smax[threadIdx.x] = smax[threadIdx.x + w] > smax[threadIdx.x] ? smax[threadIdx.x + w] : smax[threadIdx.x];
+        }
+        __syncthreads();
+    }
+    lo = smin[0];
+    hi = smax[0];
+    const bool narrow = e1 > e0 && (int64_t)hi - (int64_t)lo < 65536;
+    if (threadIdx.x == 0) gbase[b] = narrow ? lo : -1;
+    if (narrow)
+        for (int32_t p = e0 + (int32_t)threadIdx.x; p < e1; p += 256) g16[p] = (uint16_t)(gidx[p] - lo);
+}
+
 // low bits of each edge's node number (its index within a node block of mask + 1 nodes)
 __global__ void k_low_bits(const int32_t* __restrict__ node, int64_t e, int32_t mask, uint8_t* __restrict__ out) {
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < e; i += (int64_t)gridDim.x * blockDim.x)
@@ -634,18 +677,24 @@ __global__ __launch_bounds__(PT) void k_source_block(const Pdhg P, double primal
     const int32_t e0 = soff[0], e1 = soff[nn];
     const int32_t k0 = tid < nn ? soff[tid] : 0, k1 = tid < nn ? soff[tid + 1] : 0;
     double sum = 0.0;
+    const int32_t gb = P.gbase_s[blockIdx.x];  // uniform: 16-bit gather offsets, or -1 for 4-byte numbers
+    // edge p (slot q of the round) with its target c
+    auto step = [&](int32_t p, int q, int32_t c) {
+        const double at = sdl[P.loc_s[p]] + P.td[c];
+        const double xj = P.x[p];
+        const double pxj = fmax(xj - primal_step * (P.cs[p] - at), 0.0);
+        const double r = 2.0 * pxj - xj;
+        if (STORE) P.px[p] = pxj;
+        if (CHECKPOINT) P.dx[p] = r - xj;
+        P.x[p] = halpern * r + keep * P.ax[p];
+        sr[q] = r;
+    };
     for (int32_t base = e0; base < e1; base += EB) {
         const int len = e1 - base < EB ? e1 - base : EB;
-        for (int q = tid; q < len; q += PT) {
-            const int32_t p = base + q;
-            const double at = sdl[P.loc_s[p]] + P.td[P.col[p]];
-            const double xj = P.x[p];
-            const double pxj = fmax(xj - primal_step * (P.cs[p] - at), 0.0);
-            const double r = 2.0 * pxj - xj;
-            if (STORE) P.px[p] = pxj;
-            if (CHECKPOINT) P.dx[p] = r - xj;
-            P.x[p] = halpern * r + keep * P.ax[p];
-            sr[q] = r;
+        if (gb >= 0) {
+            for (int q = tid; q < len; q += PT) step(base + q, q, gb + (int32_t)P.g16_s[base + q]);
+        } else {
+            for (int q = tid; q < len; q += PT) step(base + q, q, P.col[base + q]);
         }
         __syncthreads();
         sum = fold_in_order(sr, (k0 > base ? k0 : base) - base, (k1 < base + len ? k1 : base + len) - base, sum);
@@ -678,17 +727,23 @@ __global__ __launch_bounds__(PT) void k_target_block(const Pdhg P, double primal
     const int32_t e0 = soff[0], e1 = soff[nn];
     const int32_t k0 = tid < nn ? soff[tid] : 0, k1 = tid < nn ? soff[tid + 1] : 0;
     double sum = 0.0;
+    const int32_t gb = P.gbase_t[blockIdx.x];  // uniform: 16-bit gather offsets, or -1 for 4-byte numbers
+    // edge k (slot q of the round) with its source c
+    auto step = [&](int32_t k, int q, int32_t c) {
+        const double at = P.sd[c] + tdl[P.loc_t[k]];
+        const double xj = P.x_t[k];
+        const double pxj = fmax(xj - primal_step * (P.cs_t[k] - at), 0.0);
+        const double r = 2.0 * pxj - xj;
+        if (STORE) P.px_t[k] = pxj;
+        P.x_t[k] = halpern * r + keep * P.ax_t[k];
+        sr[q] = r;
+    };
     for (int32_t base = e0; base < e1; base += EB) {
         const int len = e1 - base < EB ? e1 - base : EB;
-        for (int q = tid; q < len; q += PT) {
-            const int32_t k = base + q;
-            const double at = P.sd[P.row_t[k]] + tdl[P.loc_t[k]];
-            const double xj = P.x_t[k];
-            const double pxj = fmax(xj - primal_step * (P.cs_t[k] - at), 0.0);
-            const double r = 2.0 * pxj - xj;
-            if (STORE) P.px_t[k] = pxj;
-            P.x_t[k] = halpern * r + keep * P.ax_t[k];
-            sr[q] = r;
+        if (gb >= 0) {
+            for (int q = tid; q < len; q += PT) step(base + q, q, gb + (int32_t)P.g16_t[base + q]);
+        } else {
+            for (int q = tid; q < len; q += PT) step(base + q, q, P.row_t[base + q]);
         }
         __syncthreads();
         sum = fold_in_order(sr, (k0 > base ? k0 : base) - base, (k1 < base + len ? k1 : base + len) - base, sum);
@@ -973,9 +1028,17 @@ extern "C" int hm_pdhg_solve(void* stream, const int64_t* rows, const int64_t* c
     const unsigned gr = grid_of(e > nodes ? e : nodes);
     const SidePlan src = side_plan(e, n, flag[1]), tgt = side_plan(e, nt, flag[2]);
     static_assert(PT <= 256, "a node's index within its block fits one byte");
-    if (src.u == 0) hipLaunchKernelGGL(k_low_bits, dim3(grid_of(e)), dim3(256), 0, st, P.row, e, src.npb - 1, P.loc_s);
-    if (tgt.u == 0) hipLaunchKernelGGL(k_low_bits, dim3(grid_of(e)), dim3(256), 0, st, P.col_t, e, tgt.npb - 1, P.loc_t);
-    HM_LAUNCH_CHECK("k_low_bits");
+    if (src.u == 0) {
+        hipLaunchKernelGGL(k_low_bits, dim3(grid_of(e)), dim3(256), 0, st, P.row, e, src.npb - 1, P.loc_s);
+        hipLaunchKernelGGL(k_gather_base, dim3((unsigned)((n + src.npb - 1) / src.npb)), dim3(256), 0, st, P.off, n,
+                           src.npb, 0, P.col, P.gbase_s, P.g16_s);
+    }
+    if (tgt.u == 0) {
+        hipLaunchKernelGGL(k_low_bits, dim3(grid_of(e)), dim3(256), 0, st, P.col_t, e, tgt.npb - 1, P.loc_t);
+        hipLaunchKernelGGL(k_gather_base, dim3((unsigned)((nt + tgt.npb - 1) / tgt.npb)), dim3(256), 0, st, P.off + n,
+                           nt, tgt.npb, (int32_t)e, P.row_t, P.gbase_t, P.g16_t);
+    }
+    HM_LAUNCH_CHECK("node-block setup");
     for (;;) {
         if (local_count % freq == 0) {
             hipLaunchKernelGGL(k_evaluate, dim3(RB), dim3(RT), 0, st, P, masses, costs, variable, bound, objective,
