@@ -213,6 +213,71 @@ def test_pdhg_node_blocks_of_several_nodes_across_rounds_match_oracle(cuda):
     np.testing.assert_allclose(r.y.cpu().numpy(), ref["y"], rtol=1e-9, atol=1e-12)
 
 
+def _nodes_per_block(nodes):
+    """The node-block pass's nodes per workgroup: about 2048 workgroups, at most 256 nodes each."""
+    npb = 1
+    while npb < 256 and npb * 2 * 2048 <= nodes:
+        npb *= 2
+    return npb
+
+
+def _gather_kinds(node, other, nodes):
+    """How each node block of a side reads its edges' other-side node numbers: as 16-bit offsets from the smallest
+    when they span fewer than 65536 nodes ("offsets"), else as 4-byte numbers ("numbers")."""
+    npb = _nodes_per_block(nodes)
+    blk = node // npb
+    order = np.argsort(blk, kind="stable")
+    blk, g = blk[order], other[order]
+    starts = np.searchsorted(blk, np.arange((nodes + npb - 1) // npb + 1))
+    kinds = []
+    for b in range(starts.size - 1):
+        e = g[starts[b]:starts[b + 1]]
+        kinds.append("offsets" if e.size and e.max() - e.min() < 65536 else "numbers")
+    return np.array(kinds)
+
+
+def test_pdhg_node_blocks_with_16_bit_gather_offsets_match_oracle(cuda, monkeypatch):
+    """131072 nodes a side, node blocks on both (hub nodes of degree 26-30 against a mean of 6.3), each source
+    joined to the next 6 targets (wrapping round), and far edges 65536 nodes away from the blocks they start in (3
+    from every eighth block, 80 from every eighth block shifted by two, each group landing in one or two blocks of
+    the other side). Both ways of reading a block's gathered node numbers then run on both sides, each in at least
+    100 blocks (checked on the host first): 16-bit offsets from the block's smallest, and 4-byte numbers."""
+    ns = nt = 131072
+    rng = np.random.default_rng(5)
+    rs = [np.repeat(np.arange(ns), 6)]
+    cs = [(np.repeat(np.arange(ns), 6) + np.tile(np.arange(6), ns)) % nt]
+    hub_s, hub_t = np.arange(7, ns, 4096), np.arange(100, nt, 4096)
+    rs.append(np.repeat(hub_s, 24))
+    cs.append((np.repeat(hub_s, 24) + 6 + np.tile(np.arange(24), hub_s.size)) % nt)
+    cs.append(np.repeat(hub_t, 20))
+    rs.append((np.repeat(hub_t, 20) - 6 - np.tile(np.arange(20), hub_t.size)) % ns)
+    for own_side, far_side, nodes, other_nodes in ((rs, cs, ns, nt), (cs, rs, nt, ns)):
+        npb = _nodes_per_block(nodes)
+        for blk in range(nodes // npb):
+            if blk % 8 in (3, 5):
+                cnt = 3 if blk % 8 == 3 else 80
+                own_side.append(rng.integers(blk * npb, (blk + 1) * npb, cnt))
+                far_side.append((blk * npb + 65536 + rng.integers(-32, 33, cnt)) % other_nodes)
+    key = np.unique(np.concatenate(rs).astype(np.int64) * nt + np.concatenate(cs).astype(np.int64))
+    perm = rng.permutation(key.size)
+    rows, cols = key[perm] // nt, key[perm] % nt
+    assert max(np.bincount(rows).max(), np.bincount(cols).max()) > 8 >= rows.size / ns   # node blocks, both sides
+    for node, other, nodes in ((rows, cols, ns), (cols, rows, nt)):
+        kinds = _gather_kinds(node, other, nodes)
+        assert all(np.count_nonzero(kinds == kind) >= 100 for kind in ("offsets", "numbers"))
+    costs = rng.random(rows.size)
+    a, b = rng.random(ns), rng.random(nt)
+    a, b = a / a.sum(), b / b.sum()
+    monkeypatch.setenv("HELLOOT_PDHG_REORDER", "off")   # the caller's numbers, whose blocks are checked above
+    ref = oracle.pdhg_solve(rows, cols, costs, a, b, evaluation_frequency=50, iteration_limit=300, tolerance=0.0)
+    r = NativeRestrictedOTPDLP(device=cuda, evaluation_frequency=50, iteration_limit=300).solve_restricted(
+        rows=rows, cols=cols, costs=costs, source_mass=a, target_mass=b, tolerance=0.0)
+    assert r.iterations == ref["iterations"] == 300
+    assert r.solver_diag["restart_count"] == ref["restart_count"]
+    np.testing.assert_allclose(r.x.cpu().numpy(), ref["x"], rtol=1e-9, atol=1e-12)
+    np.testing.assert_allclose(r.y.cpu().numpy(), ref["y"], rtol=1e-9, atol=1e-12)
+
+
 def test_pdhg_c3_shape_1000_iterations_against_oracle(cuda):
     """C3 structure (16 sorted uniform columns per row, uniform marginals, SDDMM costs), 1000 iterations,
     at m = n = 8192 where the CPU oracle finishes in seconds."""
