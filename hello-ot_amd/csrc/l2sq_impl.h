@@ -535,7 +535,7 @@ __device__ __forceinline__ void sweep_row_init(SweepRow<K1>& s, int64_t row, int
 // passes the tile's scores scale*dot + qb through LDS so that each Y row keeps its best K1 over the workgroup's
 // 128 X rows, CPASS Y rows at a time (sC holds CPASS * CST floats; 256 / CPASS threads scan each row and merge
 // their lists). Ends with a barrier: the next tile may rewrite sDB / sGE / sC.
-template <int K1, bool COLS, bool APPEND, int CPASS, bool FULL, bool ST>
+template <int K1, bool COLS, bool APPEND, int CPASS, bool FULL, bool ST, bool SRT = false>
 __device__ __forceinline__ void sweep_epilogue(const v16f (&tot)[NB], SweepRow<K1>& s, int tid, int wave, int h,
                                                int r, int64_t ytile, int64_t y_end, int64_t x0, int64_t panel,
                                                int64_t n, float scale, int STATS_, float slack, const double* sQB64,
@@ -543,7 +543,7 @@ __device__ __forceinline__ void sweep_epilogue(const v16f (&tot)[NB], SweepRow<K
                                                float* sC, Entry* __restrict__ colpart,
                                                unsigned int* __restrict__ colthr, int* __restrict__ wcnt,
                                                int* __restrict__ wbuf, int wcap, unsigned int* __restrict__ rowthr,
-                                               int64_t xb, Entry* sQ) {
+                                               int64_t xb, Entry* sQ, const unsigned int* sRT = nullptr) {
     // ST = false (sweeps without the certificate) drops the certificate code, and with it a per-score test of the
     // runtime flag (a scalar branch per score). With ST = true the flag stays a runtime test: as a compile-time
     // constant the certificate terms get scheduled across scores and the sweeps spill.
@@ -556,8 +556,13 @@ __device__ __forceinline__ void sweep_epilogue(const v16f (&tot)[NB], SweepRow<K
     // (FULL: the whole tile lies inside the segment and the whole panel inside the chunk, so every pair is inside)
     const int ylim = FULL ? NB * 32 : (int)(y_end - ytile < (int64_t)(NB * 32) ? y_end - ytile : (int64_t)(NB * 32));
     const bool rok = FULL || s.ok;
-    // the row's shared threshold: scores at or below it cannot enter the row's merged lists (row_threshold_*)
-    const float rthr = (!APPEND && rok) ? row_threshold_get(rowthr, s.row - xb) : -INFINITY;
+    // the row's shared threshold: scores at or below it cannot enter the row's merged lists (row_threshold_*);
+    // with SRT, sRT holds the panel's thresholds as read at the start of the tile
+    float rthr = -INFINITY;
+    if (!APPEND && rok && rowthr) {
+        if constexpr (SRT) rthr = key_float(sRT[wave * 32 + r]);
+        else rthr = row_threshold_get(rowthr, s.row - xb);
+    }
     const float last0 = APPEND ? 0.0f : s.lv[K1 - 1];
     // Row candidates of the tile: every score above the lane's threshold at the start of the tile is queued in the
     // lane's LDS slots, without branches (a full queue writes its spare slot), and inserted after the tile in pair
@@ -567,6 +572,10 @@ __device__ __forceinline__ void sweep_epilogue(const v16f (&tot)[NB], SweepRow<K
     int qn = 0;
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
+        // the lane's largest score among its 16 pairs of the block (pairs outside the tile excluded): the block's
+        // scores are queued only when some lane of the wave has one above its threshold, which past a segment's
+        // first tiles is rare
+        float bmax = -INFINITY;
 #pragma unroll
         for (int a = 0; a < 4; ++a) {
             const int jl0 = b * 32 + 8 * a + 4 * h;
@@ -588,11 +597,26 @@ __device__ __forceinline__ void sweep_epilogue(const v16f (&tot)[NB], SweepRow<K
                         if (pos < wcap) wbuf[s.row * (int64_t)wcap + pos] = (int)j;
                     }
                 } else {
-                    const bool cand = ok && w > qthr;
-                    myq[qn < QN ? qn : QN] = Entry{w, (int)j};
-                    qn += cand ? 1 : 0;
+                    bmax = fmaxf(bmax, ok ? w : -INFINITY);
                 }
                 if (STATS) cert_fast(ok, w, ges[cc], s.pi, s.qbi, slack, tden, s.cmax, tnum, tcnt, near);
+            }
+        }
+        if (!APPEND && __any(bmax > qthr)) {
+            // every score above the threshold, in pair order, as if each had been tested
+#pragma unroll
+            for (int a = 0; a < 4; ++a) {
+                const int jl0 = b * 32 + 8 * a + 4 * h;
+                const float4 dbv = *reinterpret_cast<const float4*>(&sDB[jl0]);
+                const float dbs[4] = {dbv.x, dbv.y, dbv.z, dbv.w};
+#pragma unroll
+                for (int cc = 0; cc < 4; ++cc) {
+                    const float w = fmaf(scale, tot[b][4 * a + cc], dbs[cc]);
+                    const bool ok = rok && (FULL || 4 * h < ylim - (b * 32 + 8 * a + cc));
+                    const bool cand = ok && w > qthr;
+                    myq[qn < QN ? qn : QN] = Entry{w, (int)(ytile + jl0 + cc)};
+                    qn += cand ? 1 : 0;
+                }
             }
         }
     }
@@ -1021,6 +1045,30 @@ __device__ __forceinline__ void load_lds16(const char* g, unsigned lds_byte) {
         : "v"(g), "s"(lds_byte));
 }
 
+// the wave-uniform LDS byte address of a shared-memory pointer (for M0)
+__device__ __forceinline__ unsigned lds_addr(const void* p) {
+    return __builtin_amdgcn_readfirstlane((unsigned)(uintptr_t)p);
+}
+
+// the lane's index, computed where it is used: the compiler cannot hoist it out of a loop and keep it (or what is
+// derived from it) live across the loop, where it would spill
+__device__ __forceinline__ unsigned lane_here() {
+    unsigned l;
+    asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
+    return l;
+}
+
+// 4 bytes per lane from global memory straight to LDS: lane l reads base + off (a wave-uniform base, a 32-bit
+// byte offset per lane) and writes lds_byte + 4 l. As load_lds16.
+__device__ __forceinline__ void load_lds4(const void* base, unsigned off, unsigned lds_byte) {
+    unsigned saved;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\ts_nop 0\n\tglobal_load_lds_dword %1, %2\n\ts_nop 0\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "v"(off), "s"(base), "s"(lds_byte));
+}
+
 // s_waitcnt that waits for the vector-memory counter only (gfx9 encoding: vmcnt in bits 3:0 and 15:14, expcnt
 // and lgkmcnt at their maxima)
 template <int N>
@@ -1071,6 +1119,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(COLS ? 1 : 
     // queued row candidates (sweep_epilogue); with column lists they use the column-score tile's space
     __shared__ Entry sQ[(APPEND || COLS) ? 1 : 256 * (QN + 1)];
     __shared__ double sRed[4][5];
+    __shared__ unsigned int sRT[APPEND ? 1 : BX];  // the panel's shared row thresholds, read per tile
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -1085,6 +1134,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(COLS ? 1 : 
     sweep_row_init<K1, APPEND>(s, x0 + wave * 32 + r, xe, STATS, qb32, p32, wthr);
     const float slack = row_cert_slack(STATS, cert, s.row, s.ok, scale);
     if (!APPEND && tid < BX) sQB64[tid] = (STATS && x0 + tid < xe) ? cert.qb[x0 + tid] : 0.0;
+    const bool stats = ST && STATS != 0;  // the certificate's biases are loaded per tile
 
     const int nchunks = d / KC;
     const int64_t bstride = (int64_t)ld * 32;          // words per 32-row block
@@ -1197,12 +1247,28 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(COLS ? 1 : 
 #pragma unroll
             for (int q = 0; q < 16; ++q) acc[b][q] = 0.0f;
         }
-        // biases of this tile's Y rows (read in the epilogue, after at least one chunk barrier)
-        if (tid < BY) {
-            const int64_t j = ytile + tid;
-            sDB[tid] = j < y_end ? db32[j] : 0.0f;
-            sGE[tid] = (STATS && j < y_end) ? ge32[j] : 0.0f;
-            if (!APPEND) sDB64[tid] = (STATS && j < y_end) ? cert.db[j] : 0.0;
+        // biases of this tile's Y rows and the panel's shared row thresholds, straight to LDS; the epilogue reads
+        // them after the first chunk's ring barrier, which waits for them as for any load older than the chunk's
+        // (loads into registers would need a wait of their own, and with it for the Y chunks in flight). Columns
+        // past the segment read the last one in it; the epilogue skips their pairs.
+        {
+            // offsets within the tile, the last column of the segment for those past it (wave-uniform bases)
+            const unsigned ln = lane_here();
+            const unsigned jlim = (unsigned)(y_end - 1 - ytile);
+            auto col = [&](unsigned t) { return t < jlim ? t : jlim; };
+            if (wave < 2) {
+                load_lds4(db32 + ytile, col(wave * 64 + ln) * 4u, lds_addr(sDB + wave * 64));
+                if (!APPEND && rowthr) {
+                    const unsigned xlim = (unsigned)(xe - 1 - x0);
+                    const unsigned t = wave * 64 + ln;
+                    load_lds4(rowthr + (x0 - xb), (t < xlim ? t : xlim) * 4u, lds_addr(sRT + wave * 64));
+                }
+            } else if (stats) {
+                load_lds4(ge32 + ytile, col((wave - 2) * 64 + ln) * 4u, lds_addr(sGE + (wave - 2) * 64));
+            }
+            if (stats && !APPEND)  // the fp64 biases as 256 dwords, 64 per wave
+                load_lds4(cert.db + ytile, col(wave * 32 + (ln >> 1)) * 8u + (ln & 1) * 4u,
+                          lds_addr(sDB64 + wave * 32));
         }
         step(I0{});
         if (nchunks > 1) step(I1{});
@@ -1211,10 +1277,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(COLS ? 1 : 
             step(I3{});
         }
 #define HM_EPILOGUE(FULL_TILE)                                                                                  \
-    sweep_epilogue<K1, COLS, APPEND, BY, FULL_TILE, ST>(acc, s, tid, wave, h, r, ytile, y_end, x0, panel, n, scale,  \
-                                                   STATS, slack, sQB64, sDB64, sDB, sGE, sC, colpart, colthr,    \
-                                                   wcnt, wbuf, wcap, rowthr, xb,                                 \
-                                                   COLS ? reinterpret_cast<Entry*>(sC) : sQ)
+    sweep_epilogue<K1, COLS, APPEND, BY, FULL_TILE, ST, true>(acc, s, tid, wave, h, r, ytile, y_end, x0, panel, n,   \
+                                                   scale, STATS, slack, sQB64, sDB64, sDB, sGE, sC, colpart,     \
+                                                   colthr, wcnt, wbuf, wcap, rowthr, xb,                         \
+                                                   COLS ? reinterpret_cast<Entry*>(sC) : sQ, sRT)
         if (y_end - ytile >= (int64_t)(NB * 32) && x0 + BX <= xe) HM_EPILOGUE(true);
         else HM_EPILOGUE(false);
 #undef HM_EPILOGUE
