@@ -572,12 +572,11 @@ __device__ __forceinline__ void sweep_epilogue(const v16f (&tot)[NB], SweepRow<K
     int qn = 0;
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
-        // the lane's largest score among its 16 pairs of the block (pairs outside the tile excluded): the block's
-        // scores are queued only when some lane of the wave has one above its threshold, which past a segment's
-        // first tiles is rare
-        float bmax = -INFINITY;
 #pragma unroll
         for (int a = 0; a < 4; ++a) {
+            // the lane's largest score among its 4 pairs of the group (pairs outside the tile excluded): the group's
+            // scores are queued only when some lane of the wave has one above its threshold
+            float amax = -INFINITY;
             const int jl0 = b * 32 + 8 * a + 4 * h;
             const float4 dbv = *reinterpret_cast<const float4*>(&sDB[jl0]);
             float4 gev = make_float4(0, 0, 0, 0);
@@ -597,18 +596,12 @@ __device__ __forceinline__ void sweep_epilogue(const v16f (&tot)[NB], SweepRow<K
                         if (pos < wcap) wbuf[s.row * (int64_t)wcap + pos] = (int)j;
                     }
                 } else {
-                    bmax = fmaxf(bmax, ok ? w : -INFINITY);
+                    amax = fmaxf(amax, ok ? w : -INFINITY);
                 }
                 if (STATS) cert_fast(ok, w, ges[cc], s.pi, s.qbi, slack, tden, s.cmax, tnum, tcnt, near);
             }
-        }
-        if (!APPEND && __any(bmax > qthr)) {
-            // every score above the threshold, in pair order, as if each had been tested
-#pragma unroll
-            for (int a = 0; a < 4; ++a) {
-                const int jl0 = b * 32 + 8 * a + 4 * h;
-                const float4 dbv = *reinterpret_cast<const float4*>(&sDB[jl0]);
-                const float dbs[4] = {dbv.x, dbv.y, dbv.z, dbv.w};
+            if (!APPEND && __any(amax > qthr)) {
+                // every score above the threshold, in pair order, as if each had been tested
 #pragma unroll
                 for (int cc = 0; cc < 4; ++cc) {
                     const float w = fmaf(scale, tot[b][4 * a + cc], dbs[cc]);
@@ -999,13 +992,16 @@ __device__ __forceinline__ float4 ld16(const float* base, unsigned byte_off) {
 }
 __device__ __forceinline__ bf16x8 as_bf16x8(const float4& v) { return __builtin_bit_cast(bf16x8, v); }
 
-// one K-step: acc[b] += Y_hi*X_hi, then Y_hi*X_lo, then Y_lo*X_hi
+// one K-step: acc[b] += Y_hi*X_hi, then Y_hi*X_lo, then Y_lo*X_hi; with ZERO the first products start from 0
+// (the accumulators' first K-step of a tile: the MFMA takes 0 as its addend, so no clearing is needed)
+template <bool ZERO = false>
 __device__ __forceinline__ void split_kstep(v16f (&acc)[NB], const YOps& a, const float4& xh4, const float4& xl4) {
     const bf16x8 xh = as_bf16x8(xh4), xl = as_bf16x8(xl4);
-    acc[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a.h0), xh, acc[0], 0, 0, 0);
-    acc[1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a.h1), xh, acc[1], 0, 0, 0);
-    acc[2] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a.h2), xh, acc[2], 0, 0, 0);
-    acc[3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a.h3), xh, acc[3], 0, 0, 0);
+    const v16f zero = {};
+    acc[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a.h0), xh, ZERO ? zero : acc[0], 0, 0, 0);
+    acc[1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a.h1), xh, ZERO ? zero : acc[1], 0, 0, 0);
+    acc[2] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a.h2), xh, ZERO ? zero : acc[2], 0, 0, 0);
+    acc[3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a.h3), xh, ZERO ? zero : acc[3], 0, 0, 0);
     acc[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a.h0), xl, acc[0], 0, 0, 0);
     acc[1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a.h1), xl, acc[1], 0, 0, 0);
     acc[2] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a.h2), xl, acc[2], 0, 0, 0);
@@ -1043,6 +1039,22 @@ __device__ __forceinline__ void load_lds16(const char* g, unsigned lds_byte) {
         "s_mov_b32 m0, %0"
         : "=&s"(saved)
         : "v"(g), "s"(lds_byte));
+}
+
+// Four loads as load_lds16 from one per-lane offset: lane l reads b_i + off (b_i wave-uniform) and writes
+// lds_i + 16 l; M0 is saved once.
+__device__ __forceinline__ void load_lds16x4(const char* b0, const char* b1, const char* b2, const char* b3,
+                                             unsigned off, unsigned l0, unsigned l1, unsigned l2, unsigned l3) {
+    unsigned saved;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %6\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2\n\ts_nop 0\n\t"
+        "s_mov_b32 m0, %7\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %3\n\ts_nop 0\n\t"
+        "s_mov_b32 m0, %8\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %4\n\ts_nop 0\n\t"
+        "s_mov_b32 m0, %9\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %5\n\ts_nop 0\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "v"(off), "s"(b0), "s"(b1), "s"(b2), "s"(b3), "s"(l0), "s"(l1), "s"(l2), "s"(l3));
 }
 
 // the wave-uniform LDS byte address of a shared-memory pointer (for M0)
@@ -1142,10 +1154,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(COLS ? 1 : 
     const unsigned lane16 = (unsigned)lane * 16u;
     const unsigned tid16 = (unsigned)tid * 16u;
     const unsigned ystep = (unsigned)(bstride * 4);     // bytes between consecutive Y blocks
-    auto ystage = [&](int st) -> float4* {
-        static_assert(NS == 3, "stage table");
-        return st == 0 ? sY0 : st == 1 ? sY1 : sY2;
-    };
 
     auto load_x = [&](XOps& o, int cc) {
         const float* b = Xw + cc * 1024;
@@ -1154,22 +1162,24 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(COLS ? 1 : 
         o.h1 = ld16(b, 2048u + lane16);
         o.l1 = ld16(b, 3072u + lane16);
     };
-    // Y chunk position AHEAD chunks past the one multiplied (ta, ca); past the segment any in-bounds chunk will
-    // do, its data is never multiplied. Branch-free, so that a chunk step stays one scheduling region.
+    // Y chunk position AHEAD chunks past the one multiplied (ta, ca) and its address ya (chunk ca of the tile at
+    // row ta: Y + ta*ld + ca*1024 words), advanced chunk by chunk; past the segment any in-bounds chunk will do, its
+    // data is never multiplied. Branch-free, so that a chunk step stays one scheduling region.
     int64_t ta = y_begin;
     int ca = 0;
+    const char* const yfirst = reinterpret_cast<const char*>(Y + (y_begin >> 5) * bstride);
+    const char* ya = yfirst;
+    const int64_t wrap_bytes = (4 * bstride - (int64_t)(nchunks - 1) * 1024) * 4;  // last chunk -> next tile's first
     auto load_ahead = [&](float4* stage) {
-        const bool past = ta >= y_end;
-        const char* b = reinterpret_cast<const char*>(Y + ((past ? y_begin : ta) >> 5) * bstride + (past ? 0 : ca) * 1024);
+        const char* b = ta < y_end ? ya : yfirst;
         // thread t's 16 bytes of block i go to stage + i*4 KiB + t*16; one wave instruction fills 1 KiB
-        float4* dst = stage + wave * 64;
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-            load_lds16(b + i * ystep + tid16, __builtin_amdgcn_readfirstlane((unsigned)(uintptr_t)(dst + i * 256)));
+        const unsigned dst = lds_addr(stage + wave * 64);
+        load_lds16x4(b, b + ystep, b + 2 * ystep, b + 3 * ystep, tid16, dst, dst + 4096u, dst + 8192u, dst + 12288u);
         ++ca;
         const bool wrap = ca == nchunks;
         ca = wrap ? 0 : ca;
         ta = wrap ? ta + BY : ta;
+        ya += wrap ? wrap_bytes : 4096;
     };
     auto read_ops = [&](YOps& o, const float4* stage, int ks) {
         const float4* src = stage + ks * 128 + lane;
@@ -1185,7 +1195,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(COLS ? 1 : 
 
     XOps xs0, xs1, xs2, xs3;  // X operands of chunks 0..3
     YOps o0, o1;              // Y operands of K-steps 0 and 1
-    int st0 = 0;              // LDS stage of the chunk being multiplied
+    // LDS stages of the chunk being multiplied, the next one, and the one refilled (with the chunk AHEAD further)
+    float4 *cur = sY0, *nxt = sY1, *fill = sY2;
+    static_assert(NS == 3, "three stages rotate");
 
     static_assert(AHEAD == 2, "initial ring fill");
     load_ahead(sY0);
@@ -1207,12 +1219,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(COLS ? 1 : 
         constexpr int U = decltype(uc)::value;
         XOps& xs = xset<U>(xs0, xs1, xs2, xs3);
         // K-step 0, then the Y chunk AHEAD further into the stage chunk - 1 used
-        const int st1 = st0 == NS - 1 ? 0 : st0 + 1;
-        float4* cur = ystage(st0);
-        float4* nxt = ystage(st1);
-        float4* fill = ystage(st0 == 0 ? NS - 1 : st0 - 1);
         read_ops(o1, cur, 1);
-        split_kstep(acc, o0, xs.h0, xs.l0);
+        split_kstep<U == 0>(acc, o0, xs.h0, xs.l0);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
@@ -1234,7 +1242,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(COLS ? 1 : 
         }
         __builtin_amdgcn_sched_group_barrier(SG_MFMA, 8, 0);
         __builtin_amdgcn_sched_barrier(0);
-        st0 = st1;
+        float4* const used = cur;
+        cur = nxt;
+        nxt = fill;
+        fill = used;
     };
     using I0 = std::integral_constant<int, 0>;
     using I1 = std::integral_constant<int, 1>;
@@ -1242,11 +1253,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(COLS ? 1 : 
     using I3 = std::integral_constant<int, 3>;
 
     for (int64_t ytile = y_begin; ytile < y_end; ytile += BY) {
-#pragma unroll
-        for (int b = 0; b < NB; ++b) {
-#pragma unroll
-            for (int q = 0; q < 16; ++q) acc[b][q] = 0.0f;
-        }
+        // (the tile's first K-step starts the accumulators from 0)
         // biases of this tile's Y rows and the panel's shared row thresholds, straight to LDS; the epilogue reads
         // them after the first chunk's ring barrier, which waits for them as for any load older than the chunk's
         // (loads into registers would need a wait of their own, and with it for the Y chunks in flight). Columns
