@@ -7,9 +7,11 @@ stay in the caller's host tensor and pass, in the solver's shuffled order, throu
 chunk each (bounded pinned memory, as in the reference): the host gathers chunk c into a staging buffer once that
 buffer's previous upload has finished, a side stream of default priority uploads it into one of two device buffers
 once the work queued on that buffer's previous chunk has finished, and the caller's stream waits for the upload.
-Uploads and host copies run one chunk ahead of the caller's work.
+Host copies and uploads of the next chunk run on a worker thread while the caller works on the current one.
 """
 from __future__ import annotations
+
+from concurrent.futures import ThreadPoolExecutor
 
 import torch
 
@@ -76,7 +78,9 @@ class HostRows:
 
     def chunks(self, start: int = 0, stop: int | None = None, rows: int | None = None):
         """Yields (s, e, x): x holds rows [s, e) on the device, valid on the current stream until the next step.
-        ``rows`` (at most ``chunk``) reads smaller chunks, with smaller buffers."""
+        ``rows`` (at most ``chunk``) reads smaller chunks, with smaller buffers. While the caller works on a chunk, a
+        worker thread gathers the next one into its staging buffer and queues its upload, so neither the host gather
+        nor the upload waits for the caller's work to be queued (the caller's calls synchronise the device)."""
         stop = self.rows if stop is None else int(stop)
         if stop <= start:
             return
@@ -93,29 +97,43 @@ class HostRows:
         bounds = [(s, min(stop, s + rows)) for s in range(start, stop, rows)]
         copy.wait_stream(compute)   # the device buffers were allocated on the caller's stream
 
-        def issue(index):
+        def prepare(index):
+            # chunk `index` into slot index % 2: its staging buffer once the slot's previous upload has finished,
+            # then its upload once the caller's work on the slot's previous chunk (recorded before this runs)
             slot = index % 2
             s, e = bounds[index]
             if used[slot]:
-                uploaded[slot].synchronize()     # the staging buffer's previous upload has finished
+                uploaded[slot].synchronize()
             self._read(s, e, staging[slot][: e - s])
-            with torch.cuda.stream(copy):
+            with torch.cuda.device(self.device), torch.cuda.stream(copy):
                 if used[slot]:
                     copy.wait_event(released[slot])
                 buffers[slot][: e - s].copy_(staging[slot][: e - s], non_blocking=True)
                 uploaded[slot].record(copy)
 
+        pool = ThreadPoolExecutor(max_workers=1) if len(bounds) > 1 else None
+        pending = None
         try:
-            issue(0)
+            prepare(0)
             for index, (s, e) in enumerate(bounds):
-                if index + 1 < len(bounds):
-                    issue(index + 1)
                 slot = index % 2
+                if index + 1 < len(bounds):
+                    pending = pool.submit(prepare, index + 1)
                 compute.wait_event(uploaded[slot])
                 yield s, e, buffers[slot][: e - s]
                 released[slot].record(compute)
                 used[slot] = True
+                if pending is not None:
+                    pending.result()   # the next chunk is gathered and its upload queued
+                    pending = None
         finally:
+            if pending is not None:
+                try:
+                    pending.result()
+                except Exception:   # the caller's own error is the one to report
+                    pass
+            if pool is not None:
+                pool.shutdown(wait=True)
             # later work on the caller's stream (including reuse of the buffers' memory) follows every upload, and
             # the staging buffers are not released while an upload still reads them
             compute.wait_stream(copy)
