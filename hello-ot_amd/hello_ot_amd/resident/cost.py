@@ -85,7 +85,8 @@ def merge_columns(best, new, k: int):
     holding only lower row indices than ``new``: the merged order puts ``best``'s entry first among equal values,
     which is the lowest row index. Each entry's merged rank is its own position plus the entries of the other list
     ahead of it (strictly greater values from ``new``, greater or equal ones from ``best``), found by binary search
-    in the other row; the entries of rank below k are scattered to their ranks."""
+    in the other row; every entry is scattered to its rank, those of rank k or more into one spare column that is
+    dropped (no data-dependent sizes, so nothing waits for the device)."""
     if best is None:
         return new
     av, ai = best
@@ -94,14 +95,13 @@ def merge_columns(best, new, k: int):
     na, nb = (-av).contiguous(), (-bv).contiguous()          # ascending rows for the binary searches
     rank_a = pos + torch.searchsorted(nb, na, right=False)   # entries of `new` strictly greater
     rank_b = pos[:, : bv.shape[1]] + torch.searchsorted(na, nb, right=True)   # entries of `best` greater or equal
-    out_v = torch.empty((av.shape[0], k), dtype=av.dtype, device=av.device)
-    out_i = torch.empty((av.shape[0], k), dtype=ai.dtype, device=av.device)
+    out_v = torch.empty((av.shape[0], k + 1), dtype=av.dtype, device=av.device)
+    out_i = torch.empty((av.shape[0], k + 1), dtype=ai.dtype, device=av.device)
     for rank, v, i in ((rank_a, av, ai), (rank_b, bv, bi)):
-        keep = rank < k
-        rows = torch.nonzero(keep, as_tuple=True)[0]
-        out_v[rows, rank[keep]] = v[keep]
-        out_i[rows, rank[keep]] = i[keep]
-    return out_v, out_i
+        r = rank.clamp(max=k)
+        out_v.scatter_(1, r, v)
+        out_i.scatter_(1, r, i)
+    return out_v[:, :k].contiguous(), out_i[:, :k].contiguous()
 
 
 @dataclass

@@ -379,3 +379,27 @@ def test_streamed_rows_in_shuffle_order_without_a_copy():
     assert copied.order is None and torch.equal(copied.host, host[perm])
     with pytest.raises(ValueError, match="vector"):
         HostRows(host, "cpu", order=perm.view(5, 10))
+
+
+def test_column_list_merge_against_a_sort():
+    """merge_columns on the CPU: the best k of two sorted lists per column, equal values taking the running list's
+    entries first (their rows are the lower ones), -inf sentinels included, against a stable sort of the union."""
+    from hello_ot_amd.resident.cost import merge_columns
+
+    rng = np.random.default_rng(12)
+    for _ in range(300):
+        rows, k = int(rng.integers(1, 12)), int(rng.integers(1, 6))
+        kb = int(rng.integers(1, k + 1))
+        lists = []
+        for width, base in ((k, 0), (kb, 1000)):
+            v = rng.integers(0, 4, (rows, width)).astype(np.float64)
+            v[rng.random((rows, width)) < 0.2] = -np.inf
+            lists.append((-np.sort(-v, axis=1), base + np.tile(np.arange(width), (rows, 1))))
+        (av, ai), (bv, bi) = lists
+        gv, gi = merge_columns((torch.tensor(av), torch.tensor(ai)), (torch.tensor(bv), torch.tensor(bi)), k)
+        for r in range(rows):
+            union = [(-av[r, j], 0, j, ai[r, j], av[r, j]) for j in range(k)]
+            union += [(-bv[r, j], 1, j, bi[r, j], bv[r, j]) for j in range(kb)]
+            union.sort()
+            assert gv[r].tolist() == [u[4] for u in union[:k]]
+            assert gi[r].tolist() == [u[3] for u in union[:k]]
