@@ -51,8 +51,8 @@ def offsets(features) -> torch.Tensor:
 
 # device bytes a streamed l2^2 scan's library call may take for its workspace: a call with both directions keeps
 # column lists per 256-row panel of its chunk for every column (6.6 GiB for 19968 x 1.28M), so such scans read the
-# streamed side in smaller chunks
-STREAMED_WORKSPACE_BYTES = 4 * _host.STREAM_CHUNK_BYTES
+# streamed side in smaller chunks (8192 rows for the C5 certificate, 2.9 GiB)
+STREAMED_WORKSPACE_BYTES = 3 << 30
 
 
 def fused_chunk_rows(chunk: int, n: int, d: int, k: int, certificate: bool, precision: str) -> int:
