@@ -1028,21 +1028,11 @@ __device__ __forceinline__ XOps& xset(XOps& a, XOps& b, XOps& c, XOps& d) {
     else return d;
 }
 
-// 16 bytes per lane from global memory straight to LDS: lane l writes lds_byte + 16 l (M0 holds the wave-uniform
-// LDS address). Issued from assembly: the compiler would otherwise treat every later LDS read as a possible alias
-// of these writes and wait for all outstanding loads before it. The caller waits (wait_vmcnt) before the data is
-// read, and before the workgroup ends.
-__device__ __forceinline__ void load_lds16(const char* g, unsigned lds_byte) {
-    unsigned saved;  // M0 is restored, so the compiler's use of it (if any) is untouched
-    asm volatile(
-        "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off\n\ts_nop 0\n\t"
-        "s_mov_b32 m0, %0"
-        : "=&s"(saved)
-        : "v"(g), "s"(lds_byte));
-}
-
-// Four loads as load_lds16 from one per-lane offset: lane l reads b_i + off (b_i wave-uniform) and writes
-// lds_i + 16 l; M0 is saved once.
+// Four loads of 16 bytes per lane from global memory straight to LDS: lane l reads b_i + off (b_i wave-uniform, a
+// 32-bit byte offset per lane) and writes lds_i + 16 l (M0 holds the wave-uniform LDS address; it is saved once and
+// restored, so the compiler's use of it, if any, is untouched). Issued from assembly: the compiler would otherwise
+// treat every later LDS read as a possible alias of these writes and wait for all outstanding loads before it. The
+// caller waits (wait_vmcnt) before the data is read, and before the workgroup ends.
 __device__ __forceinline__ void load_lds16x4(const char* b0, const char* b1, const char* b2, const char* b3,
                                              unsigned off, unsigned l0, unsigned l1, unsigned l2, unsigned l3) {
     unsigned saved;
@@ -1071,7 +1061,7 @@ __device__ __forceinline__ unsigned lane_here() {
 }
 
 // 4 bytes per lane from global memory straight to LDS: lane l reads base + off (a wave-uniform base, a 32-bit
-// byte offset per lane) and writes lds_byte + 4 l. As load_lds16.
+// byte offset per lane) and writes lds_byte + 4 l. As load_lds16x4.
 __device__ __forceinline__ void load_lds4(const void* base, unsigned off, unsigned lds_byte) {
     unsigned saved;
     asm volatile(
