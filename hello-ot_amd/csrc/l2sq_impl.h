@@ -1454,6 +1454,9 @@ __device__ __forceinline__ void sweep_epilogue_w(const float (&tot)[NB][16], int
             if (STATS) gev = *reinterpret_cast<const float4*>(&sGE[jl0]);
             const float dbs[4] = {dbv.x, dbv.y, dbv.z, dbv.w};
             const float ges[4] = {gev.x, gev.y, gev.z, gev.w};
+            // the lane's largest score of the group: its scores are tested for the list only when some lane of
+            // the wave has one above its list's last entry and the shared threshold
+            float amax = -INFINITY;
 #pragma unroll
             for (int cc = 0; cc < 4; ++cc) {
                 const float t = tot[y][4 * a + cc];
@@ -1465,22 +1468,34 @@ __device__ __forceinline__ void sweep_epilogue_w(const float (&tot)[NB][16], int
                         const int pos = atomicAdd(&wcnt[row], 1);
                         if (pos < wcap) wbuf[row * (int64_t)wcap + pos] = (int)j;
                     }
-                } else if (okj && w > lv[K1 - 1] && w > rthr) {
-                    float cv = w;
-                    int ci = (int)j;
+                } else {
+                    amax = fmaxf(amax, okj ? w : -INFINITY);
+                }
+                if (STATS) cert_fast(okj, w, ges[cc], pi, qbi, slack, tden, cmax, tnum, tcnt, near);
+            }
+            if (!APPEND && __any(amax > fmaxf(lv[K1 - 1], rthr))) {
+                // the group's scores in pair order, each inserted when it beats the list's last entry (as if
+                // every score had been tested)
 #pragma unroll
-                    for (int i = 0; i < K1; ++i) {
-                        if (cv > lv[i]) {
-                            const float tv = lv[i];
-                            const int ti = li[i];
-                            lv[i] = cv;
-                            li[i] = ci;
-                            cv = tv;
-                            ci = ti;
+                for (int cc = 0; cc < 4; ++cc) {
+                    const float w = fmaf(scale, tot[y][4 * a + cc], dbs[cc]);
+                    const bool okj = ok && 4 * h < ylim - (y * 32 + 8 * a + cc);
+                    if (okj && w > lv[K1 - 1] && w > rthr) {
+                        float cv = w;
+                        int ci = (int)(ytile + jl0 + cc);
+#pragma unroll
+                        for (int i = 0; i < K1; ++i) {
+                            if (cv > lv[i]) {
+                                const float tv = lv[i];
+                                const int ti = li[i];
+                                lv[i] = cv;
+                                li[i] = ci;
+                                cv = tv;
+                                ci = ti;
+                            }
                         }
                     }
                 }
-                if (STATS) cert_fast(okj, w, ges[cc], pi, qbi, slack, tden, cmax, tnum, tcnt, near);
             }
             // one group of pairs at a time: the scheduler would otherwise hoist every group's LDS reads to the
             // top of the epilogue and spill them
